@@ -1,0 +1,122 @@
+/*
+ * rlt_mi355x -- C ABI of the MI355X (gfx950) speculative-verification hot path.
+ *
+ * Plain pointers, sizes and strides only.  Every entry point:
+ *   - enqueues its kernels on `stream` and never synchronizes the host;
+ *   - allocates nothing: callers pass a device workspace of at least the size the
+ *     matching *_workspace_size() query returns;
+ *   - never writes its inputs;
+ *   - returns 0 (RLT_OK) or an rlt_status error code; numerical failure of the
+ *     sampler is reported through its `error` / `valid` outputs, not the status.
+ *
+ * Element types: RLT_F32 = 0, RLT_F16 = 1, RLT_BF16 = 2, RLT_FP8_E4M3 = 3 (OCP e4m3fn).
+ * Status codes:  0 ok, 1 bad argument, 2 unsupported, 3 workspace, 4 launch failure.
+ * Strides are in elements of the tensor they describe.
+ */
+#ifndef RLT_MI355X_H
+#define RLT_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- attention */
+
+/*
+ * Paged GQA attention over one layer's KV pool view [block, token, kv_head, dim]
+ * (the strided `key_cache[:, layer]` view of the reference pool
+ * [num_blocks, layers, block_size, kv_heads, head_dim]).
+ *
+ * Replaces, behind the same tensors and semantics:
+ *   - per-row form (cu_seqlens_q == NULL, one sequence per q row):
+ *       vllm_rlt/kernels/paged_attention.py:13-47   torch_paged_attention
+ *       vllm_rlt/kernels/triton_attention.py:176-246 paged_attention (split-KV decode)
+ *       vllm_rlt/attention/backend.py:54-55          AttentionBackend.__call__
+ *   - sliding window (window > 0):
+ *       vllm_rlt/kernels/paged_attention.py:50-90   torch_paged_attention_windowed
+ *   - packed verify window (cu_seqlens_q != NULL, int32 [num_seqs + 1]):
+ *       vllm_rlt/kernels/triton_attention.py:386-404 paged_prefill_attention
+ *       vllm_rlt/attention/backend.py:68-69          AttentionBackend.prefill
+ *     query i of sequence s sees keys < context_lengths[s] - q_len(s) + i + 1.
+ *
+ * q / out: [num_q_rows, num_q_heads, head_dim] (dim stride 1).
+ * block_tables: int32 [num_seqs, >= table_width] with row stride table_stride.
+ * context_lengths: int32 [num_seqs].  Entries outside [0, num_blocks) read block 0.
+ * Scales (FP8 pools): scale_mode 0 none, 1 per-tensor (key_scale / value_scale
+ * point at one float), 2 per-vector pools [block, token, kv_head] with the given
+ * strides (vllm_rlt/core/kv_cache_manager.py:267-271, :936-942).
+ * The grid is static (independent of lengths): safe under HIP graph capture.
+ */
+size_t rlt_paged_attention_workspace_size(int32_t num_q_rows, int32_t num_q_heads, int32_t head_dim,
+                                          int32_t table_width, int32_t block_size);
+
+int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                        const void* key_cache, const void* value_cache, int64_t k_block_stride,
+                        int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                        int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                        const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                        const int32_t* context_lengths, const int32_t* cu_seqlens_q,
+                        int32_t num_seqs, int32_t max_q_len, int32_t num_q_rows,
+                        const float* key_scale, const float* value_scale, int32_t scale_mode,
+                        int64_t s_block_stride, int64_t s_token_stride, int64_t s_head_stride,
+                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t block_size, int32_t q_dtype, int32_t kv_dtype, int32_t window,
+                        void* out, int64_t out_row_stride, int64_t out_head_stride,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* 1 when (q dtype, kv dtype, head_dim) runs on the MFMA kernel, else 0 (vector kernel). */
+int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim);
+
+/* ---------------------------------------------------------------- sampler */
+
+/*
+ * Batched speculative rejection sampling, bit-exact with the reference's torch-CPU
+ * arithmetic given identical fp32 p, q and uniforms.
+ * Replaces vllm_rlt/worker/speculative_sampling.py:104-181 speculative_accept
+ * (AcceptResult :88-101).
+ *   draft_tokens int64 [n, w1], drafts int64 [n], q fp32 [n, w1, V],
+ *   p fp32 [n, w1 + 1, V], u_accept fp32 [n, w1], u_final fp32 [n]  (contiguous)
+ *   -> tokens int64 [n, w1 + 1], accepted int64 [n], final_token int64 [n],
+ *      error uint8 (bool) [n].
+ * 0 <= w1 <= 32, 1 <= V < 2^25.
+ */
+size_t rlt_speculative_accept_workspace_size(int64_t n, int32_t w1, int64_t vocab);
+
+int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
+                           const float* p, const float* u_accept, const float* u_final, int64_t n,
+                           int32_t w1, int64_t vocab, int64_t* tokens, int64_t* accepted,
+                           int64_t* final_token, uint8_t* error, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Inverse-CDF draw from nonnegative, possibly unnormalized fp32 weights [m, V]
+ * (contiguous) with uniforms u [m]: float64 cumulative sum, threshold
+ * min(u * mass, nextafter(mass, 0)), right-bisect; invalid rows (mass not finite
+ * and positive) give index 0 and valid = 0.
+ * Replaces vllm_rlt/worker/speculative_sampling.py:59-85 categorical.
+ */
+size_t rlt_categorical_workspace_size(int64_t m, int64_t vocab);
+
+int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t vocab,
+                    int64_t* index, uint8_t* valid, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream);
+
+/*
+ * Row sums x.sum(-1, dtype=float32) of a contiguous fp32 [rows, V] matrix in the
+ * exact summation order of torch's CPU kernel (the masses computed at
+ * vllm_rlt/worker/speculative_sampling.py:138,146).
+ */
+size_t rlt_row_mass_workspace_size(int64_t rows, int64_t vocab);
+
+int rlt_row_mass_f32(const float* x, int64_t rows, int64_t vocab, float* out, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLT_MI355X_H */

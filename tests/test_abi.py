@@ -1,0 +1,78 @@
+"""The C ABI: the library loads, exports every declared entry point, and its
+host-side argument checks answer without a GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "rlt_mi355x.h")).read()
+    return sorted(set(re.findall(r"^(?:size_t|int)\s+(rlt_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    declared = _declared()
+    assert len(declared) >= 9
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.EXPORTED)
+
+
+def test_workspace_queries_are_host_only(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    assert lib.rlt_speculative_accept_workspace_size(32, 4, 49152) > 0
+    assert lib.rlt_categorical_workspace_size(8, 65536) > 0
+    # 160 rows x 16 heads x (512 blocks x 16 / 512 chunks) x (2 + 128) floats
+    n = lib.rlt_paged_attention_workspace_size(160, 16, 128, 512, 16)
+    assert n >= 160 * 16 * 16 * 130 * 4
+    assert lib.rlt_paged_attention_uses_mfma(2, 2, 128) == 1
+    assert lib.rlt_paged_attention_uses_mfma(2, 3, 96) == 1
+    assert lib.rlt_paged_attention_uses_mfma(0, 0, 128) == 0
+    assert lib.rlt_paged_attention_uses_mfma(2, 2, 7) == 0
+
+
+def test_argument_errors_return_status_without_launching(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null = ctypes.c_void_p(0)
+    # q heads not a multiple of kv heads -> RLT_ERR_ARGUMENT (1)
+    st = lib.rlt_paged_attention(null, 0, 0, null, null, 0, 0, 0, 0, 0, 0, 1, null, 0, 1, null,
+                                 null, 1, 1, 1, null, null, 0, 0, 0, 0, 6, 4, 128, 16, 2, 2, 0,
+                                 null, 0, 0, null, 0, null)
+    assert st == 1
+    # missing workspace -> RLT_ERR_WORKSPACE (3)
+    st = lib.rlt_speculative_accept(null, null, null, null, null, null, 4, 4, 1000, null, null, null,
+                                    null, null, 0, null)
+    assert st == 3
+    # vocabulary too large -> RLT_ERR_UNSUPPORTED (2)
+    st = lib.rlt_speculative_accept(null, null, null, null, null, null, 4, 4, 1 << 25, null, null,
+                                    null, null, null, 0, null)
+    assert st == 2
+
+
+def test_host_api_validates_before_touching_a_device(pkg):
+    import torch
+
+    with pytest.raises(ValueError):
+        pkg.create_backend("triton", torch.device("cpu"), torch.bfloat16, 128, 16)
+    with pytest.raises(ValueError):
+        pkg.create_backend("auto", torch.device("cpu"), torch.bfloat16, 128, 16)
+    with pytest.raises(ValueError):
+        pkg.speculative_accept(torch.zeros(2, 3, dtype=torch.long), torch.zeros(3, dtype=torch.long),
+                               torch.zeros(2, 3, 4), torch.zeros(2, 4, 4), torch.zeros(2, 3),
+                               torch.zeros(2))
+    with pytest.raises(ValueError):
+        pkg.categorical(torch.zeros(2, 4), torch.zeros(2))  # CPU tensors are refused
+    with pytest.raises(ValueError, match="window"):
+        pkg.MI355XPagedAttention().windowed(None, None, None, None, None, 0)

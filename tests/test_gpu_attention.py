@@ -1,0 +1,275 @@
+"""gfx950 paged attention against the CPU oracle (parity), bitwise invariants,
+and the reference's edge cases.  Tolerances: bf16 2e-2 abs, fp16 2e-3, fp32
+1e-5 (rel and abs)."""
+
+import math
+import sys
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import fp8 as ofp8
+from tests.attn_cases import make_pool, random_tables
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 2e-2}
+
+
+def _say(*args):
+    print("[case]", *args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def kernel(pkg, dev):
+    return pkg.MI355XPagedAttention()
+
+
+def _close(got, want, dtype):
+    tol = TOL[dtype]
+    torch.testing.assert_close(got.float().cpu(), want.float(), atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [7, 32, 64, 96, 128])
+def test_mixed_depth_rows_match_oracle(kernel, dev, dtype, head_dim):
+    # reference shape: tests/test_attention.py:21-48 (mixed requests and depths on a
+    # fragmented pool, 6 q heads over 2 kv heads, block size 3)
+    _say("mixed", dtype, head_dim)
+    g = torch.Generator().manual_seed(48 + head_dim)
+    bs, hkv, hq = 3, 2, 6
+    kpool, vpool, k, v = make_pool(80, 2, bs, hkv, head_dim, dtype, g, layer=1)
+    lengths = [7, 5, 3, 6, 1, 33, 0, 64]
+    tables = random_tables(lengths, bs, 80, g)
+    q = torch.randn(len(lengths), hq, head_dim, generator=g).to(dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    got = kernel(q.to(dev), kpool.to(dev)[:, 1], vpool.to(dev)[:, 1], tables.to(dev), ctx.to(dev))
+    want = oatt.paged_attention(q, k, v, tables, ctx)
+    _close(got, want, dtype)
+    assert torch.count_nonzero(got[6]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_split_kv_lengths_and_batch_invariance(kernel, dev, dtype):
+    # reference: tests/test_attention.py:154-184
+    _say("split", dtype)
+    g = torch.Generator().manual_seed(1)
+    bs, hq, hkv, d = 16, 8, 4, 128
+    lengths = [0, 1, 31, 32, 33, 511, 512, 513, 4097, 10000]
+    pages = sum(-(-n // bs) for n in lengths)
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables(lengths, bs, pages, g)
+    q = torch.randn(len(lengths), hq, d, generator=g).to(dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    kd, vd, td, cd, qd = k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), q.to(dev)
+    got = kernel(qd, kd, vd, td, cd)
+    _close(got, oatt.paged_attention(q, k, v, tables, ctx), dtype)
+    assert torch.count_nonzero(got[0]) == 0
+    for row in (1, 5, 8, 9):
+        alone = kernel(qd[row:row + 1], kd, vd, td[row:row + 1], cd[row:row + 1])
+        assert torch.equal(alone[0], got[row])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(64, 4, 2), (96, 8, 8), (128, 16, 4),
+                                                     (128, 16, 16)])
+def test_packed_window_matches_oracle_and_per_row_bitwise(kernel, dev, dtype, head_dim, heads,
+                                                          kv_heads):
+    # reference: tests/test_attention.py:110-151 (prefixes 32, 0, 0, 60, 9; pages out of order)
+    _say("packed", dtype, head_dim, heads, kv_heads)
+    g = torch.Generator().manual_seed(0)
+    bs = 16
+    seqs = [(37, 5), (100, 100), (3, 3), (130, 70), (129, 120), (700, 5), (5, 5)]
+    pages = sum(-(-n // bs) for n, _ in seqs) + 3
+    _, _, k, v = make_pool(pages, 1, bs, kv_heads, head_dim, dtype, g)
+    tables = random_tables([n for n, _ in seqs], bs, pages, g)
+    total = sum(c for _, c in seqs)
+    q = torch.randn(total, heads, head_dim, generator=g).to(dtype)
+    lengths = torch.tensor([n for n, _ in seqs], dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor([c for _, c in seqs]).cumsum(0)), dtype=torch.int32)
+    kd, vd = k.to(dev), v.to(dev)
+    packed = kernel.prefill(q.to(dev), kd, vd, tables.to(dev), lengths.to(dev), cu.to(dev),
+                            max(c for _, c in seqs))
+    want = oatt.packed_window_attention(q, k, v, tables, lengths, cu)
+    _close(packed, want, dtype)
+    seq_of_row, row_len = oatt.packed_row_layout(lengths, cu)
+    per_row = kernel(q.to(dev), kd, vd, tables[torch.tensor(seq_of_row)].to(dev),
+                     torch.tensor(row_len, dtype=torch.int32).to(dev))
+    assert torch.equal(per_row, packed), "packed window differs from per-row decode"
+
+
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("fixed", [False, True])
+def test_fp8_pool_matches_oracle(kernel, dev, q_dtype, fixed):
+    # reference: tests/test_fp8_kv_cache.py:69-84, :235-262
+    _say("fp8", q_dtype, fixed)
+    g = torch.Generator().manual_seed(5)
+    bs, hkv, hq, d, layers = 16, 2, 8, 128, 2
+    lengths = [1, 17, 300, 1025]
+    pages = sum(-(-n // bs) for n in lengths)
+    x = torch.randn(pages, layers, bs, hkv, d, generator=g) * 3
+    y = torch.randn(pages, layers, bs, hkv, d, generator=g)
+    kc, ks = ofp8.quantize_fp8(x, 0.05 if fixed else None)
+    vc, vs = ofp8.quantize_fp8(y, 0.02 if fixed else None)
+    tables = random_tables(lengths, bs, pages, g)
+    q = torch.randn(len(lengths), hq, d, generator=g).to(q_dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    if fixed:
+        kss, vss = torch.tensor(0.05), torch.tensor(0.02)
+        args_dev = (kss.to(dev), vss.to(dev))
+        args_cpu = (kss, vss)
+    else:
+        args_dev = (ks.to(dev)[:, 1], vs.to(dev)[:, 1])
+        args_cpu = (ks[:, 1], vs[:, 1])
+    got = kernel(q.to(dev), kc.to(dev)[:, 1], vc.to(dev)[:, 1], tables.to(dev), ctx.to(dev), *args_dev)
+    want = oatt.paged_attention(q, kc[:, 1], vc[:, 1], tables, ctx, *args_cpu)
+    tol = 2e-2 if q_dtype == torch.bfloat16 else 1e-5
+    torch.testing.assert_close(got.float().cpu(), want.float(), atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sliding_window_matches_oracle(kernel, dev, dtype):
+    # reference: kernels/paged_attention.py:50-90; tests/test_fp8_kv_cache.py:87-103
+    _say("window", dtype)
+    g = torch.Generator().manual_seed(9)
+    bs, hkv, hq, d = 16, 4, 8, 128
+    lengths = [1, 3, 40, 600, 2000]
+    pages = sum(-(-n // bs) for n in lengths)
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables(lengths, bs, pages, g)
+    q = torch.randn(len(lengths), hq, d, generator=g).to(dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    for window in (3, 100, 513):
+        got = kernel.windowed(q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), window)
+        _close(got, oatt.paged_attention(q, k, v, tables, ctx, window=window), dtype)
+
+
+def test_empty_batch_and_bad_arguments(kernel, dev):
+    q = torch.empty(0, 4, 128, device=dev, dtype=torch.bfloat16)
+    k = torch.zeros(4, 16, 2, 128, device=dev, dtype=torch.bfloat16)
+    t = torch.zeros(0, 1, dtype=torch.int32, device=dev)
+    out = kernel(q, k, k, t, torch.zeros(0, dtype=torch.int32, device=dev))
+    assert out.shape == (0, 4, 128)
+    with pytest.raises(ValueError):
+        kernel(torch.zeros(1, 3, 128, device=dev, dtype=torch.bfloat16), k, k,
+               torch.zeros(1, 1, dtype=torch.int32, device=dev),
+               torch.ones(1, dtype=torch.int32, device=dev))
+    with pytest.raises(ValueError):
+        kernel.windowed(q, k, k, t, t[:, 0], 0)
+
+
+def test_int32_block_ids_use_64bit_offsets(kernel, dev):
+    # reference: tests/test_attention_64bit.py:8-29
+    if torch.cuda.mem_get_info()[0] < 9 * 2**30:
+        pytest.skip("needs 9 GiB free")
+    shape, strides = (2049, 1, 1, 16), (2**20, 16, 16, 1)
+    key = torch.empty_strided(shape, strides, device=dev, dtype=torch.float16)
+    value = torch.empty_strided(shape, strides, device=dev, dtype=torch.float16)
+    key[0].zero_()
+    value[0].fill_(-3)
+    key[2048].fill_(1)
+    expected = torch.arange(16, device=dev, dtype=torch.float16).view(1, 1, 16)
+    value[2048].copy_(expected)
+    query = torch.ones((1, 1, 16), device=dev, dtype=torch.float16)
+    table = torch.tensor([[2048]], device=dev, dtype=torch.int32)
+    out = kernel(query, key, value, table, torch.tensor([1], device=dev, dtype=torch.int32))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out, expected, rtol=0, atol=0)
+
+
+def test_out_of_pool_table_entries_stay_inside_the_pool(kernel, dev):
+    # A corrupt table entry must not address memory outside the pool (reads block 0).
+    k = torch.randn(4, 16, 1, 64, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(1, 1, 64, device=dev, dtype=torch.bfloat16)
+    bad = torch.tensor([[-1, 1 << 30]], device=dev, dtype=torch.int32)
+    good = torch.tensor([[0, 0]], device=dev, dtype=torch.int32)
+    ctx = torch.tensor([32], device=dev, dtype=torch.int32)
+    assert torch.equal(kernel(q, k, k, bad, ctx), kernel(q, k, k, good, ctx))
+
+
+# ---------------------------------------------------------------- BASELINE configs
+# Shapes of BASELINE.json configs 2-5 at reduced batch (the oracle is a Python loop);
+# the full-size configs run in bench.py.
+
+def _plane_tables(n_req, planes, max_len, bs, g, pool_blocks):
+    """LAST_EXITED pools: each request owns `planes` tables of ceil(max_len/bs) blocks."""
+    per = -(-max_len // bs)
+    order = torch.randperm(pool_blocks, generator=g)
+    return order[: n_req * planes * per].view(n_req, planes, per).int()
+
+
+def test_config2_depth_aware_decode(kernel, dev):
+    _say("config2")
+    g = torch.Generator().manual_seed(2)
+    n, planes, bs, h, d, layers = 8, 4, 16, 16, 128, 2
+    lengths = torch.randint(512, 4097, (n,), generator=g)
+    exit_depth = torch.randint(1, 5, (n,), generator=g)
+    pool = n * planes * 256
+    kpool, vpool, k, v = make_pool(pool, layers, bs, h, d, torch.bfloat16, g, layer=1)
+    tables = _plane_tables(n, planes, 4096, bs, g, pool)
+    row_tables = tables[torch.arange(n), exit_depth - 1]
+    q = torch.randn(n, h, d, generator=g).bfloat16()
+    ctx = lengths.int()
+    got = kernel(q.to(dev), kpool.to(dev)[:, 1], vpool.to(dev)[:, 1], row_tables.to(dev), ctx.to(dev))
+    _close(got, oatt.paged_attention(q, k, v, row_tables, ctx), torch.bfloat16)
+
+
+def test_config3_verify_window_gqa4(kernel, dev):
+    _say("config3")
+    g = torch.Generator().manual_seed(3)
+    n, w, bs, hq, hkv, d = 6, 5, 16, 16, 4, 128
+    lengths = torch.randint(1024, 8193, (n,), generator=g)
+    pool = n * 512
+    _, _, k, v = make_pool(pool, 1, bs, hkv, d, torch.bfloat16, g)
+    tables = torch.randperm(pool, generator=g)[: n * 512].view(n, 512).int()
+    q = torch.randn(n * w, hq, d, generator=g).bfloat16()
+    cu = torch.arange(0, n * w + 1, w, dtype=torch.int32)
+    got = kernel.prefill(q.to(dev), k.to(dev), v.to(dev), tables.to(dev), lengths.int().to(dev),
+                         cu.to(dev), w)
+    _close(got, oatt.packed_window_attention(q, k, v, tables, lengths.int(), cu), torch.bfloat16)
+
+
+def test_config4_wide_heads_d96_32_planes(kernel, dev):
+    _say("config4")
+    g = torch.Generator().manual_seed(4)
+    n, w, planes, bs, h, d = 3, 5, 32, 16, 55, 96
+    per = 2048 // bs
+    pool = n * planes * per
+    _, _, k, v = make_pool(pool, 1, bs, h, d, torch.bfloat16, g)
+    tables = _plane_tables(n, planes, 2048, bs, g, pool)
+    exit_depth = torch.randint(8, 33, (n,), generator=g)
+    seq_tables = tables[torch.arange(n), exit_depth - 1]
+    lengths = torch.full((n,), 2048, dtype=torch.int32)
+    q = torch.randn(n * w, h, d, generator=g).bfloat16()
+    cu = torch.arange(0, n * w + 1, w, dtype=torch.int32)
+    got = kernel.prefill(q.to(dev), k.to(dev), v.to(dev), seq_tables.to(dev), lengths.to(dev),
+                         cu.to(dev), w)
+    _close(got, oatt.packed_window_attention(q, k, v, seq_tables, lengths, cu), torch.bfloat16)
+
+
+def test_config5_fp8_rows_at_different_planes(kernel, dev):
+    _say("config5")
+    g = torch.Generator().manual_seed(5)
+    n, w, planes, bs, hq, hkv, d = 2, 5, 4, 16, 16, 8, 128
+    max_len = 16384 + 8
+    per = -(-max_len // bs)
+    pool = n * planes * per
+    x = (torch.randn(pool, 1, bs, hkv, d, generator=g) * 8)
+    kc = x.clamp(-448, 448).to(torch.float8_e4m3fn)[:, 0]
+    vc = (torch.randn(pool, 1, bs, hkv, d, generator=g) * 8).clamp(-448, 448).to(torch.float8_e4m3fn)[:, 0]
+    tables = _plane_tables(n, planes, max_len, bs, g, pool)
+    start = torch.randint(16384, 16384 + 4, (n,), generator=g)
+    d0 = torch.randint(0, planes, (n,), generator=g)
+    rows_t, rows_len = [], []
+    for i in range(n):
+        for j in range(w):
+            rows_t.append(tables[i, (d0[i] + j) % planes])
+            rows_len.append(int(start[i]) + j + 1)
+    row_tables = torch.stack(rows_t)
+    ctx = torch.tensor(rows_len, dtype=torch.int32)
+    q = torch.randn(n * w, hq, d, generator=g).bfloat16()
+    sk, sv = torch.tensor(0.03), torch.tensor(0.05)
+    got = kernel(q.to(dev), kc.to(dev), vc.to(dev), row_tables.to(dev), ctx.to(dev), sk.to(dev), sv.to(dev))
+    _close(got, oatt.paged_attention(q, kc, vc, row_tables, ctx, sk, sv), torch.bfloat16)

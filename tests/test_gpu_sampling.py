@@ -1,0 +1,164 @@
+"""gfx950 acceptance sampler: reference known answers, and bit-exact parity with
+the torch-CPU oracle on seeded inputs shaped like BASELINE.json configs 1 and 3-5."""
+
+import sys
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling as osamp
+from tests import kat_sampling as kats
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*args):
+    print("[case]", *args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def impl(pkg, dev):
+    return types.SimpleNamespace(categorical=pkg.categorical, speculative_accept=pkg.speculative_accept)
+
+
+@pytest.mark.parametrize("kat", kats.ALL_KATS, ids=lambda f: f.__name__)
+def test_gpu_known_answers(impl, dev, kat):
+    _say(kat.__name__)
+    kat(impl, dev)
+
+
+@pytest.mark.parametrize("V", [1, 3, 5, 8, 9, 31, 32, 33, 100, 511, 512, 513, 4096, 8191, 8192,
+                               8193, 12345, 49152, 65536, 70001, 262144 + 77])
+def test_row_mass_is_torch_cpu_sum_bitwise(pkg, dev, V):
+    _say("row_mass", V)
+    g = torch.Generator().manual_seed(V)
+    x = torch.rand(5, V, generator=g)
+    x[0] = x[0] ** 8
+    x[1] = x[1] * 1e-38
+    x[2] = torch.randn(V, generator=g) * 1e6
+    x[3] = torch.softmax(torch.randn(V, generator=g) * 3, -1)
+    want = x.sum(-1, dtype=torch.float32)
+    got = pkg.sampling.row_mass(x.to(dev)).cpu()
+    assert np.array_equal(want.numpy().view(np.int32), got.numpy().view(np.int32))
+
+
+def _verify_inputs(n, w1, vocab, g, temperature=1.0, top_p=1.0, noise=1.0, draft_std=3.0):
+    """BASELINE config shape: draft logits ~N(0, draft_std^2), target = draft + N(0, noise^2)."""
+    dl = torch.randn(n, w1 + 1, vocab, generator=g) * draft_std
+    tl = dl + torch.randn(n, w1 + 1, vocab, generator=g) * noise
+    t = torch.full((n * w1,), temperature)
+    k = torch.full((n * w1,), -1, dtype=torch.int64)
+    pp = torch.full((n * w1,), top_p)
+    q = osamp.batched_probabilities(dl[:, :w1].reshape(-1, vocab), t, k, pp, max_top_k=0,
+                                    apply_top_p=top_p < 1).view(n, w1, vocab)
+    t2 = torch.full((n * (w1 + 1),), temperature)
+    p = osamp.batched_probabilities(tl.reshape(-1, vocab), t2, torch.full_like(t2, -1).long(),
+                                    torch.full_like(t2, top_p), max_top_k=0,
+                                    apply_top_p=top_p < 1).view(n, w1 + 1, vocab)
+    u = osamp.request_uniforms(torch.randint(0, 2**31, (n,), generator=g).tolist(), w1)
+    drafts_tok = torch.stack([osamp.categorical(q[:, j], u[:, j])[0] for j in range(w1)], 1)
+    return q, p, u, drafts_tok
+
+
+def _check_accept(pkg, dev, q, p, u, draft_tokens, drafts):
+    w1 = draft_tokens.shape[1]
+    ua, uf = u[:, w1:2 * w1].contiguous(), u[:, 2 * w1].contiguous()
+    want = osamp.speculative_accept(draft_tokens, drafts, q, p, ua, uf)
+    got = pkg.speculative_accept(draft_tokens.to(dev), drafts.to(dev), q.to(dev), p.to(dev),
+                                 ua.to(dev), uf.to(dev))
+    for a, b, name in zip(got, want, want._fields):
+        assert torch.equal(a.cpu(), b), name
+    return want
+
+
+@pytest.mark.parametrize("name,n,vocab,temperature,top_p", [
+    ("config1", 8, 49152, 1.0, 1.0),
+    ("config3", 32, 49152, 0.7, 0.9),
+    ("config4", 16, 65536, 1.0, 1.0),
+    ("config5", 64, 65536, 1.0, 1.0),
+])
+def test_accept_bit_exact_on_baseline_configs(pkg, dev, name, n, vocab, temperature, top_p):
+    _say("accept", name)
+    g = torch.Generator().manual_seed(hash(name) % 1000)
+    w1 = 4
+    q, p, u, dt = _verify_inputs(n, w1, vocab, g, temperature, top_p)
+    drafts = torch.full((n,), w1, dtype=torch.int64)
+    want = _check_accept(pkg, dev, q, p, u, dt, drafts)
+    assert not want.error.any()
+
+
+def test_accept_ragged_drafts_and_poisoned_padding(pkg, dev):
+    _say("accept ragged")
+    g = torch.Generator().manual_seed(77)
+    n, w1, vocab = 40, 4, 3000
+    q, p, u, dt = _verify_inputs(n, w1, vocab, g, noise=0.3)
+    drafts = torch.randint(0, w1 + 1, (n,), generator=g)
+    for i in range(n):
+        d = int(drafts[i])
+        q[i, d:] = float("nan")
+        p[i, d + 1:] = float("nan")
+    drafts[3] = 7  # out of range count: flagged, not honoured
+    drafts[4] = -1
+    dt[5, 0] = vocab + 3  # out-of-range token
+    _check_accept(pkg, dev, q, p, u, dt, drafts)
+
+
+def test_accept_high_acceptance_and_unnormalized_weights(pkg, dev):
+    _say("accept unnormalized")
+    g = torch.Generator().manual_seed(78)
+    n, w1, vocab = 24, 4, 49152
+    q, p, u, dt = _verify_inputs(n, w1, vocab, g, noise=0.05)
+    q = q * torch.rand(n, w1, 1, generator=g) * 7  # raw weights: normalized inside
+    p = p * torch.rand(n, w1 + 1, 1, generator=g) * 3
+    _check_accept(pkg, dev, q, p, u, dt, torch.full((n,), w1, dtype=torch.int64))
+
+
+@pytest.mark.parametrize("vocab", [1, 2, 7, 2047, 2048, 2049, 49152, 65536])
+def test_categorical_bit_exact_random(pkg, dev, vocab):
+    _say("categorical", vocab)
+    g = torch.Generator().manual_seed(vocab)
+    m = 64
+    w = torch.rand(m, vocab, generator=g) ** 6
+    w[w < 0.05] = 0
+    w[1] = 0
+    w[2, vocab // 2] = float("nan")
+    u = torch.rand(m, generator=g)
+    u[3], u[4], u[5] = 0.0, kats.BELOW_ONE, 1.0
+    want = osamp.categorical(w, u)
+    got = pkg.categorical(w.to(dev), u.to(dev))
+    assert torch.equal(got[0].cpu(), want[0]) and torch.equal(got[1].cpu(), want[1])
+
+
+def test_categorical_boundary_thresholds_take_the_exact_path(pkg, dev):
+    # Thresholds placed exactly on cumulative boundaries (dyadic weights, exact
+    # sums): the fast path cannot certify them, so the sequential replay decides.
+    _say("categorical boundaries")
+    vocab = 5000
+    w = torch.zeros(vocab)
+    w[::7] = 0.25
+    w[3::11] = 0.5
+    m = 256
+    c = w.double().cumsum(0)
+    mass = c[-1].item()
+    picks = torch.linspace(0, vocab - 1, m).long()
+    u = (c[picks] / mass).float()
+    u = torch.where(u >= 1, torch.tensor(kats.BELOW_ONE), u)
+    ww = w.expand(m, -1).contiguous()
+    want = osamp.categorical(ww, u)
+    got = pkg.categorical(ww.to(dev), u.to(dev))
+    assert torch.equal(got[0].cpu(), want[0]) and torch.equal(got[1].cpu(), want[1])
+
+
+def test_inputs_are_not_modified(pkg, dev):
+    g = torch.Generator().manual_seed(9)
+    q, p, u, dt = _verify_inputs(4, 3, 777, g)
+    args = [dt.to(dev), torch.full((4,), 3).to(dev), q.to(dev), p.to(dev),
+            u[:, 3:6].contiguous().to(dev), u[:, 6].contiguous().to(dev)]
+    before = [a.clone() for a in args]
+    pkg.speculative_accept(*args)
+    torch.cuda.synchronize()
+    for a, b in zip(args, before):
+        assert torch.equal(a, b)

@@ -1,0 +1,105 @@
+"""ctypes binding of librlt_mi355x.so (the C ABI declared in include/rlt_mi355x.h).
+
+There is no fallback: if the library is missing or the device is not a ROCm
+GPU, every op raises.  Build it with ``python vllm-rlt_amd/build.py`` (or
+``__graft_entry__.build()``).
+"""
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librlt_mi355x.so")
+
+RLT_F32, RLT_F16, RLT_BF16, RLT_FP8_E4M3 = 0, 1, 2, 3
+_DTYPE_CODE = {
+    torch.float32: RLT_F32,
+    torch.float16: RLT_F16,
+    torch.bfloat16: RLT_BF16,
+    torch.float8_e4m3fn: RLT_FP8_E4M3,
+}
+_STATUS = {
+    1: "invalid argument",
+    2: "unsupported configuration",
+    3: "workspace too small",
+    4: "kernel launch failed",
+}
+
+_i32, _i64, _sz, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
+
+_SIGNATURES = {
+    "rlt_paged_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "rlt_paged_attention_uses_mfma": (ctypes.c_int, [_i32, _i32, _i32]),
+    "rlt_paged_attention": (ctypes.c_int, [
+        _p, _i64, _i64,                 # q
+        _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,  # k, v, strides
+        _i32,                           # num_blocks
+        _p, _i64, _i32,                 # tables
+        _p, _p, _i32, _i32, _i32,       # lengths, cu, num_seqs, max_q_len, num_q_rows
+        _p, _p, _i32, _i64, _i64, _i64,  # scales
+        _i32, _i32, _i32, _i32,         # hq, hkv, head_dim, block_size
+        _i32, _i32, _i32,               # q dtype, kv dtype, window
+        _p, _i64, _i64,                 # out
+        _p, _sz, _p,                    # workspace, bytes, stream
+    ]),
+    "rlt_speculative_accept_workspace_size": (_sz, [_i64, _i32, _i64]),
+    "rlt_speculative_accept": (ctypes.c_int, [
+        _p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _p, _p, _p, _p, _p, _sz, _p]),
+    "rlt_categorical_workspace_size": (_sz, [_i64, _i64]),
+    "rlt_categorical": (ctypes.c_int, [_p, _p, _i64, _i64, _p, _p, _p, _sz, _p]),
+    "rlt_row_mass_workspace_size": (_sz, [_i64, _i64]),
+    "rlt_row_mass_f32": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _sz, _p]),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lib = None
+
+
+def library():
+    """Load the shared library once; raise if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python vllm-rlt_amd/build.py`; "
+                "there is no fallback implementation")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def dtype_code(dtype):
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}") from None
+
+
+def check(status, what):
+    if status != 0:
+        raise RuntimeError(f"{what}: {_STATUS.get(status, f'status {status}')}")
+
+
+def require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("the MI355X kernels require ROCm device tensors")
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,238 @@
+"""MI355X paged-attention backend behind the reference attention-backend interface.
+
+Mirrors vllm_rlt/attention/backend.py (``BackendCapabilities`` :19-36,
+``AttentionBackend`` :40-83, ``create_backend`` :177-276) and the kernel-object
+protocol of vllm_rlt/kernels/paged_attention.py (``__call__`` / ``windowed`` /
+``prefill``), so the KV cache manager's call sites
+(vllm_rlt/core/kv_cache_manager.py:993-1018) and the graph-time call site
+(vllm_rlt/worker/cuda_graph.py:161-167) drive it unchanged.
+
+Every call launches the gfx950 kernels of librlt_mi355x.so on the current HIP
+stream: no host synchronization, no fallback, static grids (capturable in HIP
+graphs).  The per-row, windowed and packed forms share one kernel whose per-row
+arithmetic is independent of batch composition, which is why this backend can
+declare ``packed_matches_decode``.
+"""
+
+import logging
+from dataclasses import dataclass, replace
+
+import torch
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class BackendCapabilities:
+    """Execution features; field meanings follow vllm_rlt/attention/backend.py:19-36."""
+
+    packed_prefill: bool = False
+    cuda_graphs: bool = False
+    async_scheduling: bool = False
+    packed_matches_decode: bool = False
+    fp8_kv: bool = False
+    fp8_kv_static: bool = False
+    device_context_lengths: bool = False
+    sliding_window: bool = False
+    packed_sliding_window: bool = False
+
+
+@dataclass
+class AttentionBackend:
+    """Kernel adapter with declared features; reference: backend.py:40-83."""
+
+    kernel: object
+    capabilities: BackendCapabilities
+    info: dict
+
+    def __call__(self, *args, **kwargs):
+        return self.kernel(*args, **kwargs)
+
+    def attend_metadata(self, q, keys, values, batch, **kwargs):
+        method = getattr(self.kernel, "attend_metadata", None)
+        if method is not None:
+            return method(q, keys, values, batch, **kwargs)
+        if getattr(batch, "cu_seqlens_q", None) is not None:
+            return self.prefill(q, keys, values, batch.block_tables, batch.context_lengths,
+                                batch.cu_seqlens_q, batch.max_seqlen_q, **kwargs)
+        return self(q, keys, values, batch.block_tables, batch.context_lengths, **kwargs)
+
+    def prefill(self, *args, **kwargs):
+        return self.kernel.prefill(*args, **kwargs)
+
+    def windowed(self, *args, **kwargs):
+        method = getattr(self.kernel, "windowed", None)
+        if method is None:
+            selected = self.info.get("selected_backend", "this attention backend")
+            raise NotImplementedError(f"{selected} does not implement sliding-window masking")
+        return method(*args, **kwargs)
+
+    @property
+    def generation(self):
+        return getattr(self.kernel, "generation", None)
+
+
+MI355X_CAPABILITIES = BackendCapabilities(
+    packed_prefill=True,
+    cuda_graphs=True,
+    async_scheduling=True,
+    packed_matches_decode=True,
+    fp8_kv=True,
+    fp8_kv_static=True,
+    device_context_lengths=True,
+    sliding_window=True,
+    packed_sliding_window=True,
+)
+
+
+def _scale_args(key_scale, value_scale):
+    """(mode, key ptr tensor, value ptr tensor, strides) of the FP8 scale arguments."""
+    if key_scale is None and value_scale is None:
+        return 0, None, None, (0, 0, 0)
+    if key_scale is None or value_scale is None:
+        raise ValueError("key_scale and value_scale must be given together")
+    for s in (key_scale, value_scale):
+        if s.dtype != torch.float32:
+            raise ValueError("FP8 scales must be float32")
+    if key_scale.dim() == 0 and value_scale.dim() == 0:
+        return 1, key_scale, value_scale, (0, 0, 0)
+    if key_scale.dim() != 3 or key_scale.stride() != value_scale.stride():
+        raise ValueError("per-vector FP8 scales must be [block, token, kv_head] views sharing strides")
+    return 2, key_scale, value_scale, tuple(key_scale.stride())
+
+
+class MI355XPagedAttention:
+    """Split-KV paged GQA attention on gfx950 (per-row, windowed and packed forms)."""
+
+    generation = None
+
+    def _run(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+             max_seqlen_q, key_scale, value_scale, window):
+        if type(window) is not int or window < 0:
+            raise ValueError("window must be a nonnegative integer")
+        _lib.require_gpu(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+                         key_scale, value_scale)
+        if q.ndim != 3 or key_cache.ndim != 4 or value_cache.ndim != 4:
+            raise ValueError("q must be [rows, heads, dim] and caches [block, token, kv_head, dim]")
+        head_dim = q.shape[-1]
+        if head_dim > 256:
+            raise ValueError("the MI355X attention backend supports head_dim <= 256")
+        if key_cache.shape != value_cache.shape or key_cache.dtype != value_cache.dtype:
+            raise ValueError("key and value caches must share shape and dtype")
+        num_blocks, block_size, kv_heads, kdim = key_cache.shape
+        if kdim != head_dim or q.shape[1] % kv_heads:
+            raise ValueError("q heads must be a positive multiple of KV heads with equal head_dim")
+        if key_cache.stride(3) != 1 or value_cache.stride(3) != 1:
+            raise ValueError("paged attention requires a contiguous head dimension")
+        output = torch.empty_like(q)
+        rows = q.shape[0]
+        if rows == 0 or block_tables.shape[0] == 0:
+            return output
+        if q.stride(2) != 1:
+            q = q.contiguous()
+        mode, ks, vs, s_strides = _scale_args(key_scale, value_scale)
+        if key_cache.dtype == torch.float8_e4m3fn and mode == 0:
+            raise ValueError("an FP8 KV pool needs key_scale / value_scale")
+        tables = block_tables if block_tables.dtype == torch.int32 else block_tables.int()
+        lengths = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.int()
+        if tables.stride(1) != 1:
+            tables = tables.contiguous()
+        lengths = lengths.contiguous()
+        num_seqs = tables.shape[0]
+        if cu_seqlens_q is None:
+            if num_seqs != rows or lengths.shape[0] != rows:
+                raise ValueError("per-row attention needs one block table and length per q row")
+            cu = None
+            max_q = 1
+        else:
+            cu = cu_seqlens_q if cu_seqlens_q.dtype == torch.int32 else cu_seqlens_q.int()
+            cu = cu.contiguous()
+            if cu.shape[0] != num_seqs + 1 or lengths.shape[0] != num_seqs:
+                raise ValueError("cu_seqlens_q must be [sequences + 1] and lengths [sequences]")
+            max_q = int(max_seqlen_q)
+        lib = _lib.library()
+        heads = q.shape[1]
+        width = tables.shape[1]
+        nbytes = lib.rlt_paged_attention_workspace_size(rows, heads, head_dim, width, block_size)
+        ws = _lib.workspace(nbytes, q.device)
+        status = lib.rlt_paged_attention(
+            _lib.ptr(q), q.stride(0), q.stride(1),
+            _lib.ptr(key_cache), _lib.ptr(value_cache),
+            key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+            value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
+            num_blocks,
+            _lib.ptr(tables), tables.stride(0), width,
+            _lib.ptr(lengths), _lib.ptr(cu), num_seqs, max_q, rows,
+            _lib.ptr(ks), _lib.ptr(vs), mode, *s_strides,
+            heads, kv_heads, head_dim, block_size,
+            _lib.dtype_code(q.dtype), _lib.dtype_code(key_cache.dtype), window,
+            _lib.ptr(output), output.stride(0), output.stride(1),
+            _lib.ptr(ws), ws.numel(), _lib.stream_of(q.device))
+        _lib.check(status, "rlt_paged_attention")
+        return output
+
+    def __call__(self, q, key_cache, value_cache, block_tables, context_lengths,
+                 key_scale=None, value_scale=None):
+        """Per-row decode / verify; reference: kernels/paged_attention.py:13-47, :210-220."""
+        return self._run(q, key_cache, value_cache, block_tables, context_lengths, None, 1,
+                         key_scale, value_scale, 0)
+
+    def windowed(self, q, key_cache, value_cache, block_tables, context_lengths, window,
+                 key_scale=None, value_scale=None):
+        """Last-``window``-keys masking; reference: kernels/paged_attention.py:50-90."""
+        if isinstance(window, bool) or not isinstance(window, int) or window <= 0:
+            raise ValueError("window must be a positive integer")
+        return self._run(q, key_cache, value_cache, block_tables, context_lengths, None, 1,
+                         key_scale, value_scale, window)
+
+    def prefill(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+                max_seqlen_q, key_scale=None, value_scale=None, *, window=0):
+        """Packed causal window, bottom-right aligned; reference: triton_attention.py:386-404."""
+        return self._run(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+                         max_seqlen_q, key_scale, value_scale, window)
+
+    def uses_mfma(self, q_dtype, kv_dtype, head_dim):
+        lib = _lib.library()
+        return bool(lib.rlt_paged_attention_uses_mfma(_lib.dtype_code(q_dtype),
+                                                      _lib.dtype_code(kv_dtype), head_dim))
+
+
+_BACKEND_NAMES = ("auto", "mi355x")
+
+
+def create_backend(backend, device, dtype, head_dim, block_size, *,
+                   required_capabilities=BackendCapabilities(), prefer_packed_prefill=False,
+                   packed_window_shape=None, allow_fp8_calibration=False):
+    """Select the MI355X backend; explicit failures, no silent fallback.
+
+    reference: vllm_rlt/attention/backend.py:177-276.  There is exactly one
+    implementation, so ``auto`` and ``mi355x`` are the same choice; any other
+    name, a non-ROCm device, head_dim > 256 or a missing capability raises.
+    """
+    if backend not in _BACKEND_NAMES:
+        raise ValueError("unknown attention backend")
+    device = torch.device(device)
+    if device.type != "cuda" or torch.version.hip is None:
+        raise ValueError("the MI355X attention backend requires a ROCm device")
+    if head_dim > 256:
+        raise ValueError("the MI355X attention backend supports head_dim <= 256")
+    if dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError(f"unsupported attention dtype {dtype}")
+    _lib.library()  # fail at selection time, before the KV pool is allocated
+    capabilities = MI355X_CAPABILITIES
+    names = ("packed_prefill", "cuda_graphs", "async_scheduling", "device_context_lengths",
+             "fp8_kv", "fp8_kv_static", "sliding_window", "packed_sliding_window")
+    missing = [n for n in names
+               if getattr(required_capabilities, n) and not getattr(capabilities, n)]
+    if missing:
+        raise ValueError(f"mi355x lacks required capabilities: {', '.join(missing)}")
+    kernel = MI355XPagedAttention()
+    info = {
+        "backend": "mi355x",
+        "requested_backend": backend,
+        "selected_backend": "mi355x",
+        "selection_reason": "single gfx950 implementation",
+        "math": "mfma" if kernel.uses_mfma(dtype, dtype, head_dim) else "vector",
+    }
+    logging.getLogger(__name__).info("Attention selection: %s", info)
+    return AttentionBackend(kernel, replace(capabilities), info)

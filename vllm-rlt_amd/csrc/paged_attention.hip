@@ -1,0 +1,932 @@
+// Depth-aware paged-KV attention for speculative verification on MI355X (gfx950).
+//
+// One kernel family serves both forms of the reference attention boundary:
+//  * per-row decode / verify (``AttentionBackend.__call__``,
+//    vllm_rlt/kernels/paged_attention.py:13-47, triton_attention.py:176-246): every
+//    q row has its own block table and context length;
+//  * packed verify window (``AttentionBackend.prefill``, triton_attention.py:386-404):
+//    sequence s owns q rows cu[s]:cu[s+1], one block table, and query i sees keys
+//    < len - q_len + i + 1 (bottom-right aligned causal window).
+// The per-row form is the packed form with q_len = 1 per row.
+//
+// Work decomposition (all static, graph-capturable: no length-dependent grid):
+//  grid (sequence x row-group, kv head, chunk).  A chunk is kChunk = 512 absolute
+//  key positions [512c, 512c + 512); its workgroup runs 4 waves on 128 positions
+//  each, in 16-position tiles.  Every row of the sequence (q_len window rows x
+//  GQA group) that attends to a kv head is handled by the SAME workgroup, so each
+//  KV byte is read once per (sequence, kv head) instead of once per q row.
+//  Partial (max, sum, unnormalized output) per (row, head, chunk) go to a
+//  workspace; rlt_merge_kernel combines a row's chunks in chunk order.
+//
+// A row's arithmetic depends only on its own length, the absolute tile / chunk
+// boundaries and its own q vector -- never on which other rows share its
+// workgroup -- so packed verify equals per-row decode bit for bit and results are
+// batch invariant (the reference's ``packed_matches_decode`` contract,
+// vllm_rlt/attention/backend.py:25-27).
+//
+// Math paths (chosen by dtype and head_dim only, never by row count):
+//  * MFMA (q bf16/fp16, KV same type or fp8-e4m3, head_dim % 32 == 0, <= 256):
+//    S^T = K Q^T with v_mfma_f32_16x16x32_{bf16,f16} straight from global memory
+//    (each lane holds one key position's contiguous head_dim/4 slice, which is the
+//    A-operand layout), online softmax in fp32 (log2 domain), then
+//    O^T = V^T P^T with v_mfma_f32_16x16x16: the P^T operand is exactly the
+//    S^T accumulator layout, V^T comes from a wave-private LDS transpose.
+//  * vector (fp32 q, or any other head_dim <= 256): fp32 FMA dot products.
+
+#include "common.h"
+#include "rlt_mi355x.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int kChunk = 512;       // key positions per workgroup (split unit)
+constexpr int kWaves = 4;
+constexpr int kWaveSpan = kChunk / kWaves;  // 128 positions per wave
+constexpr int kTileTok = 16;
+constexpr int kTilesPerWave = kWaveSpan / kTileTok;  // 8
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnParams {
+  const void* q;
+  int64_t q_row_stride, q_head_stride;
+  const void* k;
+  const void* v;
+  int64_t k_block_stride, k_token_stride, k_head_stride;
+  int64_t v_block_stride, v_token_stride, v_head_stride;
+  const int32_t* tables;
+  int64_t table_stride;
+  int32_t table_width;
+  int32_t num_blocks;  // physical blocks in the pool: out-of-range table entries read block 0
+  const int32_t* lengths;
+  const int32_t* cu_q;  // nullptr: per-row form
+  const float* k_scale;
+  const float* v_scale;
+  int64_t s_block_stride, s_token_stride, s_head_stride;
+  int32_t scale_mode;  // 0 none, 1 per-tensor (0-d), 2 per-vector [blk, tok, kvh]
+  int32_t num_seqs;
+  int32_t num_rows;  // total q rows
+  int32_t hq, hkv, group, head_dim, block_size;
+  int32_t window;  // 0: full context
+  int32_t rows_per_rg;
+  int32_t rowgroups;
+  int32_t max_chunks;
+  float qk_scale_log2;  // log2(e) / sqrt(head_dim)
+  void* out;
+  int64_t out_row_stride, out_head_stride;
+  float* part_ml;  // [rows][hq][max_chunks][2]  (max in log2 units, sum)
+  float* part_o;   // [rows][hq][max_chunks][head_dim]
+};
+
+struct SeqView {
+  int32_t q_begin, q_len, kv_len;
+};
+
+__device__ __forceinline__ SeqView seq_view(const AttnParams& P, int seq) {
+  SeqView s;
+  if (P.cu_q) {
+    s.q_begin = P.cu_q[seq];
+    s.q_len = P.cu_q[seq + 1] - s.q_begin;
+  } else {
+    s.q_begin = seq;
+    s.q_len = 1;
+  }
+  s.kv_len = P.lengths[seq];
+  return s;
+}
+
+// Row (window index qi) of a sequence: visible key range [lo, hi).
+__device__ __forceinline__ void row_range(const AttnParams& P, const SeqView& s, int qi, int& lo,
+                                          int& hi) {
+  hi = s.kv_len - s.q_len + 1 + qi;
+  if (hi < 0) hi = 0;
+  // Never read past the row's block table (a length beyond it is a caller error).
+  const int cap = P.table_width * P.block_size;
+  if (hi > cap) hi = cap;
+  lo = P.window > 0 ? max(0, hi - P.window) : 0;
+}
+
+// Physical block of key position `pos`; entries outside the pool read block 0
+// so that a corrupt table can never address memory outside the KV pool.
+__device__ __forceinline__ int64_t block_of(const AttnParams& P, int seq, int pos) {
+  const int32_t blk = P.tables[(int64_t)seq * P.table_stride + pos / P.block_size];
+  return (blk >= 0 && blk < P.num_blocks) ? (int64_t)blk : 0;
+}
+
+__device__ __forceinline__ int64_t kv_token_base(const AttnParams& P, int seq, int pos,
+                                                 int64_t block_stride, int64_t token_stride) {
+  const int64_t blk = block_of(P, seq, pos);
+  return (int64_t)blk * block_stride + (int64_t)(pos % P.block_size) * token_stride;
+}
+
+__device__ __forceinline__ float scale_at(const AttnParams& P, const float* s, int seq, int pos,
+                                          int kvh) {
+  const int64_t blk = block_of(P, seq, pos);
+  return s[blk * P.s_block_stride + (int64_t)(pos % P.block_size) * P.s_token_stride +
+           (int64_t)kvh * P.s_head_stride];
+}
+
+// Merge two online-softmax states (log2 domain) in a fixed operand order.
+__device__ __forceinline__ void merge_scales(float m1, float m2, float& mo, float& s1, float& s2) {
+  mo = fmaxf(m1, m2);
+  s1 = m1 == -INFINITY ? 0.f : exp2f(m1 - mo);
+  s2 = m2 == -INFINITY ? 0.f : exp2f(m2 - mo);
+}
+
+// ============================================================ MFMA path
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT>
+struct Mfma;
+
+template <>
+struct Mfma<RLT_BF16> {
+  __device__ static f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+    bf16x8 av, bv;
+    __builtin_memcpy(&av, &a, 16);
+    __builtin_memcpy(&bv, &b, 16);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, c, 0, 0, 0);
+  }
+  __device__ static f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+    s16x4 av, bv;
+    __builtin_memcpy(&av, &a, 8);
+    __builtin_memcpy(&bv, &b, 8);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, c, 0, 0, 0);
+  }
+  __device__ static uint16_t from_f32(float x) { return f32_to_bf16_bits(x); }
+};
+
+template <>
+struct Mfma<RLT_F16> {
+  __device__ static f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+    f16x8 av, bv;
+    __builtin_memcpy(&av, &a, 16);
+    __builtin_memcpy(&bv, &b, 16);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c, 0, 0, 0);
+  }
+  __device__ static f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+    f16x4 av, bv;
+    __builtin_memcpy(&av, &a, 8);
+    __builtin_memcpy(&bv, &b, 8);
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, c, 0, 0, 0);
+  }
+  __device__ static uint16_t from_f32(float x) { return f32_to_f16_bits(x); }
+};
+
+// Four fp8 codes -> four 16-bit values of the MFMA type (exact for e4m3).
+template <int QT>
+__device__ __forceinline__ uint2 fp8x4_to_16(uint32_t w) {
+  const float2 lo = fp8x2_to_f32<false>(w);
+  const float2 hi = fp8x2_to_f32<true>(w);
+  uint2 r;
+  if (QT == RLT_BF16) {
+    // e4m3 values are exact in bf16: truncation of the fp32 bits is exact.
+    r.x = (__float_as_uint(lo.x) >> 16) | (__float_as_uint(lo.y) & 0xffff0000u);
+    r.y = (__float_as_uint(hi.x) >> 16) | (__float_as_uint(hi.y) & 0xffff0000u);
+  } else {
+    r.x = (uint32_t)f32_to_f16_bits(lo.x) | ((uint32_t)f32_to_f16_bits(lo.y) << 16);
+    r.y = (uint32_t)f32_to_f16_bits(hi.x) | ((uint32_t)f32_to_f16_bits(hi.y) << 16);
+  }
+  return r;
+}
+
+// One lane's head_dim/4 slice of one key or value vector, in MFMA element type.
+template <int QT, int KVT, int D>
+struct KvSlice {
+  static constexpr int kElems = D / 4;       // 16-bit elements per lane
+  static constexpr int kVec = kElems / 8;    // 16-byte vectors per lane
+  uint4 x[kVec];
+
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) x[i] = make_uint4(0, 0, 0, 0);
+  }
+  __device__ __forceinline__ void load(const void* base, int64_t elem_off) {
+    if (KVT == QT) {
+      const uint4* p = (const uint4*)((const uint16_t*)base + elem_off);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) x[i] = p[i];
+    } else {  // fp8: kElems bytes
+      const uint8_t* p = (const uint8_t*)base + elem_off;
+      if (kVec % 2 == 0) {
+        const uint4* pv = (const uint4*)p;
+#pragma unroll
+        for (int i = 0; i < kVec / 2; ++i) {
+          const uint4 w = pv[i];
+          uint2 a = fp8x4_to_16<QT>(w.x), b = fp8x4_to_16<QT>(w.y);
+          uint2 c = fp8x4_to_16<QT>(w.z), d = fp8x4_to_16<QT>(w.w);
+          x[2 * i] = make_uint4(a.x, a.y, b.x, b.y);
+          x[2 * i + 1] = make_uint4(c.x, c.y, d.x, d.y);
+        }
+      } else {
+        const uint2* pv = (const uint2*)p;
+#pragma unroll
+        for (int i = 0; i < kVec; ++i) {
+          const uint2 w = pv[i];
+          uint2 a = fp8x4_to_16<QT>(w.x), b = fp8x4_to_16<QT>(w.y);
+          x[i] = make_uint4(a.x, a.y, b.x, b.y);
+        }
+      }
+    }
+  }
+};
+
+template <int QT, int KVT, int D, int NT>
+struct MfmaShared {
+  static constexpr int kPad = 8;  // 16-bit elements of row padding (bank spread)
+  union {
+    uint16_t vt[kWaves][kTileTok][D + kPad];  // tile loop: wave-private V tiles
+    f32x4 o[2][NT * (D / 16)][64];            // wave combine
+  };
+  float ml[2][NT * 16][2];
+};
+
+template <int QT, int KVT, int D, int NT>
+__global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
+  using M = Mfma<QT>;
+  constexpr int NQS = D / 32;  // 32-wide contraction slices
+  constexpr int ND = D / 16;   // 16-wide output column tiles
+  constexpr int DQ = D / 4;    // elements per lane group
+  __shared__ MfmaShared<QT, KVT, D, NT> sh;
+
+  const int seq = blockIdx.x / P.rowgroups;
+  const int rg = blockIdx.x % P.rowgroups;
+  const int kvh = blockIdx.y;
+  const int chunk = blockIdx.z;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15;
+  const int grp = lane >> 4;
+
+  const SeqView sv = seq_view(P, seq);
+  const int rows_total = sv.q_len * P.group;
+  const int rg_begin = rg * P.rows_per_rg;
+  if (rg_begin >= rows_total) return;
+  const int rg_rows = min(P.rows_per_rg, rows_total - rg_begin);
+  int lo_first, hi_first, lo_last, hi_last;
+  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
+  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  const int c_begin = chunk * kChunk;
+  if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
+
+  // This lane's rows (one per 16-row tile): B operand of S^T = K Q^T.
+  int row_lo[NT], row_hi[NT];
+  uint4 qreg[NT][NQS];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int rho = rg_begin + nt * 16 + l16;
+    if (nt * 16 + l16 < rg_rows) {
+      const int qi = rho / P.group;
+      const int head = kvh * P.group + rho % P.group;
+      row_range(P, sv, qi, row_lo[nt], row_hi[nt]);
+      const uint16_t* qp = (const uint16_t*)P.q + (int64_t)(sv.q_begin + qi) * P.q_row_stride +
+                           (int64_t)head * P.q_head_stride + grp * DQ;
+#pragma unroll
+      for (int s = 0; s < NQS; ++s) qreg[nt][s] = *(const uint4*)(qp + 8 * s);
+    } else {
+      row_lo[nt] = 0;
+      row_hi[nt] = 0;
+#pragma unroll
+      for (int s = 0; s < NQS; ++s) qreg[nt][s] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  float qk_scale = P.qk_scale_log2;
+  float v_mul = 1.f;
+  if (P.scale_mode == 1) {
+    qk_scale *= P.k_scale[0];
+    v_mul = P.v_scale[0];
+  }
+
+  f32x4 oacc[NT][ND];
+  float m_run[NT], l_run[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Tiles of this wave: absolute 16-aligned positions within [span_lo, span_hi).
+  const int w_begin = c_begin + wave * kWaveSpan;
+  const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
+  const int span_hi = min(w_begin + kWaveSpan, hi_last);
+  const int t0 = span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok;
+  const int t1 = span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok;
+
+  // Key position of this lane in tile t (A-operand row = l16) and its KV offset.
+  auto tile_off = [&](int t, int64_t& koff, int64_t& voff, bool& ok) {
+    const int pos = w_begin + t * kTileTok + l16;
+    ok = pos < hi_last;
+    koff = voff = 0;
+    if (ok) {
+      const int64_t blk = block_of(P, seq, pos);
+      const int64_t off = pos % P.block_size;
+      koff = blk * P.k_block_stride + off * P.k_token_stride +
+             (int64_t)kvh * P.k_head_stride + grp * DQ;
+      voff = blk * P.v_block_stride + off * P.v_token_stride +
+             (int64_t)kvh * P.v_head_stride + grp * DQ;
+    }
+  };
+
+  KvSlice<QT, KVT, D> kcur, vcur, knext, vnext;
+  {
+    int64_t ko, vo;
+    bool ok;
+    if (t0 < t1) {
+      tile_off(t0, ko, vo, ok);
+      if (ok) {
+        kcur.load(P.k, ko);
+        vcur.load(P.v, vo);
+      } else {
+        kcur.zero();
+        vcur.zero();
+      }
+    }
+  }
+  auto& vt = sh.vt[wave];
+
+  for (int t = t0; t < t1; ++t) {
+    if (t + 1 < t1) {
+      int64_t ko, vo;
+      bool ok;
+      tile_off(t + 1, ko, vo, ok);
+      if (ok) {
+        knext.load(P.k, ko);
+        vnext.load(P.v, vo);
+      } else {
+        knext.zero();
+        vnext.zero();
+      }
+    }
+    const int tb = w_begin + t * kTileTok;
+    // ---- S^T = K Q^T : lane holds (positions tb + 4*grp + r, row l16 of tile nt)
+    f32x4 sc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      sc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NQS; ++s) sc[nt] = M::qk(kcur.x[s], qreg[nt][s], sc[nt]);
+    }
+    // ---- V tile to LDS (row = key position, contiguous head_dim)
+#pragma unroll
+    for (int i = 0; i < KvSlice<QT, KVT, D>::kVec; ++i)
+      *(uint4*)&vt[l16][grp * DQ + 8 * i] = vcur.x[i];
+    // per-position scales of this lane's 4 positions (per-vector FP8)
+    float ks[4] = {1.f, 1.f, 1.f, 1.f}, vs[4] = {1.f, 1.f, 1.f, 1.f};
+    if (P.scale_mode == 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = tb + 4 * grp + r;
+        if (pos < hi_last) {
+          ks[r] = scale_at(P, P.k_scale, seq, pos, kvh);
+          vs[r] = scale_at(P, P.v_scale, seq, pos, kvh);
+        }
+      }
+    }
+    // ---- online softmax (log2 domain) and P^T operand
+    uint2 pop[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float sv4[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = tb + 4 * grp + r;
+        const bool vis = pos >= row_lo[nt] && pos < row_hi[nt];
+        const float x = sc[nt][r] * ks[r] * qk_scale;
+        sv4[r] = vis ? x : -INFINITY;
+        mx = fmaxf(mx, sv4[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, RLT_WAVE));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, RLT_WAVE));
+      const float m_new = fmaxf(m_run[nt], mx);
+      float pr[4];
+      float corr = 1.f;
+      if (m_new == -INFINITY) {
+        pr[0] = pr[1] = pr[2] = pr[3] = 0.f;
+      } else {
+        corr = exp2f(m_run[nt] - m_new);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = exp2f(sv4[r] - m_new);
+      }
+      float rs = ((pr[0] + pr[1]) + pr[2]) + pr[3];
+      rs += __shfl_xor(rs, 16, RLT_WAVE);
+      rs += __shfl_xor(rs, 32, RLT_WAVE);
+      l_run[nt] = l_run[nt] * corr + rs;
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] *= corr;
+      pop[nt].x = (uint32_t)M::from_f32(pr[0] * vs[0]) | ((uint32_t)M::from_f32(pr[1] * vs[1]) << 16);
+      pop[nt].y = (uint32_t)M::from_f32(pr[2] * vs[2]) | ((uint32_t)M::from_f32(pr[3] * vs[3]) << 16);
+    }
+    // ---- O^T += V^T P^T : A = V^T (dims 16dt + l16, positions 4grp..+3)
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      const int d = dt * 16 + l16;
+      uint2 a;
+      a.x = (uint32_t)vt[4 * grp + 0][d] | ((uint32_t)vt[4 * grp + 1][d] << 16);
+      a.y = (uint32_t)vt[4 * grp + 2][d] | ((uint32_t)vt[4 * grp + 3][d] << 16);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::pv(a, pop[nt], oacc[nt][dt]);
+    }
+    if (t + 1 < t1) {
+      kcur = knext;
+      vcur = vnext;
+    }
+  }
+
+  // ---- combine the 4 waves: ((w0 + w2) + (w1 + w3)), then write the chunk partial.
+  auto publish = [&](int buf) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (grp == 0) {
+        sh.ml[buf][nt * 16 + l16][0] = m_run[nt];
+        sh.ml[buf][nt * 16 + l16][1] = l_run[nt];
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) sh.o[buf][nt * ND + dt][lane] = oacc[nt][dt];
+    }
+  };
+  auto absorb = [&](int buf) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float m2 = sh.ml[buf][nt * 16 + l16][0];
+      const float l2 = sh.ml[buf][nt * 16 + l16][1];
+      float mo, s1, s2;
+      merge_scales(m_run[nt], m2, mo, s1, s2);
+      m_run[nt] = mo;
+      l_run[nt] = l_run[nt] * s1 + l2 * s2;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = oacc[nt][dt] * s1 + sh.o[buf][nt * ND + dt][lane] * s2;
+    }
+  };
+  __syncthreads();  // vt no longer needed; ml / o buffers are free
+  if (wave >= 2) publish(wave - 2);
+  __syncthreads();
+  if (wave < 2) absorb(wave);
+  __syncthreads();
+  if (wave == 1) publish(0);
+  __syncthreads();
+  if (wave != 0) return;
+  absorb(0);
+
+  // ---- chunk partial for rows whose merge range contains this chunk
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int r_local = nt * 16 + l16;
+    if (r_local >= rg_rows) continue;
+    const int lo_c = row_lo[nt] / kChunk;
+    const int hi_c = (row_hi[nt] + kChunk - 1) / kChunk;
+    if (chunk < lo_c || chunk >= hi_c) continue;
+    const int rho = rg_begin + r_local;
+    const int qrow = sv.q_begin + rho / P.group;
+    const int head = kvh * P.group + rho % P.group;
+    const int64_t slot = ((int64_t)qrow * P.hq + head) * P.max_chunks + chunk;
+    if (grp == 0) {
+      P.part_ml[2 * slot] = m_run[nt];
+      P.part_ml[2 * slot + 1] = l_run[nt];
+    }
+    float* po = P.part_o + slot * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      const f32x4 o = oacc[nt][dt] * v_mul;
+      *(float4*)(po + dt * 16 + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// ============================================================ vector path
+
+constexpr int kVecRows = 8;  // rows per row-group on the vector path
+
+struct VecShared {
+  float q[kVecRows][256];
+  float p[kWaves][kVecRows][kTileTok];
+  float ml[2][kVecRows][2];
+  float o[2][kVecRows][256];
+};
+
+// Scores: lane (position l16, dim quarter grp) dots its quarter with every row's
+// q (LDS broadcast) and reduces across quarters.  P * V: lane owns dims
+// lane + 64e and reads the tile's 16 value vectors straight from memory.
+template <int QT, int KVT>
+__global__ __launch_bounds__(256) void rlt_attn_vec_kernel(AttnParams P) {
+  __shared__ VecShared sh;
+  const int D = P.head_dim;
+  const int DQ = (D + 3) / 4;
+  const int seq = blockIdx.x / P.rowgroups;
+  const int rg = blockIdx.x % P.rowgroups;
+  const int kvh = blockIdx.y;
+  const int chunk = blockIdx.z;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15;
+  const int grp = lane >> 4;
+
+  const SeqView sv = seq_view(P, seq);
+  const int rows_total = sv.q_len * P.group;
+  const int rg_begin = rg * kVecRows;
+  if (rg_begin >= rows_total) return;
+  const int rg_rows = min(kVecRows, rows_total - rg_begin);
+  int lo_first, hi_first, lo_last, hi_last;
+  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
+  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  const int c_begin = chunk * kChunk;
+  if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
+
+  int rlo[kVecRows], rhi[kVecRows];
+#pragma unroll
+  for (int r = 0; r < kVecRows; ++r) {
+    if (r < rg_rows) row_range(P, sv, (rg_begin + r) / P.group, rlo[r], rhi[r]);
+    else rlo[r] = rhi[r] = 0;
+  }
+  for (int idx = threadIdx.x; idx < kVecRows * D; idx += blockDim.x) {
+    const int r = idx / D, d = idx % D;
+    float x = 0.f;
+    if (r < rg_rows) {
+      const int rho = rg_begin + r;
+      const int head = kvh * P.group + rho % P.group;
+      x = load_as_f32<QT>(P.q, (int64_t)(sv.q_begin + rho / P.group) * P.q_row_stride +
+                                   (int64_t)head * P.q_head_stride + d);
+    }
+    sh.q[r][d] = x;
+  }
+  __syncthreads();
+
+  float qk_scale = P.qk_scale_log2;
+  float v_mul = 1.f;
+  if (P.scale_mode == 1) {
+    qk_scale *= P.k_scale[0];
+    v_mul = P.v_scale[0];
+  }
+  float m_run[kVecRows], l_run[kVecRows], acc[kVecRows][4];
+#pragma unroll
+  for (int r = 0; r < kVecRows; ++r) {
+    m_run[r] = -INFINITY;
+    l_run[r] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[r][e] = 0.f;
+  }
+  const int w_begin = c_begin + wave * kWaveSpan;
+  const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
+  const int span_hi = min(w_begin + kWaveSpan, hi_last);
+  const int t0 = span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok;
+  const int t1 = span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok;
+  for (int t = t0; t < t1; ++t) {
+    const int tb = w_begin + t * kTileTok;
+    const int pos = tb + l16;
+    const bool ok = pos < hi_last;
+    int64_t kb = 0;
+    float ksc = 1.f;
+    if (ok) {
+      kb = kv_token_base(P, seq, pos, P.k_block_stride, P.k_token_stride) + (int64_t)kvh * P.k_head_stride;
+      if (P.scale_mode == 2) ksc = scale_at(P, P.k_scale, seq, pos, kvh);
+    }
+    float s_row[kVecRows];
+#pragma unroll
+    for (int r = 0; r < kVecRows; ++r) s_row[r] = 0.f;
+    for (int e = 0; e < DQ; ++e) {
+      const int d = grp * DQ + e;
+      if (d < D) {
+        const float kx = ok ? load_as_f32<KVT>(P.k, kb + d) * ksc : 0.f;
+#pragma unroll
+        for (int r = 0; r < kVecRows; ++r) s_row[r] = fmaf(kx, sh.q[r][d], s_row[r]);
+      }
+    }
+    float corr[kVecRows];
+#pragma unroll
+    for (int r = 0; r < kVecRows; ++r) {
+      float s = s_row[r];
+      s += __shfl_xor(s, 16, RLT_WAVE);
+      s += __shfl_xor(s, 32, RLT_WAVE);
+      const bool vis = pos >= rlo[r] && pos < rhi[r];
+      s = vis ? s * qk_scale : -INFINITY;
+      float mx = s;
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, RLT_WAVE));
+      const float m_new = fmaxf(m_run[r], mx);
+      float pr = 0.f;
+      corr[r] = 1.f;
+      if (m_new != -INFINITY) {
+        corr[r] = exp2f(m_run[r] - m_new);
+        pr = exp2f(s - m_new);
+      }
+      float rs = pr;
+      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, RLT_WAVE);
+      l_run[r] = l_run[r] * corr[r] + rs;
+      m_run[r] = m_new;
+      if (grp == 0) sh.p[wave][r][l16] = pr;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r = 0; r < kVecRows; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][e] *= corr[r];
+    // P * V over the tile's 16 positions; lane owns dims lane + 64e.
+    for (int j = 0; j < kTileTok; ++j) {
+      const int pj = tb + j;
+      if (pj >= hi_last) break;
+      const int64_t vb =
+          kv_token_base(P, seq, pj, P.v_block_stride, P.v_token_stride) + (int64_t)kvh * P.v_head_stride;
+      const float vsc = P.scale_mode == 2 ? scale_at(P, P.v_scale, seq, pj, kvh) : 1.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d < D) {
+          const float vx = load_as_f32<KVT>(P.v, vb + d) * vsc;
+#pragma unroll
+          for (int r = 0; r < kVecRows; ++r) acc[r][e] = fmaf(sh.p[wave][r][j], vx, acc[r][e]);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  auto publish = [&](int buf) {
+    if (lane < kVecRows) {
+      float mv = 0.f, lv = 0.f;
+#pragma unroll
+      for (int r = 0; r < kVecRows; ++r)
+        if (r == lane) { mv = m_run[r]; lv = l_run[r]; }
+      sh.ml[buf][lane][0] = mv;
+      sh.ml[buf][lane][1] = lv;
+    }
+#pragma unroll
+    for (int r = 0; r < kVecRows; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d < D) sh.o[buf][r][d] = acc[r][e];
+      }
+  };
+  auto absorb = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < kVecRows; ++r) {
+      float mo, s1, s2;
+      merge_scales(m_run[r], sh.ml[buf][r][0], mo, s1, s2);
+      m_run[r] = mo;
+      l_run[r] = l_run[r] * s1 + sh.ml[buf][r][1] * s2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d < D) acc[r][e] = acc[r][e] * s1 + sh.o[buf][r][d] * s2;
+      }
+    }
+  };
+  __syncthreads();
+  if (wave >= 2) publish(wave - 2);
+  __syncthreads();
+  if (wave < 2) absorb(wave);
+  __syncthreads();
+  if (wave == 1) publish(0);
+  __syncthreads();
+  if (wave != 0) return;
+  absorb(0);
+#pragma unroll
+  for (int r = 0; r < kVecRows; ++r) {
+    if (r >= rg_rows) continue;
+    const int lo_c = rlo[r] / kChunk;
+    const int hi_c = (rhi[r] + kChunk - 1) / kChunk;
+    if (chunk < lo_c || chunk >= hi_c) continue;
+    const int rho = rg_begin + r;
+    const int qrow = sv.q_begin + rho / P.group;
+    const int head = kvh * P.group + rho % P.group;
+    const int64_t slot = ((int64_t)qrow * P.hq + head) * P.max_chunks + chunk;
+    if (lane == 0) {
+      P.part_ml[2 * slot] = m_run[r];
+      P.part_ml[2 * slot + 1] = l_run[r];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = lane + 64 * e;
+      if (d < D) P.part_o[slot * D + d] = acc[r][e] * v_mul;
+    }
+  }
+}
+
+// ============================================================ merge
+
+// grid (rows, hq), 64 threads: combine a row's chunks in chunk order and normalize.
+// reference: triton_attention.py:145-173 (empty rows give zeros; 1e-30 floor).
+template <int OT>
+__global__ __launch_bounds__(64) void rlt_merge_kernel(AttnParams P) {
+  const int row = blockIdx.x;
+  const int head = blockIdx.y;
+  int seq, qi;
+  if (P.cu_q) {
+    int lo = 0, hi = P.num_seqs;  // last seq with cu[seq] <= row
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (P.cu_q[mid] <= row) lo = mid;
+      else hi = mid;
+    }
+    seq = lo;
+    qi = row - P.cu_q[seq];
+  } else {
+    seq = row;
+    qi = 0;
+  }
+  const SeqView sv = seq_view(P, seq);
+  int lo, hi;
+  row_range(P, sv, qi, lo, hi);
+  const int c0 = lo / kChunk, c1 = (hi + kChunk - 1) / kChunk;
+  const int64_t base = ((int64_t)row * P.hq + head) * P.max_chunks;
+  float mmax = -INFINITY;
+  for (int c = c0; c < c1; ++c) mmax = fmaxf(mmax, P.part_ml[2 * (base + c)]);
+  float l = 0.f;
+  for (int c = c0; c < c1; ++c) {
+    const float m = P.part_ml[2 * (base + c)];
+    const float s = m == -INFINITY ? 0.f : exp2f(m - mmax);
+    l += P.part_ml[2 * (base + c) + 1] * s;
+  }
+  const float inv_den = 1.f / fmaxf(l, 1.0e-30f);
+  for (int d = threadIdx.x; d < P.head_dim; d += blockDim.x) {
+    float o = 0.f;
+    for (int c = c0; c < c1; ++c) {
+      const float m = P.part_ml[2 * (base + c)];
+      const float s = m == -INFINITY ? 0.f : exp2f(m - mmax);
+      o += P.part_o[(base + c) * P.head_dim + d] * s;
+    }
+    store_from_f32<OT>(P.out, (int64_t)row * P.out_row_stride + (int64_t)head * P.out_head_stride + d,
+                       c0 < c1 ? o * inv_den : 0.f);
+  }
+}
+
+// ============================================================ dispatch
+
+template <int QT, int KVT, int D>
+int launch_mfma_d(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
+  if (nt == 1) rlt_attn_mfma_kernel<QT, KVT, D, 1><<<grid, 256, 0, stream>>>(P);
+  else rlt_attn_mfma_kernel<QT, KVT, D, 2><<<grid, 256, 0, stream>>>(P);
+  return RLT_OK;
+}
+
+template <int QT, int KVT>
+int launch_mfma(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
+  switch (P.head_dim) {
+    case 64: return launch_mfma_d<QT, KVT, 64>(P, grid, nt, stream);
+    case 96: return launch_mfma_d<QT, KVT, 96>(P, grid, nt, stream);
+    case 128: return launch_mfma_d<QT, KVT, 128>(P, grid, nt, stream);
+    case 256: return launch_mfma_d<QT, KVT, 256>(P, grid, nt, stream);
+    default: return RLT_ERR_UNSUPPORTED;
+  }
+}
+
+bool mfma_head_dim(int d) { return d == 64 || d == 96 || d == 128 || d == 256; }
+
+template <int QT>
+int launch_vec_q(const AttnParams& P, int kv_dtype, dim3 grid, hipStream_t stream) {
+  switch (kv_dtype) {
+    case RLT_F32: rlt_attn_vec_kernel<QT, RLT_F32><<<grid, 256, 0, stream>>>(P); break;
+    case RLT_F16: rlt_attn_vec_kernel<QT, RLT_F16><<<grid, 256, 0, stream>>>(P); break;
+    case RLT_BF16: rlt_attn_vec_kernel<QT, RLT_BF16><<<grid, 256, 0, stream>>>(P); break;
+    case RLT_FP8_E4M3: rlt_attn_vec_kernel<QT, RLT_FP8_E4M3><<<grid, 256, 0, stream>>>(P); break;
+    default: return RLT_ERR_ARGUMENT;
+  }
+  return RLT_OK;
+}
+
+int max_chunks_for(int32_t table_width, int32_t block_size) {
+  const int64_t tokens = (int64_t)table_width * block_size;
+  return (int)((tokens + kChunk - 1) / kChunk);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim) {
+  const bool qok = q_dtype == RLT_BF16 || q_dtype == RLT_F16;
+  const bool kvok = kv_dtype == q_dtype || kv_dtype == RLT_FP8_E4M3;
+  return qok && kvok && mfma_head_dim(head_dim);
+}
+
+size_t rlt_paged_attention_workspace_size(int32_t num_q_rows, int32_t num_q_heads, int32_t head_dim,
+                                          int32_t table_width, int32_t block_size) {
+  const int64_t slots = (int64_t)num_q_rows * num_q_heads * max_chunks_for(table_width, block_size);
+  return rlt_align_up(sizeof(float) * slots * 2, 256) + rlt_align_up(sizeof(float) * slots * head_dim, 256);
+}
+
+int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                        const void* key_cache, const void* value_cache, int64_t k_block_stride,
+                        int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                        int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                        const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                        const int32_t* context_lengths,
+                        const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                        int32_t num_q_rows, const float* key_scale, const float* value_scale,
+                        int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
+                        int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
+                        int32_t window, void* out, int64_t out_row_stride, int64_t out_head_stride,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return RLT_ERR_ARGUMENT;
+  if (head_dim <= 0 || head_dim > 256 || block_size <= 0 || window < 0) return RLT_ERR_ARGUMENT;
+  if (num_seqs < 0 || num_q_rows < 0 || max_q_len < 0 || table_width < 0) return RLT_ERR_ARGUMENT;
+  if (scale_mode < 0 || scale_mode > 2 || (scale_mode && (!key_scale || !value_scale)))
+    return RLT_ERR_ARGUMENT;
+  if (kv_dtype == RLT_FP8_E4M3 && scale_mode == 0) return RLT_ERR_ARGUMENT;
+  if (q_dtype == RLT_FP8_E4M3) return RLT_ERR_ARGUMENT;
+  if (num_blocks <= 0) return RLT_ERR_ARGUMENT;
+  if (num_q_rows == 0 || num_seqs == 0) return RLT_OK;
+  if (!cu_seqlens_q && num_seqs != num_q_rows) return RLT_ERR_ARGUMENT;
+  const size_t need = rlt_paged_attention_workspace_size(num_q_rows, num_q_heads, head_dim,
+                                                         table_width, block_size);
+  if (!workspace || workspace_bytes < need) return RLT_ERR_WORKSPACE;
+
+  AttnParams P;
+  P.q = q;
+  P.q_row_stride = q_row_stride;
+  P.q_head_stride = q_head_stride;
+  P.k = key_cache;
+  P.v = value_cache;
+  P.k_block_stride = k_block_stride;
+  P.k_token_stride = k_token_stride;
+  P.k_head_stride = k_head_stride;
+  P.v_block_stride = v_block_stride;
+  P.v_token_stride = v_token_stride;
+  P.v_head_stride = v_head_stride;
+  P.tables = block_tables;
+  P.table_stride = table_stride;
+  P.table_width = table_width;
+  P.num_blocks = num_blocks;
+  P.lengths = context_lengths;
+  P.cu_q = cu_seqlens_q;
+  P.k_scale = key_scale;
+  P.v_scale = value_scale;
+  P.s_block_stride = s_block_stride;
+  P.s_token_stride = s_token_stride;
+  P.s_head_stride = s_head_stride;
+  P.scale_mode = scale_mode;
+  P.num_seqs = num_seqs;
+  P.num_rows = num_q_rows;
+  P.hq = num_q_heads;
+  P.hkv = num_kv_heads;
+  P.group = num_q_heads / num_kv_heads;
+  P.head_dim = head_dim;
+  P.block_size = block_size;
+  P.window = window;
+  P.max_chunks = max_chunks_for(table_width, block_size);
+  P.qk_scale_log2 = kLog2e / sqrtf((float)head_dim);
+  P.out = out;
+  P.out_row_stride = out_row_stride;
+  P.out_head_stride = out_head_stride;
+  const int64_t slots = (int64_t)num_q_rows * num_q_heads * P.max_chunks;
+  P.part_ml = (float*)workspace;
+  P.part_o = (float*)((char*)workspace + rlt_align_up(sizeof(float) * slots * 2, 256));
+  if (P.max_chunks == 0) P.max_chunks = 1;  // zero-width tables: every row is empty
+
+  const int rows_per_seq = max_q_len * P.group;
+  const bool mfma = rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim);
+  int st = RLT_OK;
+  if (mfma) {
+    // 16-byte vector loads of q and of every lane's KV slice.
+    const int64_t kv_elt = kv_dtype == RLT_FP8_E4M3 ? 1 : 2;
+    const int64_t kv_align = kv_dtype == RLT_FP8_E4M3 ? 8 : 16;
+    const bool aligned =
+        ((uintptr_t)q % 16 == 0) && (q_row_stride * 2) % 16 == 0 && (q_head_stride * 2) % 16 == 0 &&
+        ((uintptr_t)key_cache % 16 == 0) && ((uintptr_t)value_cache % 16 == 0) &&
+        (k_block_stride * kv_elt) % kv_align == 0 && (k_token_stride * kv_elt) % kv_align == 0 &&
+        (k_head_stride * kv_elt) % kv_align == 0 && (v_block_stride * kv_elt) % kv_align == 0 &&
+        (v_token_stride * kv_elt) % kv_align == 0 && (v_head_stride * kv_elt) % kv_align == 0;
+    if (!aligned) return RLT_ERR_ARGUMENT;
+    const int nt = (rows_per_seq > 16 && head_dim <= 128) ? 2 : 1;
+    P.rows_per_rg = 16 * nt;
+    P.rowgroups = (rows_per_seq + P.rows_per_rg - 1) / P.rows_per_rg;
+    if (P.rowgroups < 1) P.rowgroups = 1;
+    dim3 grid((unsigned)(num_seqs * P.rowgroups), (unsigned)num_kv_heads, (unsigned)P.max_chunks);
+    if (q_dtype == RLT_BF16)
+      st = kv_dtype == RLT_BF16 ? launch_mfma<RLT_BF16, RLT_BF16>(P, grid, nt, stream)
+                                : launch_mfma<RLT_BF16, RLT_FP8_E4M3>(P, grid, nt, stream);
+    else
+      st = kv_dtype == RLT_F16 ? launch_mfma<RLT_F16, RLT_F16>(P, grid, nt, stream)
+                               : launch_mfma<RLT_F16, RLT_FP8_E4M3>(P, grid, nt, stream);
+  } else {
+    P.rows_per_rg = kVecRows;
+    P.rowgroups = (rows_per_seq + kVecRows - 1) / kVecRows;
+    if (P.rowgroups < 1) P.rowgroups = 1;
+    dim3 grid((unsigned)(num_seqs * P.rowgroups), (unsigned)num_kv_heads, (unsigned)P.max_chunks);
+    switch (q_dtype) {
+      case RLT_F32: st = launch_vec_q<RLT_F32>(P, kv_dtype, grid, stream); break;
+      case RLT_F16: st = launch_vec_q<RLT_F16>(P, kv_dtype, grid, stream); break;
+      case RLT_BF16: st = launch_vec_q<RLT_BF16>(P, kv_dtype, grid, stream); break;
+      default: st = RLT_ERR_ARGUMENT;
+    }
+  }
+  if (st != RLT_OK) return st;
+  dim3 mgrid((unsigned)num_q_rows, (unsigned)num_q_heads);
+  switch (q_dtype) {
+    case RLT_F32: rlt_merge_kernel<RLT_F32><<<mgrid, 64, 0, stream>>>(P); break;
+    case RLT_F16: rlt_merge_kernel<RLT_F16><<<mgrid, 64, 0, stream>>>(P); break;
+    case RLT_BF16: rlt_merge_kernel<RLT_BF16><<<mgrid, 64, 0, stream>>>(P); break;
+  }
+  return rlt_launch_status();
+}
+
+}  // extern "C"

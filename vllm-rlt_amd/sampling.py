@@ -1,0 +1,120 @@
+"""MI355X acceptance sampler behind the reference sampler API.
+
+Same signatures, dtypes, shape errors and flag-not-raise conventions as
+vllm_rlt/worker/speculative_sampling.py (``categorical`` :59-85,
+``AcceptResult`` :88-101, ``speculative_accept`` :104-181); results are
+bit-exact with the reference's torch-CPU arithmetic when fed identical fp32
+probabilities and uniforms.  Every call enqueues gfx950 kernels on the current
+stream without host synchronization; inputs are never modified.
+"""
+
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+
+
+class AcceptResult(NamedTuple):
+    """Device-side verification result; reference: speculative_sampling.py:88-101."""
+
+    tokens: torch.Tensor
+    accepted: torch.Tensor
+    final: torch.Tensor
+    error: torch.Tensor
+
+
+def _f32(t):
+    t = t if t.dtype == torch.float32 else t.float()
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _i64(t):
+    t = t if t.dtype == torch.int64 else t.long()
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def categorical(weights, u):
+    """Inverse-CDF draw from ``[m, V]`` nonnegative weights with ``[m]`` uniforms.
+
+    Returns ``(index int64 [m], valid bool [m])``; reference: speculative_sampling.py:59-85.
+    """
+    if weights.ndim != 2 or weights.shape[-1] < 1:
+        raise ValueError("weights must be a 2-D [m, V] tensor with V >= 1")
+    if u.shape != weights.shape[:1]:
+        raise ValueError(f"u must have shape [{weights.shape[0]}], got {tuple(u.shape)}")
+    _lib.require_gpu(weights, u)
+    m, vocab = weights.shape
+    index = torch.empty(m, dtype=torch.int64, device=weights.device)
+    valid = torch.empty(m, dtype=torch.bool, device=weights.device)
+    if m == 0:
+        return index, valid
+    w, uu = _f32(weights), _f32(u)
+    lib = _lib.library()
+    ws = _lib.workspace(lib.rlt_categorical_workspace_size(m, vocab), w.device)
+    status = lib.rlt_categorical(_lib.ptr(w), _lib.ptr(uu), m, vocab, _lib.ptr(index),
+                                 _lib.ptr(valid), _lib.ptr(ws), ws.numel(), _lib.stream_of(w.device))
+    _lib.check(status, "rlt_categorical")
+    return index, valid
+
+
+def speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final):
+    """Batched speculative rejection sampling; reference: speculative_sampling.py:104-181."""
+    n, w1 = draft_tokens.shape
+    vocab = p.shape[-1]
+    if drafts.shape != (n,) or u_final.shape != (n,) or u_accept.shape != (n, w1):
+        raise ValueError("drafts, u_accept and u_final must match draft_tokens [n, W1]")
+    if q.shape != (n, w1, vocab) or p.shape != (n, w1 + 1, vocab):
+        raise ValueError("q must be [n, W1, V] and p must be [n, W1 + 1, V]")
+    _lib.require_gpu(draft_tokens, drafts, q, p, u_accept, u_final)
+    device = p.device
+    tokens = torch.empty((n, w1 + 1), dtype=torch.int64, device=device)
+    accepted = torch.empty(n, dtype=torch.int64, device=device)
+    final = torch.empty(n, dtype=torch.int64, device=device)
+    error = torch.empty(n, dtype=torch.bool, device=device)
+    if n == 0:
+        return AcceptResult(tokens, accepted, final, error)
+    if w1 > 32:
+        raise ValueError("at most 32 draft tokens per request are supported")
+    dt, dr = _i64(draft_tokens), _i64(drafts)
+    qq, pp, ua, uf = _f32(q), _f32(p), _f32(u_accept), _f32(u_final)
+    lib = _lib.library()
+    ws = _lib.workspace(lib.rlt_speculative_accept_workspace_size(n, w1, vocab), device)
+    status = lib.rlt_speculative_accept(
+        _lib.ptr(dt), _lib.ptr(dr), _lib.ptr(qq), _lib.ptr(pp), _lib.ptr(ua), _lib.ptr(uf),
+        n, w1, vocab, _lib.ptr(tokens), _lib.ptr(accepted), _lib.ptr(final), _lib.ptr(error),
+        _lib.ptr(ws), ws.numel(), _lib.stream_of(device))
+    _lib.check(status, "rlt_speculative_accept")
+    return AcceptResult(tokens, accepted, final, error)
+
+
+def row_mass(x):
+    """``x.sum(-1, dtype=float32)`` of a 2-D fp32 tensor in torch-CPU summation order."""
+    if x.ndim != 2:
+        raise ValueError("x must be 2-D")
+    _lib.require_gpu(x)
+    rows, vocab = x.shape
+    out = torch.empty(rows, dtype=torch.float32, device=x.device)
+    if rows == 0:
+        return out
+    xx = _f32(x)
+    lib = _lib.library()
+    ws = _lib.workspace(lib.rlt_row_mass_workspace_size(rows, vocab), x.device)
+    status = lib.rlt_row_mass_f32(_lib.ptr(xx), rows, vocab, _lib.ptr(out), _lib.ptr(ws),
+                                  ws.numel(), _lib.stream_of(x.device))
+    _lib.check(status, "rlt_row_mass_f32")
+    return out
+
+
+def greedy_accept(candidates, targets):
+    """Host prefix match of one request; reference: vllm_rlt/worker/speculative.py:41-53.
+
+    ``targets[j]`` is the target argmax of verify row j.  Returns the committed
+    tokens (the target prefix through the first mismatch) and the accepted count.
+    """
+    accepted = 0
+    for candidate, target in zip(candidates, targets):
+        if candidate != target:
+            break
+        accepted += 1
+    return list(targets[: accepted + 1]), accepted
