@@ -1,0 +1,258 @@
+"""Verify-step benchmark on one MI355X: packed-window paged attention + acceptance.
+
+Workload (the verify-step config the metric is quoted on):
+batch 32 requests x verify window q_len = k + 1 = 5 with the intra-window causal
+mask; 16 q heads / 4 kv heads (GQA 4), head_dim 128, bf16 KV in the SHARED layout
+(one plane), context lengths uniform in [1024, 8192]; block size 16, block tables a
+seeded random permutation of the pool.  Acceptance over vocab 49152 with target /
+draft distributions built at temperature 0.7, top-p 0.9, seeded per-request
+uniforms.  Synthetic data, random values: there is no model or dataset.
+
+One step = the attention call over all 160 verify rows + speculative_accept over
+the 32 requests, both replayed from HIP graphs (the reference runs its recurrent
+core under graphs too).  ``value`` = verified tokens (32 x 5) / step time.
+
+Output: one JSON line (see the driver contract) with ``roofline`` for the
+attention launch (algorithmic bytes / average launch time, HIP events on the launch
+stream) and ``cpu_baseline`` (the torch-CPU oracle on this host).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import __graft_entry__  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "verified tokens/sec on 1 MI355X (verify attn+accept); % of HBM peak GB/s"
+
+
+def probabilities(logits, temperature, top_p):
+    """softmax(logits / T) restricted to the top-p nucleus (data generation only)."""
+    x = logits.float() / temperature
+    if top_p < 1:
+        sx, idx = x.sort(dim=-1, descending=True)
+        drop = sx.softmax(-1).cumsum(-1) > top_p
+        drop[..., 1:] = drop[..., :-1].clone()
+        drop[..., 0] = False
+        x = x.scatter(-1, idx, sx.masked_fill(drop, -torch.inf))
+    return x.softmax(-1)
+
+
+def build_workload(dev, seed=0):
+    n, window, hq, hkv, d, bs, layers, vocab = 32, 5, 16, 4, 128, 16, 2, 49152
+    k_drafts = window - 1
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(1024, 8193, (n,), generator=g, dtype=torch.int64)
+    width = 8192 // bs
+    pool = n * width
+    tables = torch.randperm(pool, generator=g)[: n * width].view(n, width).int()
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    shape = (pool, layers, bs, hkv, d)
+    key_pool = torch.randn(shape, generator=gd, device=dev, dtype=torch.bfloat16)
+    value_pool = torch.randn(shape, generator=gd, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(n * window, hq, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    cu = torch.arange(0, n * window + 1, window, dtype=torch.int32)
+    draft_logits = torch.randn(n, window, vocab, generator=gd, device=dev) * 3.0
+    target_logits = draft_logits + torch.randn(n, window, vocab, generator=gd, device=dev)
+    qprob = probabilities(draft_logits[:, :k_drafts], 0.7, 0.9).contiguous()
+    pprob = probabilities(target_logits, 0.7, 0.9).contiguous()
+    seeds = torch.randint(0, 2**31, (n,), generator=g).tolist()
+    u = torch.stack([torch.rand(2 * k_drafts + 1, generator=torch.Generator().manual_seed(s))
+                     for s in seeds])
+    return dict(n=n, window=window, hq=hq, hkv=hkv, d=d, bs=bs, vocab=vocab, k=k_drafts,
+                lengths=lengths, tables=tables, key_pool=key_pool, value_pool=value_pool, q=q,
+                cu=cu, qprob=qprob, pprob=pprob, u=u, layer=1)
+
+
+def attention_bytes(w):
+    """Algorithmic HBM bytes of one attention launch: each needed KV byte once per
+    (request, plane) up to the last window row, plus q, out and the table entries."""
+    elt = 2
+    kv = int(w["lengths"].sum()) * 2 * w["hkv"] * w["d"] * elt
+    qo = 2 * w["n"] * w["window"] * w["hq"] * w["d"] * elt
+    tables = int(sum(math.ceil(int(n) / w["bs"]) for n in w["lengths"])) * 4
+    return kv + qo + tables
+
+
+def accept_bytes(w):
+    n, k, v = w["n"], w["k"], w["vocab"]
+    return 4 * n * (k + 1) * v + 4 * n * k * v + 4 * n * (2 * k + 1) + 8 * n * (k + 1) + 8 * n * 3 + 8 * n * k
+
+
+def cpu_baseline(w, repeats=1):
+    """The torch-CPU oracle (restatement of the reference Torch path) on this host."""
+    from oracle import attention as oatt
+    from oracle import sampling as osamp
+
+    k_view = w["key_pool"][:, w["layer"]].cpu()
+    v_view = w["value_pool"][:, w["layer"]].cpu()
+    q, tables, lengths, cu = w["q"].cpu(), w["tables"], w["lengths"].int(), w["cu"]
+    qprob, pprob, u = w["qprob"].cpu(), w["pprob"].cpu(), w["u"]
+    drafts_tok = w["draft_tokens"].cpu()
+    drafts = torch.full((w["n"],), w["k"], dtype=torch.int64)
+    k = w["k"]
+    t0 = time.perf_counter()
+    for _ in range(repeats):
+        oatt.packed_window_attention(q, k_view, v_view, tables, lengths, cu)
+        osamp.speculative_accept(drafts_tok, drafts, qprob, pprob, u[:, k:2 * k].contiguous(),
+                                 u[:, 2 * k].contiguous())
+    dt = (time.perf_counter() - t0) / repeats
+    return {"value": round(w["n"] * w["window"] / dt, 2), "unit": "verified tokens/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"full config3 verify step (32 requests x 5 rows, ctx U[1024,8192]) x {repeats}, "
+                      f"{dt * 1e3:.0f} ms per step, torch-CPU oracle "
+                      f"(os.cpu_count={os.cpu_count()})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=("attention", "accept"),
+                    help="replay only this part K times and exit (for counter collection)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the verify path has no "
+                                   "cross-GPU exchange (requests shard by data parallelism); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    w = build_workload(dev)
+    backend = pkg.create_backend("auto", dev, torch.bfloat16, w["d"], w["bs"])
+    k = w["k"]
+    kc = w["key_pool"][:, w["layer"]]
+    vc = w["value_pool"][:, w["layer"]]
+    tables, lengths, cu = w["tables"].to(dev), w["lengths"].int().to(dev), w["cu"].to(dev)
+    u = w["u"].to(dev)
+    ua, uf = u[:, k:2 * k].contiguous(), u[:, 2 * k].contiguous()
+    drafts = torch.full((w["n"],), k, dtype=torch.int64, device=dev)
+    # draft tokens sampled from q with the draft uniforms (the _draft step)
+    w["draft_tokens"] = torch.stack(
+        [pkg.categorical(w["qprob"][:, j].contiguous(), u[:, j].contiguous())[0] for j in range(k)], 1)
+    dt_tok = w["draft_tokens"]
+
+    def attn():
+        return backend.prefill(w["q"], kc, vc, tables, lengths, cu, w["window"])
+
+    def accept():
+        return pkg.speculative_accept(dt_tok, drafts, w["qprob"], w["pprob"], ua, uf)
+
+    for _ in range(max(args.warmup, 1)):
+        attn()
+        accept()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            attn()
+            accept()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g_attn, g_acc, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_attn):
+        out_attn = attn()
+    with torch.cuda.graph(g_acc):
+        out_acc = accept()
+    with torch.cuda.graph(g_step):
+        attn()
+        accept()
+    for _ in range(args.warmup):
+        g_step.replay()
+    torch.cuda.synchronize()
+    if args.only:
+        graph = g_attn if args.only == "attention" else g_acc
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "steps": args.steps}), flush=True)
+        return
+
+    # ---- timed region: K whole verify steps
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        g_step.replay()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+
+    # ---- per-launch durations with HIP events on the launch stream, queue pre-filled
+    def launch_time(graph, reps):
+        s = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        torch.cuda._sleep(50_000_000)  # keep the GPU busy while the host enqueues
+        for a, b in ev:
+            a.record(s)
+            graph.replay()
+            b.record(s)
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3
+
+    t_attn = launch_time(g_attn, args.steps)
+    t_acc = launch_time(g_acc, args.steps)
+
+    # ---- correctness of the measured outputs against an eager run
+    eager_attn = attn()
+    eager_acc = accept()
+    torch.cuda.synchronize()
+    assert torch.equal(eager_attn, out_attn)
+    for a, b in zip(eager_acc, out_acc):
+        assert torch.equal(a, b)
+
+    a_bytes, c_bytes = attention_bytes(w), accept_bytes(w)
+    achieved = a_bytes / t_attn / 1e9
+    tokens = w["n"] * w["window"]
+    result = {
+        "metric": METRIC,
+        "value": round(tokens / step_s, 1),
+        "unit": "verified tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random KV, q and logits; no model or dataset)",
+        "config": {
+            "workload": "config3 verify step: packed q_len=5 causal window, 16q/4kv heads, D=128, "
+                        "bf16 SHARED KV, batch 32, ctx U[1024,8192]; acceptance V=49152, T=0.7, top-p 0.9",
+            "batch": w["n"], "window": w["window"], "q_heads": w["hq"], "kv_heads": w["hkv"],
+            "head_dim": w["d"], "block_size": w["bs"], "vocab": w["vocab"],
+            "ctx_sum": int(w["lengths"].sum()),
+        },
+        "hbm_frac_step": round((a_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
+        "attention_ms": round(t_attn * 1e3, 4),
+        "accept_ms": round(t_acc * 1e3, 4),
+        "roofline": {
+            "kernel": "attention launch (rlt_attn_mfma_kernel + rlt_merge_kernel)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": a_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -159,6 +159,12 @@ struct Mfma<RLT_BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, c, 0, 0, 0);
   }
   __device__ static uint16_t from_f32(float x) { return f32_to_bf16_bits(x); }
+  // two floats -> packed pair (v_cvt_pk_bf16_f32, round to nearest even)
+  __device__ static uint32_t pack2(float a, float b) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 };
 
 template <>
@@ -176,6 +182,16 @@ struct Mfma<RLT_F16> {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, c, 0, 0, 0);
   }
   __device__ static uint16_t from_f32(float x) { return f32_to_f16_bits(x); }
+  __device__ static uint32_t pack2(float a, float b) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
 };
 
 // Four fp8 codes -> four 16-bit values of the MFMA type (exact for e4m3).
@@ -195,44 +211,44 @@ __device__ __forceinline__ uint2 fp8x4_to_16(uint32_t w) {
   return r;
 }
 
-// One lane's head_dim/4 slice of one key or value vector, in MFMA element type.
+// One lane's raw head_dim/4 slice of a key or value vector, as loaded from HBM.
+// Conversion to the MFMA element type happens at use, so a load in flight never
+// forces a wait.
 template <int QT, int KVT, int D>
-struct KvSlice {
-  static constexpr int kElems = D / 4;       // 16-bit elements per lane
-  static constexpr int kVec = kElems / 8;    // 16-byte vectors per lane
-  uint4 x[kVec];
+struct RawSlice {
+  static constexpr int kBytes = (KVT == QT ? 2 : 1) * (D / 4);
+  static constexpr int kWords = kBytes / 4;
+  static constexpr bool kQuad = kBytes % 16 == 0;  // dwordx4 loads, else dwordx2
+  uint32_t w[kWords];
 
-  __device__ __forceinline__ void zero() {
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    if (kQuad) {
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) x[i] = make_uint4(0, 0, 0, 0);
-  }
-  __device__ __forceinline__ void load(const void* base, int64_t elem_off) {
-    if (KVT == QT) {
-      const uint4* p = (const uint4*)((const uint16_t*)base + elem_off);
+      for (int i = 0; i < kWords / 4; ++i) {
+        const uint4 v = ((const uint4*)p)[i];
+        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+      }
+    } else {
 #pragma unroll
-      for (int i = 0; i < kVec; ++i) x[i] = p[i];
-    } else {  // fp8: kElems bytes
-      const uint8_t* p = (const uint8_t*)base + elem_off;
-      if (kVec % 2 == 0) {
-        const uint4* pv = (const uint4*)p;
-#pragma unroll
-        for (int i = 0; i < kVec / 2; ++i) {
-          const uint4 w = pv[i];
-          uint2 a = fp8x4_to_16<QT>(w.x), b = fp8x4_to_16<QT>(w.y);
-          uint2 c = fp8x4_to_16<QT>(w.z), d = fp8x4_to_16<QT>(w.w);
-          x[2 * i] = make_uint4(a.x, a.y, b.x, b.y);
-          x[2 * i + 1] = make_uint4(c.x, c.y, d.x, d.y);
-        }
-      } else {
-        const uint2* pv = (const uint2*)p;
-#pragma unroll
-        for (int i = 0; i < kVec; ++i) {
-          const uint2 w = pv[i];
-          uint2 a = fp8x4_to_16<QT>(w.x), b = fp8x4_to_16<QT>(w.y);
-          x[i] = make_uint4(a.x, a.y, b.x, b.y);
-        }
+      for (int i = 0; i < kWords / 2; ++i) {
+        const uint2 v = ((const uint2*)p)[i];
+        w[2 * i] = v.x; w[2 * i + 1] = v.y;
       }
     }
+  }
+  // Eight consecutive elements [8s, 8s + 8) of the slice as MFMA operand bits;
+  // zeros when `ok` is false (positions past the sequence may hold any bits).
+  __device__ __forceinline__ uint4 op(int s, bool ok) const {
+    uint4 r;
+    if (KVT == QT) {
+      r = make_uint4(w[4 * s], w[4 * s + 1], w[4 * s + 2], w[4 * s + 3]);
+    } else {
+      const uint2 a = fp8x4_to_16<QT>(w[2 * s]);
+      const uint2 b = fp8x4_to_16<QT>(w[2 * s + 1]);
+      r = make_uint4(a.x, a.y, b.x, b.y);
+    }
+    if (!ok) r = make_uint4(0, 0, 0, 0);
+    return r;
   }
 };
 
@@ -246,12 +262,16 @@ struct MfmaShared {
   float ml[2][NT * 16][2];
 };
 
-template <int QT, int KVT, int D, int NT>
+// SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).
+template <int QT, int KVT, int D, int NT, int SM>
 __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   using M = Mfma<QT>;
+  using Raw = RawSlice<QT, KVT, D>;
   constexpr int NQS = D / 32;  // 32-wide contraction slices
   constexpr int ND = D / 16;   // 16-wide output column tiles
   constexpr int DQ = D / 4;    // elements per lane group
+  constexpr int KV_ELT = KVT == QT ? 2 : 1;
+  constexpr int TW = kTilesPerWave;
   __shared__ MfmaShared<QT, KVT, D, NT> sh;
 
   const int seq = blockIdx.x / P.rowgroups;
@@ -273,6 +293,25 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
   const int c_begin = chunk * kChunk;
   if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
+
+  // Tiles of this wave: absolute 16-aligned positions [w_begin + 16t, +16), t in [t0, t1).
+  const int w_begin = c_begin + wave * kWaveSpan;
+  const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
+  const int span_hi = min(w_begin + kWaveSpan, hi_last);
+  // wave-uniform (scalar) bounds: keeps the tile loop free of divergent branches
+  const int t0 = __builtin_amdgcn_readfirstlane(
+      span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok);
+  const int t1 = __builtin_amdgcn_readfirstlane(
+      span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok);
+
+  // Block-table entries of all this lane's positions, issued before any KV load.
+  int32_t blk[TW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    const int pos = w_begin + t * kTileTok + l16;
+    const int idx = min(pos / P.block_size, P.table_width - 1);
+    blk[t] = P.tables[(int64_t)seq * P.table_stride + idx];
+  }
 
   // This lane's rows (one per 16-row tile): B operand of S^T = K Q^T.
   int row_lo[NT], row_hi[NT];
@@ -298,7 +337,7 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
 
   float qk_scale = P.qk_scale_log2;
   float v_mul = 1.f;
-  if (P.scale_mode == 1) {
+  if (SM == 1) {
     qk_scale *= P.k_scale[0];
     v_mul = P.v_scale[0];
   }
@@ -313,132 +352,135 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
     for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Tiles of this wave: absolute 16-aligned positions within [span_lo, span_hi).
-  const int w_begin = c_begin + wave * kWaveSpan;
-  const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
-  const int span_hi = min(w_begin + kWaveSpan, hi_last);
-  const int t0 = span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok;
-  const int t1 = span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok;
-
-  // Key position of this lane in tile t (A-operand row = l16) and its KV offset.
-  auto tile_off = [&](int t, int64_t& koff, int64_t& voff, bool& ok) {
-    const int pos = w_begin + t * kTileTok + l16;
-    ok = pos < hi_last;
-    koff = voff = 0;
-    if (ok) {
-      const int64_t blk = block_of(P, seq, pos);
-      const int64_t off = pos % P.block_size;
-      koff = blk * P.k_block_stride + off * P.k_token_stride +
-             (int64_t)kvh * P.k_head_stride + grp * DQ;
-      voff = blk * P.v_block_stride + off * P.v_token_stride +
-             (int64_t)kvh * P.v_head_stride + grp * DQ;
-    }
-  };
-
-  KvSlice<QT, KVT, D> kcur, vcur, knext, vnext;
-  {
-    int64_t ko, vo;
-    bool ok;
-    if (t0 < t1) {
-      tile_off(t0, ko, vo, ok);
-      if (ok) {
-        kcur.load(P.k, ko);
-        vcur.load(P.v, vo);
-      } else {
-        kcur.zero();
-        vcur.zero();
-      }
-    }
-  }
-  auto& vt = sh.vt[wave];
-
-  for (int t = t0; t < t1; ++t) {
-    if (t + 1 < t1) {
-      int64_t ko, vo;
-      bool ok;
-      tile_off(t + 1, ko, vo, ok);
-      if (ok) {
-        knext.load(P.k, ko);
-        vnext.load(P.v, vo);
-      } else {
-        knext.zero();
-        vnext.zero();
-      }
-    }
-    const int tb = w_begin + t * kTileTok;
-    // ---- S^T = K Q^T : lane holds (positions tb + 4*grp + r, row l16 of tile nt)
-    f32x4 sc[NT];
+  if (t0 < t1) {
+    Raw kb[2], vb[2];
+    float ksc[2][4], vsc[2][4];
+    bool okb[2];
+    // Loads of tile t into stage b.  Branch-free: a position outside the wave's
+    // range reads block 0 (always inside the pool) and is zeroed at use.
+    auto issue = [&](int t, int b) {
+      const int pos = w_begin + t * kTileTok + l16;
+      const bool ok = t >= t0 && t < t1 && pos < hi_last;
+      okb[b] = ok;
+      // entries outside the pool read block 0, as everywhere else in this file
+      const int64_t bk = (ok && blk[t] >= 0 && blk[t] < P.num_blocks) ? (int64_t)blk[t] : 0;
+      const int64_t off = ok ? (int64_t)(pos % P.block_size) : 0;
+      const uint8_t* kp = (const uint8_t*)P.k +
+          (bk * P.k_block_stride + off * P.k_token_stride + (int64_t)kvh * P.k_head_stride + grp * DQ) * KV_ELT;
+      const uint8_t* vp = (const uint8_t*)P.v +
+          (bk * P.v_block_stride + off * P.v_token_stride + (int64_t)kvh * P.v_head_stride + grp * DQ) * KV_ELT;
+      kb[b].load(kp);
+      vb[b].load(vp);
+      if (SM == 2) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      sc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < NQS; ++s) sc[nt] = M::qk(kcur.x[s], qreg[nt][s], sc[nt]);
-    }
-    // ---- V tile to LDS (row = key position, contiguous head_dim)
-#pragma unroll
-    for (int i = 0; i < KvSlice<QT, KVT, D>::kVec; ++i)
-      *(uint4*)&vt[l16][grp * DQ + 8 * i] = vcur.x[i];
-    // per-position scales of this lane's 4 positions (per-vector FP8)
-    float ks[4] = {1.f, 1.f, 1.f, 1.f}, vs[4] = {1.f, 1.f, 1.f, 1.f};
-    if (P.scale_mode == 2) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pos = tb + 4 * grp + r;
-        if (pos < hi_last) {
-          ks[r] = scale_at(P, P.k_scale, seq, pos, kvh);
-          vs[r] = scale_at(P, P.v_scale, seq, pos, kvh);
+        for (int r = 0; r < 4; ++r) {
+          const int p4 = w_begin + t * kTileTok + 4 * grp + r;
+          const bool ok4 = t >= t0 && t < t1 && p4 < hi_last;
+          ksc[b][r] = ok4 ? scale_at(P, P.k_scale, seq, p4, kvh) : 0.f;
+          vsc[b][r] = ok4 ? scale_at(P, P.v_scale, seq, p4, kvh) : 0.f;
         }
       }
-    }
-    // ---- online softmax (log2 domain) and P^T operand
-    uint2 pop[NT];
+    };
+    auto& vt = sh.vt[wave];
+    // Wave-uniform fast-path bound: a tile inside [lo of the last row, hi of the
+    // first row) is visible to every row of the row-group and fully stored, so
+    // it needs no position masks.  Both paths compute identical bits for a row.
+    const int full_lo = lo_last;
+    const int full_hi = hi_first;
+    auto compute = [&](int t, int b, auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      const int tb = w_begin + t * kTileTok;
+      const bool okv = FULL ? true : okb[b];
+      // ---- S^T = K Q^T : lane holds (positions tb + 4*grp + r, row l16 of tile nt)
+      f32x4 sc[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float sv4[4];
-      float mx = -INFINITY;
+      for (int nt = 0; nt < NT; ++nt) sc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pos = tb + 4 * grp + r;
-        const bool vis = pos >= row_lo[nt] && pos < row_hi[nt];
-        const float x = sc[nt][r] * ks[r] * qk_scale;
-        sv4[r] = vis ? x : -INFINITY;
-        mx = fmaxf(mx, sv4[r]);
+      for (int s = 0; s < NQS; ++s) {
+        const uint4 a = kb[b].op(s, okv);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) sc[nt] = M::qk(a, qreg[nt][s], sc[nt]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, RLT_WAVE));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, RLT_WAVE));
-      const float m_new = fmaxf(m_run[nt], mx);
-      float pr[4];
-      float corr = 1.f;
-      if (m_new == -INFINITY) {
-        pr[0] = pr[1] = pr[2] = pr[3] = 0.f;
-      } else {
-        corr = exp2f(m_run[nt] - m_new);
+      // ---- V tile to LDS (row = key position, contiguous head_dim)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = exp2f(sv4[r] - m_new);
+      for (int i = 0; i < NQS; ++i) *(uint4*)&vt[l16][grp * DQ + 8 * i] = vb[b].op(i, okv);
+      // ---- online softmax (log2 domain) and the P^T operand
+      uint2 pop[NT];
+      bool rescale = false;
+      float corr[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        float sv4[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = sc[nt][r];
+          if (SM == 2) x *= ksc[b][r];
+          x *= qk_scale;
+          if (!FULL) {
+            const int pos = tb + 4 * grp + r;
+            x = (pos >= row_lo[nt] && pos < row_hi[nt]) ? x : -INFINITY;
+          }
+          sv4[r] = x;
+          mx = fmaxf(mx, x);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, RLT_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, RLT_WAVE));
+        const float m_new = fmaxf(m_run[nt], mx);
+        float pr[4];
+        corr[nt] = 1.f;
+        if (m_new == -INFINITY) {
+          pr[0] = pr[1] = pr[2] = pr[3] = 0.f;
+        } else {
+          corr[nt] = exp2f(m_run[nt] - m_new);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pr[r] = exp2f(sv4[r] - m_new);
+        }
+        rescale |= corr[nt] != 1.f;
+        float rs = ((pr[0] + pr[1]) + pr[2]) + pr[3];
+        rs += __shfl_xor(rs, 16, RLT_WAVE);
+        rs += __shfl_xor(rs, 32, RLT_WAVE);
+        l_run[nt] = l_run[nt] * corr[nt] + rs;
+        m_run[nt] = m_new;
+        if (SM == 2) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pr[r] *= vsc[b][r];
+        }
+        pop[nt].x = M::pack2(pr[0], pr[1]);
+        pop[nt].y = M::pack2(pr[2], pr[3]);
       }
-      float rs = ((pr[0] + pr[1]) + pr[2]) + pr[3];
-      rs += __shfl_xor(rs, 16, RLT_WAVE);
-      rs += __shfl_xor(rs, 32, RLT_WAVE);
-      l_run[nt] = l_run[nt] * corr + rs;
-      m_run[nt] = m_new;
+      // multiplying by exactly 1 changes no bit: skip the rescale when no row's
+      // running max moved in this tile (wave-uniform vote)
+      if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] *= corr;
-      pop[nt].x = (uint32_t)M::from_f32(pr[0] * vs[0]) | ((uint32_t)M::from_f32(pr[1] * vs[1]) << 16);
-      pop[nt].y = (uint32_t)M::from_f32(pr[2] * vs[2]) | ((uint32_t)M::from_f32(pr[3] * vs[3]) << 16);
-    }
-    // ---- O^T += V^T P^T : A = V^T (dims 16dt + l16, positions 4grp..+3)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) {
-      const int d = dt * 16 + l16;
-      uint2 a;
-      a.x = (uint32_t)vt[4 * grp + 0][d] | ((uint32_t)vt[4 * grp + 1][d] << 16);
-      a.y = (uint32_t)vt[4 * grp + 2][d] | ((uint32_t)vt[4 * grp + 3][d] << 16);
+          for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] *= corr[nt];
+      }
+      // ---- O^T += V^T P^T : A = V^T (dims 16dt + l16, positions 4grp..+3)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::pv(a, pop[nt], oacc[nt][dt]);
-    }
-    if (t + 1 < t1) {
-      kcur = knext;
-      vcur = vnext;
+      for (int dt = 0; dt < ND; ++dt) {
+        const int d = dt * 16 + l16;
+        uint2 a;
+        a.x = (uint32_t)vt[4 * grp + 0][d] | ((uint32_t)vt[4 * grp + 1][d] << 16);
+        a.y = (uint32_t)vt[4 * grp + 2][d] | ((uint32_t)vt[4 * grp + 3][d] << 16);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::pv(a, pop[nt], oacc[nt][dt]);
+      }
+    };
+    // Two-stage pipeline: tile t + 2 is issued into the stage tile t just freed.
+    // Issues are unconditional (tiles outside [t0, t1) read block 0 and are
+    // masked) so the wait counts stay exact: no branch merges pending loads.
+    issue(0, 0);
+    issue(1, 1);
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+      if (t >= t0 && t < t1) {
+        const int tb = w_begin + t * kTileTok;
+        if (tb >= full_lo && tb + kTileTok <= full_hi) compute(t, t & 1, Flag<true>{});
+        else compute(t, t & 1, Flag<false>{});
+      }
+      if (t + 2 < TW) issue(t + 2, t & 1);
     }
   }
 
@@ -712,12 +754,18 @@ __global__ __launch_bounds__(256) void rlt_attn_vec_kernel(AttnParams P) {
 
 // ============================================================ merge
 
-// grid (rows, hq), 64 threads: combine a row's chunks in chunk order and normalize.
-// reference: triton_attention.py:145-173 (empty rows give zeros; 1e-30 floor).
+// grid (rows, ceil(hq / 4)), 256 threads: one wave per (row, head).  Combines the
+// row's chunks: lane c holds chunk c's (max, sum), the scale exp2(m_c - M) and the
+// normalizer come from fixed-order wave reductions, then every lane accumulates
+// its head dims over the chunks in chunk order.  The order depends only on the
+// row's own chunk range.  reference: triton_attention.py:145-173 (empty rows give
+// zeros; 1e-30 floor).
 template <int OT>
-__global__ __launch_bounds__(64) void rlt_merge_kernel(AttnParams P) {
+__global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
   const int row = blockIdx.x;
-  const int head = blockIdx.y;
+  const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (head >= P.hq) return;
   int seq, qi;
   if (P.cu_q) {
     int lo = 0, hi = P.num_seqs;  // last seq with cu[seq] <= row
@@ -736,35 +784,86 @@ __global__ __launch_bounds__(64) void rlt_merge_kernel(AttnParams P) {
   int lo, hi;
   row_range(P, sv, qi, lo, hi);
   const int c0 = lo / kChunk, c1 = (hi + kChunk - 1) / kChunk;
-  const int64_t base = ((int64_t)row * P.hq + head) * P.max_chunks;
-  float mmax = -INFINITY;
-  for (int c = c0; c < c1; ++c) mmax = fmaxf(mmax, P.part_ml[2 * (base + c)]);
-  float l = 0.f;
-  for (int c = c0; c < c1; ++c) {
-    const float m = P.part_ml[2 * (base + c)];
-    const float s = m == -INFINITY ? 0.f : exp2f(m - mmax);
-    l += P.part_ml[2 * (base + c) + 1] * s;
+  const int nc = c1 - c0;
+  const int64_t base = ((int64_t)row * P.hq + head) * P.max_chunks + c0;
+  const int64_t out_off = (int64_t)row * P.out_row_stride + (int64_t)head * P.out_head_stride;
+  if (nc <= 0) {
+    for (int d = lane; d < P.head_dim; d += 64) store_from_f32<OT>(P.out, out_off + d, 0.f);
+    return;
   }
-  const float inv_den = 1.f / fmaxf(l, 1.0e-30f);
-  for (int d = threadIdx.x; d < P.head_dim; d += blockDim.x) {
-    float o = 0.f;
-    for (int c = c0; c < c1; ++c) {
+  // chunk statistics, 64 chunks per pass (a row has at most max_chunks)
+  float mmax = -INFINITY;
+  for (int c = lane; c < nc; c += 64) mmax = fmaxf(mmax, P.part_ml[2 * (base + c)]);
+  for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off, RLT_WAVE));
+  float l = 0.f;
+  for (int c0p = 0; c0p < nc; c0p += 64) {
+    const int c = c0p + lane;
+    float part = 0.f;
+    if (c < nc) {
       const float m = P.part_ml[2 * (base + c)];
       const float s = m == -INFINITY ? 0.f : exp2f(m - mmax);
-      o += P.part_o[(base + c) * P.head_dim + d] * s;
+      part = P.part_ml[2 * (base + c) + 1] * s;
     }
-    store_from_f32<OT>(P.out, (int64_t)row * P.out_row_stride + (int64_t)head * P.out_head_stride + d,
-                       c0 < c1 ? o * inv_den : 0.f);
+    for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, RLT_WAVE);
+    l += part;
+  }
+  const float inv_den = 1.f / fmaxf(l, 1.0e-30f);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0p = 0; c0p < nc; c0p += 64) {
+    const int cn = min(64, nc - c0p);
+    float my_s = 0.f;
+    if (lane < cn) {
+      const float m = P.part_ml[2 * (base + c0p + lane)];
+      my_s = m == -INFINITY ? 0.f : exp2f(m - mmax);
+    }
+    int c = 0;
+    for (; c + 4 <= cn; c += 4) {  // four chunks of loads in flight
+      float v[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = lane + 64 * e;
+          v[u][e] = d < P.head_dim ? P.part_o[(base + c0p + c + u) * P.head_dim + d] : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float s = __shfl(my_s, c + u, RLT_WAVE);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += v[u][e] * s;
+      }
+    }
+    for (; c < cn; ++c) {
+      const float s = __shfl(my_s, c, RLT_WAVE);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d < P.head_dim) acc[e] += P.part_o[(base + c0p + c) * P.head_dim + d] * s;
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = lane + 64 * e;
+    if (d < P.head_dim) store_from_f32<OT>(P.out, out_off + d, acc[e] * inv_den);
   }
 }
 
 // ============================================================ dispatch
 
+template <int QT, int KVT, int D, int SM>
+int launch_mfma_sm(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
+  if (nt == 1) rlt_attn_mfma_kernel<QT, KVT, D, 1, SM><<<grid, 256, 0, stream>>>(P);
+  else if (D <= 128) rlt_attn_mfma_kernel<QT, KVT, D, (D <= 128 ? 2 : 1), SM><<<grid, 256, 0, stream>>>(P);
+  else return RLT_ERR_UNSUPPORTED;
+  return RLT_OK;
+}
+
 template <int QT, int KVT, int D>
 int launch_mfma_d(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
-  if (nt == 1) rlt_attn_mfma_kernel<QT, KVT, D, 1><<<grid, 256, 0, stream>>>(P);
-  else rlt_attn_mfma_kernel<QT, KVT, D, 2><<<grid, 256, 0, stream>>>(P);
-  return RLT_OK;
+  if (KVT == QT) return launch_mfma_sm<QT, KVT, D, 0>(P, grid, nt, stream);
+  if (P.scale_mode == 1) return launch_mfma_sm<QT, KVT, D, 1>(P, grid, nt, stream);
+  return launch_mfma_sm<QT, KVT, D, 2>(P, grid, nt, stream);
 }
 
 template <int QT, int KVT>
@@ -920,11 +1019,11 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     }
   }
   if (st != RLT_OK) return st;
-  dim3 mgrid((unsigned)num_q_rows, (unsigned)num_q_heads);
+  dim3 mgrid((unsigned)num_q_rows, (unsigned)((num_q_heads + 3) / 4));
   switch (q_dtype) {
-    case RLT_F32: rlt_merge_kernel<RLT_F32><<<mgrid, 64, 0, stream>>>(P); break;
-    case RLT_F16: rlt_merge_kernel<RLT_F16><<<mgrid, 64, 0, stream>>>(P); break;
-    case RLT_BF16: rlt_merge_kernel<RLT_BF16><<<mgrid, 64, 0, stream>>>(P); break;
+    case RLT_F32: rlt_merge_kernel<RLT_F32><<<mgrid, 256, 0, stream>>>(P); break;
+    case RLT_F16: rlt_merge_kernel<RLT_F16><<<mgrid, 256, 0, stream>>>(P); break;
+    case RLT_BF16: rlt_merge_kernel<RLT_BF16><<<mgrid, 256, 0, stream>>>(P); break;
   }
   return rlt_launch_status();
 }

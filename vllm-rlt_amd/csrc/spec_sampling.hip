@@ -1,24 +1,26 @@
 // Acceptance / rejection sampler for speculative verification on MI355X (gfx950).
 //
 // Replaces the eager torch chain of vllm_rlt/worker/speculative_sampling.py:59-181
-// (``categorical`` and ``speculative_accept``) with four vocab-wide passes that are
+// (``categorical`` and ``speculative_accept``) with three launches that are
 // bit-exact against the torch-CPU arithmetic the reference defines:
 //
-//  1. rlt_mass_groups_kernel  -- every p and q row, split into 8192-float groups:
-//     each group's per-stream partial of torch's fp32 cascade row sum.
-//  2. rlt_accept_stop_kernel  -- one wave per request: finishes the exact fp32
-//     masses, then the accept chain (px >= qx or u*qx < px), the stop point s and
-//     the stop-point validity.
-//  3. rlt_weight_tiles_kernel -- the final distribution (p[s]/mass at the end of
-//     the drafts, else clamp_min(p[s]/pm - q[s]/qm, 0)) in 2048-token tiles:
-//     per-tile float64 totals plus non-finite / negative / positive flags.
-//  4. rlt_draw_kernel         -- per request: locates the tile and token where the
-//     float64 CDF crosses t = u * mass, certifies the crossing against a bound on
-//     the difference between any float64 summation order and torch's sequential
-//     cumsum, and otherwise replays the sequential cumsum on one lane (exact by
-//     construction).  Writes tokens / accepted / final / error.
+//  1. rlt_mass_groups_kernel -- every p and q row of the batch, split into
+//     8192-float groups across the whole GPU: each group's per-stream partial of
+//     torch's fp32 cascade row sum (the HBM-bound pass: p and q read once).
+//  2. rlt_accept_tiles_kernel -- (request, 4096-token tile) workgroups: the exact
+//     fp32 row masses from the partials, the accept chain (px >= qx or
+//     u*qx < px), stop point s and validity (recomputed identically by every tile
+//     of a request), then the tile's float64 total of the final distribution
+//     (p[s]/mass at the end of the drafts, else clamp_min(p[s]/pm - q[s]/qm, 0))
+//     with NaN / +inf / negative / positive flags.
+//  3. rlt_accept_draw_kernel -- one workgroup per request: the inverse-CDF draw.
+//     It locates the tile and token where the float64 CDF crosses t = u * mass,
+//     certifies the crossing against a bound on the difference between any
+//     float64 summation order and torch's sequential cumsum, and otherwise replays
+//     the sequential cumsum on one lane (exact by construction); then tokens /
+//     accepted / final / error.
 //
-// The standalone ``categorical`` runs passes 3 and 4 on raw weights.
+// ``categorical`` runs one workgroup per row on raw weights (tile totals + draw).
 //
 // torch's fp32 row-sum order (what ``p.sum(-1, dtype=float32)`` computes on CPU):
 // 32 streams, stream s = 8k + l owns elements 32*i + s (8-lane vectors, 4 in
@@ -38,10 +40,12 @@ constexpr int kStreams = 32;          // 8 lanes x ILP 4
 constexpr int kChunkSteps = 16;       // stream steps per level-0 chunk
 constexpr int kGroupChunks = 16;      // chunks per level-1 group
 constexpr int kGroupFloats = kStreams * kChunkSteps * kGroupChunks;  // 8192
-constexpr int kTileThreads = 256;
-constexpr int kTileElems = 8;                              // per thread
-constexpr int kTile = kTileThreads * kTileElems;           // 2048 tokens
-constexpr int kMaxTiles = 1024;                            // V <= 2M on the fast path
+constexpr int kDrawThreads = 512;
+constexpr int kDrawWaves = kDrawThreads / 64;
+constexpr int kElems = 8;                           // weights per thread per tile
+constexpr int kTile = kDrawThreads * kElems;        // 4096 tokens
+constexpr int kMaxTiles = 512;                      // V <= 2M on the fast path
+constexpr int kMaxW1 = 32;
 
 struct RowGeom {
   int64_t vs;  // whole 8-lane vectors
@@ -59,7 +63,7 @@ __host__ __device__ inline RowGeom row_geom(int64_t V) {
   return g;
 }
 
-// ------------------------------------------------------------------ pass 1
+// ------------------------------------------------------------------ kernel 1
 
 // grid (groups, rows), 128 threads: thread t sums chunk t/8 of the group for the
 // four streams 4*(t%8)..+3 (16 sequential fp32 adds each), then 32 threads add the
@@ -104,16 +108,15 @@ __global__ __launch_bounds__(128) void rlt_mass_groups_kernel(const float* __res
     chunk_sum[cc][quad * 4 + 3] = a3;
   }
   __syncthreads();
-  if (t < kStreams) {
+  if (t < kStreams && chunks_here > 0) {
     float acc1 = 0.f;
     for (int c = 0; c < chunks_here; ++c) acc1 += chunk_sum[c][t];
     out[(row * groups + g) * kStreams + t] = acc1;
   }
 }
 
-// Exact torch-CPU fp32 row sum of x[0..V) from the group partials (or from
-// memory alone when V < 32 / partials == nullptr).  Called by one full wave; the
-// result is valid in every lane.
+// Exact torch-CPU fp32 row sum of x[0..V) from the group partials (nullptr when
+// the row has no complete chunk).  Called by one full wave; valid in every lane.
 __device__ float rlt_row_mass_finish(const float* __restrict__ x, int64_t V,
                                      const float* __restrict__ partials) {
   const int lane = threadIdx.x & 63;
@@ -132,7 +135,21 @@ __device__ float rlt_row_mass_finish(const float* __restrict__ x, int64_t V,
     const int s = lane;
     float acc2 = 0.f, acc3 = 0.f, acc1 = 0.f;
     const int64_t complete = geo.full_chunks / kGroupChunks;
-    for (int64_t g = 0; g < complete; ++g) {
+    int64_t g = 0;
+    for (; g + 8 <= complete; g += 8) {  // 8 independent loads in flight
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = partials[(g + u) * kStreams + s];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        acc2 += v[u];
+        if ((g + u + 1) % 16 == 0) {
+          acc3 += acc2;
+          acc2 = 0.f;
+        }
+      }
+    }
+    for (; g < complete; ++g) {
       acc2 += partials[g * kStreams + s];
       if ((g + 1) % 16 == 0) {
         acc3 += acc2;
@@ -158,79 +175,55 @@ __device__ float rlt_row_mass_finish(const float* __restrict__ x, int64_t V,
   return f;
 }
 
-__device__ __forceinline__ bool finite_pos(float m) { return isfinite(m) && m > 0.f; }
-
-// ------------------------------------------------------------------ pass 2
-
-struct StopState {
-  int32_t s;        // leading valid accepts
-  int32_t at_end;   // s == d: the final draw is the bonus from p[s]
-  int32_t stop_ok;  // the stop point is numerically valid
-  int32_t err0;     // drafts out of [0, W1]
-  float pm;         // p[s] mass
-  float qm;         // q[s] mass (residual only)
-  int32_t pad[2];
-};
-
-// grid (n), 64 threads.  reference: speculative_sampling.py:136-172.
-__global__ __launch_bounds__(64) void rlt_accept_stop_kernel(
-    const int64_t* __restrict__ draft_tokens, const int64_t* __restrict__ drafts,
-    const float* __restrict__ q, const float* __restrict__ p, const float* __restrict__ u_accept,
-    int64_t n, int W1, int64_t V, const float* __restrict__ partials, int64_t groups,
-    StopState* __restrict__ state) {
-  const int64_t i = blockIdx.x;
-  const int lane = threadIdx.x;
-  // Masses: rows j of p (W1 + 1) and q (W1), exact torch order.
-  __shared__ float pm_s[33], qm_s[32];
-  for (int j = 0; j <= W1; ++j) {
-    const int64_t row = i * (W1 + 1) + j;
-    float m = rlt_row_mass_finish(p + row * V, V, partials ? partials + row * groups * kStreams : nullptr);
-    if (lane == 0) pm_s[j] = m;
+// Same as rlt_row_mass_finish for one 32-lane half of a wave (lanes 32h..32h+31
+// serve row x): two rows per wave at once.  Valid in every lane of the half.
+__device__ float rlt_row_mass_half(const float* __restrict__ x, int64_t V,
+                                   const float* __restrict__ partials) {
+  const int lane = threadIdx.x & 63;
+  const int s = lane & 31;
+  const int base = lane & 32;
+  if (V < 8) {
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    const int64_t si = V / 4;
+    for (int64_t i = 0; i < si; ++i)
+      for (int k = 0; k < 4; ++k) ps[k] += x[4 * i + k];
+    for (int64_t i = si * 4; i < V; ++i) ps[0] += x[i];
+    return ((ps[0] + ps[1]) + ps[2]) + ps[3];
   }
-  for (int j = 0; j < W1; ++j) {
-    const int64_t row = i * W1 + j;
-    const int64_t prow = n * (W1 + 1) + row;
-    float m = rlt_row_mass_finish(q + row * V, V, partials ? partials + prow * groups * kStreams : nullptr);
-    if (lane == 0) qm_s[j] = m;
-  }
-  __syncthreads();
-  if (lane != 0) return;
-  const int64_t dr = drafts[i];
-  const int64_t d = dr < 0 ? 0 : (dr > W1 ? W1 : dr);
-  int s = 0;
-  bool chain = true;
-  bool invalid_at_s = false;
-  for (int j = 0; j < W1; ++j) {
-    const int64_t tok = draft_tokens[i * W1 + j];
-    const bool in_range = tok >= 0 && tok < V;
-    const int64_t x = tok < 0 ? 0 : (tok > V - 1 ? V - 1 : tok);
-    const float pmj = pm_s[j], qmj = qm_s[j];
-    const float px = __fdiv_rn(p[(i * (W1 + 1) + j) * V + x], pmj);
-    const float qx = __fdiv_rn(q[(i * W1 + j) * V + x], qmj);
-    const bool invalid = !(finite_pos(pmj) && finite_pos(qmj) && in_range && isfinite(px) &&
-                           isfinite(qx) && qx > 0.f);
-    const float ua = u_accept[i * W1 + j];
-    const bool accept = !invalid && ((px >= qx) || (ua * qx < px)) && (j < d);
-    if (chain) {
-      if (accept) {
-        ++s;
-      } else {
-        chain = false;
-        invalid_at_s = invalid;  // meaningful only when s < d
+  const RowGeom geo = row_geom(V);
+  float acc2 = 0.f, acc3 = 0.f, acc1 = 0.f;
+  const int64_t complete = geo.full_chunks / kGroupChunks;
+  for (int64_t g = 0; g < complete; g += 8) {  // up to 8 independent loads in flight
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = g + u < complete ? partials[(g + u) * kStreams + s] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (g + u >= complete) break;
+      acc2 += v[u];
+      if ((g + u + 1) % 16 == 0) {
+        acc3 += acc2;
+        acc2 = 0.f;
       }
     }
   }
-  const bool at_end = s == d;
-  StopState st;
-  st.s = s;
-  st.at_end = at_end;
-  st.stop_ok = at_end ? finite_pos(pm_s[s]) : !invalid_at_s;
-  st.err0 = dr != d;
-  st.pm = pm_s[s];
-  st.qm = at_end ? 1.f : qm_s[s];
-  st.pad[0] = st.pad[1] = 0;
-  state[i] = st;
+  if (geo.full_chunks % kGroupChunks) acc1 = partials[complete * kStreams + s];
+  float acc0 = 0.f;
+  for (int64_t i = geo.full_chunks * kChunkSteps; i < geo.si; ++i) acc0 += x[32 * i + s];
+  float st = ((acc0 + acc1) + acc2) + acc3;
+  if (s < 8)
+    for (int64_t v = geo.si * 4; v < geo.vs; ++v) st += x[v * 8 + s];
+  const float s8 = __shfl(st, base + ((s + 8) & 31), RLT_WAVE);
+  const float s16 = __shfl(st, base + ((s + 16) & 31), RLT_WAVE);
+  const float s24 = __shfl(st, base + ((s + 24) & 31), RLT_WAVE);
+  const float lanes = ((st + s8) + s16) + s24;
+  float f = 0.f;
+  for (int64_t e = geo.vs * 8; e < V; ++e) f += x[e];
+  for (int l = 0; l < 8; ++l) f += __shfl(lanes, base + l, RLT_WAVE);
+  return f;
 }
+
+__device__ __forceinline__ bool finite_pos(float m) { return isfinite(m) && m > 0.f; }
 
 // ------------------------------------------------------------------ weights
 
@@ -242,28 +235,7 @@ struct WeightRow {
   bool raw;
 };
 
-__device__ __forceinline__ WeightRow weight_row(int mode, int64_t i, const float* p, const float* q,
-                                                int W1, int64_t V, const StopState* state) {
-  WeightRow w;
-  if (mode == 0) {
-    w.a = p + i * V;
-    w.b = nullptr;
-    w.am = w.bm = 1.f;
-    w.residual = false;
-    w.raw = true;
-    return w;
-  }
-  const StopState st = state[i];
-  w.a = p + (i * (W1 + 1) + st.s) * V;
-  w.am = st.pm;
-  w.residual = !st.at_end;
-  w.b = w.residual ? q + (i * W1 + st.s) * V : nullptr;
-  w.bm = st.qm;
-  w.raw = false;
-  return w;
-}
-
-// The fp32 weight of token k exactly as torch computes it:
+// The fp32 weight of one token exactly as torch computes it:
 //   at_end: p/pm; else (p/pm - q/qm).clamp_min(0) (NaN propagates).
 __device__ __forceinline__ float weight_of(float a, float b, const WeightRow& w) {
   if (w.raw) return a;
@@ -273,17 +245,11 @@ __device__ __forceinline__ float weight_of(float a, float b, const WeightRow& w)
   return r < 0.f ? 0.f : r;
 }
 
-struct TileFlags {
-  uint32_t nan_or_inf;  // bit0: NaN seen, bit1: +inf seen
-  uint32_t neg;         // a negative weight (or -inf) seen
-  uint32_t pos;         // a positive weight seen
-};
-
-// Loads this thread's 8 weights of tile `tile` (zero past V).
+// This thread's kElems weights of tile `tile` (zero past V).
 __device__ __forceinline__ void load_weights(const WeightRow& w, int64_t V, int64_t tile, int t,
-                                             bool vec_ok, float out[kTileElems]) {
-  const int64_t base = tile * kTile + (int64_t)t * kTileElems;
-  if (vec_ok && base + kTileElems <= V) {
+                                             bool vec_ok, float out[kElems]) {
+  const int64_t base = tile * kTile + (int64_t)t * kElems;
+  if (vec_ok && base + kElems <= V) {
     const float4 a0 = *(const float4*)(w.a + base);
     const float4 a1 = *(const float4*)(w.a + base + 4);
     float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
@@ -295,71 +261,15 @@ __device__ __forceinline__ void load_weights(const WeightRow& w, int64_t V, int6
       bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
     }
 #pragma unroll
-    for (int e = 0; e < kTileElems; ++e) out[e] = weight_of(av[e], bv[e], w);
+    for (int e = 0; e < kElems; ++e) out[e] = weight_of(av[e], bv[e], w);
   } else {
 #pragma unroll
-    for (int e = 0; e < kTileElems; ++e) {
+    for (int e = 0; e < kElems; ++e) {
       const int64_t k = base + e;
       out[e] = k < V ? weight_of(w.a[k], w.residual ? w.b[k] : 0.f, w) : 0.f;
     }
   }
 }
-
-// Deterministic block sum of one double per thread (fixed tree over 256 lanes).
-__device__ double block_sum_f64(double v, double* scratch) {
-  const int t = threadIdx.x;
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, RLT_WAVE);
-  if ((t & 63) == 0) scratch[t >> 6] = v;
-  __syncthreads();
-  const double r = ((scratch[0] + scratch[1]) + scratch[2]) + scratch[3];
-  __syncthreads();
-  return r;
-}
-
-// ------------------------------------------------------------------ pass 3
-
-// grid (tiles, n), 256 threads: per-tile float64 total of the final weights.
-__global__ __launch_bounds__(kTileThreads) void rlt_weight_tiles_kernel(
-    int mode, const float* __restrict__ p, const float* __restrict__ q, int W1, int64_t V,
-    const StopState* __restrict__ state, int64_t tiles, double* __restrict__ tile_sum,
-    TileFlags* __restrict__ tile_flags) {
-  __shared__ double red[4];
-  __shared__ uint32_t fl[3];
-  const int64_t i = blockIdx.y;
-  const int64_t tile = blockIdx.x;
-  const int t = threadIdx.x;
-  if (t < 3) fl[t] = 0;
-  const WeightRow w = weight_row(mode, i, p, q, W1, V, state);
-  const bool vec_ok = (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
-  float wv[kTileElems];
-  load_weights(w, V, tile, t, vec_ok, wv);
-  double local = 0.0;
-  uint32_t nf = 0, neg = 0, pos = 0;
-#pragma unroll
-  for (int e = 0; e < kTileElems; ++e) {
-    const float x = wv[e];
-    if (isnan(x)) nf |= 1u;
-    else if (isinf(x) && x > 0.f) nf |= 2u;
-    if (x < 0.f) neg = 1;
-    if (x > 0.f) pos = 1;
-    local += (double)x;
-  }
-  __syncthreads();
-  if (nf) atomicOr(&fl[0], nf);
-  if (neg) atomicOr(&fl[1], 1u);
-  if (pos) atomicOr(&fl[2], 1u);
-  const double total = block_sum_f64(local, red);
-  if (t == 0) {
-    tile_sum[i * tiles + tile] = total;
-    TileFlags f;
-    f.nan_or_inf = fl[0];
-    f.neg = fl[1];
-    f.pos = fl[2];
-    tile_flags[i * tiles + tile] = f;
-  }
-}
-
-// ------------------------------------------------------------------ pass 4
 
 // Sequential float64 replay of torch's cumsum + searchsorted(right=True) on one
 // lane: exact by construction.  reference: speculative_sampling.py:74-84.
@@ -404,116 +314,114 @@ __device__ int64_t slow_draw(const WeightRow& w, int64_t V, float u, bool* valid
   return lo > V - 1 ? V - 1 : lo;
 }
 
-// grid (n), 256 threads.
-__global__ __launch_bounds__(kTileThreads) void rlt_draw_kernel(
-    int mode, const float* __restrict__ p, const float* __restrict__ q, int W1, int64_t V,
-    const float* __restrict__ u_final, const int64_t* __restrict__ draft_tokens,
-    const StopState* __restrict__ state, int64_t tiles, const double* __restrict__ tile_sum,
-    const TileFlags* __restrict__ tile_flags, int64_t* __restrict__ out_index,
-    uint8_t* __restrict__ out_valid, int64_t* __restrict__ tokens, int64_t* __restrict__ accepted,
-    uint8_t* __restrict__ error, int32_t* __restrict__ slow_count) {
-  __shared__ double scan[kTileThreads];
-  __shared__ int s_decision;  // 0 fast, 1 slow, 2 invalid (index 0)
-  __shared__ int64_t s_tile;
-  __shared__ double s_tilestart, s_t, s_margin;
-  __shared__ int64_t s_best;
-  __shared__ double s_before, s_at;
-  const int64_t i = blockIdx.x;
+// ------------------------------------------------------------------ draw
+
+struct DrawScratch {
+  double tile_total[kMaxTiles];
+  double wave_sum[kDrawWaves];
+  int decision;  // 0 fast, 1 exact replay, 2 invalid row
+  int64_t tile;
+  double tile_start, t, margin;
+  unsigned long long best;
+  double before, at;
+};
+
+// Inverse-CDF draw given the float64 tile totals (in ds.tile_total) and the row's
+// flags.  Called by all kDrawThreads threads; the result is valid in thread 0.
+// Locates the tile and token where the float64 CDF crosses t = u * mass and
+// certifies the crossing against a bound on the difference between any float64
+// summation order and torch's sequential cumsum; otherwise (or for out-of-contract
+// inputs) replays torch's sequential cumsum + right bisect on one lane.
+__device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t tiles,
+                                bool any_nan, bool any_inf, bool any_neg, bool any_pos,
+                                bool vec_ok, DrawScratch& ds, int32_t* slow_count,
+                                int64_t* index_out, bool* valid_out) {
   const int t = threadIdx.x;
-  const WeightRow w = weight_row(mode, i, p, q, W1, V, state);
-  const float u = u_final[i];
+  const int wave = t >> 6;
+  const int lane = t & 63;
   if (t == 0) {
-    bool any_nan = false, any_inf = false, any_neg = false, any_pos = false;
-    double m = 0.0;
-    for (int64_t k = 0; k < tiles; ++k) {
-      const TileFlags f = tile_flags[i * tiles + k];
-      any_nan |= (f.nan_or_inf & 1u) != 0;
-      any_inf |= (f.nan_or_inf & 2u) != 0;
-      any_neg |= f.neg != 0;
-      any_pos |= f.pos != 0;
-      m += tile_sum[i * tiles + k];
-    }
     int decision = 0;
-    if (any_neg || !(u >= 0.f && u < 1.f) || tiles > kMaxTiles) {
-      decision = 1;  // out-of-contract input: exact replay
+    double m = 0.0;
+    if (tiles > kMaxTiles || any_neg || !(u >= 0.f && u < 1.f)) {
+      decision = 1;  // out-of-contract input or huge vocabulary: exact replay
     } else if (any_nan || any_inf || !any_pos) {
       decision = 2;  // mass NaN / inf / zero: invalid row
+    } else {
+      for (int64_t k = 0; k < tiles; ++k) m += ds.tile_total[k];
     }
     const double tt = (double)u * m;
-    // |any float64 order - sequential cumsum| <= (#adds) * 2^-53 * mass per side;
-    // doubled for t's own dependence on the mass, plus rounding of u * mass.
-    const double margin = (4.0 * (double)V + 64.0) * 0x1p-52 * m;
-    int64_t tile = -1;
-    double start = 0.0;
+    // |any float64 summation order - torch's sequential cumsum| <= (#adds) * 2^-53 *
+    // mass per side; doubled for t's own dependence on the mass, plus the rounding
+    // of u * mass.
+    ds.margin = (4.0 * (double)V + 64.0) * 0x1p-52 * m;
+    ds.t = tt;
+    ds.tile = -1;
     if (decision == 0) {
       double acc = 0.0;
       for (int64_t k = 0; k < tiles; ++k) {
-        const double nx = acc + tile_sum[i * tiles + k];
+        const double nx = acc + ds.tile_total[k];
         if (nx > tt) {
-          tile = k;
-          start = acc;
+          ds.tile = k;
+          ds.tile_start = acc;
           break;
         }
         acc = nx;
       }
-      if (tile < 0) decision = 1;
+      if (ds.tile < 0) decision = 1;
     }
-    s_decision = decision;
-    s_tile = tile;
-    s_tilestart = start;
-    s_t = tt;
-    s_margin = margin;
-    s_best = INT64_MAX;
+    ds.decision = decision;
+    ds.best = ~0ull;
   }
   __syncthreads();
-  int decision = s_decision;
+  int decision = ds.decision;
   int64_t index = 0;
   bool valid = decision != 2;
   if (decision == 0) {
-    const bool vec_ok =
-        (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
-    float wv[kTileElems];
-    load_weights(w, V, s_tile, t, vec_ok, wv);
+    float wv[kElems];
+    load_weights(w, V, ds.tile, t, vec_ok, wv);
     double local = 0.0;
 #pragma unroll
-    for (int e = 0; e < kTileElems; ++e) local += (double)wv[e];
-    // exclusive scan of thread partials in index order (Hillis-Steele in LDS)
-    scan[t] = local;
-    __syncthreads();
-    for (int off = 1; off < kTileThreads; off <<= 1) {
-      const double add = t >= off ? scan[t - off] : 0.0;
-      __syncthreads();
-      scan[t] += add;
-      __syncthreads();
+    for (int e = 0; e < kElems; ++e) local += (double)wv[e];
+    // exclusive scan of thread partials in index order: wave scan, then wave offsets
+    double incl = local;
+    for (int off = 1; off < 64; off <<= 1) {
+      const double y = __shfl_up(incl, off, RLT_WAVE);
+      if (lane >= off) incl += y;
     }
-    double run = s_tilestart + (scan[t] - local);
-    const double tt = s_t;
-    for (int e = 0; e < kTileElems; ++e) {
+    if (lane == 63) ds.wave_sum[wave] = incl;
+    __syncthreads();
+    double wave_off = 0.0;
+    for (int wv2 = 0; wv2 < wave; ++wv2) wave_off += ds.wave_sum[wv2];
+    const double start = ds.tile_start + (wave_off + (incl - local));
+    const double tt = ds.t;
+    double run = start;
+    int e_hit = -1;
+    for (int e = 0; e < kElems; ++e) {
       run += (double)wv[e];
       if (run > tt) {
-        const int64_t k = s_tile * kTile + (int64_t)t * kTileElems + e;
-        atomicMin((unsigned long long*)&s_best, (unsigned long long)k);
+        e_hit = e;
         break;
       }
     }
+    if (e_hit >= 0)
+      atomicMin(&ds.best, (unsigned long long)(ds.tile * kTile + (int64_t)t * kElems + e_hit));
     __syncthreads();
-    // the owner of the crossing publishes its neighbours' prefix values
-    const int64_t best = s_best;
-    if (best != INT64_MAX && (best - s_tile * kTile) / kTileElems == t) {
-      double r = s_tilestart + (scan[t] - local);
-      const int e_best = (int)((best - s_tile * kTile) % kTileElems);
-      for (int e = 0; e < e_best; ++e) r += (double)wv[e];
-      s_before = r;
-      s_at = r + (double)wv[e_best];
+    const unsigned long long best = ds.best;
+    if (best != ~0ull && (int64_t)(best - ds.tile * kTile) / kElems == t) {
+      double r = start;
+      const int eb = (int)((best - ds.tile * kTile) % kElems);
+      for (int e = 0; e < eb; ++e) r += (double)wv[e];
+      ds.before = r;
+      ds.at = r + (double)wv[eb];
     }
     __syncthreads();
     if (t == 0) {
-      const bool ok = best != INT64_MAX && s_before <= tt - s_margin && s_at > tt + s_margin;
-      s_decision = ok ? 0 : 1;
+      const bool ok = best != ~0ull && ds.before <= tt - ds.margin && ds.at > tt + ds.margin;
+      ds.decision = ok ? 0 : 1;
     }
     __syncthreads();
-    decision = s_decision;
-    index = best;
+    decision = ds.decision;
+    index = (int64_t)best;
   }
   if (t != 0) return;
   if (decision == 1) {
@@ -525,21 +433,274 @@ __global__ __launch_bounds__(kTileThreads) void rlt_draw_kernel(
   if (!valid) index = 0;
   if (index > V - 1) index = V - 1;
   if (index < 0) index = 0;
-  if (mode == 0) {
+  *index_out = index;
+  *valid_out = valid;
+}
+
+// This thread's tile weights -> (wave-reduced float64 sum in lane 0, flag bits).
+__device__ __forceinline__ double tile_partial(const float wv[kElems], uint32_t& flags) {
+  double local = 0.0;
+#pragma unroll
+  for (int e = 0; e < kElems; ++e) {
+    const float x = wv[e];
+    if (isnan(x)) flags |= 1u;
+    else if (isinf(x) && x > 0.f) flags |= 2u;
+    if (x < 0.f) flags |= 4u;
+    if (x > 0.f) flags |= 8u;
+    local += (double)x;
+  }
+  for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, RLT_WAVE);
+  return local;
+}
+
+// ------------------------------------------------------------------ categorical
+
+struct CatShared {
+  DrawScratch ds;
+  double wave_tile[kMaxTiles][kDrawWaves];
+  uint32_t flags;
+};
+
+// grid (m), kDrawThreads threads: one row of raw weights per workgroup.
+__global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
+    const float* __restrict__ weights, int64_t V, const float* __restrict__ u,
+    int64_t* __restrict__ out_index, uint8_t* __restrict__ out_valid,
+    int32_t* __restrict__ slow_count) {
+  __shared__ CatShared sh;
+  const int64_t i = blockIdx.x;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  if (t == 0) sh.flags = 0;
+  WeightRow w;
+  w.a = weights + i * V;
+  w.b = nullptr;
+  w.am = w.bm = 1.f;
+  w.residual = false;
+  w.raw = true;
+  const bool vec_ok = (V % 4 == 0) && ((uintptr_t)w.a % 16 == 0);
+  const int64_t tiles = (V + kTile - 1) / kTile;
+  __syncthreads();
+  if (tiles <= kMaxTiles) {
+    uint32_t fl = 0;
+    for (int64_t k0 = 0; k0 < tiles; k0 += 4) {
+      float wv[4][kElems];
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu)
+        if (k0 + uu < tiles) load_weights(w, V, k0 + uu, t, vec_ok, wv[uu]);
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        if (k0 + uu >= tiles) break;
+        const double part = tile_partial(wv[uu], fl);
+        if (lane == 0) sh.wave_tile[k0 + uu][wave] = part;
+      }
+    }
+    if (fl) atomicOr(&sh.flags, fl);
+  }
+  __syncthreads();
+  for (int64_t k = t; k < tiles && k < kMaxTiles; k += kDrawThreads) {
+    double tk = 0.0;
+    for (int wv = 0; wv < kDrawWaves; ++wv) tk += sh.wave_tile[k][wv];
+    sh.ds.tile_total[k] = tk;
+  }
+  __syncthreads();
+  const uint32_t f = sh.flags;
+  int64_t index;
+  bool valid;
+  draw_from_tiles(w, V, u[i], tiles, f & 1u, f & 2u, f & 4u, f & 8u, vec_ok, sh.ds, slow_count,
+                  &index, &valid);
+  if (t == 0) {
     out_index[i] = index;
     out_valid[i] = valid;
-    return;
   }
-  const StopState st = state[i];
+}
+
+// ------------------------------------------------------------------ accept
+
+// Stop state of one request, written by its tile-0 workgroup for the draw kernel.
+struct StopState {
+  int32_t s;        // leading valid accepts
+  int32_t at_end;   // s == d: the final draw is the bonus from p[s]
+  int32_t stop_ok;  // the stop point is numerically valid
+  int32_t err0;     // drafts outside [0, W1]
+  float pm, qm;     // masses of p[s] and q[s] (qm only for a residual)
+  int64_t tok[kMaxW1];
+};
+
+struct AcceptShared {
+  float pm[kMaxW1 + 1], qm[kMaxW1];
+  float px_raw[kMaxW1], qx_raw[kMaxW1], ua[kMaxW1];
+  int64_t tok[kMaxW1];
+  int64_t drafts;
+  double wave_part[kDrawWaves];
+  uint32_t flags;
+  int s, at_end, stop_ok, err0;
+};
+
+__device__ __forceinline__ WeightRow stop_weights(const float* p, const float* q, int64_t i, int W1,
+                                                  int64_t V, int s, bool at_end, float pm, float qm) {
+  WeightRow w;
+  w.a = p + (i * (W1 + 1) + s) * V;
+  w.am = pm;
+  w.residual = !at_end;
+  w.b = w.residual ? q + (i * W1 + s) * V : nullptr;
+  w.bm = w.residual ? qm : 1.f;
+  w.raw = false;
+  return w;
+}
+
+// grid (n, tiles), kDrawThreads threads.  Each workgroup recomputes its request's
+// stop state from the mass partials (cheap and identical in every workgroup) and
+// totals its 4096-token tile of the final weights; tile 0 also publishes the stop
+// state.  reference: speculative_sampling.py:136-172.
+__global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
+    const float* __restrict__ p, const float* __restrict__ q, int W1, int64_t V, int64_t n,
+    const float* __restrict__ partials, int64_t groups, const int64_t* __restrict__ draft_tokens,
+    const int64_t* __restrict__ drafts, const float* __restrict__ u_accept,
+    double* __restrict__ tile_sum, uint32_t* __restrict__ tile_flags,
+    StopState* __restrict__ stop) {
+  __shared__ AcceptShared sh;
+  const int64_t i = blockIdx.x;
+  const int64_t k = blockIdx.y;
+  const int64_t tiles = gridDim.y;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  if (t == 0) sh.flags = 0;
+  // draft tokens, uniforms and the gathers p[x], q[x]: issued first, one lane each
+  if (t < W1) {
+    const int64_t tok = draft_tokens[i * W1 + t];
+    const int64_t x = tok < 0 ? 0 : (tok > V - 1 ? V - 1 : tok);
+    sh.tok[t] = tok;
+    sh.ua[t] = u_accept[i * W1 + t];
+    sh.px_raw[t] = p[(i * (W1 + 1) + t) * V + x];
+    sh.qx_raw[t] = q[(i * W1 + t) * V + x];
+  }
+  if (t == kDrawThreads - 1) sh.drafts = drafts[i];
+  // ---- exact masses: rows 0..W1 of p, then 0..W1-1 of q, one half-wave per row
+  const int rows = 2 * W1 + 1;
+  for (int r = 2 * wave + (lane >> 5); r < rows; r += 2 * kDrawWaves) {
+    const bool is_p = r <= W1;
+    const int j = is_p ? r : r - W1 - 1;
+    const int64_t row = is_p ? i * (W1 + 1) + j : i * W1 + j;
+    const float* x = is_p ? p + row * V : q + row * V;
+    const int64_t prow = is_p ? row : n * (W1 + 1) + row;
+    const float m = rlt_row_mass_half(x, V, partials ? partials + prow * groups * kStreams : nullptr);
+    if ((lane & 31) == 0) {
+      if (is_p) sh.pm[j] = m;
+      else sh.qm[j] = m;
+    }
+  }
+  __syncthreads();
+  // ---- accept chain
+  if (t == 0) {
+    const int64_t dr = sh.drafts;
+    const int64_t d = dr < 0 ? 0 : (dr > W1 ? W1 : dr);
+    int s = 0;
+    bool chain = true, invalid_at_s = false;
+    for (int j = 0; j < W1; ++j) {
+      const int64_t tok = sh.tok[j];
+      const bool in_range = tok >= 0 && tok < V;
+      const float pmj = sh.pm[j], qmj = sh.qm[j];
+      const float px = __fdiv_rn(sh.px_raw[j], pmj);
+      const float qx = __fdiv_rn(sh.qx_raw[j], qmj);
+      const bool invalid = !(finite_pos(pmj) && finite_pos(qmj) && in_range && isfinite(px) &&
+                             isfinite(qx) && qx > 0.f);
+      const bool accept = !invalid && ((px >= qx) || (sh.ua[j] * qx < px)) && (j < d);
+      if (chain) {
+        if (accept) {
+          ++s;
+        } else {
+          chain = false;
+          invalid_at_s = invalid;  // meaningful only when s < d
+        }
+      }
+    }
+    const bool at_end = s == d;
+    sh.s = s;
+    sh.at_end = at_end;
+    sh.stop_ok = at_end ? finite_pos(sh.pm[s]) : !invalid_at_s;
+    sh.err0 = dr != d;
+  }
+  __syncthreads();
+  const WeightRow w = stop_weights(p, q, i, W1, V, sh.s, sh.at_end, sh.pm[sh.s],
+                                   sh.at_end ? 1.f : sh.qm[sh.s]);
+  const bool vec_ok =
+      (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
+  // ---- this workgroup's tile of the final weights
+  {
+    float wv[kElems];
+    load_weights(w, V, k, t, vec_ok, wv);
+    uint32_t fl = 0;
+    const double part = tile_partial(wv, fl);
+    if (lane == 0) sh.wave_part[wave] = part;
+    if (fl) atomicOr(&sh.flags, fl);
+  }
+  __syncthreads();
+  if (t == 0) {
+    double tk = 0.0;
+    for (int wv = 0; wv < kDrawWaves; ++wv) tk += sh.wave_part[wv];
+    tile_sum[i * tiles + k] = tk;
+    tile_flags[i * tiles + k] = sh.flags;
+  }
+  if (k == 0) {
+    StopState& st = stop[i];
+    if (t < W1) st.tok[t] = sh.tok[t];
+    if (t == 0) {
+      st.s = sh.s;
+      st.at_end = sh.at_end;
+      st.stop_ok = sh.stop_ok;
+      st.err0 = sh.err0;
+      st.pm = sh.pm[sh.s];
+      st.qm = sh.at_end ? 1.f : sh.qm[sh.s];
+    }
+  }
+}
+
+struct FinalShared {
+  DrawScratch ds;
+  uint32_t flags;
+};
+
+// grid (n), kDrawThreads threads: the inverse-CDF draw and the outputs of request i.
+// reference: speculative_sampling.py:174-181.
+__global__ __launch_bounds__(kDrawThreads) void rlt_accept_draw_kernel(
+    const float* __restrict__ p, const float* __restrict__ q, int W1, int64_t V, int64_t tiles,
+    const float* __restrict__ u_final, const double* __restrict__ tile_sum,
+    const uint32_t* __restrict__ tile_flags, const StopState* __restrict__ stop,
+    int64_t* __restrict__ final_token, int64_t* __restrict__ tokens,
+    int64_t* __restrict__ accepted, uint8_t* __restrict__ error, int32_t* __restrict__ slow_count) {
+  __shared__ FinalShared sh;
+  const int64_t i = blockIdx.x;
+  const int t = threadIdx.x;
+  const StopState& st = stop[i];
+  if (t == 0) sh.flags = 0;
+  uint32_t fl = 0;
+  for (int64_t k = t; k < tiles && k < kMaxTiles; k += kDrawThreads) {
+    sh.ds.tile_total[k] = tile_sum[i * tiles + k];
+    fl |= tile_flags[i * tiles + k];
+  }
+  const WeightRow w = stop_weights(p, q, i, W1, V, st.s, st.at_end, st.pm, st.qm);
+  const bool vec_ok =
+      (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
+  __syncthreads();
+  if (fl) atomicOr(&sh.flags, fl);
+  __syncthreads();
+  const uint32_t f = sh.flags;
+  int64_t index;
+  bool valid;
+  draw_from_tiles(w, V, u_final[i], tiles, f & 1u, f & 2u, f & 4u, f & 8u, vec_ok, sh.ds,
+                  slow_count, &index, &valid);
+  if (t != 0) return;
   const bool err = st.err0 || !(st.stop_ok && valid);
   const int64_t fin = err ? 0 : index;
-  out_index[i] = fin;
+  final_token[i] = fin;
   error[i] = err;
   accepted[i] = st.s;
   for (int j = 0; j <= W1; ++j) {
     int64_t v = 0;
     if (j < st.s) {
-      const int64_t tok = draft_tokens[i * W1 + j];
+      const int64_t tok = st.tok[j];
       v = tok < 0 ? 0 : (tok > V - 1 ? V - 1 : tok);
     } else if (j == st.s) {
       v = fin;
@@ -548,30 +709,52 @@ __global__ __launch_bounds__(kTileThreads) void rlt_draw_kernel(
   }
 }
 
+__global__ __launch_bounds__(64) void rlt_row_mass_kernel(const float* __restrict__ x, int64_t V,
+                                                          const float* __restrict__ partials,
+                                                          int64_t groups, float* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const float m =
+      rlt_row_mass_finish(x + r * V, V, partials ? partials + r * groups * kStreams : nullptr);
+  if (threadIdx.x == 0) out[r] = m;
+}
+
 // ------------------------------------------------------------------ workspace
 
-struct AcceptLayout {
-  size_t partials, state, tile_sum, tile_flags, slow, total;
+struct Layout {
+  size_t partials, tile_sum, tile_flags, stop, slow, total;
 };
 
-AcceptLayout accept_layout(int64_t n, int W1, int64_t V) {
+Layout layout_for(int64_t rows, int64_t n, int64_t V) {
   const RowGeom geo = row_geom(V);
-  const int64_t rows = n * (2 * W1 + 1);
   const int64_t tiles = (V + kTile - 1) / kTile;
-  AcceptLayout l;
+  Layout l;
   size_t off = 0;
   l.partials = off;
   off = rlt_align_up(off + sizeof(float) * rows * geo.groups * kStreams, 256);
-  l.state = off;
-  off = rlt_align_up(off + sizeof(StopState) * n, 256);
   l.tile_sum = off;
   off = rlt_align_up(off + sizeof(double) * n * tiles, 256);
   l.tile_flags = off;
-  off = rlt_align_up(off + sizeof(TileFlags) * n * tiles, 256);
+  off = rlt_align_up(off + sizeof(uint32_t) * n * tiles, 256);
+  l.stop = off;
+  off = rlt_align_up(off + sizeof(StopState) * n, 256);
   l.slow = off;
   off = rlt_align_up(off + sizeof(int32_t), 256);
   l.total = off;
   return l;
+}
+
+void launch_mass_groups(const float* p, const float* q, int64_t p_rows, int64_t rows, int64_t V,
+                        float* partials, hipStream_t stream) {
+  const RowGeom geo = row_geom(V);
+  if (geo.groups == 0 || rows == 0) return;
+  const bool vec = (V % 4 == 0) && ((uintptr_t)p % 16 == 0) && (q == nullptr || (uintptr_t)q % 16 == 0);
+  dim3 grid((unsigned)geo.groups, (unsigned)rows);
+  if (vec)
+    rlt_mass_groups_kernel<true><<<grid, 128, 0, stream>>>(p, q, p_rows, V, geo.groups,
+                                                           geo.full_chunks, partials);
+  else
+    rlt_mass_groups_kernel<false><<<grid, 128, 0, stream>>>(p, q, p_rows, V, geo.groups,
+                                                            geo.full_chunks, partials);
 }
 
 }  // namespace
@@ -579,11 +762,12 @@ AcceptLayout accept_layout(int64_t n, int W1, int64_t V) {
 extern "C" {
 
 size_t rlt_speculative_accept_workspace_size(int64_t n, int32_t w1, int64_t vocab) {
-  return accept_layout(n, w1, vocab).total;
+  return layout_for(n * (2 * (int64_t)w1 + 1), n, vocab).total;
 }
 
 size_t rlt_categorical_workspace_size(int64_t m, int64_t vocab) {
-  return accept_layout(m, 0, vocab).total;
+  (void)m;
+  return layout_for(0, 0, vocab).total;
 }
 
 int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
@@ -591,39 +775,28 @@ int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, c
                            int32_t w1, int64_t vocab, int64_t* tokens, int64_t* accepted,
                            int64_t* final_token, uint8_t* error, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-  if (n < 0 || w1 < 0 || w1 > 32 || vocab < 1) return RLT_ERR_ARGUMENT;
+  if (n < 0 || w1 < 0 || w1 > kMaxW1 || vocab < 1) return RLT_ERR_ARGUMENT;
   if (vocab >= ((int64_t)1 << 25)) return RLT_ERR_UNSUPPORTED;
   if (n == 0) return RLT_OK;
-  const AcceptLayout l = accept_layout(n, w1, vocab);
+  const int64_t rows = n * (2 * (int64_t)w1 + 1);
+  const Layout l = layout_for(rows, n, vocab);
   if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
   char* ws = (char*)workspace;
   float* partials = (float*)(ws + l.partials);
-  StopState* state = (StopState*)(ws + l.state);
   double* tile_sum = (double*)(ws + l.tile_sum);
-  TileFlags* tile_flags = (TileFlags*)(ws + l.tile_flags);
+  uint32_t* tile_flags = (uint32_t*)(ws + l.tile_flags);
+  StopState* stop = (StopState*)(ws + l.stop);
   int32_t* slow = (int32_t*)(ws + l.slow);
   const RowGeom geo = row_geom(vocab);
-  const int64_t rows = n * (2 * w1 + 1);
-  const int64_t p_rows = n * (w1 + 1);
-  if (geo.groups > 0) {
-    const bool vec = (vocab % 4 == 0) && ((uintptr_t)p % 16 == 0) && ((uintptr_t)q % 16 == 0 || w1 == 0);
-    dim3 grid((unsigned)geo.groups, (unsigned)rows);
-    if (vec)
-      rlt_mass_groups_kernel<true><<<grid, 128, 0, stream>>>(p, q, p_rows, vocab, geo.groups,
-                                                             geo.full_chunks, partials);
-    else
-      rlt_mass_groups_kernel<false><<<grid, 128, 0, stream>>>(p, q, p_rows, vocab, geo.groups,
-                                                              geo.full_chunks, partials);
-  }
-  rlt_accept_stop_kernel<<<(unsigned)n, 64, 0, stream>>>(
-      draft_tokens, drafts, q, p, u_accept, n, w1, vocab, geo.groups > 0 ? partials : nullptr,
-      geo.groups, state);
   const int64_t tiles = (vocab + kTile - 1) / kTile;
-  rlt_weight_tiles_kernel<<<dim3((unsigned)tiles, (unsigned)n), kTileThreads, 0, stream>>>(
-      1, p, q, w1, vocab, state, tiles, tile_sum, tile_flags);
-  rlt_draw_kernel<<<(unsigned)n, kTileThreads, 0, stream>>>(
-      1, p, q, w1, vocab, u_final, draft_tokens, state, tiles, tile_sum, tile_flags, final_token,
-      nullptr, tokens, accepted, error, slow);
+  if (tiles > 65535) return RLT_ERR_UNSUPPORTED;  // grid.y of the tile kernel
+  launch_mass_groups(p, w1 > 0 ? q : nullptr, n * (w1 + 1), rows, vocab, partials, stream);
+  rlt_accept_tiles_kernel<<<dim3((unsigned)n, (unsigned)tiles), kDrawThreads, 0, stream>>>(
+      p, q, w1, vocab, n, geo.groups > 0 ? partials : nullptr, geo.groups, draft_tokens, drafts,
+      u_accept, tile_sum, tile_flags, stop);
+  rlt_accept_draw_kernel<<<(unsigned)n, kDrawThreads, 0, stream>>>(
+      p, q, w1, vocab, tiles, u_final, tile_sum, tile_flags, stop, final_token, tokens, accepted,
+      error, slow);
   return rlt_launch_status();
 }
 
@@ -632,63 +805,31 @@ int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t voc
                     hipStream_t stream) {
   if (m < 0 || vocab < 1) return RLT_ERR_ARGUMENT;
   if (m == 0) return RLT_OK;
-  const AcceptLayout l = accept_layout(m, 0, vocab);
+  const Layout l = layout_for(0, 0, vocab);
   if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
-  char* ws = (char*)workspace;
-  double* tile_sum = (double*)(ws + l.tile_sum);
-  TileFlags* tile_flags = (TileFlags*)(ws + l.tile_flags);
-  int32_t* slow = (int32_t*)(ws + l.slow);
-  const int64_t tiles = (vocab + kTile - 1) / kTile;
-  rlt_weight_tiles_kernel<<<dim3((unsigned)tiles, (unsigned)m), kTileThreads, 0, stream>>>(
-      0, weights, nullptr, 0, vocab, nullptr, tiles, tile_sum, tile_flags);
-  rlt_draw_kernel<<<(unsigned)m, kTileThreads, 0, stream>>>(
-      0, weights, nullptr, 0, vocab, u, nullptr, nullptr, tiles, tile_sum, tile_flags, index,
-      valid, nullptr, nullptr, nullptr, slow);
+  int32_t* slow = (int32_t*)((char*)workspace + l.slow);
+  rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(weights, vocab, u, index, valid,
+                                                                  slow);
   return rlt_launch_status();
 }
 
-// Exact torch-CPU fp32 row sums (``x.sum(-1, dtype=float32)``) of a contiguous
-// [rows, V] fp32 matrix; exposed for tests and for callers that need the masses.
+size_t rlt_row_mass_workspace_size(int64_t rows, int64_t vocab) {
+  return layout_for(rows, 0, vocab).total;
+}
+
 int rlt_row_mass_f32(const float* x, int64_t rows, int64_t vocab, float* out, void* workspace,
-                     size_t workspace_bytes, hipStream_t stream);
-
-}  // extern "C"
-
-namespace {
-__global__ __launch_bounds__(64) void rlt_row_mass_kernel(const float* __restrict__ x, int64_t V,
-                                                          const float* __restrict__ partials,
-                                                          int64_t groups, float* __restrict__ out) {
-  const int64_t r = blockIdx.x;
-  const float m = rlt_row_mass_finish(x + r * V, V, partials ? partials + r * groups * kStreams : nullptr);
-  if (threadIdx.x == 0) out[r] = m;
-}
-}  // namespace
-
-extern "C" size_t rlt_row_mass_workspace_size(int64_t rows, int64_t vocab) {
-  const RowGeom geo = row_geom(vocab);
-  return rlt_align_up(sizeof(float) * rows * geo.groups * kStreams + 1, 256);
-}
-
-extern "C" int rlt_row_mass_f32(const float* x, int64_t rows, int64_t vocab, float* out,
-                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                     size_t workspace_bytes, hipStream_t stream) {
   if (rows < 0 || vocab < 1) return RLT_ERR_ARGUMENT;
   if (vocab >= ((int64_t)1 << 25)) return RLT_ERR_UNSUPPORTED;
   if (rows == 0) return RLT_OK;
+  const Layout l = layout_for(rows, 0, vocab);
+  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
+  float* partials = (float*)((char*)workspace + l.partials);
   const RowGeom geo = row_geom(vocab);
-  if (workspace_bytes < rlt_row_mass_workspace_size(rows, vocab) || !workspace)
-    return RLT_ERR_WORKSPACE;
-  float* partials = (float*)workspace;
-  if (geo.groups > 0) {
-    const bool vec = (vocab % 4 == 0) && ((uintptr_t)x % 16 == 0);
-    dim3 grid((unsigned)geo.groups, (unsigned)rows);
-    if (vec)
-      rlt_mass_groups_kernel<true><<<grid, 128, 0, stream>>>(x, x, rows, vocab, geo.groups,
-                                                             geo.full_chunks, partials);
-    else
-      rlt_mass_groups_kernel<false><<<grid, 128, 0, stream>>>(x, x, rows, vocab, geo.groups,
-                                                              geo.full_chunks, partials);
-  }
+  launch_mass_groups(x, nullptr, rows, rows, vocab, partials, stream);
   rlt_row_mass_kernel<<<(unsigned)rows, 64, 0, stream>>>(x, vocab, geo.groups > 0 ? partials : nullptr,
                                                          geo.groups, out);
   return rlt_launch_status();
 }
+
+}  // extern "C"
