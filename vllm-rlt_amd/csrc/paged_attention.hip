@@ -10,7 +10,7 @@
 // The per-row form is the packed form with q_len = 1 per row.
 //
 // Work decomposition (all static, graph-capturable: no length-dependent grid):
-//  grid (sequence x row-group, kv head, chunk).  A chunk is kChunk = 512 absolute
+//  1-D grid over (sequence x row-group, kv head, chunk).  A chunk is kChunk = 512 absolute
 //  key positions [512c, 512c + 512); its workgroup runs 4 waves on 128 positions
 //  each, in 16-position tiles.  Every row of the sequence (q_len window rows x
 //  GQA group) that attends to a kv head is handled by the SAME workgroup, so each
@@ -81,6 +81,26 @@ struct AttnParams {
 struct SeqView {
   int32_t q_begin, q_len, kv_len;
 };
+
+// Work item of a flat workgroup id.  Consecutive ids go to different XCDs (the
+// dispatcher deals workgroups round-robin over the 8 XCDs), so the chunk index is
+// rotated by the (sequence, row-group, kv head) index: every sequence's chunks then
+// spread evenly over all XCDs whatever the mix of sequence lengths.
+struct WorkItem {
+  int seq, rg, kvh, chunk;
+};
+
+__device__ __forceinline__ WorkItem work_item(const AttnParams& P, int64_t id) {
+  WorkItem w;
+  const int64_t pair = id / P.max_chunks;
+  const int j = (int)(id % P.max_chunks);
+  w.chunk = (int)((j + pair) % P.max_chunks);
+  w.kvh = (int)(pair % P.hkv);
+  const int64_t sr = pair / P.hkv;
+  w.rg = (int)(sr % P.rowgroups);
+  w.seq = (int)(sr / P.rowgroups);
+  return w;
+}
 
 __device__ __forceinline__ SeqView seq_view(const AttnParams& P, int seq) {
   SeqView s;
@@ -274,10 +294,11 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   constexpr int TW = kTilesPerWave;
   __shared__ MfmaShared<QT, KVT, D, NT> sh;
 
-  const int seq = blockIdx.x / P.rowgroups;
-  const int rg = blockIdx.x % P.rowgroups;
-  const int kvh = blockIdx.y;
-  const int chunk = blockIdx.z;
+  const WorkItem wi = work_item(P, blockIdx.x);
+  const int seq = wi.seq;
+  const int rg = wi.rg;
+  const int kvh = wi.kvh;
+  const int chunk = wi.chunk;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
@@ -563,10 +584,11 @@ __global__ __launch_bounds__(256) void rlt_attn_vec_kernel(AttnParams P) {
   __shared__ VecShared sh;
   const int D = P.head_dim;
   const int DQ = (D + 3) / 4;
-  const int seq = blockIdx.x / P.rowgroups;
-  const int rg = blockIdx.x % P.rowgroups;
-  const int kvh = blockIdx.y;
-  const int chunk = blockIdx.z;
+  const WorkItem wi = work_item(P, blockIdx.x);
+  const int seq = wi.seq;
+  const int rg = wi.rg;
+  const int kvh = wi.kvh;
+  const int chunk = wi.chunk;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
@@ -768,13 +790,16 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
   if (head >= P.hq) return;
   int seq, qi;
   if (P.cu_q) {
-    int lo = 0, hi = P.num_seqs;  // last seq with cu[seq] <= row
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (P.cu_q[mid] <= row) lo = mid;
-      else hi = mid;
+    // seq = (number of sequences s >= 1 with cu[s] <= row), counted 64 at a time
+    // with one load per lane instead of a chain of dependent bisection loads
+    int count = 0;
+    for (int s0 = 1; s0 < P.num_seqs; s0 += 64) {
+      const int s = s0 + lane;
+      const bool le = s < P.num_seqs && P.cu_q[s] <= row;
+      count += __popcll(__builtin_amdgcn_ballot_w64(le));
+      if (!__builtin_amdgcn_ballot_w64(s < P.num_seqs && le && s == s0 + 63)) break;
     }
-    seq = lo;
+    seq = count;
     qi = row - P.cu_q[seq];
   } else {
     seq = row;
@@ -999,7 +1024,9 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     P.rows_per_rg = 16 * nt;
     P.rowgroups = (rows_per_seq + P.rows_per_rg - 1) / P.rows_per_rg;
     if (P.rowgroups < 1) P.rowgroups = 1;
-    dim3 grid((unsigned)(num_seqs * P.rowgroups), (unsigned)num_kv_heads, (unsigned)P.max_chunks);
+    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads * P.max_chunks;
+    if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
+    dim3 grid((unsigned)wgs);
     if (q_dtype == RLT_BF16)
       st = kv_dtype == RLT_BF16 ? launch_mfma<RLT_BF16, RLT_BF16>(P, grid, nt, stream)
                                 : launch_mfma<RLT_BF16, RLT_FP8_E4M3>(P, grid, nt, stream);
@@ -1010,7 +1037,9 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     P.rows_per_rg = kVecRows;
     P.rowgroups = (rows_per_seq + kVecRows - 1) / kVecRows;
     if (P.rowgroups < 1) P.rowgroups = 1;
-    dim3 grid((unsigned)(num_seqs * P.rowgroups), (unsigned)num_kv_heads, (unsigned)P.max_chunks);
+    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads * P.max_chunks;
+    if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
+    dim3 grid((unsigned)wgs);
     switch (q_dtype) {
       case RLT_F32: st = launch_vec_q<RLT_F32>(P, kv_dtype, grid, stream); break;
       case RLT_F16: st = launch_vec_q<RLT_F16>(P, kv_dtype, grid, stream); break;

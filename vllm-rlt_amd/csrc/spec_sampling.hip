@@ -339,38 +339,45 @@ __device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t 
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  if (t == 0) {
+  if (wave == 0) {
+    // wave 0: inclusive scan of the tile totals (64 tiles per pass, fixed order)
+    // gives the mass and the first tile whose cumulative total exceeds t = u*mass
     int decision = 0;
+    if (tiles > kMaxTiles || any_neg || !(u >= 0.f && u < 1.f)) decision = 1;
+    else if (any_nan || any_inf || !any_pos) decision = 2;
     double m = 0.0;
-    if (tiles > kMaxTiles || any_neg || !(u >= 0.f && u < 1.f)) {
-      decision = 1;  // out-of-contract input or huge vocabulary: exact replay
-    } else if (any_nan || any_inf || !any_pos) {
-      decision = 2;  // mass NaN / inf / zero: invalid row
-    } else {
-      for (int64_t k = 0; k < tiles; ++k) m += ds.tile_total[k];
+    if (decision == 0) {
+      for (int64_t k0 = 0; k0 < tiles; k0 += 64) {
+        double v = k0 + lane < tiles ? ds.tile_total[k0 + lane] : 0.0;
+        for (int off = 1; off < 64; off <<= 1) {
+          const double y = __shfl_up(v, off, RLT_WAVE);
+          if (lane >= off) v += y;
+        }
+        if (k0 + lane < tiles) ds.tile_total[k0 + lane] = m + v;  // cumulative total
+        m += __shfl(v, 63, RLT_WAVE);
+      }
     }
     const double tt = (double)u * m;
-    // |any float64 summation order - torch's sequential cumsum| <= (#adds) * 2^-53 *
-    // mass per side; doubled for t's own dependence on the mass, plus the rounding
-    // of u * mass.
-    ds.margin = (4.0 * (double)V + 64.0) * 0x1p-52 * m;
-    ds.t = tt;
-    ds.tile = -1;
+    int64_t tile = -1;
     if (decision == 0) {
-      double acc = 0.0;
-      for (int64_t k = 0; k < tiles; ++k) {
-        const double nx = acc + ds.tile_total[k];
-        if (nx > tt) {
-          ds.tile = k;
-          ds.tile_start = acc;
-          break;
-        }
-        acc = nx;
+      for (int64_t k0 = 0; k0 < tiles && tile < 0; k0 += 64) {
+        const bool over = k0 + lane < tiles && ds.tile_total[k0 + lane] > tt;
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(over);
+        if (mask) tile = k0 + __builtin_ctzll(mask);
       }
-      if (ds.tile < 0) decision = 1;
+      if (tile < 0) decision = 1;
     }
-    ds.decision = decision;
-    ds.best = ~0ull;
+    if (lane == 0) {
+      // |any float64 summation order - torch's sequential cumsum| <= (#adds) * 2^-53
+      // * mass per side; doubled for t's own dependence on the mass, plus the
+      // rounding of u * mass.
+      ds.margin = (4.0 * (double)V + 64.0) * 0x1p-52 * m;
+      ds.t = tt;
+      ds.tile = tile;
+      ds.tile_start = tile > 0 ? ds.tile_total[tile - 1] : 0.0;
+      ds.decision = decision;
+      ds.best = ~0ull;
+    }
   }
   __syncthreads();
   int decision = ds.decision;
