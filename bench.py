@@ -89,6 +89,17 @@ def accept_bytes(w):
     return 4 * n * (k + 1) * v + 4 * n * k * v + 4 * n * (2 * k + 1) + 8 * n * (k + 1) + 8 * n * 3 + 8 * n * k
 
 
+def measured_traffic():
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (calibrated against a 1 GiB copy), or None."""
+    path = os.path.join(ROOT, "profiles", "verify_step_config3_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["attention_launch_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(w, repeats=1):
     """The torch-CPU oracle (restatement of the reference Torch path) on this host."""
     from oracle import attention as oatt
@@ -120,8 +131,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("attention", "accept"),
-                    help="replay only this part K times and exit (for counter collection)")
+    ap.add_argument("--only", choices=("attention", "accept", "copy"),
+                    help="replay only this part K times and exit (for counter collection); "
+                         "'copy' copies a 1 GiB buffer K times (counter calibration)")
+    ap.add_argument("--steps-per-graph", type=int, default=10,
+                    help="verify steps captured back to back in one HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the verify path has no "
@@ -130,6 +144,14 @@ def main():
         sys.exit(2)
     pkg = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
+    if args.only == "copy":
+        src_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst_buf = torch.empty_like(src_buf)
+        for _ in range(args.steps):
+            dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes_per_launch": 1 << 30, "steps": args.steps}), flush=True)
+        return
     w = build_workload(dev)
     backend = pkg.create_backend("auto", dev, torch.bfloat16, w["d"], w["bs"])
     k = w["k"]
@@ -162,31 +184,39 @@ def main():
             accept()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
+    # Graphs of `spg` launches back to back: in-graph kernel boundaries cost ~0,
+    # so per-launch timings are not inflated by the per-replay launch overhead.
+    spg = max(1, min(args.steps_per_graph, args.steps))
     g_attn, g_acc, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_attn):
-        out_attn = attn()
+        for _ in range(spg):
+            out_attn = attn()
     with torch.cuda.graph(g_acc):
-        out_acc = accept()
+        for _ in range(spg):
+            out_acc = accept()
     with torch.cuda.graph(g_step):
-        attn()
-        accept()
-    for _ in range(args.warmup):
+        for _ in range(spg):
+            attn()
+            accept()
+    for _ in range(max(1, args.warmup // spg)):
         g_step.replay()
     torch.cuda.synchronize()
     if args.only:
         graph = g_attn if args.only == "attention" else g_acc
-        for _ in range(args.steps):
+        for _ in range(max(1, args.steps // spg)):
             graph.replay()
         torch.cuda.synchronize()
-        print(json.dumps({"only": args.only, "steps": args.steps}), flush=True)
+        print(json.dumps({"only": args.only, "launches": max(1, args.steps // spg) * spg}), flush=True)
         return
 
-    # ---- timed region: K whole verify steps
+    # ---- timed region: exactly K whole verify steps
+    replays = -(-args.steps // spg)
+    steps = replays * spg
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(replays):
         g_step.replay()
     torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
+    step_s = (time.perf_counter() - t0) / steps
 
     # ---- per-launch durations with HIP events on the launch stream, queue pre-filled
     def launch_time(graph, reps):
@@ -199,10 +229,10 @@ def main():
             graph.replay()
             b.record(s)
         torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3
+        return sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3 / spg
 
-    t_attn = launch_time(g_attn, args.steps)
-    t_acc = launch_time(g_acc, args.steps)
+    t_attn = launch_time(g_attn, replays)
+    t_acc = launch_time(g_acc, replays)
 
     # ---- correctness of the measured outputs against an eager run
     eager_attn = attn()
@@ -220,7 +250,7 @@ def main():
         "value": round(tokens / step_s, 1),
         "unit": "verified tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_s * 1e3, 4),
         "higher_is_better": True,
@@ -238,6 +268,7 @@ def main():
         "hbm_frac_step": round((a_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
         "attention_ms": round(t_attn * 1e3, 4),
         "accept_ms": round(t_acc * 1e3, 4),
+        "steps_per_graph": spg,
         "roofline": {
             "kernel": "attention launch (rlt_attn_mfma_kernel + rlt_merge_kernel)",
             "bound": "hbm",
@@ -245,7 +276,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "profiles/verify_step_config3_hbm_traffic.md (bytes per launch)",
             "algorithmic_bytes": a_bytes,
         },
     }
