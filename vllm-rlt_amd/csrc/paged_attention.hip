@@ -38,6 +38,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kChunk = 512;       // key positions per workgroup (split unit)
@@ -272,23 +274,116 @@ struct RawSlice {
   }
 };
 
+// Four key positions' value slices of one lane for O^T = V^T P^T.  The output
+// dimension of accumulator row m of column tile dt is DPL * m + dt (DPL =
+// head_dim / 16), so lane (m = lane % 16, group g = lane / 16) needs dims
+// [DPL m, DPL m + DPL) of positions 4g .. 4g + 3: one contiguous DPL-element
+// load per position, and no transpose through LDS.
+template <int QT, int KVT, int D>
+struct ValueQuad {
+  static constexpr int DPL = D / 16;
+  static constexpr bool kFp8 = KVT != QT;
+  static constexpr int kBytes = DPL * (kFp8 ? 1 : 2);
+  static constexpr bool kHalfWords = kBytes % 4 != 0;  // fp8 with head_dim 96
+  static constexpr int kUnits = kHalfWords ? kBytes / 2 : kBytes / 4;
+  uint32_t w[4][kUnits];
+
+  __device__ __forceinline__ void load(int i, const uint8_t* p) {
+    if (kHalfWords) {
+#pragma unroll
+      for (int j = 0; j < kUnits; ++j) w[i][j] = ((const uint16_t*)p)[j];
+    } else if (kBytes % 16 == 0) {
+#pragma unroll
+      for (int j = 0; j < kUnits / 4; ++j) {
+        const uint4 v = ((const uint4*)p)[j];
+        w[i][4 * j] = v.x; w[i][4 * j + 1] = v.y; w[i][4 * j + 2] = v.z; w[i][4 * j + 3] = v.w;
+      }
+    } else if (kBytes % 8 == 0) {
+#pragma unroll
+      for (int j = 0; j < kUnits / 2; ++j) {
+        const uint2 v = ((const uint2*)p)[j];
+        w[i][2 * j] = v.x; w[i][2 * j + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kUnits; ++j) w[i][j] = ((const uint32_t*)p)[j];
+    }
+  }
+  __device__ __forceinline__ void zero(int i) {
+#pragma unroll
+    for (int j = 0; j < kUnits; ++j) w[i][j] = 0;
+  }
+  // A operands of the column tiles 2k and 2k + 1: four 16-bit values each, of
+  // positions 0..3 at that tile's dimension.
+  template <int K>
+  __device__ __forceinline__ void op2(uint2& a0, uint2& a1) const {
+    if (!kFp8) {
+      // element pair k of each position is word k: low half -> tile 2k, high -> 2k + 1
+      a0.x = __builtin_amdgcn_perm(w[1][K], w[0][K], 0x05040100u);
+      a1.x = __builtin_amdgcn_perm(w[1][K], w[0][K], 0x07060302u);
+      a0.y = __builtin_amdgcn_perm(w[3][K], w[2][K], 0x05040100u);
+      a1.y = __builtin_amdgcn_perm(w[3][K], w[2][K], 0x07060302u);
+    } else {
+      float2 f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (kHalfWords) f[i] = fp8x2_to_f32<false>(w[i][K]);
+        else f[i] = (K & 1) ? fp8x2_to_f32<true>(w[i][K / 2]) : fp8x2_to_f32<false>(w[i][K / 2]);
+      }
+      if (QT == RLT_BF16) {
+        // e4m3 values are exact in bf16: the high half of the fp32 bits
+        a0.x = __builtin_amdgcn_perm(__float_as_uint(f[1].x), __float_as_uint(f[0].x), 0x07060302u);
+        a1.x = __builtin_amdgcn_perm(__float_as_uint(f[1].y), __float_as_uint(f[0].y), 0x07060302u);
+        a0.y = __builtin_amdgcn_perm(__float_as_uint(f[3].x), __float_as_uint(f[2].x), 0x07060302u);
+        a1.y = __builtin_amdgcn_perm(__float_as_uint(f[3].y), __float_as_uint(f[2].y), 0x07060302u);
+      } else {
+        a0.x = (uint32_t)f32_to_f16_bits(f[0].x) | ((uint32_t)f32_to_f16_bits(f[1].x) << 16);
+        a1.x = (uint32_t)f32_to_f16_bits(f[0].y) | ((uint32_t)f32_to_f16_bits(f[1].y) << 16);
+        a0.y = (uint32_t)f32_to_f16_bits(f[2].x) | ((uint32_t)f32_to_f16_bits(f[3].x) << 16);
+        a1.y = (uint32_t)f32_to_f16_bits(f[2].y) | ((uint32_t)f32_to_f16_bits(f[3].y) << 16);
+      }
+    }
+  }
+};
+
+template <int ND, int NT, class F, int K = 0>
+__device__ __forceinline__ void for_pairs(F&& f) {
+  if constexpr (K < ND / 2) {
+    f(std::integral_constant<int, K>{});
+    for_pairs<ND, NT, F, K + 1>(static_cast<F&&>(f));
+  }
+}
+
+// Row maximum / sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48)
+// with the gfx950 lane-swap instructions; every lane gets the same bits.
+__device__ __forceinline__ float group_max(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group_sum(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int QT, int KVT, int D, int NT>
 struct MfmaShared {
-  static constexpr int kPad = 8;  // 16-bit elements of row padding (bank spread)
-  union {
-    uint16_t vt[kWaves][kTileTok][D + kPad];  // tile loop: wave-private V tiles
-    f32x4 o[2][NT * (D / 16)][64];            // wave combine
-  };
+  f32x4 o[2][NT * (D / 16)][64];  // wave combine
   float ml[2][NT * 16][2];
 };
 
-// SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).
-template <int QT, int KVT, int D, int NT, int SM>
+// SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).  UB: block_size is a
+// multiple of 16, so the 16 positions of a tile share one block.
+template <int QT, int KVT, int D, int NT, int SM, bool UB>
 __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   using M = Mfma<QT>;
   using Raw = RawSlice<QT, KVT, D>;
+  using VQ = ValueQuad<QT, KVT, D>;
   constexpr int NQS = D / 32;  // 32-wide contraction slices
-  constexpr int ND = D / 16;   // 16-wide output column tiles
+  constexpr int ND = D / 16;   // 16-wide output column tiles (= dims per lane)
   constexpr int DQ = D / 4;    // elements per lane group
   constexpr int KV_ELT = KVT == QT ? 2 : 1;
   constexpr int TW = kTilesPerWave;
@@ -325,11 +420,12 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   const int t1 = __builtin_amdgcn_readfirstlane(
       span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok);
 
-  // Block-table entries of all this lane's positions, issued before any KV load.
+  // Block-table entries of all this lane's positions, issued before any KV load
+  // (index clamped into the table: any entry is a safe address once range-checked).
   int32_t blk[TW];
 #pragma unroll
   for (int t = 0; t < TW; ++t) {
-    const int pos = w_begin + t * kTileTok + l16;
+    const int pos = w_begin + t * kTileTok + (UB ? 0 : l16);
     const int idx = min(pos / P.block_size, P.table_width - 1);
     blk[t] = P.tables[(int64_t)seq * P.table_stride + idx];
   }
@@ -374,35 +470,62 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   }
 
   if (t0 < t1) {
-    Raw kb[2], vb[2];
+    Raw kb[2];
+    VQ vq[2];
     float ksc[2][4], vsc[2][4];
-    bool okb[2];
-    // Loads of tile t into stage b.  Branch-free: a position outside the wave's
-    // range reads block 0 (always inside the pool) and is zeroed at use.
+    bool okk[2];
+    uint32_t okv[2];  // bit i: value position 4 * grp + i is inside the sequence
+    const int64_t k_head = (int64_t)kvh * P.k_head_stride + grp * DQ;
+    const int64_t v_head = (int64_t)kvh * P.v_head_stride + l16 * ND;
+    // Loads of tile t into stage b.  Branch-free: every address is inside the pool
+    // (table index clamped, entries outside the pool read block 0), and positions
+    // outside the wave's range are zeroed at use.
     auto issue = [&](int t, int b) {
-      const int pos = w_begin + t * kTileTok + l16;
-      const bool ok = t >= t0 && t < t1 && pos < hi_last;
-      okb[b] = ok;
-      // entries outside the pool read block 0, as everywhere else in this file
-      const int64_t bk = (ok && blk[t] >= 0 && blk[t] < P.num_blocks) ? (int64_t)blk[t] : 0;
-      const int64_t off = ok ? (int64_t)(pos % P.block_size) : 0;
-      const uint8_t* kp = (const uint8_t*)P.k +
-          (bk * P.k_block_stride + off * P.k_token_stride + (int64_t)kvh * P.k_head_stride + grp * DQ) * KV_ELT;
-      const uint8_t* vp = (const uint8_t*)P.v +
-          (bk * P.v_block_stride + off * P.v_token_stride + (int64_t)kvh * P.v_head_stride + grp * DQ) * KV_ELT;
-      kb[b].load(kp);
-      vb[b].load(vp);
+      const int tb = w_begin + t * kTileTok;
+      const bool tile_ok = t >= t0 && t < t1;
+      okk[b] = tile_ok && tb + l16 < hi_last;
+      uint32_t m4 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m4 |= (tile_ok && tb + 4 * grp + i < hi_last) ? (1u << i) : 0u;
+      okv[b] = m4;
+      if (UB) {
+        const int32_t e = __builtin_amdgcn_readfirstlane(blk[t]);
+        const int64_t bk = (e >= 0 && e < P.num_blocks) ? (int64_t)e : 0;
+        const int in_blk = tb % P.block_size;
+        const uint8_t* kp = (const uint8_t*)P.k +
+            (bk * P.k_block_stride + (int64_t)(in_blk + l16) * P.k_token_stride + k_head) * KV_ELT;
+        kb[b].load(kp);
+        const uint8_t* vbase = (const uint8_t*)P.v + (bk * P.v_block_stride + v_head) * KV_ELT;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          vq[b].load(i, vbase + (int64_t)(in_blk + 4 * grp + i) * P.v_token_stride * KV_ELT);
+      } else {
+        const int64_t bk = (blk[t] >= 0 && blk[t] < P.num_blocks) ? (int64_t)blk[t] : 0;
+        const uint8_t* kp = (const uint8_t*)P.k +
+            (bk * P.k_block_stride + (int64_t)((tb + l16) % P.block_size) * P.k_token_stride + k_head) *
+                KV_ELT;
+        kb[b].load(kp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // lane 4 * grp + i holds the entry of position tb + 4 * grp + i
+          const int32_t e = __shfl(blk[t], 4 * grp + i, RLT_WAVE);
+          const int64_t bv = (e >= 0 && e < P.num_blocks) ? (int64_t)e : 0;
+          const uint8_t* vp = (const uint8_t*)P.v +
+              (bv * P.v_block_stride + (int64_t)((tb + 4 * grp + i) % P.block_size) * P.v_token_stride +
+               v_head) * KV_ELT;
+          vq[b].load(i, vp);
+        }
+      }
       if (SM == 2) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int p4 = w_begin + t * kTileTok + 4 * grp + r;
-          const bool ok4 = t >= t0 && t < t1 && p4 < hi_last;
+          const int p4 = tb + 4 * grp + r;
+          const bool ok4 = tile_ok && p4 < hi_last;
           ksc[b][r] = ok4 ? scale_at(P, P.k_scale, seq, p4, kvh) : 0.f;
           vsc[b][r] = ok4 ? scale_at(P, P.v_scale, seq, p4, kvh) : 0.f;
         }
       }
     };
-    auto& vt = sh.vt[wave];
     // Wave-uniform fast-path bound: a tile inside [lo of the last row, hi of the
     // first row) is visible to every row of the row-group and fully stored, so
     // it needs no position masks.  Both paths compute identical bits for a row.
@@ -411,20 +534,23 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
     auto compute = [&](int t, int b, auto full_tag) {
       constexpr bool FULL = decltype(full_tag)::value;
       const int tb = w_begin + t * kTileTok;
-      const bool okv = FULL ? true : okb[b];
+      const bool okv_k = FULL ? true : okk[b];
       // ---- S^T = K Q^T : lane holds (positions tb + 4*grp + r, row l16 of tile nt)
       f32x4 sc[NT];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) sc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < NQS; ++s) {
-        const uint4 a = kb[b].op(s, okv);
+        const uint4 a = kb[b].op(s, okv_k);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) sc[nt] = M::qk(a, qreg[nt][s], sc[nt]);
       }
-      // ---- V tile to LDS (row = key position, contiguous head_dim)
+      // positions past the sequence may hold any bits (NaN included): zero them
+      if (!FULL) {
 #pragma unroll
-      for (int i = 0; i < NQS; ++i) *(uint4*)&vt[l16][grp * DQ + 8 * i] = vb[b].op(i, okv);
+        for (int i = 0; i < 4; ++i)
+          if (!(okv[b] >> i & 1u)) vq[b].zero(i);
+      }
       // ---- online softmax (log2 domain) and the P^T operand
       uint2 pop[NT];
       bool rescale = false;
@@ -445,8 +571,7 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
           sv4[r] = x;
           mx = fmaxf(mx, x);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, RLT_WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, RLT_WAVE));
+        mx = group_max(mx);
         const float m_new = fmaxf(m_run[nt], mx);
         float pr[4];
         corr[nt] = 1.f;
@@ -458,9 +583,7 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
           for (int r = 0; r < 4; ++r) pr[r] = exp2f(sv4[r] - m_new);
         }
         rescale |= corr[nt] != 1.f;
-        float rs = ((pr[0] + pr[1]) + pr[2]) + pr[3];
-        rs += __shfl_xor(rs, 16, RLT_WAVE);
-        rs += __shfl_xor(rs, 32, RLT_WAVE);
+        const float rs = group_sum(((pr[0] + pr[1]) + pr[2]) + pr[3]);
         l_run[nt] = l_run[nt] * corr[nt] + rs;
         m_run[nt] = m_new;
         if (SM == 2) {
@@ -478,20 +601,21 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
 #pragma unroll
           for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] *= corr[nt];
       }
-      // ---- O^T += V^T P^T : A = V^T (dims 16dt + l16, positions 4grp..+3)
+      // ---- O^T += V^T P^T : A = V^T (dims ND * l16 + dt, positions 4grp..+3)
+      for_pairs<ND, NT>([&](auto kc) {
+        constexpr int K = decltype(kc)::value;
+        uint2 a0, a1;
+        vq[b].template op2<K>(a0, a1);
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) {
-        const int d = dt * 16 + l16;
-        uint2 a;
-        a.x = (uint32_t)vt[4 * grp + 0][d] | ((uint32_t)vt[4 * grp + 1][d] << 16);
-        a.y = (uint32_t)vt[4 * grp + 2][d] | ((uint32_t)vt[4 * grp + 3][d] << 16);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::pv(a, pop[nt], oacc[nt][dt]);
-      }
+        for (int nt = 0; nt < NT; ++nt) {
+          oacc[nt][2 * K] = M::pv(a0, pop[nt], oacc[nt][2 * K]);
+          oacc[nt][2 * K + 1] = M::pv(a1, pop[nt], oacc[nt][2 * K + 1]);
+        }
+      });
     };
     // Two-stage pipeline: tile t + 2 is issued into the stage tile t just freed.
-    // Issues are unconditional (tiles outside [t0, t1) read block 0 and are
-    // masked) so the wait counts stay exact: no branch merges pending loads.
+    // Issues are unconditional (tiles outside [t0, t1) read in-pool addresses and
+    // are masked) so the wait counts stay exact: no branch merges pending loads.
     issue(0, 0);
     issue(1, 1);
 #pragma unroll
@@ -530,7 +654,6 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
       for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = oacc[nt][dt] * s1 + sh.o[buf][nt * ND + dt][lane] * s2;
     }
   };
-  __syncthreads();  // vt no longer needed; ml / o buffers are free
   if (wave >= 2) publish(wave - 2);
   __syncthreads();
   if (wave < 2) absorb(wave);
@@ -557,10 +680,20 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
       P.part_ml[2 * slot + 1] = l_run[nt];
     }
     float* po = P.part_o + slot * D;
+    // accumulator element r of column tile dt is dim ND * (4 * grp + r) + dt
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) {
-      const f32x4 o = oacc[nt][dt] * v_mul;
-      *(float4*)(po + dt * 16 + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
+    for (int r = 0; r < 4; ++r) {
+      float* dst = po + ND * (4 * grp + r);
+      if (ND % 4 == 0) {
+#pragma unroll
+        for (int d4 = 0; d4 < ND; d4 += 4)
+          *(float4*)(dst + d4) = make_float4(oacc[nt][d4][r] * v_mul, oacc[nt][d4 + 1][r] * v_mul,
+                                             oacc[nt][d4 + 2][r] * v_mul, oacc[nt][d4 + 3][r] * v_mul);
+      } else {
+#pragma unroll
+        for (int d2 = 0; d2 < ND; d2 += 2)
+          *(float2*)(dst + d2) = make_float2(oacc[nt][d2][r] * v_mul, oacc[nt][d2 + 1][r] * v_mul);
+      }
     }
   }
 }
@@ -876,12 +1009,18 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
 
 // ============================================================ dispatch
 
-template <int QT, int KVT, int D, int SM>
-int launch_mfma_sm(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
-  if (nt == 1) rlt_attn_mfma_kernel<QT, KVT, D, 1, SM><<<grid, 256, 0, stream>>>(P);
-  else if (D <= 128) rlt_attn_mfma_kernel<QT, KVT, D, (D <= 128 ? 2 : 1), SM><<<grid, 256, 0, stream>>>(P);
+template <int QT, int KVT, int D, int SM, bool UB>
+int launch_mfma_ub(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
+  if (nt == 1) rlt_attn_mfma_kernel<QT, KVT, D, 1, SM, UB><<<grid, 256, 0, stream>>>(P);
+  else if (D <= 128) rlt_attn_mfma_kernel<QT, KVT, D, (D <= 128 ? 2 : 1), SM, UB><<<grid, 256, 0, stream>>>(P);
   else return RLT_ERR_UNSUPPORTED;
   return RLT_OK;
+}
+
+template <int QT, int KVT, int D, int SM>
+int launch_mfma_sm(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
+  if (P.block_size % kTileTok == 0) return launch_mfma_ub<QT, KVT, D, SM, true>(P, grid, nt, stream);
+  return launch_mfma_ub<QT, KVT, D, SM, false>(P, grid, nt, stream);
 }
 
 template <int QT, int KVT, int D>
