@@ -10,11 +10,14 @@
 // The per-row form is the packed form with q_len = 1 per row.
 //
 // Work decomposition (all static, graph-capturable: no length-dependent grid):
-//  1-D grid over (sequence x row-group, kv head, chunk).  A chunk is kChunk = 512 absolute
-//  key positions [512c, 512c + 512); its workgroup runs 4 waves on 128 positions
-//  each, in 16-position tiles.  Every row of the sequence (q_len window rows x
-//  GQA group) that attends to a kv head is handled by the SAME workgroup, so each
-//  KV byte is read once per (sequence, kv head) instead of once per q row.
+//  1-D grid over (sequence x row-group, kv-head group, chunk).  A chunk is kChunk =
+//  512 absolute key positions [512c, 512c + 512), processed in 16-position tiles.
+//  On the MFMA path a workgroup's 4 waves serve up to 4 kv heads of the chunk
+//  (one wave per head when kv heads are a multiple of 4; otherwise the waves of a
+//  head split the chunk and combine in LDS); on the vector path the 4 waves split
+//  the chunk of one kv head.  Every row of the sequence (q_len window rows x GQA
+//  group) that attends to a kv head is handled by the SAME wave(s), so each KV
+//  byte is read once per (sequence, kv head) instead of once per q row.
 //  Partial (max, sum, unnormalized output) per (row, head, chunk) go to a
 //  workspace; rlt_merge_kernel combines a row's chunks in chunk order.
 //
@@ -27,10 +30,11 @@
 // Math paths (chosen by dtype and head_dim only, never by row count):
 //  * MFMA (q bf16/fp16, KV same type or fp8-e4m3, head_dim % 32 == 0, <= 256):
 //    S^T = K Q^T with v_mfma_f32_16x16x32_{bf16,f16} straight from global memory
-//    (each lane holds one key position's contiguous head_dim/4 slice, which is the
-//    A-operand layout), online softmax in fp32 (log2 domain), then
-//    O^T = V^T P^T with v_mfma_f32_16x16x16: the P^T operand is exactly the
-//    S^T accumulator layout, V^T comes from a wave-private LDS transpose.
+//    (the contraction order is permuted so that each lane's eight elements per
+//    step are contiguous in memory: the A-operand layout), online softmax in fp32
+//    (log2 domain), then O^T = V^T P^T with v_mfma_f32_16x16x16: the P^T operand
+//    is exactly the S^T accumulator layout, and the output dimensions are permuted
+//    so that V^T operands are contiguous loads too (no LDS transpose).
 //  * vector (fp32 q, or any other head_dim <= 256): fp32 FMA dot products.
 
 #include "common.h"
@@ -46,7 +50,7 @@ constexpr int kChunk = 512;       // key positions per workgroup (split unit)
 constexpr int kWaves = 4;
 constexpr int kWaveSpan = kChunk / kWaves;  // 128 positions per wave
 constexpr int kTileTok = 16;
-constexpr int kTilesPerWave = kWaveSpan / kTileTok;  // 8
+constexpr int kStages = 2;  // KV tiles in flight per wave (MFMA path)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -72,6 +76,8 @@ struct AttnParams {
   int32_t window;  // 0: full context
   int32_t rows_per_rg;
   int32_t rowgroups;
+  int32_t heads_per_wg;  // kv heads per workgroup (1, 2 or 4)
+  int32_t head_groups;   // hkv / heads_per_wg
   int32_t max_chunks;
   float qk_scale_log2;  // log2(e) / sqrt(head_dim)
   void* out;
@@ -89,7 +95,7 @@ struct SeqView {
 // rotated by the (sequence, row-group, kv head) index: every sequence's chunks then
 // spread evenly over all XCDs whatever the mix of sequence lengths.
 struct WorkItem {
-  int seq, rg, kvh, chunk;
+  int seq, rg, hg, chunk;  // hg: kv-head group (heads_per_wg heads)
 };
 
 __device__ __forceinline__ WorkItem work_item(const AttnParams& P, int64_t id) {
@@ -97,8 +103,8 @@ __device__ __forceinline__ WorkItem work_item(const AttnParams& P, int64_t id) {
   const int64_t pair = id / P.max_chunks;
   const int j = (int)(id % P.max_chunks);
   w.chunk = (int)((j + pair) % P.max_chunks);
-  w.kvh = (int)(pair % P.hkv);
-  const int64_t sr = pair / P.hkv;
+  w.hg = (int)(pair % P.head_groups);
+  const int64_t sr = pair / P.head_groups;
   w.rg = (int)(sr % P.rowgroups);
   w.seq = (int)(sr / P.rowgroups);
   return w;
@@ -233,32 +239,32 @@ __device__ __forceinline__ uint2 fp8x4_to_16(uint32_t w) {
   return r;
 }
 
-// One lane's raw head_dim/4 slice of a key or value vector, as loaded from HBM.
-// Conversion to the MFMA element type happens at use, so a load in flight never
-// forces a wait.
+// One lane's raw key elements, as loaded from HBM: for contraction step s the
+// eight elements [32 s + 8 g, + 8) of its position (g = lane group), so the four
+// lane groups of one load instruction read 64 (32 for fp8) contiguous bytes of
+// each position.  Conversion to the MFMA element type happens at use, so a load
+// in flight never forces a wait.
 template <int QT, int KVT, int D>
 struct RawSlice {
-  static constexpr int kBytes = (KVT == QT ? 2 : 1) * (D / 4);
-  static constexpr int kWords = kBytes / 4;
-  static constexpr bool kQuad = kBytes % 16 == 0;  // dwordx4 loads, else dwordx2
+  static constexpr int kElt = KVT == QT ? 2 : 1;
+  static constexpr int kSteps = D / 32;
+  static constexpr int kWords = kSteps * 2 * kElt;  // 8 elements per step
   uint32_t w[kWords];
 
+  // p: element 8 g of the position's head vector
   __device__ __forceinline__ void load(const uint8_t* p) {
-    if (kQuad) {
 #pragma unroll
-      for (int i = 0; i < kWords / 4; ++i) {
-        const uint4 v = ((const uint4*)p)[i];
-        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kWords / 2; ++i) {
-        const uint2 v = ((const uint2*)p)[i];
-        w[2 * i] = v.x; w[2 * i + 1] = v.y;
+    for (int s = 0; s < kSteps; ++s) {
+      if (kElt == 2) {
+        const uint4 v = *(const uint4*)(p + s * 32 * kElt);
+        w[4 * s] = v.x; w[4 * s + 1] = v.y; w[4 * s + 2] = v.z; w[4 * s + 3] = v.w;
+      } else {
+        const uint2 v = *(const uint2*)(p + s * 32 * kElt);
+        w[2 * s] = v.x; w[2 * s + 1] = v.y;
       }
     }
   }
-  // Eight consecutive elements [8s, 8s + 8) of the slice as MFMA operand bits;
+  // The eight elements of step s as MFMA operand bits;
   // zeros when `ok` is false (positions past the sequence may hold any bits).
   __device__ __forceinline__ uint4 op(int s, bool ok) const {
     uint4 r;
@@ -373,10 +379,18 @@ template <int QT, int KVT, int D, int NT>
 struct MfmaShared {
   f32x4 o[2][NT * (D / 16)][64];  // wave combine
   float ml[2][NT * 16][2];
+  int32_t tbl[kChunk];  // block of every position of the chunk
 };
 
 // SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).  UB: block_size is a
 // multiple of 16, so the 16 positions of a tile share one block.
+//
+// Workgroup = (sequence, row-group, kv-head group, chunk).  Its 4 waves cover
+// H4 = heads_per_wg kv heads x S = 4 / H4 parts of the chunk: wave w serves kv
+// head hg * H4 + w / S on positions [c_begin + (w % S) * 512 / S, + 512 / S).
+// With H4 = 4 (kv heads a multiple of 4) each wave streams one head over the whole
+// chunk and no cross-wave combine is needed; the four waves read neighbouring
+// slices of the same KV blocks at the same time.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
 __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   using M = Mfma<QT>;
@@ -384,22 +398,33 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   using VQ = ValueQuad<QT, KVT, D>;
   constexpr int NQS = D / 32;  // 32-wide contraction slices
   constexpr int ND = D / 16;   // 16-wide output column tiles (= dims per lane)
-  constexpr int DQ = D / 4;    // elements per lane group
   constexpr int KV_ELT = KVT == QT ? 2 : 1;
-  constexpr int TW = kTilesPerWave;
   __shared__ MfmaShared<QT, KVT, D, NT> sh;
 
   const WorkItem wi = work_item(P, blockIdx.x);
   const int seq = wi.seq;
   const int rg = wi.rg;
-  const int kvh = wi.kvh;
   const int chunk = wi.chunk;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
   const int grp = lane >> 4;
+  const int S = 4 / P.heads_per_wg;  // waves per kv head (workgroup-uniform)
+  const int head_in_wg = wave / S;
+  const int part = wave - head_in_wg * S;
+  const int kvh = wi.hg * P.heads_per_wg + head_in_wg;
+  const int c_begin = chunk * kChunk;
 
-  const SeqView sv = seq_view(P, seq);
+  // Block-table slice of the chunk into LDS (issued before the sequence metadata
+  // is known: the index is clamped into the table and every entry is range
+  // checked, so each stored block id addresses memory inside the pool).
+  for (int i = threadIdx.x; i < kChunk; i += 256) {
+    const int idx = min((c_begin + i) / P.block_size, P.table_width - 1);
+    const int32_t e = P.tables[(int64_t)seq * P.table_stride + idx];
+    sh.tbl[i] = (e >= 0 && e < P.num_blocks) ? e : 0;
+  }
+
+  SeqView sv = seq_view(P, seq);
   const int rows_total = sv.q_len * P.group;
   const int rg_begin = rg * P.rows_per_rg;
   if (rg_begin >= rows_total) return;
@@ -407,28 +432,18 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   int lo_first, hi_first, lo_last, hi_last;
   row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
   row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
-  const int c_begin = chunk * kChunk;
   if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
 
   // Tiles of this wave: absolute 16-aligned positions [w_begin + 16t, +16), t in [t0, t1).
-  const int w_begin = c_begin + wave * kWaveSpan;
+  const int span = kChunk / S;
+  const int w_begin = c_begin + part * span;
   const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
-  const int span_hi = min(w_begin + kWaveSpan, hi_last);
+  const int span_hi = min(w_begin + span, hi_last);
   // wave-uniform (scalar) bounds: keeps the tile loop free of divergent branches
   const int t0 = __builtin_amdgcn_readfirstlane(
       span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok);
   const int t1 = __builtin_amdgcn_readfirstlane(
       span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok);
-
-  // Block-table entries of all this lane's positions, issued before any KV load
-  // (index clamped into the table: any entry is a safe address once range-checked).
-  int32_t blk[TW];
-#pragma unroll
-  for (int t = 0; t < TW; ++t) {
-    const int pos = w_begin + t * kTileTok + (UB ? 0 : l16);
-    const int idx = min(pos / P.block_size, P.table_width - 1);
-    blk[t] = P.tables[(int64_t)seq * P.table_stride + idx];
-  }
 
   // This lane's rows (one per 16-row tile): B operand of S^T = K Q^T.
   int row_lo[NT], row_hi[NT];
@@ -441,9 +456,9 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
       const int head = kvh * P.group + rho % P.group;
       row_range(P, sv, qi, row_lo[nt], row_hi[nt]);
       const uint16_t* qp = (const uint16_t*)P.q + (int64_t)(sv.q_begin + qi) * P.q_row_stride +
-                           (int64_t)head * P.q_head_stride + grp * DQ;
+                           (int64_t)head * P.q_head_stride + grp * 8;
 #pragma unroll
-      for (int s = 0; s < NQS; ++s) qreg[nt][s] = *(const uint4*)(qp + 8 * s);
+      for (int s = 0; s < NQS; ++s) qreg[nt][s] = *(const uint4*)(qp + 32 * s);
     } else {
       row_lo[nt] = 0;
       row_hi[nt] = 0;
@@ -469,28 +484,28 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
     for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  __syncthreads();  // block-table slice visible to every wave
+
   if (t0 < t1) {
-    Raw kb[2];
-    VQ vq[2];
-    float ksc[2][4], vsc[2][4];
-    bool okk[2];
-    uint32_t okv[2];  // bit i: value position 4 * grp + i is inside the sequence
-    const int64_t k_head = (int64_t)kvh * P.k_head_stride + grp * DQ;
+    Raw kb[kStages];
+    VQ vq[kStages];
+    float ksc[kStages][4], vsc[kStages][4];
+    bool okk[kStages];
+    uint32_t okv[kStages];  // bit i: value position 4 * grp + i is inside the sequence
+    const int64_t k_head = (int64_t)kvh * P.k_head_stride + grp * 8;
     const int64_t v_head = (int64_t)kvh * P.v_head_stride + l16 * ND;
-    // Loads of tile t into stage b.  Branch-free: every address is inside the pool
-    // (table index clamped, entries outside the pool read block 0), and positions
-    // outside the wave's range are zeroed at use.
+    const int32_t* tbl = sh.tbl - c_begin;  // tbl[pos] for pos in the chunk
+    // Loads of tile t into stage b.  Branch-free: every address is inside the
+    // pool, and positions outside the sequence are zeroed at use.
     auto issue = [&](int t, int b) {
       const int tb = w_begin + t * kTileTok;
-      const bool tile_ok = t >= t0 && t < t1;
-      okk[b] = tile_ok && tb + l16 < hi_last;
+      okk[b] = tb + l16 < hi_last;
       uint32_t m4 = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) m4 |= (tile_ok && tb + 4 * grp + i < hi_last) ? (1u << i) : 0u;
+      for (int i = 0; i < 4; ++i) m4 |= (tb + 4 * grp + i < hi_last) ? (1u << i) : 0u;
       okv[b] = m4;
       if (UB) {
-        const int32_t e = __builtin_amdgcn_readfirstlane(blk[t]);
-        const int64_t bk = (e >= 0 && e < P.num_blocks) ? (int64_t)e : 0;
+        const int64_t bk = __builtin_amdgcn_readfirstlane(tbl[tb]);
         const int in_blk = tb % P.block_size;
         const uint8_t* kp = (const uint8_t*)P.k +
             (bk * P.k_block_stride + (int64_t)(in_blk + l16) * P.k_token_stride + k_head) * KV_ELT;
@@ -500,19 +515,17 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
         for (int i = 0; i < 4; ++i)
           vq[b].load(i, vbase + (int64_t)(in_blk + 4 * grp + i) * P.v_token_stride * KV_ELT);
       } else {
-        const int64_t bk = (blk[t] >= 0 && blk[t] < P.num_blocks) ? (int64_t)blk[t] : 0;
+        const int64_t bk = tbl[tb + l16];
         const uint8_t* kp = (const uint8_t*)P.k +
             (bk * P.k_block_stride + (int64_t)((tb + l16) % P.block_size) * P.k_token_stride + k_head) *
                 KV_ELT;
         kb[b].load(kp);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // lane 4 * grp + i holds the entry of position tb + 4 * grp + i
-          const int32_t e = __shfl(blk[t], 4 * grp + i, RLT_WAVE);
-          const int64_t bv = (e >= 0 && e < P.num_blocks) ? (int64_t)e : 0;
+          const int pv = tb + 4 * grp + i;
+          const int64_t bv = tbl[pv];
           const uint8_t* vp = (const uint8_t*)P.v +
-              (bv * P.v_block_stride + (int64_t)((tb + 4 * grp + i) % P.block_size) * P.v_token_stride +
-               v_head) * KV_ELT;
+              (bv * P.v_block_stride + (int64_t)(pv % P.block_size) * P.v_token_stride + v_head) * KV_ELT;
           vq[b].load(i, vp);
         }
       }
@@ -520,9 +533,12 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p4 = tb + 4 * grp + r;
-          const bool ok4 = tile_ok && p4 < hi_last;
-          ksc[b][r] = ok4 ? scale_at(P, P.k_scale, seq, p4, kvh) : 0.f;
-          vsc[b][r] = ok4 ? scale_at(P, P.v_scale, seq, p4, kvh) : 0.f;
+          const int64_t so = (int64_t)tbl[p4] * P.s_block_stride +
+                             (int64_t)(p4 % P.block_size) * P.s_token_stride +
+                             (int64_t)kvh * P.s_head_stride;
+          const bool ok4 = p4 < hi_last;
+          ksc[b][r] = ok4 ? P.k_scale[so] : 0.f;
+          vsc[b][r] = ok4 ? P.v_scale[so] : 0.f;
         }
       }
     };
@@ -573,15 +589,12 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
         }
         mx = group_max(mx);
         const float m_new = fmaxf(m_run[nt], mx);
+        // a row that has seen no visible key keeps m = -inf and weights 0
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        corr[nt] = m_new == m_run[nt] ? 1.f : __builtin_amdgcn_exp2f(m_run[nt] - m_use);
         float pr[4];
-        corr[nt] = 1.f;
-        if (m_new == -INFINITY) {
-          pr[0] = pr[1] = pr[2] = pr[3] = 0.f;
-        } else {
-          corr[nt] = exp2f(m_run[nt] - m_new);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) pr[r] = exp2f(sv4[r] - m_new);
-        }
+        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(sv4[r] - m_use);
         rescale |= corr[nt] != 1.f;
         const float rs = group_sum(((pr[0] + pr[1]) + pr[2]) + pr[3]);
         l_run[nt] = l_run[nt] * corr[nt] + rs;
@@ -613,23 +626,27 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
         }
       });
     };
-    // Two-stage pipeline: tile t + 2 is issued into the stage tile t just freed.
-    // Issues are unconditional (tiles outside [t0, t1) read in-pool addresses and
-    // are masked) so the wait counts stay exact: no branch merges pending loads.
-    issue(0, 0);
-    issue(1, 1);
+    auto step = [&](int t, int b) {
+      const int tb = w_begin + t * kTileTok;
+      if (tb >= full_lo && tb + kTileTok <= full_hi) compute(t, b, Flag<true>{});
+      else compute(t, b, Flag<false>{});
+    };
+    // kStages-deep pipeline: tile t + kStages is issued into the stage tile t just freed.
+    // Issues are unconditional -- past the last tile the last tile is re-read (a
+    // cache hit) -- so no branch merges pending loads and the wait counts stay exact.
+    const int tl = t1 - 1;
 #pragma unroll
-    for (int t = 0; t < TW; ++t) {
-      if (t >= t0 && t < t1) {
-        const int tb = w_begin + t * kTileTok;
-        if (tb >= full_lo && tb + kTileTok <= full_hi) compute(t, t & 1, Flag<true>{});
-        else compute(t, t & 1, Flag<false>{});
+    for (int b = 0; b < kStages; ++b) issue(min(t0 + b, tl), b);
+    for (int t = t0; t < t1; t += kStages) {
+#pragma unroll
+      for (int b = 0; b < kStages; ++b) {
+        if (b == 0 || t + b < t1) step(t + b, b);
+        issue(min(t + b + kStages, tl), b);
       }
-      if (t + 2 < TW) issue(t + 2, t & 1);
     }
   }
 
-  // ---- combine the 4 waves: ((w0 + w2) + (w1 + w3)), then write the chunk partial.
+  // ---- combine the S waves of a kv head, then write the chunk partial.
   auto publish = [&](int buf) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -654,14 +671,21 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
       for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = oacc[nt][dt] * s1 + sh.o[buf][nt * ND + dt][lane] * s2;
     }
   };
-  if (wave >= 2) publish(wave - 2);
-  __syncthreads();
-  if (wave < 2) absorb(wave);
-  __syncthreads();
-  if (wave == 1) publish(0);
-  __syncthreads();
-  if (wave != 0) return;
-  absorb(0);
+  if (S == 4) {  // ((w0 + w2) + (w1 + w3))
+    if (wave >= 2) publish(wave - 2);
+    __syncthreads();
+    if (wave < 2) absorb(wave);
+    __syncthreads();
+    if (wave == 1) publish(0);
+    __syncthreads();
+    if (wave != 0) return;
+    absorb(0);
+  } else if (S == 2) {  // (w0 + w1), (w2 + w3)
+    if (part == 1) publish(head_in_wg);
+    __syncthreads();
+    if (part == 1) return;
+    absorb(head_in_wg);
+  }
 
   // ---- chunk partial for rows whose merge range contains this chunk
 #pragma unroll
@@ -720,7 +744,7 @@ __global__ __launch_bounds__(256) void rlt_attn_vec_kernel(AttnParams P) {
   const WorkItem wi = work_item(P, blockIdx.x);
   const int seq = wi.seq;
   const int rg = wi.rg;
-  const int kvh = wi.kvh;
+  const int kvh = wi.hg;  // one kv head per workgroup on this path
   const int chunk = wi.chunk;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -1163,7 +1187,9 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     P.rows_per_rg = 16 * nt;
     P.rowgroups = (rows_per_seq + P.rows_per_rg - 1) / P.rows_per_rg;
     if (P.rowgroups < 1) P.rowgroups = 1;
-    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads * P.max_chunks;
+    P.heads_per_wg = num_kv_heads % 4 == 0 ? 4 : (num_kv_heads % 2 == 0 ? 2 : 1);
+    P.head_groups = num_kv_heads / P.heads_per_wg;
+    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * P.head_groups * P.max_chunks;
     if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
     dim3 grid((unsigned)wgs);
     if (q_dtype == RLT_BF16)
@@ -1176,7 +1202,9 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     P.rows_per_rg = kVecRows;
     P.rowgroups = (rows_per_seq + kVecRows - 1) / kVecRows;
     if (P.rowgroups < 1) P.rowgroups = 1;
-    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads * P.max_chunks;
+    P.heads_per_wg = 1;
+    P.head_groups = num_kv_heads;
+    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * P.head_groups * P.max_chunks;
     if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
     dim3 grid((unsigned)wgs);
     switch (q_dtype) {
