@@ -225,6 +225,56 @@ __device__ float rlt_row_mass_half(const float* __restrict__ x, int64_t V,
 
 __device__ __forceinline__ bool finite_pos(float m) { return isfinite(m) && m > 0.f; }
 
+// ------------------------------------------------------------------ wave scans
+
+// A float64 moved across lanes by a DPP pattern (both 32-bit halves).
+template <int kCtrl>
+__device__ __forceinline__ double dpp_move(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, kCtrl, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), kCtrl, 0xf, 0xf, false);
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+// Inclusive prefix sum over the 64 lanes in a fixed order: Hillis-Steele steps
+// within each 16-lane row (row_shr 1, 2, 4, 8), then row 0 -> 1 and 2 -> 3
+// (row_bcast 15), then lanes 0..31 -> 32..63 (row_bcast 31).
+__device__ __forceinline__ double wave_inclusive_sum(double x) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  double y;
+  y = dpp_move<0x111>(x);
+  if (r >= 1) x += y;
+  y = dpp_move<0x112>(x);
+  if (r >= 2) x += y;
+  y = dpp_move<0x114>(x);
+  if (r >= 4) x += y;
+  y = dpp_move<0x118>(x);
+  if (r >= 8) x += y;
+  y = dpp_move<0x142>(x);
+  if (lane & 16) x += y;
+  y = dpp_move<0x143>(x);
+  if (lane >= 32) x += y;
+  return x;
+}
+
+// The value of lane 63 in every lane.
+__device__ __forceinline__ double lane63(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// OR of the flag bits (1 NaN, 2 +inf, 4 negative, 8 positive) over the wave.
+__device__ __forceinline__ uint32_t wave_or_flags(uint32_t fl) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    if (__builtin_amdgcn_ballot_w64((fl >> b) & 1u)) r |= 1u << b;
+  return r;
+}
+
 // ------------------------------------------------------------------ weights
 
 struct WeightRow {
@@ -245,30 +295,29 @@ __device__ __forceinline__ float weight_of(float a, float b, const WeightRow& w)
   return r < 0.f ? 0.f : r;
 }
 
+// This thread's kElems raw floats [base, base + kElems) of a row (zero past V).
+__device__ __forceinline__ void load_raw(const float* row, int64_t V, int64_t base, bool vec_ok,
+                                         float out[kElems]) {
+  if (vec_ok && base + kElems <= V) {
+    const float4 a0 = *(const float4*)(row + base);
+    const float4 a1 = *(const float4*)(row + base + 4);
+    out[0] = a0.x; out[1] = a0.y; out[2] = a0.z; out[3] = a0.w;
+    out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) out[e] = base + e < V ? row[base + e] : 0.f;
+  }
+}
+
 // This thread's kElems weights of tile `tile` (zero past V).
 __device__ __forceinline__ void load_weights(const WeightRow& w, int64_t V, int64_t tile, int t,
                                              bool vec_ok, float out[kElems]) {
   const int64_t base = tile * kTile + (int64_t)t * kElems;
-  if (vec_ok && base + kElems <= V) {
-    const float4 a0 = *(const float4*)(w.a + base);
-    const float4 a1 = *(const float4*)(w.a + base + 4);
-    float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    float bv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (w.residual) {
-      const float4 b0 = *(const float4*)(w.b + base);
-      const float4 b1 = *(const float4*)(w.b + base + 4);
-      bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
-      bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
-    }
+  float av[kElems], bv[kElems];
+  load_raw(w.a, V, base, vec_ok, av);
+  if (w.residual) load_raw(w.b, V, base, vec_ok, bv);
 #pragma unroll
-    for (int e = 0; e < kElems; ++e) out[e] = weight_of(av[e], bv[e], w);
-  } else {
-#pragma unroll
-    for (int e = 0; e < kElems; ++e) {
-      const int64_t k = base + e;
-      out[e] = k < V ? weight_of(w.a[k], w.residual ? w.b[k] : 0.f, w) : 0.f;
-    }
-  }
+  for (int e = 0; e < kElems; ++e) out[e] = base + e < V ? weight_of(av[e], w.residual ? bv[e] : 0.f, w) : 0.f;
 }
 
 // Sequential float64 replay of torch's cumsum + searchsorted(right=True) on one
@@ -318,12 +367,13 @@ __device__ int64_t slow_draw(const WeightRow& w, int64_t V, float u, bool* valid
 
 struct DrawScratch {
   double tile_total[kMaxTiles];
+  uint32_t tile_flags[kMaxTiles];  // per-tile flag bits (accept draw only)
   double wave_sum[kDrawWaves];
+  int64_t cand[kDrawWaves];  // per wave: first token whose cumulative weight exceeds t, or -1
+  double cand_before[kDrawWaves], cand_at[kDrawWaves];
   int decision;  // 0 fast, 1 exact replay, 2 invalid row
   int64_t tile;
   double tile_start, t, margin;
-  unsigned long long best;
-  double before, at;
 };
 
 // Inverse-CDF draw given the float64 tile totals (in ds.tile_total) and the row's
@@ -332,14 +382,19 @@ struct DrawScratch {
 // certifies the crossing against a bound on the difference between any float64
 // summation order and torch's sequential cumsum; otherwise (or for out-of-contract
 // inputs) replays torch's sequential cumsum + right bisect on one lane.
-__device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t tiles,
-                                bool any_nan, bool any_inf, bool any_neg, bool any_pos,
-                                bool vec_ok, DrawScratch& ds, int32_t* slow_count,
-                                int64_t* index_out, bool* valid_out) {
+__device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t tiles, uint32_t flags,
+                                bool flags_in_lds, bool vec_ok, DrawScratch& ds,
+                                int32_t* slow_count, int64_t* index_out, bool* valid_out) {
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
   if (wave == 0) {
+    if (flags_in_lds) {
+      uint32_t f = 0;
+      for (int64_t k = lane; k < tiles && k < kMaxTiles; k += 64) f |= ds.tile_flags[k];
+      flags = wave_or_flags(f);
+    }
+    const bool any_nan = flags & 1u, any_inf = flags & 2u, any_neg = flags & 4u, any_pos = flags & 8u;
     // wave 0: inclusive scan of the tile totals (64 tiles per pass, fixed order)
     // gives the mass and the first tile whose cumulative total exceeds t = u*mass
     int decision = 0;
@@ -349,12 +404,9 @@ __device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t 
     if (decision == 0) {
       for (int64_t k0 = 0; k0 < tiles; k0 += 64) {
         double v = k0 + lane < tiles ? ds.tile_total[k0 + lane] : 0.0;
-        for (int off = 1; off < 64; off <<= 1) {
-          const double y = __shfl_up(v, off, RLT_WAVE);
-          if (lane >= off) v += y;
-        }
+        v = wave_inclusive_sum(v);
         if (k0 + lane < tiles) ds.tile_total[k0 + lane] = m + v;  // cumulative total
-        m += __shfl(v, 63, RLT_WAVE);
+        m += lane63(v);
       }
     }
     const double tt = (double)u * m;
@@ -376,7 +428,6 @@ __device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t 
       ds.tile = tile;
       ds.tile_start = tile > 0 ? ds.tile_total[tile - 1] : 0.0;
       ds.decision = decision;
-      ds.best = ~0ull;
     }
   }
   __syncthreads();
@@ -390,45 +441,44 @@ __device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t 
 #pragma unroll
     for (int e = 0; e < kElems; ++e) local += (double)wv[e];
     // exclusive scan of thread partials in index order: wave scan, then wave offsets
-    double incl = local;
-    for (int off = 1; off < 64; off <<= 1) {
-      const double y = __shfl_up(incl, off, RLT_WAVE);
-      if (lane >= off) incl += y;
-    }
+    const double incl = wave_inclusive_sum(local);
     if (lane == 63) ds.wave_sum[wave] = incl;
     __syncthreads();
     double wave_off = 0.0;
     for (int wv2 = 0; wv2 < wave; ++wv2) wave_off += ds.wave_sum[wv2];
-    const double start = ds.tile_start + (wave_off + (incl - local));
     const double tt = ds.t;
-    double run = start;
+    double run = ds.tile_start + (wave_off + (incl - local));
     int e_hit = -1;
+    double before = 0.0, at = 0.0;
+#pragma unroll
     for (int e = 0; e < kElems; ++e) {
-      run += (double)wv[e];
-      if (run > tt) {
+      const double next = run + (double)wv[e];
+      if (e_hit < 0 && next > tt) {
         e_hit = e;
-        break;
+        before = run;
+        at = next;
       }
+      run = next;
     }
-    if (e_hit >= 0)
-      atomicMin(&ds.best, (unsigned long long)(ds.tile * kTile + (int64_t)t * kElems + e_hit));
-    __syncthreads();
-    const unsigned long long best = ds.best;
-    if (best != ~0ull && (int64_t)(best - ds.tile * kTile) / kElems == t) {
-      double r = start;
-      const int eb = (int)((best - ds.tile * kTile) % kElems);
-      for (int e = 0; e < eb; ++e) r += (double)wv[e];
-      ds.before = r;
-      ds.at = r + (double)wv[eb];
-    }
-    __syncthreads();
-    if (t == 0) {
-      const bool ok = best != ~0ull && ds.before <= tt - ds.margin && ds.at > tt + ds.margin;
-      ds.decision = ok ? 0 : 1;
+    // each wave reports its first hit; the first reporting wave holds the crossing
+    const uint64_t hits = __builtin_amdgcn_ballot_w64(e_hit >= 0);
+    if (hits == 0) {
+      if (lane == 0) ds.cand[wave] = -1;
+    } else if (lane == __builtin_ctzll(hits)) {
+      ds.cand[wave] = ds.tile * kTile + (int64_t)t * kElems + e_hit;
+      ds.cand_before[wave] = before;
+      ds.cand_at[wave] = at;
     }
     __syncthreads();
-    decision = ds.decision;
-    index = (int64_t)best;
+    if (t != 0) return;
+    decision = 1;
+    for (int wv2 = 0; wv2 < kDrawWaves; ++wv2) {
+      if (ds.cand[wv2] < 0) continue;
+      index = ds.cand[wv2];
+      const bool ok = ds.cand_before[wv2] <= tt - ds.margin && ds.cand_at[wv2] > tt + ds.margin;
+      decision = ok ? 0 : 1;
+      break;
+    }
   }
   if (t != 0) return;
   if (decision == 1) {
@@ -444,7 +494,7 @@ __device__ void draw_from_tiles(const WeightRow& w, int64_t V, float u, int64_t 
   *valid_out = valid;
 }
 
-// This thread's tile weights -> (wave-reduced float64 sum in lane 0, flag bits).
+// This thread's tile weights -> (wave-reduced float64 sum in every lane, flag bits).
 __device__ __forceinline__ double tile_partial(const float wv[kElems], uint32_t& flags) {
   double local = 0.0;
 #pragma unroll
@@ -456,8 +506,7 @@ __device__ __forceinline__ double tile_partial(const float wv[kElems], uint32_t&
     if (x > 0.f) flags |= 8u;
     local += (double)x;
   }
-  for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, RLT_WAVE);
-  return local;
+  return lane63(wave_inclusive_sum(local));
 }
 
 // ------------------------------------------------------------------ categorical
@@ -502,7 +551,8 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
         if (lane == 0) sh.wave_tile[k0 + uu][wave] = part;
       }
     }
-    if (fl) atomicOr(&sh.flags, fl);
+    fl = wave_or_flags(fl);
+    if (lane == 0 && fl) atomicOr(&sh.flags, fl);
   }
   __syncthreads();
   for (int64_t k = t; k < tiles && k < kMaxTiles; k += kDrawThreads) {
@@ -514,8 +564,7 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
   const uint32_t f = sh.flags;
   int64_t index;
   bool valid;
-  draw_from_tiles(w, V, u[i], tiles, f & 1u, f & 2u, f & 4u, f & 8u, vec_ok, sh.ds, slow_count,
-                  &index, &valid);
+  draw_from_tiles(w, V, u[i], tiles, f, false, vec_ok, sh.ds, slow_count, &index, &valid);
   if (t == 0) {
     out_index[i] = index;
     out_valid[i] = valid;
@@ -540,7 +589,7 @@ struct AcceptShared {
   int64_t tok[kMaxW1];
   int64_t drafts;
   double wave_part[kDrawWaves];
-  uint32_t flags;
+  uint32_t wave_flags[kDrawWaves];
   int s, at_end, stop_ok, err0;
 };
 
@@ -559,7 +608,7 @@ __device__ __forceinline__ WeightRow stop_weights(const float* p, const float* q
 // grid (n, tiles), kDrawThreads threads.  Each workgroup recomputes its request's
 // stop state from the mass partials (cheap and identical in every workgroup) and
 // totals its 4096-token tile of the final weights; tile 0 also publishes the stop
-// state.  reference: speculative_sampling.py:136-172.
+// reference: speculative_sampling.py:136-172.
 __global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
     const float* __restrict__ p, const float* __restrict__ q, int W1, int64_t V, int64_t n,
     const float* __restrict__ partials, int64_t groups, const int64_t* __restrict__ draft_tokens,
@@ -573,7 +622,6 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  if (t == 0) sh.flags = 0;
   // draft tokens, uniforms and the gathers p[x], q[x]: issued first, one lane each
   if (t < W1) {
     const int64_t tok = draft_tokens[i * W1 + t];
@@ -599,39 +647,38 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
     }
   }
   __syncthreads();
-  // ---- accept chain
-  if (t == 0) {
+  // ---- accept chain: lane j decides draft j; s = leading accepts (ballot)
+  if (wave == 0) {
     const int64_t dr = sh.drafts;
     const int64_t d = dr < 0 ? 0 : (dr > W1 ? W1 : dr);
-    int s = 0;
-    bool chain = true, invalid_at_s = false;
-    for (int j = 0; j < W1; ++j) {
+    bool accept = false, invalid = false;
+    if (lane < W1) {
+      const int j = lane;
       const int64_t tok = sh.tok[j];
       const bool in_range = tok >= 0 && tok < V;
       const float pmj = sh.pm[j], qmj = sh.qm[j];
       const float px = __fdiv_rn(sh.px_raw[j], pmj);
       const float qx = __fdiv_rn(sh.qx_raw[j], qmj);
-      const bool invalid = !(finite_pos(pmj) && finite_pos(qmj) && in_range && isfinite(px) &&
-                             isfinite(qx) && qx > 0.f);
-      const bool accept = !invalid && ((px >= qx) || (sh.ua[j] * qx < px)) && (j < d);
-      if (chain) {
-        if (accept) {
-          ++s;
-        } else {
-          chain = false;
-          invalid_at_s = invalid;  // meaningful only when s < d
-        }
-      }
+      invalid = !(finite_pos(pmj) && finite_pos(qmj) && in_range && isfinite(px) && isfinite(qx) &&
+                  qx > 0.f);
+      accept = !invalid && ((px >= qx) || (sh.ua[j] * qx < px)) && (j < d);
     }
-    const bool at_end = s == d;
-    sh.s = s;
-    sh.at_end = at_end;
-    sh.stop_ok = at_end ? finite_pos(sh.pm[s]) : !invalid_at_s;
-    sh.err0 = dr != d;
+    const uint64_t am = __builtin_amdgcn_ballot_w64(accept);
+    const uint64_t im = __builtin_amdgcn_ballot_w64(invalid);
+    const int s = __builtin_ctzll(~am);  // <= W1
+    if (lane == 0) {
+      const bool at_end = s == d;
+      sh.s = s;
+      sh.at_end = at_end;
+      // invalid_at_s is meaningful only when s < d (the first rejected draft)
+      sh.stop_ok = at_end ? finite_pos(sh.pm[s]) : !((im >> s) & 1u);
+      sh.err0 = dr != d;
+    }
   }
   __syncthreads();
-  const WeightRow w = stop_weights(p, q, i, W1, V, sh.s, sh.at_end, sh.pm[sh.s],
-                                   sh.at_end ? 1.f : sh.qm[sh.s]);
+  const int s = sh.s;
+  const bool at_end = sh.at_end;
+  const WeightRow w = stop_weights(p, q, i, W1, V, s, at_end, sh.pm[s], at_end ? 1.f : sh.qm[s]);
   const bool vec_ok =
       (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
   // ---- this workgroup's tile of the final weights
@@ -640,34 +687,36 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
     load_weights(w, V, k, t, vec_ok, wv);
     uint32_t fl = 0;
     const double part = tile_partial(wv, fl);
-    if (lane == 0) sh.wave_part[wave] = part;
-    if (fl) atomicOr(&sh.flags, fl);
+    fl = wave_or_flags(fl);
+    if (lane == 0) {
+      sh.wave_part[wave] = part;
+      sh.wave_flags[wave] = fl;
+    }
   }
   __syncthreads();
   if (t == 0) {
     double tk = 0.0;
-    for (int wv = 0; wv < kDrawWaves; ++wv) tk += sh.wave_part[wv];
+    uint32_t fl = 0;
+    for (int wv = 0; wv < kDrawWaves; ++wv) {
+      tk += sh.wave_part[wv];
+      fl |= sh.wave_flags[wv];
+    }
     tile_sum[i * tiles + k] = tk;
-    tile_flags[i * tiles + k] = sh.flags;
+    tile_flags[i * tiles + k] = fl;
   }
   if (k == 0) {
     StopState& st = stop[i];
     if (t < W1) st.tok[t] = sh.tok[t];
     if (t == 0) {
-      st.s = sh.s;
-      st.at_end = sh.at_end;
+      st.s = s;
+      st.at_end = at_end;
       st.stop_ok = sh.stop_ok;
       st.err0 = sh.err0;
-      st.pm = sh.pm[sh.s];
-      st.qm = sh.at_end ? 1.f : sh.qm[sh.s];
+      st.pm = sh.pm[s];
+      st.qm = at_end ? 1.f : sh.qm[s];
     }
   }
 }
-
-struct FinalShared {
-  DrawScratch ds;
-  uint32_t flags;
-};
 
 // grid (n), kDrawThreads threads: the inverse-CDF draw and the outputs of request i.
 // reference: speculative_sampling.py:174-181.
@@ -677,27 +726,21 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_accept_draw_kernel(
     const uint32_t* __restrict__ tile_flags, const StopState* __restrict__ stop,
     int64_t* __restrict__ final_token, int64_t* __restrict__ tokens,
     int64_t* __restrict__ accepted, uint8_t* __restrict__ error, int32_t* __restrict__ slow_count) {
-  __shared__ FinalShared sh;
+  __shared__ DrawScratch ds;
   const int64_t i = blockIdx.x;
   const int t = threadIdx.x;
   const StopState& st = stop[i];
-  if (t == 0) sh.flags = 0;
-  uint32_t fl = 0;
   for (int64_t k = t; k < tiles && k < kMaxTiles; k += kDrawThreads) {
-    sh.ds.tile_total[k] = tile_sum[i * tiles + k];
-    fl |= tile_flags[i * tiles + k];
+    ds.tile_total[k] = tile_sum[i * tiles + k];
+    ds.tile_flags[k] = tile_flags[i * tiles + k];
   }
   const WeightRow w = stop_weights(p, q, i, W1, V, st.s, st.at_end, st.pm, st.qm);
   const bool vec_ok =
       (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
   __syncthreads();
-  if (fl) atomicOr(&sh.flags, fl);
-  __syncthreads();
-  const uint32_t f = sh.flags;
   int64_t index;
   bool valid;
-  draw_from_tiles(w, V, u_final[i], tiles, f & 1u, f & 2u, f & 4u, f & 8u, vec_ok, sh.ds,
-                  slow_count, &index, &valid);
+  draw_from_tiles(w, V, u_final[i], tiles, 0u, true, vec_ok, ds, slow_count, &index, &valid);
   if (t != 0) return;
   const bool err = st.err0 || !(st.stop_ok && valid);
   const int64_t fin = err ? 0 : index;
