@@ -273,3 +273,50 @@ def test_config5_fp8_rows_at_different_planes(kernel, dev):
     sk, sv = torch.tensor(0.03), torch.tensor(0.05)
     got = kernel(q.to(dev), kc.to(dev), vc.to(dev), row_tables.to(dev), ctx.to(dev), sk.to(dev), sv.to(dev))
     _close(got, oatt.paged_attention(q, kc, vc, row_tables, ctx, sk, sv), torch.bfloat16)
+
+
+def test_large_batch_rows_equal_single_row_launches_bitwise(kernel, dev):
+    # A batch's units are spread over persistent per-CU workgroups; a row's result
+    # must not depend on which workgroup or wave served it.
+    _say("persistent assignment")
+    g = torch.Generator().manual_seed(11)
+    bs, hq, hkv, d, dtype = 16, 16, 4, 128, torch.bfloat16
+    lengths = torch.randint(1, 8193, (16,), generator=g).tolist()
+    lengths[0], lengths[1] = 8192, 513
+    width = 8192 // bs
+    pages = sum(-(-n // bs) for n in lengths)
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables(lengths, bs, pages, g, width=width)
+    q = torch.randn(len(lengths), hq, d, generator=g).to(dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    kd, vd, td, cd, qd = k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), q.to(dev)
+    got = kernel(qd, kd, vd, td, cd)
+    for row in (0, 1, 7):
+        alone = kernel(qd[row:row + 1], kd, vd, td[row:row + 1], cd[row:row + 1])
+        assert torch.equal(alone[0], got[row])
+    sel = [0, 1, 7]
+    want = oatt.paged_attention(q[sel], k, v, tables[sel], ctx[sel])
+    _close(got[sel], want, dtype)
+
+
+def test_more_rows_than_the_persistent_index_uses_grid_kernel(kernel, dev):
+    # More than 8192 (sequence, row-group) pairs run one single-wave workgroup per
+    # unit; same per-unit arithmetic as the persistent kernel.
+    _say("grid fallback")
+    g = torch.Generator().manual_seed(12)
+    bs, hq, hkv, d, dtype = 16, 2, 1, 64, torch.bfloat16
+    n = 8200
+    lengths = torch.randint(0, 41, (n,), generator=g).tolist()
+    pages = sum(-(-x // bs) for x in lengths)
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables(lengths, bs, pages, g)
+    q = torch.randn(n, hq, d, generator=g).to(dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    kd, vd, td, cd, qd = k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), q.to(dev)
+    got = kernel(qd, kd, vd, td, cd)
+    sel = [0, 1, 4097, 8199] + [i for i in range(n) if lengths[i] == 0][:1]
+    for row in sel:
+        alone = kernel(qd[row:row + 1], kd, vd, td[row:row + 1], cd[row:row + 1])
+        assert torch.equal(alone[0], got[row])
+    want = oatt.paged_attention(q[sel], k, v, tables[sel], ctx[sel])
+    _close(got[sel], want, dtype)

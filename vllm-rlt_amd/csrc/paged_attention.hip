@@ -9,16 +9,16 @@
 //    < len - q_len + i + 1 (bottom-right aligned causal window).
 // The per-row form is the packed form with q_len = 1 per row.
 //
-// Work decomposition (all static, graph-capturable: no length-dependent grid):
-//  1-D grid over (sequence x row-group, kv-head group, chunk).  A chunk is kChunk =
-//  512 absolute key positions [512c, 512c + 512), processed in 16-position tiles.
-//  On the MFMA path a workgroup's 4 waves serve up to 4 kv heads of the chunk
-//  (one wave per head when kv heads are a multiple of 4; otherwise the waves of a
-//  head split the chunk and combine in LDS); on the vector path the 4 waves split
-//  the chunk of one kv head.  Every row of the sequence (q_len window rows x GQA
-//  group) that attends to a kv head is handled by the SAME wave(s), so each KV
-//  byte is read once per (sequence, kv head) instead of once per q row.
-//  Partial (max, sum, unnormalized output) per (row, head, chunk) go to a
+// Work decomposition (static grids, graph-capturable: no host-side length reads):
+//  The unit of work is (sequence x row-group, kv head, chunk), a chunk being
+//  kChunk = 512 absolute key positions [512c, 512c + 512) processed in 16-position
+//  tiles by ONE wave.  Every row of the sequence (q_len window rows x GQA group)
+//  that attends to the kv head is in that wave's row-group, so each KV byte is read
+//  once per (sequence, kv head) instead of once per q row.  On the MFMA path one
+//  persistent 8-wave workgroup per CU enumerates the active units from the
+//  sequence lengths and takes an equal share of them; the vector path runs one
+//  4-wave workgroup per (row-group, kv head, chunk) with the chunk split between
+//  waves.  Partial (max, sum, unnormalized output) per (row, head, chunk) go to a
 //  workspace; rlt_merge_kernel combines a row's chunks in chunk order.
 //
 // A row's arithmetic depends only on its own length, the absolute tile / chunk
@@ -74,10 +74,11 @@ struct AttnParams {
   int32_t num_rows;  // total q rows
   int32_t hq, hkv, group, head_dim, block_size;
   int32_t window;  // 0: full context
+  int32_t max_q;   // longest q window of a sequence (merge grid)
   int32_t rows_per_rg;
   int32_t rowgroups;
-  int32_t heads_per_wg;  // kv heads per workgroup (1, 2 or 4)
-  int32_t head_groups;   // hkv / heads_per_wg
+  int32_t head_groups;   // kv heads per grid row of work_item (one head per workgroup)
+  int32_t persistent;    // MFMA path: one persistent workgroup per CU
   int32_t max_chunks;
   float qk_scale_log2;  // log2(e) / sqrt(head_dim)
   void* out;
@@ -375,54 +376,35 @@ __device__ __forceinline__ float group_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int QT, int KVT, int D, int NT>
-struct MfmaShared {
-  f32x4 o[2][NT * (D / 16)][64];  // wave combine
-  float ml[2][NT * 16][2];
-  int32_t tbl[kChunk];  // block of every position of the chunk
-};
-
+// One work unit -- (sequence, row-group, kv head, chunk) -- on one wave: the wave
+// streams the kv head over the whole 512-position chunk for every row of the
+// row-group and writes the chunk partial of those rows.  tbl_lds: this wave's
+// 512-entry LDS slice for the chunk's block ids.
 // SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).  UB: block_size is a
 // multiple of 16, so the 16 positions of a tile share one block.
-//
-// Workgroup = (sequence, row-group, kv-head group, chunk).  Its 4 waves cover
-// H4 = heads_per_wg kv heads x S = 4 / H4 parts of the chunk: wave w serves kv
-// head hg * H4 + w / S on positions [c_begin + (w % S) * 512 / S, + 512 / S).
-// With H4 = 4 (kv heads a multiple of 4) each wave streams one head over the whole
-// chunk and no cross-wave combine is needed; the four waves read neighbouring
-// slices of the same KV blocks at the same time.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
-__global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
+__device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg, int kvh, int chunk,
+                                            int32_t* tbl_lds) {
   using M = Mfma<QT>;
   using Raw = RawSlice<QT, KVT, D>;
   using VQ = ValueQuad<QT, KVT, D>;
   constexpr int NQS = D / 32;  // 32-wide contraction slices
   constexpr int ND = D / 16;   // 16-wide output column tiles (= dims per lane)
   constexpr int KV_ELT = KVT == QT ? 2 : 1;
-  __shared__ MfmaShared<QT, KVT, D, NT> sh;
-
-  const WorkItem wi = work_item(P, blockIdx.x);
-  const int seq = wi.seq;
-  const int rg = wi.rg;
-  const int chunk = wi.chunk;
-  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
   const int grp = lane >> 4;
-  const int S = 4 / P.heads_per_wg;  // waves per kv head (workgroup-uniform)
-  const int head_in_wg = wave / S;
-  const int part = wave - head_in_wg * S;
-  const int kvh = wi.hg * P.heads_per_wg + head_in_wg;
   const int c_begin = chunk * kChunk;
 
-  // Block-table slice of the chunk into LDS (issued before the sequence metadata
-  // is known: the index is clamped into the table and every entry is range
-  // checked, so each stored block id addresses memory inside the pool).
-  for (int i = threadIdx.x; i < kChunk; i += 256) {
+  // Block ids of the chunk's positions (one per tile when blocks hold whole
+  // tiles).  Table indices are clamped into the table and every entry is range
+  // checked, so each stored id addresses memory inside the pool.
+  for (int i = UB ? lane * kTileTok : lane; i < kChunk; i += UB ? 64 * kTileTok : 64) {
     const int idx = min((c_begin + i) / P.block_size, P.table_width - 1);
     const int32_t e = P.tables[(int64_t)seq * P.table_stride + idx];
-    sh.tbl[i] = (e >= 0 && e < P.num_blocks) ? e : 0;
+    tbl_lds[i] = (e >= 0 && e < P.num_blocks) ? e : 0;
   }
+  __builtin_amdgcn_wave_barrier();
 
   SeqView sv = seq_view(P, seq);
   const int rows_total = sv.q_len * P.group;
@@ -434,11 +416,10 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
   row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
   if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
 
-  // Tiles of this wave: absolute 16-aligned positions [w_begin + 16t, +16), t in [t0, t1).
-  const int span = kChunk / S;
-  const int w_begin = c_begin + part * span;
+  // Tiles: absolute 16-aligned positions [c_begin + 16t, +16), t in [t0, t1).
+  const int w_begin = c_begin;
   const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
-  const int span_hi = min(w_begin + span, hi_last);
+  const int span_hi = min(w_begin + kChunk, hi_last);
   // wave-uniform (scalar) bounds: keeps the tile loop free of divergent branches
   const int t0 = __builtin_amdgcn_readfirstlane(
       span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok);
@@ -484,8 +465,6 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
     for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  __syncthreads();  // block-table slice visible to every wave
-
   if (t0 < t1) {
     Raw kb[kStages];
     VQ vq[kStages];
@@ -494,7 +473,7 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
     uint32_t okv[kStages];  // bit i: value position 4 * grp + i is inside the sequence
     const int64_t k_head = (int64_t)kvh * P.k_head_stride + grp * 8;
     const int64_t v_head = (int64_t)kvh * P.v_head_stride + l16 * ND;
-    const int32_t* tbl = sh.tbl - c_begin;  // tbl[pos] for pos in the chunk
+    const int32_t* tbl = tbl_lds - c_begin;  // tbl[pos] for pos in the chunk
     // Loads of tile t into stage b.  Branch-free: every address is inside the
     // pool, and positions outside the sequence are zeroed at use.
     auto issue = [&](int t, int b) {
@@ -533,7 +512,8 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p4 = tb + 4 * grp + r;
-          const int64_t so = (int64_t)tbl[p4] * P.s_block_stride +
+          // with whole tiles per block only the tile's first entry is stored
+          const int64_t so = (int64_t)tbl[UB ? tb : p4] * P.s_block_stride +
                              (int64_t)(p4 % P.block_size) * P.s_token_stride +
                              (int64_t)kvh * P.s_head_stride;
           const bool ok4 = p4 < hi_last;
@@ -646,47 +626,6 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
     }
   }
 
-  // ---- combine the S waves of a kv head, then write the chunk partial.
-  auto publish = [&](int buf) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      if (grp == 0) {
-        sh.ml[buf][nt * 16 + l16][0] = m_run[nt];
-        sh.ml[buf][nt * 16 + l16][1] = l_run[nt];
-      }
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) sh.o[buf][nt * ND + dt][lane] = oacc[nt][dt];
-    }
-  };
-  auto absorb = [&](int buf) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const float m2 = sh.ml[buf][nt * 16 + l16][0];
-      const float l2 = sh.ml[buf][nt * 16 + l16][1];
-      float mo, s1, s2;
-      merge_scales(m_run[nt], m2, mo, s1, s2);
-      m_run[nt] = mo;
-      l_run[nt] = l_run[nt] * s1 + l2 * s2;
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = oacc[nt][dt] * s1 + sh.o[buf][nt * ND + dt][lane] * s2;
-    }
-  };
-  if (S == 4) {  // ((w0 + w2) + (w1 + w3))
-    if (wave >= 2) publish(wave - 2);
-    __syncthreads();
-    if (wave < 2) absorb(wave);
-    __syncthreads();
-    if (wave == 1) publish(0);
-    __syncthreads();
-    if (wave != 0) return;
-    absorb(0);
-  } else if (S == 2) {  // (w0 + w1), (w2 + w3)
-    if (part == 1) publish(head_in_wg);
-    __syncthreads();
-    if (part == 1) return;
-    absorb(head_in_wg);
-  }
-
   // ---- chunk partial for rows whose merge range contains this chunk
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -720,6 +659,106 @@ __global__ __launch_bounds__(256, 2) void rlt_attn_mfma_kernel(AttnParams P) {
       }
     }
   }
+}
+
+// Active chunk range [c0, c1) of (sequence, row-group) pair p: the chunks that
+// hold a position some row of the row-group sees.
+__device__ __forceinline__ void pair_chunks(const AttnParams& P, int p, int& c0, int& c1) {
+  const int seq = p / P.rowgroups;
+  const int rg = p - seq * P.rowgroups;
+  const SeqView sv = seq_view(P, seq);
+  const int rows_total = sv.q_len * P.group;
+  const int rg_begin = rg * P.rows_per_rg;
+  c0 = c1 = 0;
+  if (rg_begin >= rows_total) return;
+  const int rg_rows = min(P.rows_per_rg, rows_total - rg_begin);
+  int lo_first, hi_first, lo_last, hi_last;
+  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
+  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  if (hi_last <= lo_first) return;
+  c0 = lo_first / kChunk;
+  c1 = (hi_last + kChunk - 1) / kChunk;
+}
+
+constexpr int kPersistWaves = 8;     // waves of a persistent workgroup (one per CU)
+constexpr int kMaxPairs = 8192;      // (sequence, row-group) pairs the persistent kernel indexes
+
+struct PersistShared {
+  int32_t first[kMaxPairs + 1];  // units before pair p (prefix sum)
+  int32_t c0[kMaxPairs];         // first active chunk of pair p
+  int32_t tbl[kPersistWaves][kChunk];
+  int32_t wave_total[kPersistWaves];
+};
+
+// Persistent MFMA attention: one 8-wave workgroup per CU.  Every workgroup lists
+// the active units -- (pair, chunk, kv head), kv head fastest -- from the
+// sequence lengths, and wave w of workgroup b takes units b + G (w + 8k) (G =
+// workgroups), so every CU gets the same number of units whatever the mix of
+// sequence lengths (a grid of one workgroup per unit leaves the placement of the
+// busy workgroups to the dispatcher, and CUs end up with 1 to 8 of them).  Each
+// unit's arithmetic is that of attend_unit alone: results do not depend on the
+// assignment.
+template <int QT, int KVT, int D, int NT, int SM, bool UB>
+__global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnParams P) {
+  __shared__ PersistShared sh;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int pairs = P.num_seqs * P.rowgroups;
+  // units per pair, summed per thread over a contiguous run of pairs
+  const int per = (pairs + 64 * kPersistWaves - 1) / (64 * kPersistWaves);
+  const int p_lo = t * per;
+  const int p_hi = min(pairs, p_lo + per);
+  int run = 0;
+  for (int p = p_lo; p < p_hi; ++p) {
+    int c0, c1;
+    pair_chunks(P, p, c0, c1);
+    sh.c0[p] = c0;
+    sh.first[p] = run;  // local prefix for now
+    run += (c1 - c0) * P.hkv;
+  }
+  // exclusive scan of the thread totals: wave scans, then wave offsets
+  int incl = run;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, RLT_WAVE);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) sh.wave_total[wave] = incl;
+  __syncthreads();
+  int base = incl - run;
+  for (int w = 0; w < wave; ++w) base += sh.wave_total[w];
+  for (int p = p_lo; p < p_hi; ++p) sh.first[p] += base;
+  if (t == 64 * kPersistWaves - 1) sh.first[pairs] = base + run;
+  __syncthreads();
+  const int units = sh.first[pairs];
+  const int G = gridDim.x;
+  for (int u = blockIdx.x + G * wave; u < units; u += G * kPersistWaves) {
+    // pair of unit u: the last p with first[p] <= u
+    int lo = 0, hi = pairs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sh.first[mid] <= u) lo = mid;
+      else hi = mid - 1;
+    }
+    const int j = u - sh.first[lo];
+    const int seq = lo / P.rowgroups;
+    const int rg = lo - seq * P.rowgroups;
+    // the kv head is rotated by the chunk so that every XCD (workgroup b runs on
+    // XCD b % 8, and so takes units u = b mod 8) serves every kv head
+    const int cj = j / P.hkv;
+    attend_unit<QT, KVT, D, NT, SM, UB>(P, seq, rg, (j - cj * P.hkv + cj) % P.hkv, sh.c0[lo] + cj,
+                                        sh.tbl[wave]);
+  }
+}
+
+// Fallback for batches with more than kMaxPairs pairs: one single-wave workgroup
+// per (sequence, row-group, kv head, chunk), the same per-unit arithmetic.
+template <int QT, int KVT, int D, int NT, int SM, bool UB>
+__global__ __launch_bounds__(64) void rlt_attn_mfma_grid_kernel(AttnParams P) {
+  __shared__ int32_t tbl[kChunk];
+  const WorkItem wi = work_item(P, blockIdx.x);
+  attend_unit<QT, KVT, D, NT, SM, UB>(P, wi.seq, wi.rg, wi.hg, wi.chunk, tbl);
 }
 
 // ============================================================ vector path
@@ -933,47 +972,88 @@ __global__ __launch_bounds__(256) void rlt_attn_vec_kernel(AttnParams P) {
 
 // ============================================================ merge
 
-// grid (rows, ceil(hq / 4)), 256 threads: one wave per (row, head).  Combines the
-// row's chunks: lane c holds chunk c's (max, sum), the scale exp2(m_c - M) and the
-// normalizer come from fixed-order wave reductions, then every lane accumulates
-// its head dims over the chunks in chunk order.  The order depends only on the
-// row's own chunk range.  reference: triton_attention.py:145-173 (empty rows give
-// zeros; 1e-30 floor).
-template <int OT>
+// grid (sequences x max_q, ceil(hq / 4)), 256 threads: one wave per (row, head).
+// Combines the row's chunks: the (max, sum) of up to kMergeBatch chunks and
+// their head-dim values are loaded together (one memory round trip), the scale
+// exp2(m_c - M) of chunk c comes from lane c, and every lane accumulates its dims
+// over the chunks in chunk order.  The order depends only on the row's own chunk
+// range.  reference: triton_attention.py:145-173 (empty rows give zeros; 1e-30
+// floor).
+constexpr int kMergeBatch = 16;
+
+// Lane c's value of x in every lane (c wave-uniform).
+__device__ __forceinline__ float lane_value(float x, int c) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), c));
+}
+
+// E: head dims per lane (ceil(head_dim / 64)).
+template <int OT, int E>
 __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
-  const int row = blockIdx.x;
   const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (head >= P.hq) return;
   int seq, qi;
   if (P.cu_q) {
-    // seq = (number of sequences s >= 1 with cu[s] <= row), counted 64 at a time
-    // with one load per lane instead of a chain of dependent bisection loads
-    int count = 0;
-    for (int s0 = 1; s0 < P.num_seqs; s0 += 64) {
-      const int s = s0 + lane;
-      const bool le = s < P.num_seqs && P.cu_q[s] <= row;
-      count += __popcll(__builtin_amdgcn_ballot_w64(le));
-      if (!__builtin_amdgcn_ballot_w64(s < P.num_seqs && le && s == s0 + 63)) break;
-    }
-    seq = count;
-    qi = row - P.cu_q[seq];
+    seq = blockIdx.x / P.max_q;
+    qi = blockIdx.x % P.max_q;
   } else {
-    seq = row;
+    seq = blockIdx.x;
     qi = 0;
   }
   const SeqView sv = seq_view(P, seq);
+  if (qi >= sv.q_len) return;
+  const int row = sv.q_begin + qi;
   int lo, hi;
   row_range(P, sv, qi, lo, hi);
   const int c0 = lo / kChunk, c1 = (hi + kChunk - 1) / kChunk;
   const int nc = c1 - c0;
   const int64_t base = ((int64_t)row * P.hq + head) * P.max_chunks + c0;
   const int64_t out_off = (int64_t)row * P.out_row_stride + (int64_t)head * P.out_head_stride;
+  const int D = P.head_dim;
   if (nc <= 0) {
-    for (int d = lane; d < P.head_dim; d += 64) store_from_f32<OT>(P.out, out_off + d, 0.f);
+    for (int d = lane; d < D; d += 64) store_from_f32<OT>(P.out, out_off + d, 0.f);
     return;
   }
-  // chunk statistics, 64 chunks per pass (a row has at most max_chunks)
+  if (nc <= kMergeBatch) {
+    // statistics (lane c) and values (every lane, dims lane + 64e) of all chunks
+    float m = -INFINITY, l = 0.f;
+    if (lane < nc) {
+      m = P.part_ml[2 * (base + lane)];
+      l = P.part_ml[2 * (base + lane) + 1];
+    }
+    float v[kMergeBatch][E];
+#pragma unroll
+    for (int c = 0; c < kMergeBatch; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int d = lane + 64 * e;
+        v[c][e] = (c < nc && d < D) ? P.part_o[(base + c) * D + d] : 0.f;
+      }
+    float mmax = -INFINITY;
+    for (int c = 0; c < nc; ++c) mmax = fmaxf(mmax, lane_value(m, c));
+    const float sc = (lane < nc && m != -INFINITY) ? exp2f(m - mmax) : 0.f;
+    float lsum = 0.f;
+    const float ls = l * sc;
+    for (int c = 0; c < nc; ++c) lsum += lane_value(ls, c);
+    const float inv_den = 1.f / fmaxf(lsum, 1.0e-30f);
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = 0.f;
+    // chunks past nc have scale 0 and values 0: adding them changes nothing
+#pragma unroll
+    for (int c = 0; c < kMergeBatch; ++c) {
+      const float sv = lane_value(sc, c);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] += v[c][e] * sv;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = lane + 64 * e;
+      if (d < D) store_from_f32<OT>(P.out, out_off + d, acc[e] * inv_den);
+    }
+    return;
+  }
+  // long rows: chunk statistics 64 at a time, then values chunk by chunk
   float mmax = -INFINITY;
   for (int c = lane; c < nc; c += 64) mmax = fmaxf(mmax, P.part_ml[2 * (base + c)]);
   for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off, RLT_WAVE));
@@ -1006,7 +1086,7 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int d = lane + 64 * e;
-          v[u][e] = d < P.head_dim ? P.part_o[(base + c0p + c + u) * P.head_dim + d] : 0.f;
+          v[u][e] = d < D ? P.part_o[(base + c0p + c + u) * D + d] : 0.f;
         }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -1020,23 +1100,29 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int d = lane + 64 * e;
-        if (d < P.head_dim) acc[e] += P.part_o[(base + c0p + c) * P.head_dim + d] * s;
+        if (d < D) acc[e] += P.part_o[(base + c0p + c) * D + d] * s;
       }
     }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int d = lane + 64 * e;
-    if (d < P.head_dim) store_from_f32<OT>(P.out, out_off + d, acc[e] * inv_den);
+    if (d < D) store_from_f32<OT>(P.out, out_off + d, acc[e] * inv_den);
   }
 }
 
 // ============================================================ dispatch
 
+template <int QT, int KVT, int D, int SM, bool UB, int NT>
+void launch_mfma_nt(const AttnParams& P, dim3 grid, hipStream_t stream) {
+  if (P.persistent) rlt_attn_mfma_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * kPersistWaves, 0, stream>>>(P);
+  else rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64, 0, stream>>>(P);
+}
+
 template <int QT, int KVT, int D, int SM, bool UB>
 int launch_mfma_ub(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
-  if (nt == 1) rlt_attn_mfma_kernel<QT, KVT, D, 1, SM, UB><<<grid, 256, 0, stream>>>(P);
-  else if (D <= 128) rlt_attn_mfma_kernel<QT, KVT, D, (D <= 128 ? 2 : 1), SM, UB><<<grid, 256, 0, stream>>>(P);
+  if (nt == 1) launch_mfma_nt<QT, KVT, D, SM, UB, 1>(P, grid, stream);
+  else if (D <= 128) launch_mfma_nt<QT, KVT, D, SM, UB, (D <= 128 ? 2 : 1)>(P, grid, stream);
   else return RLT_ERR_UNSUPPORTED;
   return RLT_OK;
 }
@@ -1077,6 +1163,29 @@ int launch_vec_q(const AttnParams& P, int kv_dtype, dim3 grid, hipStream_t strea
     default: return RLT_ERR_ARGUMENT;
   }
   return RLT_OK;
+}
+
+template <int OT>
+void launch_merge(const AttnParams& P, dim3 grid, hipStream_t stream) {
+  switch ((P.head_dim + 63) / 64) {
+    case 1: rlt_merge_kernel<OT, 1><<<grid, 256, 0, stream>>>(P); break;
+    case 2: rlt_merge_kernel<OT, 2><<<grid, 256, 0, stream>>>(P); break;
+    case 3: rlt_merge_kernel<OT, 3><<<grid, 256, 0, stream>>>(P); break;
+    default: rlt_merge_kernel<OT, 4><<<grid, 256, 0, stream>>>(P); break;
+  }
+}
+
+// Compute units of the current device (cached per device).
+int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev < 64) cached[dev] = n;
+  return n;
 }
 
 int max_chunks_for(int32_t table_width, int32_t block_size) {
@@ -1123,6 +1232,7 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
   if (num_blocks <= 0) return RLT_ERR_ARGUMENT;
   if (num_q_rows == 0 || num_seqs == 0) return RLT_OK;
   if (!cu_seqlens_q && num_seqs != num_q_rows) return RLT_ERR_ARGUMENT;
+  if (cu_seqlens_q && max_q_len <= 0) return RLT_ERR_ARGUMENT;
   const size_t need = rlt_paged_attention_workspace_size(num_q_rows, num_q_heads, head_dim,
                                                          table_width, block_size);
   if (!workspace || workspace_bytes < need) return RLT_ERR_WORKSPACE;
@@ -1187,9 +1297,12 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     P.rows_per_rg = 16 * nt;
     P.rowgroups = (rows_per_seq + P.rows_per_rg - 1) / P.rows_per_rg;
     if (P.rowgroups < 1) P.rowgroups = 1;
-    P.heads_per_wg = num_kv_heads % 4 == 0 ? 4 : (num_kv_heads % 2 == 0 ? 2 : 1);
-    P.head_groups = num_kv_heads / P.heads_per_wg;
-    const int64_t wgs = (int64_t)num_seqs * P.rowgroups * P.head_groups * P.max_chunks;
+    // Persistent workgroups, one per CU, unless the pair index does not fit in LDS.
+    P.head_groups = num_kv_heads;
+    const int64_t pairs = (int64_t)num_seqs * P.rowgroups;
+    P.persistent = pairs <= kMaxPairs;
+    int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads * P.max_chunks;
+    if (P.persistent) wgs = compute_units();
     if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
     dim3 grid((unsigned)wgs);
     if (q_dtype == RLT_BF16)
@@ -1202,8 +1315,8 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     P.rows_per_rg = kVecRows;
     P.rowgroups = (rows_per_seq + kVecRows - 1) / kVecRows;
     if (P.rowgroups < 1) P.rowgroups = 1;
-    P.heads_per_wg = 1;
     P.head_groups = num_kv_heads;
+    P.persistent = 0;
     const int64_t wgs = (int64_t)num_seqs * P.rowgroups * P.head_groups * P.max_chunks;
     if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
     dim3 grid((unsigned)wgs);
@@ -1215,11 +1328,14 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     }
   }
   if (st != RLT_OK) return st;
-  dim3 mgrid((unsigned)num_q_rows, (unsigned)((num_q_heads + 3) / 4));
+  P.max_q = cu_seqlens_q ? max_q_len : 1;
+  const int64_t merge_rows = cu_seqlens_q ? (int64_t)num_seqs * max_q_len : num_q_rows;
+  if (merge_rows >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
+  dim3 mgrid((unsigned)merge_rows, (unsigned)((num_q_heads + 3) / 4));
   switch (q_dtype) {
-    case RLT_F32: rlt_merge_kernel<RLT_F32><<<mgrid, 256, 0, stream>>>(P); break;
-    case RLT_F16: rlt_merge_kernel<RLT_F16><<<mgrid, 256, 0, stream>>>(P); break;
-    case RLT_BF16: rlt_merge_kernel<RLT_BF16><<<mgrid, 256, 0, stream>>>(P); break;
+    case RLT_F32: launch_merge<RLT_F32>(P, mgrid, stream); break;
+    case RLT_F16: launch_merge<RLT_F16>(P, mgrid, stream); break;
+    case RLT_BF16: launch_merge<RLT_BF16>(P, mgrid, stream); break;
   }
   return rlt_launch_status();
 }
