@@ -51,6 +51,7 @@ constexpr int kWaves = 4;
 constexpr int kWaveSpan = kChunk / kWaves;  // 128 positions per wave
 constexpr int kTileTok = 16;
 constexpr int kStages = 2;  // KV tiles in flight per wave (MFMA path)
+constexpr int kSplit = 2;   // waves per work unit on the MFMA path (equal position spans)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -376,30 +377,62 @@ __device__ __forceinline__ float group_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// One work unit -- (sequence, row-group, kv head, chunk) -- on one wave: the wave
-// streams the kv head over the whole 512-position chunk for every row of the
-// row-group and writes the chunk partial of those rows.  tbl_lds: this wave's
-// 512-entry LDS slice for the chunk's block ids.
+// Running state of one wave over its part of a unit: the online-softmax
+// accumulators of the row-group's rows (one row per 16-row tile and lane) and
+// what the partial write needs.
+template <int NT, int ND>
+struct UnitState {
+  f32x4 oacc[NT][ND];
+  float m_run[NT], l_run[NT];
+  int row_lo[NT], row_hi[NT];
+  int rg_begin, rg_rows, q_begin;
+  float v_mul;
+  bool active;  // the unit has rows and visible positions in this chunk
+};
+
+// Part `part` (of kSplit equal spans) of one work unit -- (sequence, row-group,
+// kv head, chunk) -- on one wave: the wave streams the kv head over positions
+// [512c + part * 512 / kSplit, + 512 / kSplit) for every row of the row-group.
+// tbl_lds: this wave's 512-entry LDS slice for the chunk's block ids.
 // SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).  UB: block_size is a
 // multiple of 16, so the 16 positions of a tile share one block.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
-__device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg, int kvh, int chunk,
-                                            int32_t* tbl_lds) {
+__device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg, int kvh, int chunk,
+                                            int part, int32_t* tbl_lds,
+                                            UnitState<NT, D / 16>& st) {
   using M = Mfma<QT>;
   using Raw = RawSlice<QT, KVT, D>;
   using VQ = ValueQuad<QT, KVT, D>;
   constexpr int NQS = D / 32;  // 32-wide contraction slices
   constexpr int ND = D / 16;   // 16-wide output column tiles (= dims per lane)
   constexpr int KV_ELT = KVT == QT ? 2 : 1;
+  constexpr int kSpan = kChunk / kSplit;
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
   const int grp = lane >> 4;
   const int c_begin = chunk * kChunk;
+  const int w_begin = c_begin + part * kSpan;
+
+  auto& oacc = st.oacc;
+  auto& m_run = st.m_run;
+  auto& l_run = st.l_run;
+  auto& row_lo = st.row_lo;
+  auto& row_hi = st.row_hi;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+    row_lo[nt] = row_hi[nt] = 0;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  st.active = false;
 
   // Block ids of the chunk's positions (one per tile when blocks hold whole
   // tiles).  Table indices are clamped into the table and every entry is range
   // checked, so each stored id addresses memory inside the pool.
-  for (int i = UB ? lane * kTileTok : lane; i < kChunk; i += UB ? 64 * kTileTok : 64) {
+  for (int i = part * kSpan + (UB ? lane * kTileTok : lane); i < (part + 1) * kSpan;
+       i += UB ? 64 * kTileTok : 64) {
     const int idx = min((c_begin + i) / P.block_size, P.table_width - 1);
     const int32_t e = P.tables[(int64_t)seq * P.table_stride + idx];
     tbl_lds[i] = (e >= 0 && e < P.num_blocks) ? e : 0;
@@ -415,11 +448,14 @@ __device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg
   row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
   row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
   if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
+  st.active = true;
+  st.rg_begin = rg_begin;
+  st.rg_rows = rg_rows;
+  st.q_begin = sv.q_begin;
 
-  // Tiles: absolute 16-aligned positions [c_begin + 16t, +16), t in [t0, t1).
-  const int w_begin = c_begin;
+  // Tiles: absolute 16-aligned positions [w_begin + 16t, +16), t in [t0, t1).
   const int span_lo = max(w_begin, lo_first & ~(kTileTok - 1));
-  const int span_hi = min(w_begin + kChunk, hi_last);
+  const int span_hi = min(w_begin + kSpan, hi_last);
   // wave-uniform (scalar) bounds: keeps the tile loop free of divergent branches
   const int t0 = __builtin_amdgcn_readfirstlane(
       span_lo <= w_begin ? 0 : (span_lo - w_begin) / kTileTok);
@@ -427,7 +463,6 @@ __device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg
       span_hi <= w_begin ? 0 : (span_hi - w_begin + kTileTok - 1) / kTileTok);
 
   // This lane's rows (one per 16-row tile): B operand of S^T = K Q^T.
-  int row_lo[NT], row_hi[NT];
   uint4 qreg[NT][NQS];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -449,20 +484,10 @@ __device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg
   }
 
   float qk_scale = P.qk_scale_log2;
-  float v_mul = 1.f;
+  st.v_mul = 1.f;
   if (SM == 1) {
     qk_scale *= P.k_scale[0];
-    v_mul = P.v_scale[0];
-  }
-
-  f32x4 oacc[NT][ND];
-  float m_run[NT], l_run[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    m_run[nt] = -INFINITY;
-    l_run[nt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.v_mul = P.v_scale[0];
   }
 
   if (t0 < t1) {
@@ -626,21 +651,33 @@ __device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg
     }
   }
 
-  // ---- chunk partial for rows whose merge range contains this chunk
+}
+
+// Chunk partial (max, sum, unnormalized output) of the unit's rows whose merge
+// range contains the chunk.
+template <int D, int NT>
+__device__ __forceinline__ void write_partial(const AttnParams& P, int kvh, int chunk,
+                                              const UnitState<NT, D / 16>& st) {
+  constexpr int ND = D / 16;
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15;
+  const int grp = lane >> 4;
+  const auto& oacc = st.oacc;
+  const float v_mul = st.v_mul;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int r_local = nt * 16 + l16;
-    if (r_local >= rg_rows) continue;
-    const int lo_c = row_lo[nt] / kChunk;
-    const int hi_c = (row_hi[nt] + kChunk - 1) / kChunk;
+    if (r_local >= st.rg_rows) continue;
+    const int lo_c = st.row_lo[nt] / kChunk;
+    const int hi_c = (st.row_hi[nt] + kChunk - 1) / kChunk;
     if (chunk < lo_c || chunk >= hi_c) continue;
-    const int rho = rg_begin + r_local;
-    const int qrow = sv.q_begin + rho / P.group;
+    const int rho = st.rg_begin + r_local;
+    const int qrow = st.q_begin + rho / P.group;
     const int head = kvh * P.group + rho % P.group;
     const int64_t slot = ((int64_t)qrow * P.hq + head) * P.max_chunks + chunk;
     if (grp == 0) {
-      P.part_ml[2 * slot] = m_run[nt];
-      P.part_ml[2 * slot + 1] = l_run[nt];
+      P.part_ml[2 * slot] = st.m_run[nt];
+      P.part_ml[2 * slot + 1] = st.l_run[nt];
     }
     float* po = P.part_o + slot * D;
     // accumulator element r of column tile dt is dim ND * (4 * grp + r) + dt
@@ -658,6 +695,45 @@ __device__ __forceinline__ void attend_unit(const AttnParams& P, int seq, int rg
           *(float2*)(dst + d2) = make_float2(oacc[nt][d2][r] * v_mul, oacc[nt][d2 + 1][r] * v_mul);
       }
     }
+  }
+}
+
+// LDS hand-over of a part's state to the wave that owns the unit.
+template <int NT, int ND>
+struct PartBuffer {
+  f32x4 o[NT * ND][64];
+  float ml[NT * 16][2];
+};
+
+template <int NT, int ND>
+__device__ __forceinline__ void publish_part(const UnitState<NT, ND>& st, PartBuffer<NT, ND>& buf) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    if (lane < 16) {
+      buf.ml[nt * 16 + lane][0] = st.m_run[nt];
+      buf.ml[nt * 16 + lane][1] = st.l_run[nt];
+    }
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) buf.o[nt * ND + dt][lane] = st.oacc[nt][dt];
+  }
+}
+
+// st = st (+) buffer, in that operand order.
+template <int NT, int ND>
+__device__ __forceinline__ void absorb_part(UnitState<NT, ND>& st, const PartBuffer<NT, ND>& buf) {
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float m2 = buf.ml[nt * 16 + l16][0];
+    const float l2 = buf.ml[nt * 16 + l16][1];
+    float mo, s1, s2;
+    merge_scales(st.m_run[nt], m2, mo, s1, s2);
+    st.m_run[nt] = mo;
+    st.l_run[nt] = st.l_run[nt] * s1 + l2 * s2;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) st.oacc[nt][dt] = st.oacc[nt][dt] * s1 + buf.o[nt * ND + dt][lane] * s2;
   }
 }
 
@@ -681,29 +757,55 @@ __device__ __forceinline__ void pair_chunks(const AttnParams& P, int p, int& c0,
 }
 
 constexpr int kPersistWaves = 8;     // waves of a persistent workgroup (one per CU)
+constexpr int kSlots = kPersistWaves / kSplit;  // units a persistent workgroup runs at once
 constexpr int kMaxPairs = 8192;      // (sequence, row-group) pairs the persistent kernel indexes
 
+template <int NT, int ND>
 struct PersistShared {
   int32_t first[kMaxPairs + 1];  // units before pair p (prefix sum)
   int32_t c0[kMaxPairs];         // first active chunk of pair p
   int32_t tbl[kPersistWaves][kChunk];
+  PartBuffer<NT, ND> part[kSplit > 1 ? kSlots : 1][kSplit > 1 ? kSplit / 2 : 1];
   int32_t wave_total[kPersistWaves];
 };
 
+// Unit u of the persistent list -> (sequence, row-group, kv head, chunk).
+__device__ __forceinline__ void unit_of(const AttnParams& P, const int32_t* first, const int32_t* c0s,
+                                        int pairs, int u, int& seq, int& rg, int& kvh, int& chunk) {
+  // pair of unit u: the last p with first[p] <= u
+  int lo = 0, hi = pairs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (first[mid] <= u) lo = mid;
+    else hi = mid - 1;
+  }
+  const int j = u - first[lo];
+  seq = lo / P.rowgroups;
+  rg = lo - seq * P.rowgroups;
+  // the kv head is rotated by the chunk so that every XCD (workgroup b runs on
+  // XCD b % 8, and so takes units u = b mod 8) serves every kv head
+  const int cj = j / P.hkv;
+  kvh = (j - cj * P.hkv + cj) % P.hkv;
+  chunk = c0s[lo] + cj;
+}
+
 // Persistent MFMA attention: one 8-wave workgroup per CU.  Every workgroup lists
-// the active units -- (pair, chunk, kv head), kv head fastest -- from the
-// sequence lengths, and wave w of workgroup b takes units b + G (w + 8k) (G =
-// workgroups), so every CU gets the same number of units whatever the mix of
-// sequence lengths (a grid of one workgroup per unit leaves the placement of the
-// busy workgroups to the dispatcher, and CUs end up with 1 to 8 of them).  Each
-// unit's arithmetic is that of attend_unit alone: results do not depend on the
-// assignment.
+// the active units -- (pair, chunk, kv head) -- from the sequence lengths, and
+// workgroup b takes units b, b + G, b + 2G, ... (G = workgroups), so every CU
+// gets the same number of units whatever the mix of sequence lengths (a grid of
+// one workgroup per unit leaves the placement of the busy workgroups to the
+// dispatcher, and CUs end up with 1 to 8 of them).  kSlots units run at a time,
+// each on kSplit waves that split its positions and combine through LDS in a
+// fixed order, so a unit's arithmetic never depends on the assignment.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
 __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnParams P) {
-  __shared__ PersistShared sh;
+  constexpr int ND = D / 16;
+  __shared__ PersistShared<NT, ND> sh;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
+  const int slot = wave / kSplit;
+  const int part = wave - slot * kSplit;
   const int pairs = P.num_seqs * P.rowgroups;
   // units per pair, summed per thread over a contiguous run of pairs
   const int per = (pairs + 64 * kPersistWaves - 1) / (64 * kPersistWaves);
@@ -733,32 +835,50 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
   __syncthreads();
   const int units = sh.first[pairs];
   const int G = gridDim.x;
-  for (int u = blockIdx.x + G * wave; u < units; u += G * kPersistWaves) {
-    // pair of unit u: the last p with first[p] <= u
-    int lo = 0, hi = pairs - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (sh.first[mid] <= u) lo = mid;
-      else hi = mid - 1;
+  const int mine = (int)blockIdx.x < units ? (units - (int)blockIdx.x + G - 1) / G : 0;
+  const int rounds = (mine + kSlots - 1) / kSlots;  // the same in every wave
+  for (int r = 0; r < rounds; ++r) {
+    const int k = slot + kSlots * r;  // this slot's unit: the k-th of the workgroup
+    const int u = (int)blockIdx.x + G * k;
+    UnitState<NT, ND> st;
+    int seq = 0, rg = 0, kvh = 0, chunk = 0;
+    if (k < mine) {
+      unit_of(P, sh.first, sh.c0, pairs, u, seq, rg, kvh, chunk);
+      attend_span<QT, KVT, D, NT, SM, UB>(P, seq, rg, kvh, chunk, part, sh.tbl[wave], st);
+    } else {
+      st.active = false;
     }
-    const int j = u - sh.first[lo];
-    const int seq = lo / P.rowgroups;
-    const int rg = lo - seq * P.rowgroups;
-    // the kv head is rotated by the chunk so that every XCD (workgroup b runs on
-    // XCD b % 8, and so takes units u = b mod 8) serves every kv head
-    const int cj = j / P.hkv;
-    attend_unit<QT, KVT, D, NT, SM, UB>(P, seq, rg, (j - cj * P.hkv + cj) % P.hkv, sh.c0[lo] + cj,
-                                        sh.tbl[wave]);
+    // tree combine of the unit's parts: part p absorbs part p + h, h = kSplit/2 .. 1
+#pragma unroll
+    for (int h = kSplit / 2; h >= 1; h /= 2) {
+      if (part >= h && part < 2 * h && st.active) publish_part(st, sh.part[slot][part - h]);
+      __syncthreads();
+      if (part < h && st.active) absorb_part(st, sh.part[slot][part]);
+      __syncthreads();  // the buffers are reused by the next level / round
+    }
+    if (part == 0 && st.active) write_partial<D, NT>(P, kvh, chunk, st);
   }
 }
 
-// Fallback for batches with more than kMaxPairs pairs: one single-wave workgroup
+// Fallback for batches with more than kMaxPairs pairs: one kSplit-wave workgroup
 // per (sequence, row-group, kv head, chunk), the same per-unit arithmetic.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
-__global__ __launch_bounds__(64) void rlt_attn_mfma_grid_kernel(AttnParams P) {
-  __shared__ int32_t tbl[kChunk];
+__global__ __launch_bounds__(64 * kSplit) void rlt_attn_mfma_grid_kernel(AttnParams P) {
+  constexpr int ND = D / 16;
+  __shared__ int32_t tbl[kSplit][kChunk];
+  __shared__ PartBuffer<NT, ND> buf[kSplit > 1 ? kSplit / 2 : 1];
+  const int part = threadIdx.x >> 6;
   const WorkItem wi = work_item(P, blockIdx.x);
-  attend_unit<QT, KVT, D, NT, SM, UB>(P, wi.seq, wi.rg, wi.hg, wi.chunk, tbl);
+  UnitState<NT, ND> st;
+  attend_span<QT, KVT, D, NT, SM, UB>(P, wi.seq, wi.rg, wi.hg, wi.chunk, part, tbl[part], st);
+#pragma unroll
+  for (int h = kSplit / 2; h >= 1; h /= 2) {
+    if (part >= h && part < 2 * h && st.active) publish_part(st, buf[part - h]);
+    __syncthreads();
+    if (part < h && st.active) absorb_part(st, buf[part]);
+    __syncthreads();
+  }
+  if (part == 0 && st.active) write_partial<D, NT>(P, wi.hg, wi.chunk, st);
 }
 
 // ============================================================ vector path
@@ -1116,7 +1236,7 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
 template <int QT, int KVT, int D, int SM, bool UB, int NT>
 void launch_mfma_nt(const AttnParams& P, dim3 grid, hipStream_t stream) {
   if (P.persistent) rlt_attn_mfma_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * kPersistWaves, 0, stream>>>(P);
-  else rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64, 0, stream>>>(P);
+  else rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * kSplit, 0, stream>>>(P);
 }
 
 template <int QT, int KVT, int D, int SM, bool UB>
