@@ -115,6 +115,43 @@ size_t rlt_row_mass_workspace_size(int64_t rows, int64_t vocab);
 int rlt_row_mass_f32(const float* x, int64_t rows, int64_t vocab, float* out, void* workspace,
                      size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Temperature / strict top-k / strict top-p distributions of logits rows.
+ * Replaces vllm_rlt/worker/speculative_sampling.py:8-56 batched_probabilities
+ * (row form vllm_rlt/worker/sampler.py:28-55 Sampler.probabilities).
+ *   logits [n, V] (RLT_F32 / RLT_BF16 / RLT_F16, row stride in elements),
+ *   temperature fp32 [n] (> 0), top_k int64 [n], top_p fp32 [n]
+ *   -> out fp32 [n, V] (row stride out_stride).
+ * Row i: x = logits / T; if max_top_k > 0 and 0 < top_k[i] < V, only the
+ * min(top_k[i], max_top_k) largest x survive (ties at the cut: lowest columns);
+ * if apply_top_p and top_p[i] < 1, survivors are kept in descending order while
+ * the softmax mass before them is <= top_p[i] (the token crossing the threshold is
+ * kept); then softmax over the kept set.  max_top_k and apply_top_p are the host
+ * plan's values, as in the reference.  Rows holding NaN (or with a non-finite
+ * max) are written as NaN.  No workspace; V <= 262144.
+ */
+int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t row_stride,
+                              int64_t n, int64_t vocab, const float* temperature,
+                              const int64_t* top_k, const float* top_p, int64_t max_top_k,
+                              int32_t apply_top_p, float* out, int64_t out_stride,
+                              hipStream_t stream);
+
+/*
+ * Greedy verify round: targets = argmax of every verify row (first maximal column,
+ * NaN counts as the maximum), accepted = number of leading drafts j < drafts[r]
+ * with draft_tokens[r, j] == targets[r, j], next_token = targets[r, accepted].
+ * Replaces the device greedy round of vllm_rlt/worker/async_speculative.py:706-720
+ * (host rule vllm_rlt/worker/speculative.py:41-53 greedy_accept).
+ *   draft_tokens int64 [n, w1], drafts int64 [n],
+ *   target_logits [n, w1 + 1, V] (RLT_F32 / RLT_BF16 / RLT_F16; row stride in
+ *   elements between consecutive verify rows) -> targets int64 [n, w1 + 1],
+ *   accepted int64 [n], next_token int64 [n].  No workspace.
+ */
+int rlt_greedy_accept(const int64_t* draft_tokens, const int64_t* drafts, const void* target_logits,
+                      int32_t logits_dtype, int64_t row_stride, int64_t n, int32_t w1,
+                      int64_t vocab, int64_t* targets, int64_t* accepted, int64_t* next_token,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

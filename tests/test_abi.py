@@ -76,3 +76,42 @@ def test_host_api_validates_before_touching_a_device(pkg):
         pkg.categorical(torch.zeros(2, 4), torch.zeros(2))  # CPU tensors are refused
     with pytest.raises(ValueError, match="window"):
         pkg.MI355XPagedAttention().windowed(None, None, None, None, None, 0)
+
+
+def test_probability_and_greedy_entry_points_check_arguments(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null, fake = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    # negative rows / row stride below V -> RLT_ERR_ARGUMENT (1)
+    assert lib.rlt_batched_probabilities(null, 0, 10, -1, 10, null, null, null, 0, 0, null, 10,
+                                         null) == 1
+    assert lib.rlt_batched_probabilities(fake, 0, 5, 2, 10, fake, fake, fake, 0, 0, fake, 10,
+                                         null) == 1
+    # zero rows: nothing to launch
+    assert lib.rlt_batched_probabilities(null, 0, 10, 0, 10, null, null, null, 0, 0, null, 10,
+                                         null) == 0
+    # missing pointers -> 1; V above 262144 -> RLT_ERR_UNSUPPORTED (2); fp8 logits -> 2
+    assert lib.rlt_batched_probabilities(null, 0, 10, 2, 10, fake, fake, fake, 0, 0, fake, 10,
+                                         null) == 1
+    big = 262144 + 1
+    assert lib.rlt_batched_probabilities(fake, 0, big, 2, big, fake, fake, fake, 0, 0, fake, big,
+                                         null) == 2
+    assert lib.rlt_batched_probabilities(fake, 3, 10, 2, 10, fake, fake, fake, 0, 0, fake, 10,
+                                         null) == 2
+    assert lib.rlt_greedy_accept(null, null, null, 0, 10, -1, 4, 10, null, null, null, null) == 1
+    assert lib.rlt_greedy_accept(fake, fake, fake, 0, 5, 2, 4, 10, fake, fake, fake, null) == 1
+    assert lib.rlt_greedy_accept(fake, fake, fake, 3, 10, 2, 4, 10, fake, fake, fake, null) == 2
+    assert lib.rlt_greedy_accept(null, null, null, 0, 10, 0, 4, 10, null, null, null, null) == 0
+
+
+def test_probability_host_api_refuses_cpu_tensors(pkg):
+    import torch
+
+    x = torch.zeros(2, 8)
+    with pytest.raises(ValueError):
+        pkg.batched_probabilities(x, torch.ones(2), torch.zeros(2, dtype=torch.long),
+                                  torch.ones(2), max_top_k=0, apply_top_p=False)
+    with pytest.raises(ValueError):
+        pkg.greedy_accept_batched(torch.zeros(2, 4, dtype=torch.long),
+                                  torch.zeros(2, dtype=torch.long), torch.zeros(2, 5, 8))

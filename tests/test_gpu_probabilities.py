@@ -1,0 +1,289 @@
+"""gfx950 sampling distributions (batched_probabilities) and the device greedy round.
+
+Parity bar: probabilities within atol 1e-6 / rtol 1e-5 of the torch-CPU oracle (the
+tolerance of the reference's own test, tests/test_speculative_sampling.py:44-60).
+The top-p cut is pinned to exact arithmetic: the kernel decides it on fixed-point
+masses, and its kept count must equal the float64 cut.  torch's float32 softmax sums
+to 1 + d (|d| ~ 1e-5 at V = 65536), so its own cut may differ from the exact one by a
+few tail tokens; the support may differ from the oracle's only there.  Tokens tied at a top-k / top-p cut survive in column
+order on the GPU; the reference leaves that choice unspecified, so tie cases are
+checked by count and value.  The greedy round (argmax + prefix match) is bit-exact.
+"""
+
+import sys
+import zlib
+
+import pytest
+import torch
+
+from oracle import sampling as osamp
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-6, 1e-5
+
+
+def _say(*args):
+    print("[case]", *args, flush=True)
+    sys.stdout.flush()
+
+
+def _host_args(top_k, top_p, vocab):
+    # reference: tests/test_speculative_sampling.py:15-21
+    eff = [int(k) for k in top_k if 0 < int(k) < vocab]
+    return {"max_top_k": max(eff, default=0), "apply_top_p": any(float(p) < 1 for p in top_p)}
+
+
+def _run(pkg, dev, logits, temperature, top_k, top_p, **plan):
+    vocab = logits.shape[-1]
+    t = torch.as_tensor(temperature, dtype=torch.float32)
+    k = torch.as_tensor(top_k, dtype=torch.int64)
+    p = torch.as_tensor(top_p, dtype=torch.float32)
+    plan = plan or _host_args(k.tolist(), p.tolist(), vocab)
+    got = pkg.batched_probabilities(logits.to(dev), t.to(dev), k.to(dev), p.to(dev), **plan).cpu()
+    want = osamp.batched_probabilities(logits, t, k, p, **plan)
+    return got, want, t, k, p, plan
+
+
+def _filtered_logits(logits_row, t, k, plan):
+    """x = logits / T after the reference's top-k step (torch, as the oracle)."""
+    x = logits_row.float() / t
+    vocab = x.shape[-1]
+    if plan["max_top_k"] > 0 and 0 < k < vocab:
+        vals, idx = x.topk(min(k, plan["max_top_k"]))
+        x = torch.full_like(x, -torch.inf).scatter_(0, idx, vals)
+    return x
+
+
+def _exact_kept(sx, top_p):
+    """Top-p kept count of a descending row in float64 (the exact decision the kernel's
+    fixed-point masses reproduce), with the preceding mass of every position."""
+    fin = torch.isfinite(sx)
+    e = torch.zeros(sx.shape, dtype=torch.float64)
+    e[fin] = (sx[fin].double() - sx[0].double()).exp()
+    before = (e.cumsum(0) - e) / e.sum()
+    kept = max(1, int((before <= top_p).sum()))
+    return min(kept, int(fin.sum()) if top_p > 0 else 1), before
+
+
+def _assert_match(got, want, logits, t, k, p, plan):
+    """Tie-invariant comparison.
+
+    * The kept set must be a top set of x (as a multiset of values).
+    * Rows with top-p: its size must equal the float64 exact cut (up to positions
+      whose preceding mass is within 1e-9 of p), and may differ from torch's only at
+      positions within torch's own error: its fp32 softmax sums to 1 + d, |d| up to
+      ~1e-5 at V = 65536, which shifts every cumulative value it compares with p.
+    * Probabilities match position by position when the supports agree, else as
+      sorted values (tied tokens permuted)."""
+    assert got.dtype == torch.float32 and got.shape == want.shape
+    for i in range(got.shape[0]):
+        g, w = got[i], want[i]
+        gs, ws = g > 0, w > 0
+        x = _filtered_logits(logits[i], t[i], int(k[i]), plan)
+        sx = x.sort(descending=True).values
+        gc, wc = int(gs.sum()), int(ws.sum())
+        top_p = float(p[i])
+        if plan["apply_top_p"] and top_p < 1 and bool(torch.isfinite(sx[0])):
+            ec, before = _exact_kept(sx, top_p)
+            if gc != ec:
+                lo, hi = min(gc, ec), max(gc, ec)
+                assert ((before[lo:hi] - top_p).abs() <= 1e-9).all(), f"row {i}: {gc} vs exact {ec}"
+        if torch.equal(gs, ws):
+            torch.testing.assert_close(g, w, atol=ATOL, rtol=RTOL)
+            continue
+        assert torch.equal(x[gs].sort(descending=True).values, sx[:gc]), f"row {i}: not a top set"
+        if gc != wc:
+            assert plan["apply_top_p"] and top_p < 1, f"row {i}: {gc} vs {wc} kept"
+            sm = sx.softmax(-1)
+            band = 2 * abs(sm.double().sum().item() - 1) + 1e-6
+            tb = sm.cumsum(-1) - sm
+            lo, hi = min(gc, wc), max(gc, wc)
+            assert ((tb[lo:hi] - top_p).abs() <= band).all(), f"row {i}: {gc} vs torch {wc}"
+            continue
+        torch.testing.assert_close(g.sort().values, w.sort().values, atol=ATOL, rtol=RTOL)
+
+
+# ------------------------------------------------------------ reference known answers
+
+def test_closed_form_filters(pkg, dev):
+    # reference: tests/test_speculative.py:474-490
+    _say("closed forms")
+    logits = torch.tensor([[0.50, 0.25, 0.15, 0.10]]).log()
+    got, *_ = _run(pkg, dev, logits, [1.0], [-1], [0.8])
+    torch.testing.assert_close(got[0], torch.tensor([0.50, 0.25, 0.15, 0]) / 0.9)
+    got, *_ = _run(pkg, dev, logits, [0.5], [2], [1.0])
+    torch.testing.assert_close(got[0], torch.tensor([0.8, 0.2, 0, 0]))
+    got, *_ = _run(pkg, dev, torch.zeros(1, 4), [1.0], [1], [1.0])
+    assert int((got > 0).sum()) == 1
+    torch.testing.assert_close(got[got > 0], torch.ones(1))
+
+
+def test_matches_row_by_row_sampler(pkg, dev):
+    # reference: tests/test_speculative_sampling.py:44-60
+    _say("row-by-row matrix")
+    vocab = 17
+    g = torch.Generator().manual_seed(0)
+    top_ks = [-1, 1, 3, vocab, vocab + 5]
+    top_ps = [1.0, 0.9, 0.5]
+    temps = [0.5, 0.8, 1.0, 1.5, 2.0]
+    tk = [top_ks[i % 5] for i in range(30)]
+    tp = [top_ps[(i // 5) % 3] for i in range(30)]
+    tt = [temps[(i * 3) % 5] for i in range(30)]
+    logits = torch.randn(30, vocab, generator=g) * 3
+    got, want, t, k, p, plan = _run(pkg, dev, logits, tt, tk, tp)
+    rows = torch.stack([osamp.sampler_probabilities(logits[i], tt[i], tk[i], tp[i])
+                        for i in range(30)])
+    torch.testing.assert_close(want, rows, atol=ATOL, rtol=RTOL)
+    _assert_match(got, want, logits, t, k, p, plan)
+    torch.testing.assert_close(got.sum(-1), torch.ones(30), atol=1e-6, rtol=0)
+
+
+def test_top_k_is_strict_with_ties(pkg, dev):
+    # reference: tests/test_speculative_sampling.py:63-86
+    _say("strict top-k ties")
+    got, *_ = _run(pkg, dev, torch.tensor([[5.0, 4.0, 4.0, 1.0]]), [1.0], [2], [1.0])
+    probs = got[0]
+    assert (probs > 0).sum().item() == 2 and probs[0] > 0 and probs[3] == 0
+    assert (probs[1] > 0) != (probs[2] > 0)
+    kept = 1 if probs[1] > 0 else 2
+    torch.testing.assert_close(probs[[0, kept]], torch.tensor([5.0, 4.0]).softmax(-1))
+    got, *_ = _run(pkg, dev, torch.zeros(1, 6), [1.0], [2], [1.0])
+    assert (got[0] > 0).sum().item() == 2
+
+
+def test_top_p_one_row_keeps_full_support(pkg, dev):
+    # reference: tests/test_speculative_sampling.py:89-99
+    _say("top_p = 1 next to top_p < 1")
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn(2, 64, generator=g) * 2
+    got, want, t, k, p, plan = _run(pkg, dev, logits, [1.0, 1.0], [-1, -1], [1.0, 0.5])
+    assert (got[0] > 0).all() and (got[1] > 0).sum() < 64
+    torch.testing.assert_close(got[0], logits[0].softmax(-1), atol=ATOL, rtol=RTOL)
+    _assert_match(got, want, logits, t, k, p, plan)
+
+
+# ------------------------------------------------------------ seeded parity
+
+@pytest.mark.parametrize("name,n,vocab,temperature,top_p,dtype", [
+    ("config1-q", 32, 49152, 1.0, 1.0, torch.float32),
+    ("config3-p", 160, 49152, 0.7, 0.9, torch.float32),
+    ("config3-bf16", 64, 49152, 0.7, 0.9, torch.bfloat16),
+    ("config4", 40, 65536, 1.0, 1.0, torch.float32),
+    ("config5-p", 40, 65536, 1.0, 0.9, torch.float16),
+])
+def test_config_shaped_parity(pkg, dev, name, n, vocab, temperature, top_p, dtype):
+    _say("config", name)
+    g = torch.Generator().manual_seed(zlib.crc32(name.encode()))
+    logits = (torch.randn(n, vocab, generator=g) * 3).to(dtype)
+    got, want, t, k, p, plan = _run(pkg, dev, logits, [temperature] * n, [-1] * n, [top_p] * n)
+    _assert_match(got, want, logits, t, k, p, plan)
+
+
+@pytest.mark.parametrize("vocab", [1, 2, 17, 1000, 1024, 1025, 4096, 4097, 16384, 16385, 32768,
+                                   32769, 49152, 65536, 65537, 131072 + 3])
+def test_mixed_filters_across_vocab_sizes(pkg, dev, vocab):
+    """Every row placement (registers, registers + LDS, re-reading) with a mix of
+    temperatures, top-k (including k >= V and k <= 0) and top-p per row."""
+    _say("mixed filters V", vocab)
+    g = torch.Generator().manual_seed(vocab)
+    n = 12
+    logits = torch.randn(n, vocab, generator=g) * torch.tensor([0.5, 2, 4, 8] * 3)[:, None]
+    tt = [0.5, 0.7, 1.0, 1.3, 2.0, 0.9, 1.0, 0.6, 1.1, 0.8, 1.0, 3.0]
+    tk = [-1, 1, 5, 40, vocab, vocab + 3, 0, 1000, 7, -1, 2, 300]
+    tp = [1.0, 0.9, 0.5, 0.95, 0.3, 1.0, 0.99, 0.9, 0.0, 0.999, 0.6, 0.8]
+    got, want, t, k, p, plan = _run(pkg, dev, logits, tt, tk, tp)
+    _assert_match(got, want, logits, t, k, p, plan)
+
+
+def test_inconsistent_plan_follows_reference(pkg, dev):
+    """max_top_k below a row's k keeps max_top_k tokens; apply_top_p=False skips top-p
+    for every row (reference: speculative_sampling.py:39-55)."""
+    _say("host plan semantics")
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(4, 5000, generator=g) * 2
+    got, want, t, k, p, plan = _run(pkg, dev, logits, [1.0] * 4, [50, 10, -1, 4000],
+                                    [0.5, 0.9, 0.7, 1.0], max_top_k=20, apply_top_p=False)
+    assert [(got[i] > 0).sum().item() for i in range(4)] == [20, 10, 5000, 20]
+    _assert_match(got, want, logits, t, k, p, plan)
+
+
+def test_ties_and_degenerate_rows(pkg, dev):
+    _say("ties / -inf / NaN rows")
+    vocab = 6000
+    logits = torch.zeros(6, vocab)
+    logits[1, ::2] = -torch.inf                 # masked vocabulary, k beyond the finite count
+    logits[2, :3] = 4.0                          # three-way tie at the top
+    logits[3] = torch.arange(vocab) % 7          # large tie groups
+    logits[4, 17] = float("nan")                 # NaN row
+    logits[5, :] = -torch.inf                    # no finite logit
+    tk = [3, 4000, 2, 1000, -1, -1]
+    tp = [0.45, 1.0, 1.0, 0.5, 0.9, 0.9]
+    got, want, *_ = _run(pkg, dev, logits, [1.0] * 6, tk, tp)
+    # row 0: uniform; top-k keeps 3, top-p 0.45 then keeps the two whose preceding
+    # mass (0, 1/3) is <= 0.45
+    assert (got[0] > 0).sum().item() == 2
+    torch.testing.assert_close(got[0][got[0] > 0], torch.full((2,), 0.5))
+    # row 1: 3000 finite zeros survive top-k 4000 (the -inf picks carry no mass)
+    assert (got[1] > 0).sum().item() == 3000
+    torch.testing.assert_close(got[1][got[1] > 0], torch.full((3000,), 1 / 3000))
+    # row 2: exactly two of the three tied maxima, in column order on the GPU
+    assert (got[2] > 0).sum().item() == 2 and got[2, 0] > 0 and got[2, 1] > 0
+    # row 3: top-k 1000 keeps the 857 sixes and 143 fives; top-p 0.5 ends inside the
+    # sixes: floor(0.5 (857 + 143 / e)) + 1 = 455 of them, as many as torch keeps
+    assert (got[3] > 0).sum().item() == 455 == (want[3] > 0).sum().item()
+    assert (got[3] > 0).nonzero().flatten().tolist() == list(range(6, 7 * 455, 7))
+    assert torch.isnan(got[4]).all() and torch.isnan(got[5]).all()
+
+
+def test_strided_logits_and_inputs_unchanged(pkg, dev):
+    _say("strided logits")
+    g = torch.Generator().manual_seed(11)
+    big = torch.randn(8, 3000, generator=g).to(dev)
+    view = big[:, 100:2148]                      # row stride 3000, V = 2048
+    snap = big.clone()
+    t = torch.full((8,), 0.8, device=dev)
+    k = torch.full((8,), 50, dtype=torch.int64, device=dev)
+    p = torch.full((8,), 0.9, device=dev)
+    got = pkg.batched_probabilities(view, t, k, p, max_top_k=50, apply_top_p=True).cpu()
+    want = osamp.batched_probabilities(view.cpu(), t.cpu(), k.cpu(), p.cpu(), max_top_k=50,
+                                       apply_top_p=True)
+    assert torch.equal(big, snap)
+    _assert_match(got, want, view.cpu(), t.cpu(), k.cpu(), p.cpu(),
+                  {"max_top_k": 50, "apply_top_p": True})
+
+
+def test_shape_errors(pkg, dev):
+    x = torch.zeros(3, 10, device=dev)
+    t = torch.ones(3, device=dev)
+    k = torch.zeros(3, dtype=torch.int64, device=dev)
+    with pytest.raises(ValueError):
+        pkg.batched_probabilities(x[0], t, k, t, max_top_k=0, apply_top_p=False)
+    with pytest.raises(ValueError):
+        pkg.batched_probabilities(x, t[:2], k, t, max_top_k=0, apply_top_p=False)
+    with pytest.raises(ValueError):
+        pkg.batched_probabilities(x, t, k, t, max_top_k=-1, apply_top_p=False)
+
+
+# ------------------------------------------------------------ greedy round
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("vocab", [5, 1000, 49152, 65536])
+def test_greedy_round_bit_exact(pkg, dev, dtype, vocab):
+    _say("greedy", dtype, vocab)
+    g = torch.Generator().manual_seed(vocab)
+    n, w1 = 48, 4
+    logits = torch.randn(n, w1 + 1, vocab, generator=g).to(dtype)
+    # integer logits on some rows force ties (first column must win); NaN rows win at NaN
+    logits[::5] = torch.randint(0, 3, (len(range(0, n, 5)), w1 + 1, vocab), generator=g).to(dtype)
+    logits[7, 2, vocab // 2] = float("nan")
+    logits[7, 2, vocab - 1] = float("nan")
+    targets = logits.float().argmax(-1)
+    draft = torch.where(torch.rand(n, w1, generator=g) < 0.75, targets[:, :w1],
+                        torch.randint(0, vocab, (n, w1), generator=g))
+    drafts = torch.randint(0, w1 + 1, (n,), generator=g)
+    want = osamp.greedy_accept_batched(draft, drafts, logits.float())
+    got = pkg.greedy_accept_batched(draft.to(dev), drafts.to(dev), logits.to(dev))
+    for a, b in zip(got, want):
+        assert torch.equal(a.cpu(), b)
+    assert got[0][7, 2].item() == vocab // 2

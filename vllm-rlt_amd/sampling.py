@@ -1,8 +1,10 @@
-"""MI355X acceptance sampler behind the reference sampler API.
+"""MI355X sampling distributions and acceptance sampler behind the reference sampler API.
 
 Same signatures, dtypes, shape errors and flag-not-raise conventions as
-vllm_rlt/worker/speculative_sampling.py (``categorical`` :59-85,
-``AcceptResult`` :88-101, ``speculative_accept`` :104-181); results are
+vllm_rlt/worker/speculative_sampling.py (``batched_probabilities`` :8-56,
+``categorical`` :59-85, ``AcceptResult`` :88-101, ``speculative_accept``
+:104-181), plus the device greedy round of vllm_rlt/worker/async_speculative.py:706-720
+(``greedy_accept_batched``).  Acceptance and categorical results are
 bit-exact with the reference's torch-CPU arithmetic when fed identical fp32
 probabilities and uniforms.  Every call enqueues gfx950 kernels on the current
 stream without host synchronization; inputs are never modified.
@@ -32,6 +34,85 @@ def _f32(t):
 def _i64(t):
     t = t if t.dtype == torch.int64 else t.long()
     return t if t.is_contiguous() else t.contiguous()
+
+
+_LOGIT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _rows(t):
+    """Logits with unit column stride (row stride free), in a supported dtype."""
+    if t.dtype not in _LOGIT_DTYPES:
+        t = t.float()
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def batched_probabilities(logits, temperature, top_k, top_p, *, max_top_k, apply_top_p):
+    """Temperature / strict top-k / top-p distribution of every row as ``[n, V]`` float32.
+
+    reference: vllm_rlt/worker/speculative_sampling.py:8-56.  ``max_top_k`` and
+    ``apply_top_p`` come from the host plan (no host synchronization happens here).
+    Tokens tied at a top-k or top-p cut survive in column order (the reference
+    leaves the surviving index of a tie unspecified).
+    """
+    if logits.ndim != 2:
+        raise ValueError("logits must be a 2-D [n, V] tensor")
+    n, vocab = logits.shape
+    for name, value in (("temperature", temperature), ("top_k", top_k), ("top_p", top_p)):
+        if value.shape != (n,):
+            raise ValueError(f"{name} must have shape [{n}], got {tuple(value.shape)}")
+    if max_top_k < 0:
+        raise ValueError("max_top_k must be nonnegative")
+    _lib.require_gpu(logits, temperature, top_k, top_p)
+    out = torch.empty((n, vocab), dtype=torch.float32, device=logits.device)
+    if n == 0 or vocab == 0:
+        return out
+    x = _rows(logits)
+    temp, tk, tp = _f32(temperature), _i64(top_k), _f32(top_p)
+    lib = _lib.library()
+    status = lib.rlt_batched_probabilities(
+        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), n, vocab, _lib.ptr(temp), _lib.ptr(tk),
+        _lib.ptr(tp), int(max_top_k), int(bool(apply_top_p)), _lib.ptr(out), out.stride(0),
+        _lib.stream_of(x.device))
+    _lib.check(status, "rlt_batched_probabilities")
+    return out
+
+
+def greedy_accept_batched(draft_tokens, drafts, target_logits):
+    """Device greedy round: argmax per verify row, then the leading-match count.
+
+    reference: vllm_rlt/worker/async_speculative.py:706-720 (host rule
+    vllm_rlt/worker/speculative.py:41-53).  ``target_logits`` is ``[n, W1 + 1, V]``;
+    returns ``(targets int64 [n, W1 + 1], accepted int64 [n], next_token int64 [n])``
+    where draft j is checked against target row j and only ``drafts[r]`` drafts count.
+    """
+    n, w1 = draft_tokens.shape
+    if drafts.shape != (n,):
+        raise ValueError("drafts must have shape [n]")
+    if target_logits.ndim != 3 or target_logits.shape[:2] != (n, w1 + 1):
+        raise ValueError("target_logits must be [n, W1 + 1, V]")
+    _lib.require_gpu(draft_tokens, drafts, target_logits)
+    device = target_logits.device
+    vocab = target_logits.shape[-1]
+    targets = torch.empty((n, w1 + 1), dtype=torch.int64, device=device)
+    accepted = torch.empty(n, dtype=torch.int64, device=device)
+    next_token = torch.empty(n, dtype=torch.int64, device=device)
+    if n == 0:
+        return targets, accepted, next_token
+    if vocab == 0:
+        raise ValueError("target_logits must have V >= 1")
+    x = target_logits
+    if x.dtype not in _LOGIT_DTYPES:
+        x = x.float()
+    if not (x.stride(-1) == 1 and x.stride(0) == (w1 + 1) * x.stride(1)):
+        x = x.contiguous()
+    dt, dr = _i64(draft_tokens), _i64(drafts)
+    lib = _lib.library()
+    status = lib.rlt_greedy_accept(
+        _lib.ptr(dt), _lib.ptr(dr), _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(1), n, w1,
+        vocab, _lib.ptr(targets), _lib.ptr(accepted), _lib.ptr(next_token),
+        _lib.stream_of(device))
+    _lib.check(status, "rlt_greedy_accept")
+    return targets, accepted, next_token
 
 
 def categorical(weights, u):
