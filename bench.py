@@ -1,4 +1,5 @@
-"""Verify-step benchmark on one MI355X: packed-window paged attention + acceptance.
+"""Verify-step benchmark on one MI355X: packed-window paged attention, target
+distributions from logits, acceptance.
 
 Workload (the verify-step config the metric is quoted on):
 batch 32 requests x verify window q_len = k + 1 = 5 with the intra-window causal
@@ -8,9 +9,12 @@ seeded random permutation of the pool.  Acceptance over vocab 49152 with target 
 draft distributions built at temperature 0.7, top-p 0.9, seeded per-request
 uniforms.  Synthetic data, random values: there is no model or dataset.
 
-One step = the attention call over all 160 verify rows + speculative_accept over
-the 32 requests, both replayed from HIP graphs (the reference runs its recurrent
-core under graphs too).  ``value`` = verified tokens (32 x 5) / step time.
+One step = the attention call over all 160 verify rows + batched_probabilities of
+the 160 target-logit rows (fp32, T = 0.7, top-p 0.9: the reference's _verify,
+vllm_rlt/worker/async_speculative.py:694-704) + speculative_accept over the 32
+requests (draft distributions q are inputs, made in the draft step), all replayed
+from HIP graphs (the reference runs its recurrent core under graphs too).
+``value`` = verified tokens (32 x 5) / step time.
 
 Output: one JSON line (see the driver contract) with ``roofline`` for the
 attention launch (algorithmic bytes / average launch time, HIP events on the launch
@@ -71,7 +75,9 @@ def build_workload(dev, seed=0):
                      for s in seeds])
     return dict(n=n, window=window, hq=hq, hkv=hkv, d=d, bs=bs, vocab=vocab, k=k_drafts,
                 lengths=lengths, tables=tables, key_pool=key_pool, value_pool=value_pool, q=q,
-                cu=cu, qprob=qprob, pprob=pprob, u=u, layer=1)
+                cu=cu, qprob=qprob, pprob=pprob, u=u, layer=1,
+                target_logits=target_logits.reshape(n * window, vocab).contiguous(),
+                temperature=0.7, top_p=0.9)
 
 
 def attention_bytes(w):
@@ -82,6 +88,11 @@ def attention_bytes(w):
     qo = 2 * w["n"] * w["window"] * w["hq"] * w["d"] * elt
     tables = int(sum(math.ceil(int(n) / w["bs"]) for n in w["lengths"])) * 4
     return kv + qo + tables
+
+
+def probs_bytes(w):
+    """fp32 target logits read once, fp32 distributions written once."""
+    return 2 * 4 * w["n"] * w["window"] * w["vocab"] + 16 * w["n"] * w["window"]
 
 
 def accept_bytes(w):
@@ -108,13 +119,20 @@ def cpu_baseline(w, repeats=1):
     k_view = w["key_pool"][:, w["layer"]].cpu()
     v_view = w["value_pool"][:, w["layer"]].cpu()
     q, tables, lengths, cu = w["q"].cpu(), w["tables"], w["lengths"].int(), w["cu"]
-    qprob, pprob, u = w["qprob"].cpu(), w["pprob"].cpu(), w["u"]
+    qprob, u = w["qprob"].cpu(), w["u"]
+    logits = w["target_logits"].cpu()
+    rows = logits.shape[0]
+    temp = torch.full((rows,), w["temperature"])
+    top_k = torch.full((rows,), -1, dtype=torch.int64)
+    top_p = torch.full((rows,), w["top_p"])
     drafts_tok = w["draft_tokens"].cpu()
     drafts = torch.full((w["n"],), w["k"], dtype=torch.int64)
     k = w["k"]
     t0 = time.perf_counter()
     for _ in range(repeats):
         oatt.packed_window_attention(q, k_view, v_view, tables, lengths, cu)
+        pprob = osamp.batched_probabilities(logits, temp, top_k, top_p, max_top_k=0,
+                                            apply_top_p=True).view(w["n"], w["window"], -1)
         osamp.speculative_accept(drafts_tok, drafts, qprob, pprob, u[:, k:2 * k].contiguous(),
                                  u[:, 2 * k].contiguous())
     dt = (time.perf_counter() - t0) / repeats
@@ -131,7 +149,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("attention", "accept", "copy"),
+    ap.add_argument("--only", choices=("attention", "probs", "accept", "copy"),
                     help="replay only this part K times and exit (for counter collection); "
                          "'copy' copies a 1 GiB buffer K times (counter calibration)")
     ap.add_argument("--steps-per-graph", type=int, default=10,
@@ -166,43 +184,61 @@ def main():
         [pkg.categorical(w["qprob"][:, j].contiguous(), u[:, j].contiguous())[0] for j in range(k)], 1)
     dt_tok = w["draft_tokens"]
 
+    rows = w["n"] * w["window"]
+    logits = w["target_logits"]
+    temp = torch.full((rows,), w["temperature"], device=dev)
+    top_k = torch.full((rows,), -1, dtype=torch.int64, device=dev)
+    top_p = torch.full((rows,), w["top_p"], device=dev)
+    pbuf = {}
+
     def attn():
         return backend.prefill(w["q"], kc, vc, tables, lengths, cu, w["window"])
 
+    def probs():
+        pbuf["p"] = pkg.batched_probabilities(logits, temp, top_k, top_p, max_top_k=0,
+                                              apply_top_p=True).view(w["n"], w["window"], -1)
+        return pbuf["p"]
+
     def accept():
-        return pkg.speculative_accept(dt_tok, drafts, w["qprob"], w["pprob"], ua, uf)
+        return pkg.speculative_accept(dt_tok, drafts, w["qprob"], pbuf["p"], ua, uf)
+
+    def step():
+        attn()
+        probs()
+        accept()
 
     for _ in range(max(args.warmup, 1)):
-        attn()
-        accept()
+        step()
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for _ in range(2):
-            attn()
-            accept()
+            step()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     # Graphs of `spg` launches back to back: in-graph kernel boundaries cost ~0,
     # so per-launch timings are not inflated by the per-replay launch overhead.
     spg = max(1, min(args.steps_per_graph, args.steps))
-    g_attn, g_acc, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    g_attn, g_probs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    g_acc, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_attn):
         for _ in range(spg):
             out_attn = attn()
+    with torch.cuda.graph(g_probs):
+        for _ in range(spg):
+            out_probs = probs()
     with torch.cuda.graph(g_acc):
         for _ in range(spg):
             out_acc = accept()
     with torch.cuda.graph(g_step):
         for _ in range(spg):
-            attn()
-            accept()
+            step()
     for _ in range(max(1, args.warmup // spg)):
         g_step.replay()
     torch.cuda.synchronize()
     if args.only:
-        graph = g_attn if args.only == "attention" else g_acc
+        graph = {"attention": g_attn, "probs": g_probs, "accept": g_acc}[args.only]
         for _ in range(max(1, args.steps // spg)):
             graph.replay()
         torch.cuda.synchronize()
@@ -232,17 +268,20 @@ def main():
         return sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3 / spg
 
     t_attn = launch_time(g_attn, replays)
+    t_probs = launch_time(g_probs, replays)
     t_acc = launch_time(g_acc, replays)
 
     # ---- correctness of the measured outputs against an eager run
     eager_attn = attn()
+    eager_probs = probs()
     eager_acc = accept()
     torch.cuda.synchronize()
     assert torch.equal(eager_attn, out_attn)
+    assert torch.equal(eager_probs, out_probs)
     for a, b in zip(eager_acc, out_acc):
         assert torch.equal(a, b)
 
-    a_bytes, c_bytes = attention_bytes(w), accept_bytes(w)
+    a_bytes, p_bytes, c_bytes = attention_bytes(w), probs_bytes(w), accept_bytes(w)
     achieved = a_bytes / t_attn / 1e9
     tokens = w["n"] * w["window"]
     result = {
@@ -260,13 +299,15 @@ def main():
         "data": "synthetic (seeded random KV, q and logits; no model or dataset)",
         "config": {
             "workload": "config3 verify step: packed q_len=5 causal window, 16q/4kv heads, D=128, "
-                        "bf16 SHARED KV, batch 32, ctx U[1024,8192]; acceptance V=49152, T=0.7, top-p 0.9",
+                        "bf16 SHARED KV, batch 32, ctx U[1024,8192]; target distributions from "
+                        "fp32 logits (T=0.7, top-p 0.9) and acceptance, V=49152",
             "batch": w["n"], "window": w["window"], "q_heads": w["hq"], "kv_heads": w["hkv"],
             "head_dim": w["d"], "block_size": w["bs"], "vocab": w["vocab"],
             "ctx_sum": int(w["lengths"].sum()),
         },
-        "hbm_frac_step": round((a_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
+        "hbm_frac_step": round((a_bytes + p_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
         "attention_ms": round(t_attn * 1e3, 4),
+        "probs_ms": round(t_probs * 1e3, 4),
         "accept_ms": round(t_acc * 1e3, 4),
         "steps_per_graph": spg,
         "roofline": {

@@ -2,8 +2,9 @@
 
 Parity bar: probabilities within atol 1e-6 / rtol 1e-5 of the torch-CPU oracle (the
 tolerance of the reference's own test, tests/test_speculative_sampling.py:44-60).
-The top-p cut is pinned to exact arithmetic: the kernel decides it on fixed-point
-masses, and its kept count must equal the float64 cut.  torch's float32 softmax sums
+The top-p cut is pinned to exact arithmetic: the kernel decides it on exact
+fixed-point sums of its token masses, and its kept count must equal the float64 cut
+up to tokens within 2e-6 of the threshold (the masses' own error).  torch's float32 softmax sums
 to 1 + d (|d| ~ 1e-5 at V = 65536), so its own cut may differ from the exact one by a
 few tail tokens; the support may differ from the oracle's only there.  Tokens tied at a top-k / top-p cut survive in column
 order on the GPU; the reference leaves that choice unspecified, so tie cases are
@@ -21,6 +22,9 @@ from oracle import sampling as osamp
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 1e-6, 1e-5
+# the kernel's token masses (hardware exp2 of (l - lmax) log2(e) / T) carry ~1e-6
+# relative error, so its cut equals the float64 one except within this band
+EXACT_BAND = 2e-6
 
 
 def _say(*args):
@@ -71,7 +75,7 @@ def _assert_match(got, want, logits, t, k, p, plan):
 
     * The kept set must be a top set of x (as a multiset of values).
     * Rows with top-p: its size must equal the float64 exact cut (up to positions
-      whose preceding mass is within 1e-9 of p), and may differ from torch's only at
+      whose preceding mass is within EXACT_BAND of p), and may differ from torch's only at
       positions within torch's own error: its fp32 softmax sums to 1 + d, |d| up to
       ~1e-5 at V = 65536, which shifts every cumulative value it compares with p.
     * Probabilities match position by position when the supports agree, else as
@@ -88,7 +92,7 @@ def _assert_match(got, want, logits, t, k, p, plan):
             ec, before = _exact_kept(sx, top_p)
             if gc != ec:
                 lo, hi = min(gc, ec), max(gc, ec)
-                assert ((before[lo:hi] - top_p).abs() <= 1e-9).all(), f"row {i}: {gc} vs exact {ec}"
+                assert ((before[lo:hi] - top_p).abs() <= EXACT_BAND).all(), f"row {i}: {gc} vs exact {ec}"
         if torch.equal(gs, ws):
             torch.testing.assert_close(g, w, atol=ATOL, rtol=RTOL)
             continue

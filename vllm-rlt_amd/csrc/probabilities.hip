@@ -4,31 +4,42 @@
 // vllm_rlt/worker/speculative_sampling.py:8-56 ``batched_probabilities`` (row form
 // vllm_rlt/worker/sampler.py:28-55): x = logits / T, strict top-k by index, strict
 // top-p (sorted softmax cumulative mass > p, shifted by one so the crossing token
-// stays), softmax.  No sort is performed.  One 1024-thread workgroup owns a row and
-// keeps x in registers (j-th element of thread t is column 1024 j + t); the cut
-// is found by selection:
+// stays), softmax.  No sort over the vocabulary is performed.  One 1024-thread
+// workgroup owns a row and keeps it in registers and LDS (element j of thread t
+// is column 1024 j + t).
 //
-//   * pass 0 bins every candidate by its distance below the row max, in steps of
-//     1/16 logit (1024 bins, the last one open-ended).  The bin index is a
-//     non-increasing function of x, so "bin b and every bin before it" is a prefix
-//     of the descending order.  A block scan of the per-bin (count, mass) finds the
-//     bin where the criterion is crossed: count >= k for top-k, cumulative mass > p Z
-//     for top-p.
-//   * later passes re-bin only the crossing bin's members, uniformly in the
-//     order-preserving 32-bit key of x, in power-of-two key bins below the bin's
-//     largest key; each pass shrinks the key range at least 512-fold, so at most
-//     five passes end on a single value v (the cut).
-//   * every element above v is kept; of the elements equal to v, the first t in
-//     column order are kept (the reference leaves the surviving index of a tie
-//     unspecified), where t is what the count or the mass rule leaves room for.
+// Order.  x = l / T is monotone in the logit l for T > 0, so the kernel orders
+// tokens by (l descending, column ascending): a descending order of x in which
+// tokens tied in x are ordered by l, then by column (the reference leaves the
+// surviving index of a tie unspecified).  Every cut below is a threshold in this
+// total order: a token is kept iff it precedes the cut token.
 //
-// Masses are exp(x - max) in 2^-40 fixed point, summed as 64-bit integers: exact
-// and independent of summation order, so the crossing is found without rounding
-// drift.  The reference compares the float32 cumsum of float32 softmax values with
-// p; the two decisions can differ only for a token whose cumulative mass lies
-// within ~1e-6 relative of p Z.  Outputs are exp(x - max) * (1 / Z_kept) with Z
-// summed in float64; a row holding NaN or whose max is not finite is written as
-// NaN (torch's softmax gives NaN for such rows).
+// Masses.  A token's mass is e = 2^((l - lmax) log2(e) / T) (hardware exp2): the
+// softmax numerator exp(x - max x) to ~1e-6 relative.  e is non-decreasing in l,
+// so bins taken from the float bits of e are ordered like the tokens: 64 bins per
+// binade for e in (2^-16, 1], 4 per binade below (filled only when a cut falls
+// there).  Masses are summed in 2^-40 fixed point (64-bit integers: exact and
+// order-independent).
+//
+// Selection (top-k: the k-th token; top-p: the first token whose cumulative mass
+// exceeds p Z, Z the total):
+//   1. one pass computes e (stored in place of l), the float64 total, and the
+//      count / mass histogram of the top bins;
+//   2. a block scan finds the bin where the criterion is crossed;
+//   3. the bin's tokens (few: a bin spans 1.1% in mass) are gathered into an LDS
+//      list of (logit key, column), with their logits re-read, and bitonic-sorted;
+//      a scan over the sorted list gives the cut token.  A bin holding more tokens
+//      than the list is narrowed first by key-range histograms over its logits,
+//      and a single tied logit value by column ranks.
+// Top-p after top-k runs on the same histogram with the top-k cut bin reduced to
+// its kept tokens.  Outputs are e * 2^40 / Z_kept, Z_kept the exact fixed-point
+// total of the kept tokens; unfiltered rows sum e in float64.
+//
+// torch compares a float32 cumsum of float32 softmax values (whose total is 1 +-
+// ~1e-5 at V = 65536) with p, so the two top-p cuts can differ only for tokens
+// whose preceding mass lies that close to p Z.  A row holding NaN, with a
+// non-finite max, or with T not > 0 is written as NaN (torch's softmax gives NaN
+// for such rows).
 //
 // rlt_argmax_rows_kernel + rlt_greedy_match_kernel replace the device greedy round
 // of vllm_rlt/worker/async_speculative.py:706-720 (targets = argmax per verify row,
@@ -37,6 +48,7 @@
 // maximal column; NaN counts as the maximum (torch's argmax rule).
 
 #include "common.h"
+#include "probs_internal.h"
 #include "rlt_mi355x.h"
 
 #include <math.h>
@@ -45,11 +57,25 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / RLT_WAVE;
-constexpr int kBins = 1024;
-constexpr float kBinsPerLogit = 16.f;
-constexpr int kMaxRegChunks = 64;       // V <= 65536 keeps the row in registers
+constexpr int kMaxRegChunks = 64;       // V <= 65536 keeps the row on chip
 constexpr int kMaxStreamChunks = 256;   // V <= 262144 on the re-reading variant
 constexpr double kFixScale = 1099511627776.0;  // 2^40
+
+// Histogram bins over the float bits of e in [0, 1].
+constexpr uint32_t kOneBits = 0x3f800000u;  // 1.0f
+constexpr int kTopBins = 1024;
+constexpr uint32_t kFloor8 = 0x3b800000u;   // bits of 2^-8
+constexpr uint32_t kFloor16 = 0x37800000u;  // bits of 2^-16
+constexpr int kTailShift = 21;              // 4 bins per binade
+constexpr int kBins = kTopBins + 512;       // tail: 445 bins used
+constexpr int kBinsPerThread = (kBins + kThreads - 1) / kThreads;
+constexpr unsigned long long kCutNone = ~0ull;  // "after every token"
+
+// Bin of a token from the bits of its mass e in [0, 1]: 64 bins per binade over
+// (2^-16, 1], 4 per binade below.  Non-increasing in e, hence in the logit.
+__device__ __forceinline__ int bin_of(uint32_t b) {
+  return b > kFloor16 ? (int)((kOneBits - b) >> 17) : kTopBins + (int)((kFloor16 - b) >> kTailShift);
+}
 
 // Order-preserving key of a float (NaN excluded by the callers); -0 maps to +0.
 __device__ __forceinline__ uint32_t order_key(float x) {
@@ -58,8 +84,22 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t fixed_mass(float e) {
-  return (uint64_t)((double)e * kFixScale);
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Position of a token in the total order (ascending = l descending, column
+// ascending).
+__device__ __forceinline__ unsigned long long composite(uint32_t key, uint32_t col) {
+  return ((unsigned long long)(~key) << 32) | col;
+}
+
+// floor(e * 2^40) for e in [0, 1], from the float's bits (e = m24 * 2^(E - 150)).
+__device__ __forceinline__ unsigned long long fixed_mass(float e) {
+  const uint32_t b = __float_as_uint(e);
+  const int s = (int)(b >> 23) - 110;
+  const unsigned long long m24 = (b & 0x7fffffu) | 0x800000u;
+  return s >= 0 ? (m24 << s) : (s > -24 ? (m24 >> -s) : 0ull);
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
@@ -73,24 +113,23 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
-template <int TC>
+template <int CAP>
 struct SharedT {
-  static constexpr int kTieChunks = TC;
-  uint32_t cnt[kBins];
+  static constexpr int kCap = CAP;
   unsigned long long mass[kBins];
+  uint32_t cnt[kBins];
+  unsigned long long list[CAP];  // tokens of the crossing bin (columns, then composites)
   uint32_t wave_u32[kWaves];
   unsigned long long wave_u64[kWaves];
   double wave_f64[kWaves];
-  uint32_t tie_base[2][TC * kWaves];
+  double wave_f64x3[3][kWaves];
   // selection results broadcast to the block
   int sel_bin;
   uint32_t sel_cnt_before;
   unsigned long long sel_mass_before;
   uint32_t sel_bin_cnt;
   unsigned long long sel_bin_mass;
-  uint32_t klo, khi;
-  float row_max;
-  int bad_row;
+  uint32_t list_n;
 };
 
 // Block-wide sum of a u32 and a u64 (every thread gets the totals).
@@ -147,17 +186,29 @@ __device__ __forceinline__ void block_minmax(Shared& sh, uint32_t& lo, uint32_t&
   __syncthreads();
 }
 
-// Inclusive block scan over the histogram (thread t owns bin t), then the thread
-// whose bin first satisfies the criterion publishes it.  kMass: criterion is
-// before + cumulative mass > limit; else before + cumulative count >= limit.
+// Inclusive block scan over nb histogram bins (thread t owns bins kBinsPerThread t
+// + i), then the thread owning the first bin that satisfies the criterion
+// publishes it (sel_bin = -1 if none).  kMass: before + cumulative mass > limit;
+// else before + cumulative count >= limit.
 template <bool kMass, class Shared>
-__device__ __forceinline__ void scan_select(Shared& sh, uint32_t cnt_before, unsigned long long mass_before,
-                            unsigned long long limit) {
+__device__ __forceinline__ void scan_select(Shared& sh, int nb, uint32_t cnt_before,
+                                            unsigned long long mass_before,
+                                            unsigned long long limit) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const uint32_t c_own = sh.cnt[t];
-  const unsigned long long m_own = sh.mass[t];
-  uint32_t c = c_own;
-  unsigned long long m = m_own;
+  uint32_t c_own[kBinsPerThread];
+  unsigned long long m_own[kBinsPerThread];
+  uint32_t c = 0;
+  unsigned long long m = 0;
+#pragma unroll
+  for (int i = 0; i < kBinsPerThread; ++i) {
+    const int bin = t * kBinsPerThread + i;
+    c_own[i] = bin < nb ? sh.cnt[bin] : 0u;
+    m_own[i] = bin < nb ? sh.mass[bin] : 0ull;
+    c += c_own[i];
+    m += m_own[i];
+  }
+  const uint32_t c_run = c;
+  const unsigned long long m_run = m;
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t cy = __shfl_up(c, off, RLT_WAVE);
     const unsigned long long my = __shfl_up(m, off, RLT_WAVE);
@@ -166,50 +217,80 @@ __device__ __forceinline__ void scan_select(Shared& sh, uint32_t cnt_before, uns
       m += my;
     }
   }
+  if (t == 0) sh.sel_bin = -1;
   if (lane == 63) {
     sh.wave_u32[w] = c;
     sh.wave_u64[w] = m;
   }
   __syncthreads();
-  uint32_t cp = cnt_before;
-  unsigned long long mp = mass_before;
+  uint32_t cp = cnt_before + c - c_run;
+  unsigned long long mp = mass_before + m - m_run;
   for (int i = 0; i < w; ++i) {
     cp += sh.wave_u32[i];
     mp += sh.wave_u64[i];
   }
-  const uint32_t c_incl = cp + c, c_excl = c_incl - c_own;
-  const unsigned long long m_incl = mp + m, m_excl = m_incl - m_own;
-  const bool hit = kMass ? (m_incl > limit && !(m_excl > limit))
-                         : (c_incl >= limit && !(c_excl >= limit));
-  if (hit) {
-    sh.sel_bin = t;
-    sh.sel_cnt_before = c_excl;
-    sh.sel_mass_before = m_excl;
-    sh.sel_bin_cnt = c_own;
-    sh.sel_bin_mass = m_own;
+#pragma unroll
+  for (int i = 0; i < kBinsPerThread; ++i) {
+    const uint32_t c_incl = cp + c_own[i];
+    const unsigned long long m_incl = mp + m_own[i];
+    const bool hit = kMass ? (m_incl > limit && !(mp > limit)) : (c_incl >= limit && !(cp >= limit));
+    if (hit) {
+      sh.sel_bin = t * kBinsPerThread + i;
+      sh.sel_cnt_before = cp;
+      sh.sel_mass_before = mp;
+      sh.sel_bin_cnt = c_own[i];
+      sh.sel_bin_mass = m_own[i];
+    }
+    cp = c_incl;
+    mp = m_incl;
   }
   __syncthreads();
 }
 
-// Per-row state of one selection: elements with key > key are above the cut,
-// `take` of the elements equal to key (in column order) are kept.
+// Bitonic sort (ascending) of sh.list[0, p), p a power of two; entries past the
+// gathered count hold kCutNone.
+template <class Shared>
+__device__ __forceinline__ void sort_list(Shared& sh, int p) {
+  for (int k = 2; k <= p; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < p; i += kThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const unsigned long long a = sh.list[i], b = sh.list[ixj];
+          if ((a > b) == ((i & k) == 0)) {
+            sh.list[i] = b;
+            sh.list[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Result of one selection: tokens of bins before `bin` are kept, and of `bin`
+// (whose tokens sit sorted in sh.list) the first kept_in_bin; `kept` is the kept
+// tokens' fixed-point mass.  bin = -1: crowded, handed to the exact kernel.
 struct Cut {
-  uint32_t key;
-  uint32_t take;   // kept elements at key
-  uint32_t ties;   // elements at key (members of the selection)
-  bool partial;    // take < ties: column ranks needed
+  int bin;
+  uint32_t kept_in_bin;
+  unsigned long long kept;
 };
 
-// One row's x = logits / T.  Chunks j < NREG sit in registers, the next NLDS
-// chunks in LDS (xl, chunk-major, conflict-free); NREG = NLDS = 0 re-reads the
-// logits on every pass.
+// One row's logits.  Chunks j < NREG sit in registers, the next NLDS chunks in
+// LDS (xl, chunk-major, conflict-free); NREG = NLDS = 0 re-reads the logits on
+// every pass.  After the mass pass the on-chip slots hold e instead of l.
+// Columns past V read as NaN: rows holding a real NaN are finished before any
+// pass that tests `v == v` for validity, which keeps per-chunk bounds masks out of
+// the scalar registers.
 template <int DT, int NREG, int NLDS>
 struct Row {
   static constexpr int kNpt = NREG + NLDS;
+  static constexpr int kDtype = DT;
   const void* src;
   int V;
-  float temp;
   int npt;  // chunks per thread
+  float lmax, c;
   float* xl;
   float xr[NREG > 0 ? NREG : 1];
 
@@ -220,160 +301,252 @@ struct Row {
     if (j < NREG) xr[j] = v;
     else if (kNpt > 0) xl[(j - NREG) * kThreads + threadIdx.x] = v;
   }
+  // the on-chip value of chunk j (l before the mass pass, e after), or the logit
+  // re-read from memory on the re-reading variant
   __device__ __forceinline__ float x(int j) const {
     float v;
     if (j < NREG) v = xr[j];
     else if (kNpt > 0) v = xl[(j - NREG) * kThreads + threadIdx.x];
-    else v = valid(j) ? load_as_f32<DT>(src, (int64_t)j * kThreads + threadIdx.x) / temp : -INFINITY;
-    // opaque copy: values derived from x (key, exp, mass) are recomputed in each
-    // pass instead of being kept live across passes, which would spill
+    else v = logit(j);
+    // opaque copy: values derived from v are recomputed in each pass instead of
+    // being kept live across passes, which would spill
     asm volatile("" : "+v"(v));
     return v;
   }
+  __device__ __forceinline__ float logit(int j) const {
+    return valid(j) ? load_as_f32<DT>(src, (int64_t)j * kThreads + threadIdx.x) : NAN;
+  }
+  __device__ __forceinline__ float mass(float l) const {
+    return __builtin_amdgcn_exp2f((l - lmax) * c);
+  }
+  // e of chunk j after the mass pass (NaN for padding)
+  __device__ __forceinline__ float e(int j) const {
+    if (kNpt > 0) return x(j);
+    const float l = x(j);
+    return l == l ? mass(l) : NAN;
+  }
   // f(j) for every chunk: register chunks unrolled (static register indices),
-  // the others in a rolled loop.  Calls are wave-uniform (ballots allowed).
+  // LDS chunks in a rolled loop, re-read chunks four at a time (loads in flight).
+  // Calls are wave-uniform (ballots allowed).
   template <class F>
   __device__ __forceinline__ void for_chunks(F f) const {
 #pragma unroll
     for (int j = 0; j < NREG; ++j) f(j);
+    if (kNpt > 0) {
 #pragma unroll 1
-    for (int j = NREG; j < npt; ++j) f(j);
+      for (int j = NREG; j < npt; ++j) f(j);
+    } else {
+      int j = 0;
+#pragma unroll 1
+      for (; j + 4 <= npt; j += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f(j + u);
+      }
+#pragma unroll 1
+      for (; j < npt; ++j) f(j);
+    }
   }
 };
 
-// Column rank of each tie (elements with member && key == cut) in column order:
-// table[j * kWaves + w] = number of ties in chunks < j, plus ties of chunk j in
-// waves < w; rank = table entry + ties in lower lanes of the same wave.
-template <class Shared, class R, class Member>
-__device__ __forceinline__ void build_tie_table(Shared& sh, const R& row, uint32_t key, int which,
-                                                Member member) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  uint32_t* table = sh.tie_base[which];
-  row.for_chunks([&](int j) {
-    const bool tie = row.valid(j) && member(j) && order_key(row.x(j)) == key;
-    const uint64_t b = __ballot(tie);
-    if (lane == 0) table[j * kWaves + w] = __popcll(b);
-  });
-  __syncthreads();
-  // exclusive scan of npt * kWaves entries: thread t owns a run of `per` entries
-  const int entries = row.npt * kWaves;
-  const int per = (entries + kThreads - 1) / kThreads;
-  const int t = threadIdx.x;
-  constexpr int kPerMax = (Shared::kTieChunks * kWaves + kThreads - 1) / kThreads;
-  uint32_t vals[kPerMax];
-  uint32_t run = 0;
-#pragma unroll
-  for (int e = 0; e < kPerMax; ++e) {
-    const int idx = t * per + e;
-    vals[e] = (e < per && idx < entries) ? table[idx] : 0u;
-    run += vals[e];
+// Adds (1, fm) of every lane with `take` to its bin.
+template <class Shared>
+__device__ __forceinline__ void hist_add(Shared& sh, bool take, int bin, unsigned long long fm) {
+  if (take) {
+    atomicAdd(&sh.cnt[bin], 1u);
+    atomicAdd(&sh.mass[bin], fm);
   }
-  uint32_t incl = run;
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(incl, off, RLT_WAVE);
-    if (lane >= off) incl += y;
-  }
-  if (lane == 63) sh.wave_u32[w] = incl;
-  __syncthreads();
-  uint32_t base = incl - run;
-  for (int i = 0; i < w; ++i) base += sh.wave_u32[i];
-#pragma unroll
-  for (int e = 0; e < kPerMax; ++e) {
-    const int idx = t * per + e;
-    if (e < per && idx < entries) table[idx] = base;
-    base += vals[e];
-  }
-  __syncthreads();
 }
 
 template <class Shared>
-__device__ __forceinline__ uint32_t tie_rank(const Shared& sh, int which, int j, bool tie) {
-  const uint64_t b = __ballot(tie);
-  return sh.tie_base[which][j * kWaves + (threadIdx.x >> 6)] + __popcll(b & lanemask_lt());
-}
-
-// Bin of x in a pass: pass 0 by distance below the max in 1/16-logit steps,
-// later passes by key offset below khi in 2^shift-key steps.
-__device__ __forceinline__ int bin_of(float x, uint32_t key, float m, bool value_bins, uint32_t khi,
-                                      int shift) {
-  if (value_bins) {
-    const float d = m - x;
-    return d < (float)(kBins - 1) / kBinsPerLogit ? (int)(d * kBinsPerLogit) : kBins - 1;
+__device__ __forceinline__ void clear_hist(Shared& sh, int from, int to) {
+  for (int i = from + (int)threadIdx.x; i < to; i += kThreads) {
+    sh.cnt[i] = 0;
+    sh.mass[i] = 0;
   }
-  return (int)((khi - key) >> shift);
 }
 
-// Finds the cut of one selection.  kMass: members carry mass fixed_mass(exp(x-m))
-// and the cut is where the cumulative mass first exceeds `limit`; else every
-// member counts 1 and the cut is the `limit`-th largest member.
-template <bool kMass, class Shared, class R, class Member>
-__device__ __forceinline__ Cut select_cut(Shared& sh, const R& row, float m,
-                                          unsigned long long limit, Member member) {
-  uint32_t cnt_before = 0;
-  unsigned long long mass_before = 0;
-  uint32_t klo = 0, khi = 0xffffffffu;
-  for (int pass = 0; pass < 7; ++pass) {
-    const bool value_bins = pass == 0;
-    sh.cnt[threadIdx.x] = 0;
-    sh.mass[threadIdx.x] = 0;
+// Adds histogram stage s: the tokens with e in (2^-8, 1] (s = 0), (2^-16, 2^-8]
+// (s = 1) or [0, 2^-16] (s = 2).
+template <class Shared, class R>
+__device__ __forceinline__ void admit_stage(Shared& sh, const R& row, int s) {
+  const uint32_t lo = s == 0 ? kFloor8 + 1u : s == 1 ? kFloor16 + 1u : 0u;
+  const uint32_t hi = s == 0 ? 0xffffffffu : s == 1 ? kFloor8 : kFloor16;
+  row.for_chunks([&](int j) {
+    const float e = row.e(j);
+    const uint32_t bits = __float_as_uint(e);
+    const bool take = e == e && bits >= lo && bits <= hi;
+    hist_add(sh, take, take ? bin_of(bits) : 0, take ? fixed_mass(e) : 0ull);
+  });
+  __syncthreads();
+}
+
+// Selection over the histogram in sh, admitting histogram stages as needed.  Members: every token of a bin < mbin, and in
+// bin mbin the first mlist entries of the (sorted) list left by the previous
+// selection; (kBins, 0) takes all.
+//   kMass: the cut token is the first whose cumulative member mass exceeds limit;
+//   else the cut follows the limit-th member.
+// Leaves the crossing bin's tokens sorted in sh.list[0, sh.list_n).
+template <bool kMass, class Shared, class R>
+__device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long long limit,
+                                      int& stages, int mbin, uint32_t mlist) {
+  const int t = threadIdx.x, lane = t & 63;
+  // admit tokens into the histogram by mass range until the criterion is crossed:
+  // e > 2^-8, then (2^-16, 2^-8], then the rest (each stage a prefix of the order,
+  // so a scan over the admitted bins is exact for the cuts they contain)
+  if (stages == 0) {
+    admit_stage(sh, row, 0);
+    stages = 1;
+  }
+  scan_select<kMass>(sh, kBins, 0, 0, limit);
+  while (sh.sel_bin < 0 && stages < 3) {
     __syncthreads();
-    // key bins: the smallest power-of-two width that maps [klo, khi] to <= kBins bins
-    const uint32_t span = khi - klo;
-    const int shift = span < (uint32_t)kBins ? 0 : 22 - __clz(span);  // bit length - 10
-    row.for_chunks([&](int j) {
-      if (!row.valid(j) || !member(j)) return;
-      const float x = row.x(j);
-      const uint32_t key = order_key(x);
-      if (key < klo || key > khi) return;
-      const int bin = bin_of(x, key, m, value_bins, khi, shift);
-      atomicAdd(&sh.cnt[bin], 1u);
-      if (kMass) atomicAdd(&sh.mass[bin], (unsigned long long)fixed_mass(expf(x - m)));
-    });
-    __syncthreads();
-    scan_select<kMass>(sh, cnt_before, mass_before, limit);
-    const int b = sh.sel_bin;
-    cnt_before = sh.sel_cnt_before;
-    mass_before = sh.sel_mass_before;
-    const uint32_t bin_cnt = sh.sel_bin_cnt;
-    const unsigned long long bin_mass = sh.sel_bin_mass;
-    // key range of the crossing bin's members
-    uint32_t lo = 0xffffffffu, hi = 0;
-    row.for_chunks([&](int j) {
-      if (!row.valid(j) || !member(j)) return;
-      const float x = row.x(j);
-      const uint32_t key = order_key(x);
-      if (key < klo || key > khi) return;
-      if (bin_of(x, key, m, value_bins, khi, shift) == b) {
-        lo = min(lo, key);
-        hi = max(hi, key);
-      }
-    });
-    block_minmax(sh, lo, hi);
-    klo = lo;
-    khi = hi;
-    if (klo == khi) {
-      Cut c;
-      c.key = klo;
-      c.ties = bin_cnt;
-      if (kMass) {
-        // every tie carries the same mass; tie i (0-based) is kept while the mass
-        // above it is <= limit
-        const unsigned long long each = bin_mass / bin_cnt;
-        const unsigned long long t = (limit - mass_before) / each + 1ull;
-        c.take = t < bin_cnt ? (uint32_t)t : bin_cnt;
-      } else {
-        c.take = (uint32_t)limit - cnt_before;
-      }
-      c.partial = c.take < c.ties;
-      return c;
+    admit_stage(sh, row, stages++);
+    scan_select<kMass>(sh, kBins, 0, 0, limit);
+  }
+  const int bin = sh.sel_bin;  // >= 0: the region holds the cut by construction
+  const uint32_t cnt_before = sh.sel_cnt_before;
+  const unsigned long long mass_before = sh.sel_mass_before;
+  const uint32_t n = sh.sel_bin_cnt;
+  __syncthreads();
+
+  Cut out;
+  out.bin = bin;
+  int nl;
+  if (bin >= 0 && bin == mbin) {
+    nl = (int)mlist;  // the members are the sorted prefix already in the list
+  } else {
+    if (bin < 0 || n > (uint32_t)Shared::kCap) {
+      // crowded bin: the row goes to the exact kernel (block-uniform)
+      out.bin = -1;
+      return out;
     }
+    // gather the bin's columns (all members: bin < mbin), then their logits, one
+    // entry per thread, so no load waits inside the row loop
+    if (t == 0) sh.list_n = 0;
+    __syncthreads();
+    row.for_chunks([&](int j) {
+      const float e = row.e(j);
+      const bool take = e == e && bin_of(__float_as_uint(e)) == bin;
+      const uint64_t m = __ballot(take);
+      if (m == 0) return;
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&sh.list_n, (uint32_t)__popcll(m));
+      base = __shfl(base, 0, RLT_WAVE);
+      const uint32_t pos = base + __popcll(m & lanemask_lt());
+      if (take && pos < (uint32_t)Shared::kCap) sh.list[pos] = (uint32_t)(j * kThreads + t);
+    });
+    __syncthreads();
+    nl = min((int)sh.list_n, Shared::kCap);  // == n
+    int p = 1;
+    while (p < nl) p <<= 1;
+    for (int i = t; i < p; i += kThreads) {
+      unsigned long long v = kCutNone;
+      if (i < nl) {
+        const uint32_t col = (uint32_t)sh.list[i];
+        v = composite(order_key(load_as_f32<R::kDtype>(row.src, col)), col);
+      }
+      sh.list[i] = v;
+    }
+    __syncthreads();
+    sort_list(sh, p);
   }
-  // unreachable: five key passes reduce any 32-bit range to one key
-  Cut c;
-  c.key = klo;
-  c.take = c.ties = 0xffffffffu;
-  c.partial = false;
-  return c;
+  // scan the sorted members: masses recomputed from the keys (same arithmetic as
+  // the mass pass), kept while the cut criterion is not reached
+  constexpr int kPer = (Shared::kCap + kThreads - 1) / kThreads;
+  unsigned long long fm[kPer];
+  unsigned long long run = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int idx = t * kPer + i;
+    fm[i] = 0;
+    if (idx < nl) fm[i] = fixed_mass(row.mass(key_value(~(uint32_t)(sh.list[idx] >> 32))));
+    run += fm[i];
+  }
+  unsigned long long incl = run;
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned long long y = __shfl_up(incl, off, RLT_WAVE);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) sh.wave_u64[t >> 6] = incl;
+  __syncthreads();
+  unsigned long long before = mass_before + incl - run;
+  for (int i = 0; i < (t >> 6); ++i) before += sh.wave_u64[i];
+  uint32_t kept_here = 0;
+  unsigned long long kept_mass = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int idx = t * kPer + i;
+    const bool keep = idx < nl && (kMass ? before <= limit : (uint32_t)idx < limit - cnt_before);
+    kept_here += keep;
+    kept_mass += keep ? fm[i] : 0ull;
+    before += fm[i];
+  }
+  block_sum2(sh, kept_here, kept_mass);
+  out.kept_in_bin = kept_here;
+  out.kept = mass_before + kept_mass;
+  return out;
+}
+
+// Top-k / top-p cut and the output of one row.
+template <class Shared, class R>
+__device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __restrict__ dst,
+                                           bool do_k, bool do_p, unsigned long long kk, float p,
+                                           double z) {
+  const int t = threadIdx.x;
+  clear_hist(sh, 0, kBins);
+  __syncthreads();
+  int stages = 0;  // histogram stages admitted so far
+
+  auto hand_over = [&]() {  // crowded cut: the exact kernel computes this row
+    if (t == 0) dst[0] = __uint_as_float(kCrowdedRowMark);
+  };
+  Cut cut;
+  if (do_k) {
+    // top-k (reference: speculative_sampling.py:39-48): keeps min(k_eff, max_top_k)
+    cut = select<false>(sh, row, kk, stages, kBins, 0u);
+    if (cut.bin < 0) return hand_over();
+  }
+  if (do_p) {
+    // top-p (reference: speculative_sampling.py:49-55) over the top-k survivors:
+    // kept prefix = every token whose preceding mass is <= p Z (p <= 0 keeps one)
+    const unsigned long long zk = do_k ? cut.kept : (unsigned long long)(z * kFixScale);
+    const unsigned long long limit = p > 0.f ? (unsigned long long)((double)p * (double)zk) : 0ull;
+    if (do_k) {
+      // histogram of the survivors: bins before the top-k bin unchanged, the
+      // top-k bin reduced to its kept tokens, later bins empty
+      const Cut ck = cut;
+      if (t == 0) {
+        unsigned long long before = 0;
+        for (int i = 0; i < ck.bin; ++i) before += sh.mass[i];
+        sh.cnt[ck.bin] = ck.kept_in_bin;
+        sh.mass[ck.bin] = ck.kept - before;
+      }
+      clear_hist(sh, ck.bin + 1, kBins);
+      __syncthreads();
+      stages = 3;  // bins up to the top-k bin are complete; later ones hold no survivor
+      cut = select<true>(sh, row, limit, stages, ck.bin, ck.kept_in_bin);
+    } else {
+      cut = select<true>(sh, row, limit, stages, kBins, 0u);
+    }
+    if (cut.bin < 0) return hand_over();
+  }
+
+  // ---- softmax over the kept tokens, normalized by their exact fixed-point total:
+  // bins before the cut bin kept, later bins dropped, the cut bin's tokens written
+  // from the sorted list (its first kept_in_bin kept)
+  const float inv = (float)(kFixScale / (double)cut.kept);
+  row.for_chunks([&](int j) {
+    const float e = row.e(j);
+    if (e != e) return;
+    const int b = bin_of(__float_as_uint(e));
+    if (b != cut.bin) dst[(int64_t)j * kThreads + t] = b < cut.bin ? e * inv : 0.f;
+  });
+  const int nl = min((int)sh.list_n, Shared::kCap);
+  for (int i = t; i < nl; i += kThreads) {
+    const unsigned long long v = sh.list[i];
+    const float e = row.mass(key_value(~(uint32_t)(v >> 32)));
+    dst[(uint32_t)v] = (uint32_t)i < cut.kept_in_bin ? e * inv : 0.f;
+  }
 }
 
 template <int DT, int NREG, int NLDS>
@@ -383,7 +556,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
     int64_t out_stride) {
   constexpr int NPT = NREG + NLDS;
-  __shared__ SharedT<(NPT > 0 ? NPT : kMaxStreamChunks)> sh;
+  __shared__ SharedT<(NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048)> sh;
   __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
   const int64_t r = blockIdx.x;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -391,122 +564,101 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   row.xl = xlds;
   row.V = V;
   row.src = (const char*)logits + r * row_stride * (DT == RLT_F32 ? 4 : 2);
-  row.temp = temperature[r];
   row.npt = NPT > 0 ? NPT : (V + kThreads - 1) / kThreads;
   float* dst = out + r * out_stride;
+  const float temp = temperature[r];
+  row.c = 1.44269504088896341f / temp;  // log2(e) / T
 
-  // x = logits / T (IEEE division, as torch), row max, NaN detection
-  float m = -INFINITY;
+  // ---- row max and NaN detection (padding stored as NaN)
+  float lmax = -INFINITY;
   bool nan = false;
-  row.for_chunks([&](int j) {
-    float x = -INFINITY;
-    if (row.valid(j)) {
-      x = load_as_f32<DT>(row.src, (int64_t)j * kThreads + t) / row.temp;
-      nan |= x != x;
+  auto take_raw = [&](int j, float l) {
+    const bool ok = row.valid(j);
+    nan |= ok && l != l;
+    row.set(j, ok ? l : NAN);
+    lmax = ok ? fmaxf(lmax, l) : lmax;
+  };
+  auto fetch = [&](int j) {
+    return row.valid(j) ? load_as_f32<DT>(row.src, (int64_t)j * kThreads + t) : 0.f;
+  };
+  if (NPT > 0) {
+    // every register chunk and the first LDS batch in flight at once; each LDS
+    // batch is consumed while the next one loads
+    constexpr int kB = 16;
+    float raw[NREG > 0 ? NREG : 1];
+    float cur[kB];
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) raw[j] = fetch(j);
+#pragma unroll
+    for (int u = 0; u < kB; ++u) cur[u] = NREG + u < NPT ? fetch(NREG + u) : 0.f;
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) take_raw(j, raw[j]);
+#pragma unroll 1
+    for (int j0 = NREG; j0 < NPT; j0 += kB) {
+      float nxt[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) nxt[u] = j0 + kB + u < NPT ? fetch(j0 + kB + u) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kB; ++u)
+        if (j0 + u < NPT) take_raw(j0 + u, cur[u]);
+#pragma unroll
+      for (int u = 0; u < kB; ++u) cur[u] = nxt[u];
     }
-    row.set(j, x);
-    m = fmaxf(m, x);
-  });
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, RLT_WAVE));
+  } else {
+    row.for_chunks([&](int j) {
+      const float l = row.x(j);
+      nan |= row.valid(j) && l != l;
+      lmax = fmaxf(lmax, l);  // padding reads NaN, which fmaxf ignores
+    });
+  }
+  for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, RLT_WAVE));
   const uint64_t nan_b = __ballot(nan);
   if (lane == 0) {
-    sh.wave_f64[w] = m;
+    sh.wave_f64[w] = lmax;
     sh.wave_u32[w] = nan_b != 0;
   }
   __syncthreads();
-  m = -INFINITY;
+  lmax = -INFINITY;
   int bad = 0;
   for (int i = 0; i < kWaves; ++i) {
-    m = fmaxf(m, (float)sh.wave_f64[i]);
+    lmax = fmaxf(lmax, (float)sh.wave_f64[i]);
     bad |= sh.wave_u32[i];
   }
   __syncthreads();
-  if (bad || !isfinite(m)) {
+  if (bad || !isfinite(lmax) || !(temp > 0.f) || !isfinite(row.c)) {
     for (int64_t i = t; i < V; i += kThreads) dst[i] = NAN;
     return;
   }
+  row.lmax = lmax;
 
-  // top-k (reference: speculative_sampling.py:39-48): keeps min(k_eff, max_top_k)
   const int64_t k_req = top_k[r];
   const int64_t k_eff = (k_req > 0 && k_req < V) ? k_req : (int64_t)V;
-  Cut ck;
-  ck.key = 0;
-  ck.take = ck.ties = 0xffffffffu;
-  ck.partial = false;
-  auto all = [](int) { return true; };
-  if (max_top_k > 0 && k_eff < V) {
-    const int64_t kk = k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k;
-    ck = select_cut<false>(sh, row, m, (unsigned long long)kk, all);
-    if (ck.partial) build_tie_table(sh, row, ck.key, 0, all);
-  }
-  // top-k survivor test of a valid element (wave-uniform: ballot inside)
-  auto kept_k = [&](int j, float x) {
-    const uint32_t key = order_key(x);
-    if (!ck.partial) return key >= ck.key;
-    const uint32_t rank = tie_rank(sh, 0, j, key == ck.key);
-    return key > ck.key || (key == ck.key && rank < ck.take);
-  };
-
-  // top-p (reference: speculative_sampling.py:49-55) over the top-k survivors
+  const bool do_k = max_top_k > 0 && k_eff < V;
   const float p = top_p[r];
   const bool do_p = apply_top_p && p < 1.f;
-  Cut cp = ck;
-  if (do_p) {
-    // members: survivors with nonzero fixed mass (zero-mass tokens can never be
-    // the crossing and sit below it); z = their total mass
-    uint64_t memb = 0;
-    uint32_t dummy = 0;
-    unsigned long long z = 0;
-    row.for_chunks([&](int j) {
-      const float x = row.x(j);
-      const bool in = row.valid(j) && kept_k(j, x);
-      const unsigned long long fm = in ? fixed_mass(expf(x - m)) : 0ull;
-      if (fm && j < 64) memb |= 1ull << j;
-      z += fm;
-    });
-    block_sum2(sh, dummy, z);
-    // kept prefix: every token whose preceding mass is <= p z (p <= 0 keeps one)
-    const unsigned long long limit = p > 0.f ? (unsigned long long)((double)p * (double)z) : 0ull;
-    if (NPT > 0) {
-      auto member = [&](int j) { return ((memb >> j) & 1ull) != 0; };
-      cp = select_cut<true>(sh, row, m, limit, member);
-      if (cp.partial) build_tie_table(sh, row, cp.key, 1, member);
-    } else {
-      auto member = [&](int j) {
-        const float x = row.x(j);
-        return kept_k(j, x) && fixed_mass(expf(x - m)) != 0ull;
-      };
-      cp = select_cut<true>(sh, row, m, limit, member);
-      if (cp.partial) build_tie_table(sh, row, cp.key, 1, member);
-    }
-  }
 
-  // softmax over the kept set: everything above cp.key, the first cp.take ties
-  const int which = do_p ? 1 : 0;
-  auto keep_of = [&](int j, float x) {
-    const uint32_t key = order_key(x);
-    if (!cp.partial) return row.valid(j) && key >= cp.key;
-    const uint32_t rank = tie_rank(sh, which, j, row.valid(j) && key == cp.key);
-    return row.valid(j) && (key > cp.key || (key == cp.key && rank < cp.take));
-  };
+  // ---- mass pass: e in place of l, float64 total; then (filtered rows) the count
+  // and mass of the tokens above 2^-8 and 2^-16, which pick the histogram region
   double zs = 0.0;
   row.for_chunks([&](int j) {
-    const float x = row.x(j);
-    const float e = keep_of(j, x) ? expf(x - m) : 0.f;
-    if (NPT > 0) row.set(j, e);
+    const float l = row.x(j);
+    const float e = l == l ? row.mass(l) : 0.f;
+    if (NPT > 0) row.set(j, l == l ? e : NAN);
     zs += (double)e;
   });
-  const float inv = 1.f / (float)block_sum_f64(sh, zs);
-  row.for_chunks([&](int j) {
-    float e;
-    if (NPT > 0) {
-      e = row.x(j);
-    } else {
-      const float x = row.x(j);
-      e = keep_of(j, x) ? expf(x - m) : 0.f;
-    }
-    if (row.valid(j)) dst[(int64_t)j * kThreads + t] = e * inv;
-  });
+  const double z = block_sum_f64(sh, zs);
+  if (!do_k && !do_p) {
+    const float inv = (float)(1.0 / z);
+    row.for_chunks([&](int j) {
+      const float e = row.e(j);
+      if (e == e) dst[(int64_t)j * kThreads + t] = e * inv;
+    });
+    return;
+  }
+
+  const unsigned long long kk =
+      (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
+  filter_row(sh, row, dst, do_k, do_p, kk, p, z);
 }
 
 // ------------------------------------------------------------------ greedy round
@@ -580,12 +732,16 @@ void dispatch_probs(int64_t n, const void* logits, int64_t row_stride, int V,
   launch_probs<DT, R, L>(n, logits, row_stride, V, temperature, top_k, top_p, max_top_k,      \
                          apply_top_p, out, out_stride, stream)
   if (chunks <= 4) RLT_PROBS_CASE(4, 0);
-  else if (chunks <= 16) RLT_PROBS_CASE(16, 0);
+  else if (chunks <= 16) RLT_PROBS_CASE(8, 8);
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
   else if (chunks <= 48) RLT_PROBS_CASE(16, 32);
-  else if (chunks <= kMaxRegChunks) RLT_PROBS_CASE(32, 32);
+  else if (chunks <= kMaxRegChunks) RLT_PROBS_CASE(30, 34);
   else RLT_PROBS_CASE(0, 0);
 #undef RLT_PROBS_CASE
+  // rows handed over by the fast kernel (crowded cuts); the others return at once
+  if (max_top_k > 0 || apply_top_p)
+    rlt_probs_exact_launch(DT, n, logits, row_stride, V, temperature, top_k, top_p, max_top_k,
+                           apply_top_p, out, out_stride, stream);
 }
 
 }  // namespace
