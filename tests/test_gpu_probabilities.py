@@ -291,3 +291,26 @@ def test_greedy_round_bit_exact(pkg, dev, dtype, vocab):
     for a, b in zip(got, want):
         assert torch.equal(a.cpu(), b)
     assert got[0][7, 2].item() == vocab // 2
+
+
+@pytest.mark.parametrize("vocab", [3000, 49152, 65536, 100003])
+def test_crowded_rows_use_the_exact_kernel(pkg, dev, vocab):
+    """Near-flat rows put thousands of tokens into one mass bin, more than the fast
+    kernel's sorted list holds: those rows are recomputed by the exact kernel, the
+    others in the same call stay on the fast path."""
+    _say("crowded rows V", vocab)
+    g = torch.Generator().manual_seed(vocab + 1)
+    n = 6
+    logits = torch.randn(n, vocab, generator=g)
+    logits[0] *= 1e-3                     # flat: top-p cut inside one crowded bin
+    logits[1] *= 1e-3                     # flat: top-k cut inside one crowded bin
+    logits[2] = torch.floor(logits[2] * 2) / 2   # few distinct values, large tie groups
+    logits[3] *= 4                        # ordinary rows
+    logits[4] *= 4
+    logits[5] *= 1e-3
+    tt = [1.0, 1.0, 1.0, 0.7, 0.7, 1.0]
+    tk = [-1, vocab // 3, vocab // 2, -1, 40, vocab // 4]
+    tp = [0.5, 1.0, 0.3, 0.9, 0.95, 0.6]
+    got, want, t, k, p, plan = _run(pkg, dev, logits, tt, tk, tp)
+    _assert_match(got, want, logits, t, k, p, plan)
+    assert (got[1] > 0).sum().item() == vocab // 3
