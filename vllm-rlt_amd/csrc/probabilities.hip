@@ -365,12 +365,12 @@ __device__ __forceinline__ void clear_hist(Shared& sh, int from, int to) {
   }
 }
 
-// Adds histogram stage s: the tokens with e in (2^-8, 1] (s = 0), (2^-16, 2^-8]
-// (s = 1) or [0, 2^-16] (s = 2).
+// Histogram stages: the tokens with e in (2^-8, 1] (stage 0), (2^-16, 2^-8]
+// (stage 1) and [0, 2^-16] (stage 2); admit_stages adds stages [s0, s1).
 template <class Shared, class R>
-__device__ __forceinline__ void admit_stage(Shared& sh, const R& row, int s) {
-  const uint32_t lo = s == 0 ? kFloor8 + 1u : s == 1 ? kFloor16 + 1u : 0u;
-  const uint32_t hi = s == 0 ? 0xffffffffu : s == 1 ? kFloor8 : kFloor16;
+__device__ __forceinline__ void admit_stages(Shared& sh, const R& row, int s0, int s1) {
+  const uint32_t lo = s1 == 1 ? kFloor8 + 1u : s1 == 2 ? kFloor16 + 1u : 0u;
+  const uint32_t hi = s0 == 0 ? 0xffffffffu : s0 == 1 ? kFloor8 : kFloor16;
   row.for_chunks([&](int j) {
     const float e = row.e(j);
     const uint32_t bits = __float_as_uint(e);
@@ -388,19 +388,21 @@ __device__ __forceinline__ void admit_stage(Shared& sh, const R& row, int s) {
 // Leaves the crossing bin's tokens sorted in sh.list[0, sh.list_n).
 template <bool kMass, class Shared, class R>
 __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long long limit,
-                                      int& stages, int mbin, uint32_t mlist) {
+                                      int& stages, int first_stages, int mbin,
+                                      uint32_t mlist) {
   const int t = threadIdx.x, lane = t & 63;
   // admit tokens into the histogram by mass range until the criterion is crossed:
   // e > 2^-8, then (2^-16, 2^-8], then the rest (each stage a prefix of the order,
   // so a scan over the admitted bins is exact for the cuts they contain)
   if (stages == 0) {
-    admit_stage(sh, row, 0);
-    stages = 1;
+    admit_stages(sh, row, 0, first_stages);
+    stages = first_stages;
   }
   scan_select<kMass>(sh, kBins, 0, 0, limit);
   while (sh.sel_bin < 0 && stages < 3) {
     __syncthreads();
-    admit_stage(sh, row, stages++);
+    admit_stages(sh, row, stages, stages + 1);
+    ++stages;
     scan_select<kMass>(sh, kBins, 0, 0, limit);
   }
   const int bin = sh.sel_bin;  // >= 0: the region holds the cut by construction
@@ -491,11 +493,14 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
 template <class Shared, class R>
 __device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __restrict__ dst,
                                            bool do_k, bool do_p, unsigned long long kk, float p,
-                                           double z) {
+                                           double z, uint32_t c16) {
   const int t = threadIdx.x;
   clear_hist(sh, 0, kBins);
   __syncthreads();
   int stages = 0;  // histogram stages admitted so far
+  // first admission: stages 0 and 1 together when few tokens lie above 2^-16 (one
+  // pass instead of two when the cut lies below 2^-8), else stage 0 alone
+  const int first_stages = c16 <= 4096u ? 2 : 1;
 
   auto hand_over = [&]() {  // crowded cut: the exact kernel computes this row
     if (t == 0) dst[0] = __uint_as_float(kCrowdedRowMark);
@@ -503,7 +508,7 @@ __device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __re
   Cut cut;
   if (do_k) {
     // top-k (reference: speculative_sampling.py:39-48): keeps min(k_eff, max_top_k)
-    cut = select<false>(sh, row, kk, stages, kBins, 0u);
+    cut = select<false>(sh, row, kk, stages, first_stages, kBins, 0u);
     if (cut.bin < 0) return hand_over();
   }
   if (do_p) {
@@ -524,9 +529,9 @@ __device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __re
       clear_hist(sh, ck.bin + 1, kBins);
       __syncthreads();
       stages = 3;  // bins up to the top-k bin are complete; later ones hold no survivor
-      cut = select<true>(sh, row, limit, stages, ck.bin, ck.kept_in_bin);
+      cut = select<true>(sh, row, limit, stages, first_stages, ck.bin, ck.kept_in_bin);
     } else {
-      cut = select<true>(sh, row, limit, stages, kBins, 0u);
+      cut = select<true>(sh, row, limit, stages, first_stages, kBins, 0u);
     }
     if (cut.bin < 0) return hand_over();
   }
@@ -640,13 +645,19 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   // ---- mass pass: e in place of l, float64 total; then (filtered rows) the count
   // and mass of the tokens above 2^-8 and 2^-16, which pick the histogram region
   double zs = 0.0;
+  uint32_t c16 = 0;  // tokens with e > 2^-16
   row.for_chunks([&](int j) {
     const float l = row.x(j);
     const float e = l == l ? row.mass(l) : 0.f;
     if (NPT > 0) row.set(j, l == l ? e : NAN);
     zs += (double)e;
+    c16 += __float_as_uint(e) > kFloor16;
   });
   const double z = block_sum_f64(sh, zs);
+  {
+    unsigned long long unused = 0;
+    block_sum2(sh, c16, unused);
+  }
   if (!do_k && !do_p) {
     const float inv = (float)(1.0 / z);
     row.for_chunks([&](int j) {
@@ -658,7 +669,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
 
   const unsigned long long kk =
       (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
-  filter_row(sh, row, dst, do_k, do_p, kk, p, z);
+  filter_row(sh, row, dst, do_k, do_p, kk, p, z, c16);
 }
 
 // ------------------------------------------------------------------ greedy round
