@@ -294,9 +294,9 @@ def test_greedy_round_bit_exact(pkg, dev, dtype, vocab):
 
 
 @pytest.mark.parametrize("vocab", [3000, 49152, 65536, 100003])
-def test_crowded_rows_use_the_exact_kernel(pkg, dev, vocab):
+def test_crowded_rows_use_the_exact_path(pkg, dev, vocab):
     """Near-flat rows put thousands of tokens into one mass bin, more than the fast
-    kernel's sorted list holds: those rows are recomputed by the exact kernel, the
+    kernel's sorted list holds: those rows are recomputed by the exact path, the
     others in the same call stay on the fast path."""
     _say("crowded rows V", vocab)
     g = torch.Generator().manual_seed(vocab + 1)

@@ -28,9 +28,9 @@
 //   2. a block scan finds the bin where the criterion is crossed;
 //   3. the bin's tokens (few: a bin spans 1.1% in mass) are gathered into an LDS
 //      list of (logit key, column), with their logits re-read, and bitonic-sorted;
-//      a scan over the sorted list gives the cut token.  A bin holding more tokens
-//      than the list is narrowed first by key-range histograms over its logits,
-//      and a single tied logit value by column ranks.
+//      a scan over the sorted list gives the cut token.  A row whose cut falls in
+//      a bin holding more tokens than the list takes the exact path (probs_exact.h:
+//      key-range histograms over the re-read logits, ties ranked by column).
 // Top-p after top-k runs on the same histogram with the top-k cut bin reduced to
 // its kept tokens.  Outputs are e * 2^40 / Z_kept, Z_kept the exact fixed-point
 // total of the kept tokens; unfiltered rows sum e in float64.
@@ -48,12 +48,13 @@
 // maximal column; NaN counts as the maximum (torch's argmax rule).
 
 #include "common.h"
-#include "probs_internal.h"
 #include "rlt_mi355x.h"
 
 #include <math.h>
 
 namespace {
+
+#include "probs_exact.h"
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / RLT_WAVE;
@@ -270,7 +271,7 @@ __device__ __forceinline__ void sort_list(Shared& sh, int p) {
 
 // Result of one selection: tokens of bins before `bin` are kept, and of `bin`
 // (whose tokens sit sorted in sh.list) the first kept_in_bin; `kept` is the kept
-// tokens' fixed-point mass.  bin = -1: crowded, handed to the exact kernel.
+// tokens' fixed-point mass.  bin = -1: crowded, left to the exact path.
 struct Cut {
   int bin;
   uint32_t kept_in_bin;
@@ -418,7 +419,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
     nl = (int)mlist;  // the members are the sorted prefix already in the list
   } else {
     if (bin < 0 || n > (uint32_t)Shared::kCap) {
-      // crowded bin: the row goes to the exact kernel (block-uniform)
+      // crowded bin: the row goes to the exact path (block-uniform)
       out.bin = -1;
       return out;
     }
@@ -450,7 +451,26 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       sh.list[i] = v;
     }
     __syncthreads();
-    sort_list(sh, p);
+    if (p <= RLT_WAVE) {
+      // one wave sorts in registers (bitonic network over lane shuffles)
+      if (t < RLT_WAVE) {
+        unsigned long long v = sh.list[lane & (p - 1)];
+        if (lane >= p) v = kCutNone;
+#pragma unroll
+        for (int k = 2; k <= RLT_WAVE; k <<= 1) {
+#pragma unroll
+          for (int j = k >> 1; j > 0; j >>= 1) {
+            const unsigned long long o = __shfl_xor(v, j, RLT_WAVE);
+            const bool keep_min = ((lane & k) == 0) == ((lane & j) == 0);
+            v = keep_min ? (o < v ? o : v) : (o < v ? v : o);
+          }
+        }
+        if (lane < p) sh.list[lane] = v;
+      }
+      __syncthreads();
+    } else {
+      sort_list(sh, p);
+    }
   }
   // scan the sorted members: masses recomputed from the keys (same arithmetic as
   // the mass pass), kept while the cut criterion is not reached
@@ -489,9 +509,11 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
   return out;
 }
 
-// Top-k / top-p cut and the output of one row.
+// Top-k / top-p cut and the output of one row.  Returns false, having written
+// nothing, when a cut falls in a bin more crowded than the list (the caller then
+// runs the exact path).
 template <class Shared, class R>
-__device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __restrict__ dst,
+__device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __restrict__ dst,
                                            bool do_k, bool do_p, unsigned long long kk, float p,
                                            double z, uint32_t c16) {
   const int t = threadIdx.x;
@@ -502,14 +524,11 @@ __device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __re
   // pass instead of two when the cut lies below 2^-8), else stage 0 alone
   const int first_stages = c16 <= 4096u ? 2 : 1;
 
-  auto hand_over = [&]() {  // crowded cut: the exact kernel computes this row
-    if (t == 0) dst[0] = __uint_as_float(kCrowdedRowMark);
-  };
   Cut cut;
   if (do_k) {
     // top-k (reference: speculative_sampling.py:39-48): keeps min(k_eff, max_top_k)
     cut = select<false>(sh, row, kk, stages, first_stages, kBins, 0u);
-    if (cut.bin < 0) return hand_over();
+    if (cut.bin < 0) return false;
   }
   if (do_p) {
     // top-p (reference: speculative_sampling.py:49-55) over the top-k survivors:
@@ -533,7 +552,7 @@ __device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __re
     } else {
       cut = select<true>(sh, row, limit, stages, first_stages, kBins, 0u);
     }
-    if (cut.bin < 0) return hand_over();
+    if (cut.bin < 0) return false;
   }
 
   // ---- softmax over the kept tokens, normalized by their exact fixed-point total:
@@ -552,6 +571,7 @@ __device__ __forceinline__ void filter_row(Shared& sh, const R& row, float* __re
     const float e = row.mass(key_value(~(uint32_t)(v >> 32)));
     dst[(uint32_t)v] = (uint32_t)i < cut.kept_in_bin ? e * inv : 0.f;
   }
+  return true;
 }
 
 template <int DT, int NREG, int NLDS>
@@ -561,7 +581,15 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
     int64_t out_stride) {
   constexpr int NPT = NREG + NLDS;
-  __shared__ SharedT<(NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048)> sh;
+  // the exact path (crowded rows) reuses the fast path's LDS
+  constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
+  constexpr int kTC = NPT > 0 ? NPT : kMaxStreamChunks;
+  union Lds {
+    SharedT<kCapV> fast;
+    exact::SharedT<kTC> ex;
+  };
+  __shared__ Lds lds;
+  SharedT<kCapV>& sh = lds.fast;
   __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
   const int64_t r = blockIdx.x;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -669,7 +697,11 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
 
   const unsigned long long kk =
       (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
-  filter_row(sh, row, dst, do_k, do_p, kk, p, z, c16);
+  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z, c16)) {
+    __syncthreads();
+    exact::exact_row<DT, kTC>(lds.ex, logits, row_stride, V, temperature, top_k, top_p,
+                              max_top_k, apply_top_p, out, out_stride);
+  }
 }
 
 // ------------------------------------------------------------------ greedy round
@@ -749,10 +781,6 @@ void dispatch_probs(int64_t n, const void* logits, int64_t row_stride, int V,
   else if (chunks <= kMaxRegChunks) RLT_PROBS_CASE(30, 34);
   else RLT_PROBS_CASE(0, 0);
 #undef RLT_PROBS_CASE
-  // rows handed over by the fast kernel (crowded cuts); the others return at once
-  if (max_top_k > 0 || apply_top_p)
-    rlt_probs_exact_launch(DT, n, logits, row_stride, V, temperature, top_k, top_p, max_top_k,
-                           apply_top_p, out, out_stride, stream);
 }
 
 }  // namespace

@@ -1,10 +1,9 @@
-// Exact-selection fallback of the sampling-distribution kernel (gfx950).
+// Exact-selection path of the sampling-distribution kernel (gfx950).
 //
-// rlt_probs_exact_kernel computes the same result as rlt_probs_kernel
-// (probabilities.hip; reference vllm_rlt/worker/speculative_sampling.py:8-56) for
-// the rows that kernel hands over: rows whose top-k or top-p cut falls inside a
-// mass bin holding more tokens than its on-chip list (near-uniform rows, large
-// tie groups).  It re-reads the row on every pass and selects on x = logits / T
+// exact::exact_row computes, inside rlt_probs_kernel (probabilities.hip;
+// reference vllm_rlt/worker/speculative_sampling.py:8-56), the rows whose top-k or
+// top-p cut falls inside a mass bin holding more tokens than the fast path's
+// on-chip list (near-uniform rows, large tie groups).  It re-reads the row on every pass and selects on x = logits / T
 // (IEEE division, as torch) with expf masses:
 //
 //   * pass 0 bins every candidate by its distance below the row max, in steps of
@@ -20,15 +19,13 @@
 //     for.
 //
 // Masses are exp(x - max) in 2^-40 fixed point, summed as 64-bit integers: exact
-// and order-independent.  Every other row returns at once: its first output
-// element does not hold the hand-over marker.
+// and order-independent.  Included inside probabilities.hip's anonymous
+// namespace; it shares the fast path's LDS (the row is re-read from memory).
 
-#include "common.h"
-#include "probs_internal.h"
+#pragma once
 
-#include <math.h>
+namespace exact {
 
-namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / RLT_WAVE;
@@ -363,17 +360,19 @@ __device__ __forceinline__ Cut select_cut(Shared& sh, const R& row, float m,
   return c;
 }
 
-template <int DT, int NREG, int NLDS>
-__global__ __launch_bounds__(kThreads) void rlt_probs_exact_kernel(
-    const void* __restrict__ logits, int64_t row_stride, int V,
-    const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
-    const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
-    int64_t out_stride) {
-  constexpr int NPT = NREG + NLDS;
-  // only rows the fast kernel handed over (marker in their first output)
-  if (__float_as_uint(out[(int64_t)blockIdx.x * out_stride]) != kCrowdedRowMark) return;
-  __shared__ SharedT<(NPT > 0 ? NPT : kMaxStreamChunks)> sh;
-  __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
+// One row (block r = blockIdx.x) on the re-reading variant; sh is the caller's LDS.
+template <int DT, int TC>
+__device__ __forceinline__ void exact_row(SharedT<TC>& sh, const void* __restrict__ logits,
+                                          int64_t row_stride, int V,
+                                          const float* __restrict__ temperature,
+                                          const int64_t* __restrict__ top_k,
+                                          const float* __restrict__ top_p, int max_top_k,
+                                          int apply_top_p, float* __restrict__ out,
+                                          int64_t out_stride) {
+  constexpr int NREG = 0, NLDS = 0, NPT = 0;
+  (void)NREG;
+  (void)NLDS;
+  float* const xlds = nullptr;
   const int64_t r = blockIdx.x;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   Row<DT, NREG, NLDS> row;
@@ -498,27 +497,4 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_exact_kernel(
   });
 }
 
-}  // namespace
-
-void rlt_probs_exact_launch(int32_t dtype, int64_t n, const void* logits, int64_t row_stride,
-                            int V, const float* temperature, const int64_t* top_k,
-                            const float* top_p, int max_top_k, int apply_top_p, float* out,
-                            int64_t out_stride, hipStream_t stream) {
-  switch (dtype) {
-    case RLT_F32:
-      hipLaunchKernelGGL((rlt_probs_exact_kernel<RLT_F32, 0, 0>), dim3((unsigned)n),
-                         dim3(kThreads), 0, stream, logits, row_stride, V, temperature, top_k,
-                         top_p, max_top_k, apply_top_p, out, out_stride);
-      break;
-    case RLT_BF16:
-      hipLaunchKernelGGL((rlt_probs_exact_kernel<RLT_BF16, 0, 0>), dim3((unsigned)n),
-                         dim3(kThreads), 0, stream, logits, row_stride, V, temperature, top_k,
-                         top_p, max_top_k, apply_top_p, out, out_stride);
-      break;
-    default:
-      hipLaunchKernelGGL((rlt_probs_exact_kernel<RLT_F16, 0, 0>), dim3((unsigned)n),
-                         dim3(kThreads), 0, stream, logits, row_stride, V, temperature, top_k,
-                         top_p, max_top_k, apply_top_p, out, out_stride);
-      break;
-  }
-}
+}  // namespace exact
