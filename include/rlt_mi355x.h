@@ -152,6 +152,63 @@ int rlt_greedy_accept(const int64_t* draft_tokens, const int64_t* drafts, const 
                       int64_t vocab, int64_t* targets, int64_t* accepted, int64_t* next_token,
                       hipStream_t stream);
 
+/* ---------------------------------------------------------------- KV write side */
+
+/*
+ * Scatter of K and V rows [rows, kv_heads, head_dim] (dim stride 1; row / head
+ * strides in elements) into one layer's pool view [block, token, kv_head, dim]
+ * (`key_cache[:, layer]`, strides in elements) at (blocks[r], offsets[r]).
+ * Rows with mask[r] == 0 (mask optional, uint8 [rows]) or r >= *active (active
+ * optional, int32 scalar on the device) are skipped, as are rows whose block or
+ * offset lies outside [0, num_blocks) x [0, block_size).  dtype: the pool's and the
+ * rows' element type (RLT_F32 / RLT_F16 / RLT_BF16 / RLT_FP8_E4M3 codes copied).
+ * Replaces vllm_rlt/kernels/routing.py:183-223 masked_kv_store,
+ * vllm_rlt/kernels/graph_kv.py:7-67 write_graph_kv and the index_put of
+ * vllm_rlt/core/kv_cache_manager.py:893-895.
+ */
+int rlt_kv_store(const void* k, const void* v, int64_t k_row_stride, int64_t k_head_stride,
+                 int64_t v_row_stride, int64_t v_head_stride, void* key_cache, void* value_cache,
+                 int64_t c_block_stride, int64_t c_token_stride, int64_t c_head_stride,
+                 int64_t num_blocks, int32_t block_size, const int64_t* blocks,
+                 const int64_t* offsets, const uint8_t* mask, const int32_t* active, int64_t rows,
+                 int32_t kv_heads, int32_t head_dim, int32_t dtype, hipStream_t stream);
+
+/*
+ * Quantizing scatter into an FP8 e4m3 pool with per-vector fp32 scales
+ * [block, token, kv_head]: per (row, head) scale = max(amax * (1/448), FLT_MIN), or
+ * fixed_scale when has_fixed_scale; codes = clamp(x / scale, -448, 448) (IEEE
+ * division) rounded to e4m3fn.  Bitwise equal to
+ * vllm_rlt/core/kv_cache_manager.py:50-61 quantize_fp8.  Rows src_dtype
+ * (RLT_F32 / RLT_F16 / RLT_BF16), head_dim <= 256; mask / active / range skipping as
+ * rlt_kv_store.  Replaces vllm_rlt/kernels/triton_attention.py:505-623 store_fp8.
+ */
+int rlt_kv_store_fp8(const void* k, const void* v, int32_t src_dtype, int64_t k_row_stride,
+                     int64_t k_head_stride, int64_t v_row_stride, int64_t v_head_stride,
+                     void* key_codes, void* value_codes, int64_t c_block_stride,
+                     int64_t c_token_stride, int64_t c_head_stride, float* key_scale,
+                     float* value_scale, int64_t s_block_stride, int64_t s_token_stride,
+                     int64_t s_head_stride, int64_t num_blocks, int32_t block_size,
+                     const int64_t* blocks, const int64_t* offsets, const uint8_t* mask,
+                     const int32_t* active, int64_t rows, int32_t kv_heads, int32_t head_dim,
+                     int32_t has_fixed_scale, float fixed_scale, hipStream_t stream);
+
+/*
+ * LAST_EXITED finalize copy.  descriptors int64 [count, 3] = (slot, exit depth,
+ * position); tables int32 [slots, planes, width] (block of each page of each plane).
+ * For every plane p > exit depth, the `layers` x bytes_per_token bytes of the
+ * position's page offset are copied from the exit plane's block to plane p's block,
+ * in both pools [block, layer, token, ...] (strides in elements of elt_bytes; use the
+ * same call on the fp32 scale pools of an FP8 cache).  Descriptors or table entries
+ * outside the tables / pool copy nothing.  Replaces
+ * vllm_rlt/kernels/routing.py:147-180 finalize_kernel (host form
+ * vllm_rlt/core/kv_cache_manager.py:1053-1076 finalize_token).
+ */
+int rlt_kv_finalize(const int64_t* descriptors, int64_t count, const int32_t* tables,
+                    int64_t slots, int32_t width, int32_t planes, int32_t block_size,
+                    int32_t layers, int64_t num_blocks, void* key_pool, void* value_pool,
+                    int64_t block_stride, int64_t layer_stride, int64_t token_stride,
+                    int64_t bytes_per_token, int32_t elt_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

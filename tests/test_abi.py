@@ -115,3 +115,50 @@ def test_probability_host_api_refuses_cpu_tensors(pkg):
     with pytest.raises(ValueError):
         pkg.greedy_accept_batched(torch.zeros(2, 4, dtype=torch.long),
                                   torch.zeros(2, dtype=torch.long), torch.zeros(2, 5, 8))
+
+
+def test_kv_write_entry_points_check_arguments(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null, fake = None, 0x1000
+    # rlt_kv_store: zero rows is a no-op; bad heads / dtype / block size are refused
+    args = [fake, fake, 8, 4, 8, 4, fake, fake, 64, 8, 4, 10, 8, fake, fake, null, null]
+    assert lib.rlt_kv_store(*args, 0, 2, 4, 2, null) == 0
+    assert lib.rlt_kv_store(*args, 3, 0, 4, 2, null) == 1
+    assert lib.rlt_kv_store(*args, 3, 2, 4, 9, null) == 1
+    assert lib.rlt_kv_store(*args[:6], null, fake, *args[8:], 3, 2, 4, 2, null) == 1
+    # rlt_kv_store_fp8: head_dim above one wave's 256 elements is unsupported
+    fp8 = [fake, fake, 2, 8, 4, 8, 4, fake, fake, 64, 8, 4, fake, fake, 16, 2, 1, 10, 8,
+           fake, fake, null, null]
+    assert lib.rlt_kv_store_fp8(*fp8, 0, 2, 4, 0, 0.0, null) == 0
+    assert lib.rlt_kv_store_fp8(*fp8, 3, 2, 512, 0, 0.0, null) == 2
+    assert lib.rlt_kv_store_fp8(*fp8[:12], null, *fp8[13:], 3, 2, 4, 0, 0.0, null) == 1
+    # rlt_kv_finalize: one plane has nothing deeper to copy into
+    fin = [fake, 4, fake, 2, 8]
+    assert lib.rlt_kv_finalize(*fin, 1, 16, 2, 10, fake, fake, 64, 32, 4, 4, 1, null) == 0
+    assert lib.rlt_kv_finalize(*fin, 4, 0, 2, 10, fake, fake, 64, 32, 4, 4, 1, null) == 1
+    assert lib.rlt_kv_finalize(*fin[:2], null, *fin[3:], 4, 16, 2, 10, fake, fake, 64, 32, 4,
+                               4, 1, null) == 1
+
+
+def test_kv_write_host_api_refuses_cpu_tensors(pkg):
+    import torch
+
+    from vllm_rlt_amd import kv_write
+
+    pool = torch.zeros(4, 8, 2, 16, dtype=torch.bfloat16)
+    rows = torch.zeros(3, 2, 16, dtype=torch.bfloat16)
+    idx = torch.zeros(3, dtype=torch.long)
+    with pytest.raises(ValueError, match="ROCm"):
+        kv_write.store_kv(pool, pool.clone(), rows, rows, idx, idx)
+    with pytest.raises(ValueError, match="pool's dtype"):
+        kv_write.store_kv(pool, pool.clone(), rows.float(), rows.float(), idx, idx)
+    codes = torch.zeros(4, 8, 2, 16, dtype=torch.float8_e4m3fn)
+    scale = torch.ones(4, 8, 2)
+    with pytest.raises(ValueError, match="448"):
+        kv_write.store_fp8(rows, rows, codes, codes, scale, scale, idx, idx, 240.0)
+    with pytest.raises(ValueError, match="ROCm"):
+        kv_write.store_fp8(rows, rows, codes, codes, scale, scale, idx, idx, 448.0)
+    with pytest.raises(ValueError, match="descriptor"):
+        kv_write.finalize_rows(torch.zeros(2, 2), torch.zeros(1, 2, 3), pool, pool, 8)

@@ -10,12 +10,16 @@ Drop-in host layer over ``librlt_mi355x.so`` (hand-written gfx950 HIP kernels):
   ``AcceptResult``, ``greedy_accept`` and the device greedy round
   ``greedy_accept_batched`` (vllm_rlt/worker/speculative_sampling.py,
   vllm_rlt/worker/speculative.py:41-53, vllm_rlt/worker/async_speculative.py:706-720).
+* ``kv_write``: ``store_kv``, ``masked_kv_store``, ``write_graph_kv``, ``store_fp8`` and
+  ``finalize_rows``, the KV writers the verify window's keys and values go through
+  (vllm_rlt/kernels/routing.py:147-223, vllm_rlt/kernels/graph_kv.py:52-67,
+  vllm_rlt/kernels/triton_attention.py:579-623).
 
 The directory is named ``vllm-rlt_amd``; it is imported as ``vllm_rlt_amd``
 (see ``__graft_entry__.load_package``).
 """
 
-from . import attention, sampling  # noqa: F401
+from . import attention, kv_write, sampling  # noqa: F401
 from .attention import (  # noqa: F401
     AttentionBackend,
     BackendCapabilities,
@@ -29,4 +33,11 @@ from .sampling import (  # noqa: F401
     greedy_accept,
     greedy_accept_batched,
     speculative_accept,
+)
+from .kv_write import (  # noqa: F401
+    finalize_rows,
+    masked_kv_store,
+    store_fp8,
+    store_kv,
+    write_graph_kv,
 )

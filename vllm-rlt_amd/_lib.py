@@ -55,6 +55,16 @@ _SIGNATURES = {
         _p, _i32, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _i64, _p]),
     "rlt_greedy_accept": (ctypes.c_int, [
         _p, _p, _p, _i32, _i64, _i64, _i32, _i64, _p, _p, _p, _p]),
+    "rlt_kv_store": (ctypes.c_int, [
+        _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32,
+        _p, _p, _p, _p, _i64, _i32, _i32, _i32, _p]),
+    "rlt_kv_store_fp8": (ctypes.c_int, [
+        _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p,
+        _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+        ctypes.c_float, _p]),
+    "rlt_kv_finalize": (ctypes.c_int, [
+        _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i64, _p, _p, _i64, _i64, _i64,
+        _i64, _i32, _p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)
