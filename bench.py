@@ -9,7 +9,9 @@ seeded random permutation of the pool.  Acceptance over vocab 49152 with target 
 draft distributions built at temperature 0.7, top-p 0.9, seeded per-request
 uniforms.  Synthetic data, random values: there is no model or dataset.
 
-One step = the attention call over all 160 verify rows + batched_probabilities of
+One step = the KV write of the 160 window rows' keys and values into the pool (the
+writer that precedes attention in every layer, vllm_rlt/kernels/graph_kv.py:52-67) +
+the attention call over all 160 verify rows + batched_probabilities of
 the 160 target-logit rows (fp32, T = 0.7, top-p 0.9: the reference's _verify,
 vllm_rlt/worker/async_speculative.py:694-704) + speculative_accept over the 32
 requests (draft distributions q are inputs, made in the draft step), all replayed
@@ -73,7 +75,15 @@ def build_workload(dev, seed=0):
     seeds = torch.randint(0, 2**31, (n,), generator=g).tolist()
     u = torch.stack([torch.rand(2 * k_drafts + 1, generator=torch.Generator().manual_seed(s))
                      for s in seeds])
+    # the window's own keys / values and where they go: position len - window + j
+    k_new = torch.randn(n * window, hkv, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    v_new = torch.randn(n * window, hkv, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    pos = (lengths.view(n, 1) - window + torch.arange(window).view(1, window)).reshape(-1)
+    req = torch.arange(n).repeat_interleave(window)
+    w_blocks = tables[req, pos // bs].long()
+    w_offsets = pos % bs
     return dict(n=n, window=window, hq=hq, hkv=hkv, d=d, bs=bs, vocab=vocab, k=k_drafts,
+                k_new=k_new, v_new=v_new, w_blocks=w_blocks.to(dev), w_offsets=w_offsets.to(dev),
                 lengths=lengths, tables=tables, key_pool=key_pool, value_pool=value_pool, q=q,
                 cu=cu, qprob=qprob, pprob=pprob, u=u, layer=1,
                 target_logits=target_logits.reshape(n * window, vocab).contiguous(),
@@ -88,6 +98,12 @@ def attention_bytes(w):
     qo = 2 * w["n"] * w["window"] * w["hq"] * w["d"] * elt
     tables = int(sum(math.ceil(int(n) / w["bs"]) for n in w["lengths"])) * 4
     return kv + qo + tables
+
+
+def kv_write_bytes(w):
+    """Window K and V rows read once and written once (bf16), plus the int64 addresses."""
+    rows = w["n"] * w["window"]
+    return 2 * 2 * rows * w["hkv"] * w["d"] * 2 + 16 * rows
 
 
 def probs_bytes(w):
@@ -114,6 +130,7 @@ def measured_traffic():
 def cpu_baseline(w, repeats=1):
     """The torch-CPU oracle (restatement of the reference Torch path) on this host."""
     from oracle import attention as oatt
+    from oracle import kv_write as okv
     from oracle import sampling as osamp
 
     k_view = w["key_pool"][:, w["layer"]].cpu()
@@ -128,8 +145,11 @@ def cpu_baseline(w, repeats=1):
     drafts_tok = w["draft_tokens"].cpu()
     drafts = torch.full((w["n"],), w["k"], dtype=torch.int64)
     k = w["k"]
+    k_new, v_new = w["k_new"].cpu(), w["v_new"].cpu()
+    w_blocks, w_offsets = w["w_blocks"].cpu(), w["w_offsets"].cpu()
     t0 = time.perf_counter()
     for _ in range(repeats):
+        okv.store_kv(k_view, v_view, k_new, v_new, w_blocks, w_offsets)
         oatt.packed_window_attention(q, k_view, v_view, tables, lengths, cu)
         pprob = osamp.batched_probabilities(logits, temp, top_k, top_p, max_top_k=0,
                                             apply_top_p=True).view(w["n"], w["window"], -1)
@@ -138,7 +158,7 @@ def cpu_baseline(w, repeats=1):
     dt = (time.perf_counter() - t0) / repeats
     return {"value": round(w["n"] * w["window"] / dt, 2), "unit": "verified tokens/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"full config3 verify step (32 requests x 5 rows, ctx U[1024,8192]) x {repeats}, "
+            "sample": f"full config3 verify step (window KV write, 32 requests x 5 rows, ctx U[1024,8192]) x {repeats}, "
                       f"{dt * 1e3:.0f} ms per step, torch-CPU oracle "
                       f"(os.cpu_count={os.cpu_count()})"}
 
@@ -149,7 +169,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("attention", "probs", "accept", "copy"),
+    ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "copy"),
                     help="replay only this part K times and exit (for counter collection); "
                          "'copy' copies a 1 GiB buffer K times (counter calibration)")
     ap.add_argument("--steps-per-graph", type=int, default=10,
@@ -191,6 +211,9 @@ def main():
     top_p = torch.full((rows,), w["top_p"], device=dev)
     pbuf = {}
 
+    def kv_write():
+        pkg.store_kv(kc, vc, w["k_new"], w["v_new"], w["w_blocks"], w["w_offsets"])
+
     def attn():
         return backend.prefill(w["q"], kc, vc, tables, lengths, cu, w["window"])
 
@@ -203,6 +226,7 @@ def main():
         return pkg.speculative_accept(dt_tok, drafts, w["qprob"], pbuf["p"], ua, uf)
 
     def step():
+        kv_write()
         attn()
         probs()
         accept()
@@ -220,8 +244,11 @@ def main():
     # Graphs of `spg` launches back to back: in-graph kernel boundaries cost ~0,
     # so per-launch timings are not inflated by the per-replay launch overhead.
     spg = max(1, min(args.steps_per_graph, args.steps))
-    g_attn, g_probs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    g_kv, g_attn, g_probs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     g_acc, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_kv):
+        for _ in range(spg):
+            kv_write()
     with torch.cuda.graph(g_attn):
         for _ in range(spg):
             out_attn = attn()
@@ -238,7 +265,8 @@ def main():
         g_step.replay()
     torch.cuda.synchronize()
     if args.only:
-        graph = {"attention": g_attn, "probs": g_probs, "accept": g_acc}[args.only]
+        graph = {"kv_write": g_kv, "attention": g_attn, "probs": g_probs,
+                 "accept": g_acc}[args.only]
         for _ in range(max(1, args.steps // spg)):
             graph.replay()
         torch.cuda.synchronize()
@@ -267,6 +295,7 @@ def main():
         torch.cuda.synchronize()
         return sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3 / spg
 
+    t_kv = launch_time(g_kv, replays)
     t_attn = launch_time(g_attn, replays)
     t_probs = launch_time(g_probs, replays)
     t_acc = launch_time(g_acc, replays)
@@ -282,6 +311,7 @@ def main():
         assert torch.equal(a, b)
 
     a_bytes, p_bytes, c_bytes = attention_bytes(w), probs_bytes(w), accept_bytes(w)
+    kv_bytes = kv_write_bytes(w)
     achieved = a_bytes / t_attn / 1e9
     tokens = w["n"] * w["window"]
     result = {
@@ -298,14 +328,15 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded random KV, q and logits; no model or dataset)",
         "config": {
-            "workload": "config3 verify step: packed q_len=5 causal window, 16q/4kv heads, D=128, "
+            "workload": "config3 verify step: window KV write, packed q_len=5 causal window, 16q/4kv heads, D=128, "
                         "bf16 SHARED KV, batch 32, ctx U[1024,8192]; target distributions from "
                         "fp32 logits (T=0.7, top-p 0.9) and acceptance, V=49152",
             "batch": w["n"], "window": w["window"], "q_heads": w["hq"], "kv_heads": w["hkv"],
             "head_dim": w["d"], "block_size": w["bs"], "vocab": w["vocab"],
             "ctx_sum": int(w["lengths"].sum()),
         },
-        "hbm_frac_step": round((a_bytes + p_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
+        "hbm_frac_step": round((kv_bytes + a_bytes + p_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
+        "kv_write_ms": round(t_kv * 1e3, 4),
         "attention_ms": round(t_attn * 1e3, 4),
         "probs_ms": round(t_probs * 1e3, 4),
         "accept_ms": round(t_acc * 1e3, 4),
