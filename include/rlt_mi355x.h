@@ -209,6 +209,88 @@ int rlt_kv_finalize(const int64_t* descriptors, int64_t count, const int32_t* ta
                     int64_t block_stride, int64_t layer_stride, int64_t token_stride,
                     int64_t bytes_per_token, int32_t elt_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------- routing / metadata */
+
+/*
+ * Device routing of the asynchronous verify step.  Descriptors are int64
+ * [count, 3] = (request slot, depth, position) and may live in mapped pinned host
+ * memory.  Grids depend only on the capacities passed (`size`, `max_rows`, ...), so
+ * captured HIP graphs replay with new descriptor contents.  Indices read from
+ * memory are bounds-checked: gathers from outside a pool read zeros, scatters
+ * outside a pool are skipped, a write block that cannot be formed is -1.
+ */
+
+/* slots[row] = descriptor[row].slot for row < count, 0 for count <= row < size.
+ * Replaces vllm_rlt/kernels/routing.py:7-11 slots_kernel. */
+int rlt_route_slots(const int64_t* descriptor, int64_t* slots, int64_t count, int64_t size,
+                    hipStream_t stream);
+
+/* Per-row attention metadata from the descriptor and the slot-major plane tables
+ * int32 [table_rows = slots * planes, width]: plane = depth (planes > 1) or 0;
+ * slots / positions int64 [size], lengths int32 [size] = pos + 1 (0 past count),
+ * blocks / offsets int64 [count] = the position's write address, out_tables int32
+ * [size, out_stride] = the plane's first out_width table entries (0 past count).
+ * Replaces vllm_rlt/kernels/routing.py:14-49 metadata_kernel (caller
+ * vllm_rlt/worker/async_state.py:65-97). */
+int rlt_route_metadata(const int64_t* descriptor, const int32_t* tables, int64_t table_rows,
+                       int32_t width, int32_t page, int32_t planes, int64_t* slots,
+                       int64_t* positions, int32_t* lengths, int64_t* blocks, int64_t* offsets,
+                       int32_t* out_tables, int64_t out_stride, int32_t out_width, int64_t count,
+                       int64_t size, hipStream_t stream);
+
+/* out[row] = pool[slots[row]] (row_elems elements of elt_bytes) for row < count,
+ * zeros for count <= row < size.  Replaces vllm_rlt/kernels/routing.py:52-64
+ * gather_kernel (callers vllm_rlt/worker/async_state.py:104-113,
+ * vllm_rlt/worker/async_speculative.py:605-615). */
+int rlt_route_gather(const void* pool, int64_t pool_rows, int64_t pool_stride,
+                     const int64_t* slots, void* out, int64_t out_stride, int64_t count,
+                     int64_t size, int64_t row_elems, int32_t elt_bytes, hipStream_t stream);
+
+/* pool[slots[row]] = values[row] for row < count.  Replaces
+ * vllm_rlt/kernels/routing.py:67-82 scatter_kernel (callers
+ * vllm_rlt/worker/async_state.py:115-123, vllm_rlt/worker/async_speculative.py:754-760). */
+int rlt_route_scatter(const void* values, int64_t values_stride, const int64_t* slots, void* pool,
+                      int64_t pool_rows, int64_t pool_stride, int64_t count, int64_t row_elems,
+                      int32_t elt_bytes, hipStream_t stream);
+
+/* Segments int64 [num_segments, 5] = (slot, row offset, row count, batch row start,
+ * keep).  Gather: out[start + r] = pool[slot * rows_per_slot + offset + r] for
+ * r < min(count, max_rows).  Replaces vllm_rlt/kernels/routing.py:85-112
+ * gather_segments_kernel (caller vllm_rlt/worker/model_runner.py:519-543). */
+int rlt_route_gather_segments(const void* pool, int64_t pool_slots, int64_t rows_per_slot,
+                              int64_t pool_stride, const int64_t* segments, int64_t num_segments,
+                              int64_t max_rows, void* out, int64_t out_rows, int64_t out_stride,
+                              int64_t row_elems, int32_t elt_bytes, hipStream_t stream);
+
+/* Scatter of the kept segments: pool[slot * rows_per_slot + offset + r] =
+ * values[start + r].  Replaces vllm_rlt/kernels/routing.py:115-144
+ * scatter_segments_kernel (caller vllm_rlt/worker/model_runner.py:559-584). */
+int rlt_route_scatter_segments(const void* values, int64_t values_rows, int64_t values_stride,
+                               const int64_t* segments, int64_t num_segments, int64_t max_rows,
+                               void* pool, int64_t pool_slots, int64_t rows_per_slot,
+                               int64_t pool_stride, int64_t row_elems, int32_t elt_bytes,
+                               hipStream_t stream);
+
+/* KV write addresses of packed query rows: blocks[i] = tables[sequences[i],
+ * positions[i] / page], offsets[i] = positions[i] % page.  Replaces
+ * vllm_rlt/kernels/metadata.py:7-24 expand_kv_addresses (caller
+ * vllm_rlt/worker/buffers.py:289-335). */
+int rlt_expand_kv_addresses(const int64_t* positions, const int32_t* sequences,
+                            const int32_t* tables, int64_t num_sequences, int32_t width,
+                            int32_t page, int64_t* blocks, int64_t* offsets, int64_t n,
+                            hipStream_t stream);
+
+/* Per-row depth-table gather of the recurrent step: out_table[row] =
+ * tables[row, depth[row]] (tables int32 [n, planes, width] with the given strides),
+ * blocks / offsets = the write address of positions[row] in it (floor division),
+ * lengths = positions + 1, or 0 where active (bool, may be NULL) is false.  Replaces
+ * the tensor formulas of vllm_rlt/worker/async_speculative.py:449-466. */
+int rlt_depth_tables(const int32_t* tables, int64_t row_stride, int64_t plane_stride,
+                     int32_t planes, int32_t width, const int64_t* depth,
+                     const int64_t* positions, const uint8_t* active, int32_t block_size,
+                     int32_t* out_table, int64_t out_stride, int64_t* blocks, int64_t* offsets,
+                     int32_t* lengths, int64_t n, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -162,3 +162,23 @@ def test_kv_write_host_api_refuses_cpu_tensors(pkg):
         kv_write.store_fp8(rows, rows, codes, codes, scale, scale, idx, idx, 448.0)
     with pytest.raises(ValueError, match="descriptor"):
         kv_write.finalize_rows(torch.zeros(2, 2), torch.zeros(1, 2, 3), pool, pool, 8)
+
+
+def test_routing_entry_points_check_arguments(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null, fake = None, 0x1000
+    assert lib.rlt_route_slots(null, fake, 0, 0, null) == 0  # empty: no launch
+    assert lib.rlt_route_slots(fake, fake, 5, 4, null) == 1  # count > size
+    assert lib.rlt_route_metadata(fake, fake, 8, 4, 16, 2, *[fake] * 6, 4, 5, 1, 1, null) == 1
+    assert lib.rlt_route_metadata(fake, fake, 8, 4, 16, 2, *[fake] * 6, 4, 4, 0, 0, null) == 0
+    assert lib.rlt_route_metadata(null, null, 8, 4, 16, 2, *[fake] * 6, 4, 4, 0, 3, null) != 1
+    assert lib.rlt_route_gather(fake, 4, 8, fake, fake, 4, 1, 2, 8, 2, null) == 1  # stride < row
+    assert lib.rlt_route_scatter(fake, 8, fake, fake, 4, 8, 0, 8, 2, null) == 0
+    assert lib.rlt_route_gather_segments(fake, 2, 4, 8, fake, 3, 70000, fake, 9, 8, 8, 2,
+                                         null) == 2  # grid y beyond 65535
+    assert lib.rlt_route_scatter_segments(fake, 4, 8, null, 3, 2, fake, 2, 4, 8, 8, 2, null) == 1
+    assert lib.rlt_expand_kv_addresses(fake, fake, fake, 4, 0, 16, fake, fake, 3, null) == 1
+    assert lib.rlt_depth_tables(fake, 8, 4, 2, 4, fake, fake, null, 16, fake, 2, fake, fake,
+                                fake, 3, null) == 1  # out_stride < width

@@ -65,6 +65,21 @@ _SIGNATURES = {
     "rlt_kv_finalize": (ctypes.c_int, [
         _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i64, _p, _p, _i64, _i64, _i64,
         _i64, _i32, _p]),
+    "rlt_route_slots": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
+    "rlt_route_metadata": (ctypes.c_int, [
+        _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p]),
+    "rlt_route_gather": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "rlt_route_scatter": (ctypes.c_int, [
+        _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "rlt_route_gather_segments": (ctypes.c_int, [
+        _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
+    "rlt_route_scatter_segments": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "rlt_expand_kv_addresses": (ctypes.c_int, [
+        _p, _p, _p, _i64, _i32, _i32, _p, _p, _i64, _p]),
+    "rlt_depth_tables": (ctypes.c_int, [
+        _p, _i64, _i64, _i32, _i32, _p, _p, _p, _i32, _p, _i64, _p, _p, _p, _i64, _p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

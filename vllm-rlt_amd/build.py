@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librlt_mi355x.so")
-SOURCES = ["paged_attention.hip", "spec_sampling.hip", "probabilities.hip", "kv_write.hip"]
+SOURCES = ["paged_attention.hip", "spec_sampling.hip", "probabilities.hip", "kv_write.hip", "routing.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
