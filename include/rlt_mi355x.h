@@ -137,6 +137,25 @@ int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t 
                               hipStream_t stream);
 
 /*
+ * Draft proposals of one draft offset: proposed[i] = argmax of logits row i
+ * (i < m; first maximal column, NaN the maximum); then for the random rows
+ * random_rows[j] (j < r), q_out row j = batched_probabilities of that logits row
+ * with temperature[j] / top_k[j] / top_p[j], and proposed[random_rows[j]] =
+ * categorical(q_out row j, u[j]) (0 for an invalid row).  Replaces the draft step
+ * of vllm_rlt/worker/async_speculative.py:645-663 (argmax, _probabilities on
+ * logits[random_rows], categorical, proposed[random_rows] = sampled) in three
+ * launches without host synchronization.  q_out rows are q_stride floats apart (pass
+ * the q[:, offset] view).  Workspace: rlt_categorical_workspace_size(r, vocab).
+ * A random row index outside [0, m) gives an all-NaN q_out row and proposes nothing.
+ */
+int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_stride, int64_t m,
+                       int64_t vocab, const int64_t* random_rows, int64_t r,
+                       const float* temperature, const int64_t* top_k, const float* top_p,
+                       int64_t max_top_k, int32_t apply_top_p, const float* u, float* q_out,
+                       int64_t q_stride, int64_t* proposed, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Greedy verify round: targets = argmax of every verify row (first maximal column,
  * NaN counts as the maximum), accepted = number of leading drafts j < drafts[r]
  * with draft_tokens[r, j] == targets[r, j], next_token = targets[r, accepted].

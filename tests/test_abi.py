@@ -182,3 +182,23 @@ def test_routing_entry_points_check_arguments(pkg):
     assert lib.rlt_expand_kv_addresses(fake, fake, fake, 4, 0, 16, fake, fake, 3, null) == 1
     assert lib.rlt_depth_tables(fake, 8, 4, 2, 4, fake, fake, null, 16, fake, 2, fake, fake,
                                 fake, 3, null) == 1  # out_stride < width
+
+
+def test_propose_drafts_checks_arguments(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null, fake = None, 0x1000
+    base = [fake, 0, 100, 4, 100]
+    # nothing to do
+    assert lib.rlt_propose_drafts(fake, 0, 100, 0, 100, null, 0, null, null, null, 0, 0, null,
+                                  null, 100, fake, null, 0, null) == 0
+    # random rows without their per-row arguments
+    assert lib.rlt_propose_drafts(*base, fake, 2, null, null, null, 0, 0, null, null, 100, fake,
+                                  null, 0, null) == 1
+    # workspace too small for the draws
+    assert lib.rlt_propose_drafts(*base, fake, 2, fake, fake, fake, 0, 0, fake, fake, 100, fake,
+                                  fake, 1, null) == 3
+    # q rows narrower than the vocabulary
+    assert lib.rlt_propose_drafts(*base, fake, 2, fake, fake, fake, 0, 0, fake, fake, 50, fake,
+                                  fake, 1 << 20, null) == 1

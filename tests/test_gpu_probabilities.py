@@ -314,3 +314,62 @@ def test_crowded_rows_use_the_exact_path(pkg, dev, vocab):
     got, want, t, k, p, plan = _run(pkg, dev, logits, tt, tk, tp)
     _assert_match(got, want, logits, t, k, p, plan)
     assert (got[1] > 0).sum().item() == vocab // 3
+
+
+# ------------------------------------------------------------ draft proposals
+
+@pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 5000),
+                                         (torch.float16, 65536)])
+def test_propose_drafts_matches_reference_composition(pkg, dev, dtype, vocab):
+    """async_speculative.py:645-663: argmax for every drafting row, random rows
+    replaced by categorical(q_o, u); q_o written into the q[:, offset] view."""
+    _say("propose_drafts", dtype, vocab)
+    g = torch.Generator().manual_seed(vocab)
+    m = 12
+    logits = (torch.randn(m, vocab, generator=g) * 3).to(dtype)
+    logits[5, 17] = float("nan")  # a NaN row: argmax picks the NaN, its q row is NaN
+    random_rows = torch.tensor([0, 3, 4, 5, 9, 11])
+    r = len(random_rows)
+    t = torch.tensor([0.7, 1.0, 0.5, 1.0, 1.3, 0.9])
+    k = torch.tensor([-1, 40, 0, -1, 7, -1])
+    p = torch.tensor([0.9, 1.0, 0.8, 1.0, 1.0, 0.95])
+    u = torch.rand(r, generator=g)
+    plan = _host_args(k.tolist(), p.tolist(), vocab)
+    q = torch.full((r, 4, vocab), -1.0, device=dev)
+    offset = 2
+    proposed, q_o = pkg.propose_drafts(logits.to(dev), random_rows.to(dev), t.to(dev), k.to(dev),
+                                       p.to(dev), u.to(dev), q_out=q[:, offset], **plan)
+    assert q_o.data_ptr() == q[:, offset].data_ptr()
+    got_q = q[:, offset].cpu()
+    assert bool((q[:, :offset] == -1).all()) and bool((q[:, offset + 1:] == -1).all())
+    want_q = osamp.batched_probabilities(logits[random_rows], t, k, p, **plan)
+    good = [i for i in range(r) if int(random_rows[i]) != 5]
+    _assert_match(got_q[good], want_q[good], logits[random_rows][good], t[good], k[good],
+                  p[good], plan)
+    assert torch.isnan(got_q[3]).all()
+    # tokens: greedy rows are the argmax; random rows the bit-exact categorical of the
+    # q the kernel produced (invalid rows propose token 0)
+    want = logits.float().argmax(-1)
+    sampled, _ = osamp.categorical(got_q, u)
+    want[random_rows] = sampled
+    assert torch.equal(proposed.cpu(), want)
+
+
+def test_propose_drafts_greedy_only_and_bad_rows(pkg, dev):
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(7, 3000, generator=g)
+    proposed, q_o = pkg.propose_drafts(logits.to(dev), None, None, None, None, None,
+                                       max_top_k=0, apply_top_p=False)
+    assert q_o.shape == (0, 3000)
+    assert torch.equal(proposed.cpu(), logits.argmax(-1))
+    # a random row index outside the batch: NaN q row, no proposal written for it
+    rows = torch.tensor([1, 9])
+    ones = torch.ones(2)
+    proposed, q_o = pkg.propose_drafts(logits.to(dev), rows.to(dev), ones.to(dev),
+                                       torch.full((2,), -1).to(dev), ones.to(dev),
+                                       torch.full((2,), 0.5).to(dev), max_top_k=0,
+                                       apply_top_p=False)
+    assert torch.isnan(q_o[1]).all().item()
+    want = logits.argmax(-1)
+    want[1] = osamp.categorical(q_o[:1].cpu(), torch.full((1,), 0.5))[0][0]
+    assert torch.equal(proposed.cpu(), want)

@@ -35,6 +35,7 @@ from .sampling import (  # noqa: F401
     categorical,
     greedy_accept,
     greedy_accept_batched,
+    propose_drafts,
     speculative_accept,
 )
 from .kv_write import (  # noqa: F401

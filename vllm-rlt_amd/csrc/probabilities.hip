@@ -575,8 +575,12 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
 }
 
 template <int DT, int NREG, int NLDS>
+// Output row r (blockIdx.x) is the distribution of logits row rows[r] (rows ==
+// nullptr: row r) of n_src; temperature / top_k / top_p are indexed by r.  A source
+// row outside [0, n_src) gives an all-NaN output row.
 __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
-    const void* __restrict__ logits, int64_t row_stride, int V,
+    const void* __restrict__ logits, const int64_t* __restrict__ rows, int64_t n_src,
+    int64_t row_stride, int V,
     const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
     const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
     int64_t out_stride) {
@@ -592,11 +596,13 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   SharedT<kCapV>& sh = lds.fast;
   __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
   const int64_t r = blockIdx.x;
+  const int64_t src_r = rows ? rows[r] : r;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   Row<DT, NREG, NLDS> row;
   row.xl = xlds;
   row.V = V;
-  row.src = (const char*)logits + r * row_stride * (DT == RLT_F32 ? 4 : 2);
+  const bool src_ok = src_r >= 0 && src_r < n_src;
+  row.src = (const char*)logits + (src_ok ? src_r : 0) * row_stride * (DT == RLT_F32 ? 4 : 2);
   row.npt = NPT > 0 ? NPT : (V + kThreads - 1) / kThreads;
   float* dst = out + r * out_stride;
   const float temp = temperature[r];
@@ -658,7 +664,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     bad |= sh.wave_u32[i];
   }
   __syncthreads();
-  if (bad || !isfinite(lmax) || !(temp > 0.f) || !isfinite(row.c)) {
+  if (bad || !src_ok || !isfinite(lmax) || !(temp > 0.f) || !isfinite(row.c)) {
     for (int64_t i = t; i < V; i += kThreads) dst[i] = NAN;
     return;
   }
@@ -699,7 +705,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
       (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
   if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z, c16)) {
     __syncthreads();
-    exact::exact_row<DT, kTC>(lds.ex, logits, row_stride, V, temperature, top_k, top_p,
+    exact::exact_row<DT, kTC>(lds.ex, logits, src_r, row_stride, V, temperature, top_k, top_p,
                               max_top_k, apply_top_p, out, out_stride);
   }
 }
@@ -755,25 +761,27 @@ __global__ void rlt_greedy_match_kernel(const int64_t* __restrict__ draft_tokens
 }
 
 template <int DT, int NREG, int NLDS>
-void launch_probs(int64_t n, const void* logits, int64_t row_stride, int V, const float* temperature,
-                  const int64_t* top_k, const float* top_p, int max_top_k, int apply_top_p,
-                  float* out, int64_t out_stride, hipStream_t stream) {
+void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_src,
+                  int64_t row_stride, int V, const float* temperature, const int64_t* top_k,
+                  const float* top_p, int max_top_k, int apply_top_p, float* out,
+                  int64_t out_stride, hipStream_t stream) {
   hipLaunchKernelGGL((rlt_probs_kernel<DT, NREG, NLDS>), dim3((unsigned)n), dim3(kThreads), 0,
-                     stream, logits, row_stride, V, temperature, top_k, top_p, max_top_k,
-                     apply_top_p, out, out_stride);
+                     stream, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,
+                     max_top_k, apply_top_p, out, out_stride);
 }
 
 // Row placement by chunks per thread: registers first (at most 32, beyond which
 // the kernel spills), then LDS (at most 128 KiB), else the re-reading variant.
 template <int DT>
-void dispatch_probs(int64_t n, const void* logits, int64_t row_stride, int V,
+void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_src,
+                    int64_t row_stride, int V,
                     const float* temperature, const int64_t* top_k, const float* top_p,
                     int max_top_k, int apply_top_p, float* out, int64_t out_stride,
                     hipStream_t stream) {
   const int chunks = (V + kThreads - 1) / kThreads;
 #define RLT_PROBS_CASE(R, L)                                                                  \
-  launch_probs<DT, R, L>(n, logits, row_stride, V, temperature, top_k, top_p, max_top_k,      \
-                         apply_top_p, out, out_stride, stream)
+  launch_probs<DT, R, L>(n, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,     \
+                         max_top_k, apply_top_p, out, out_stride, stream)
   if (chunks <= 4) RLT_PROBS_CASE(4, 0);
   else if (chunks <= 16) RLT_PROBS_CASE(8, 8);
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
@@ -784,6 +792,11 @@ void dispatch_probs(int64_t n, const void* logits, int64_t row_stride, int V,
 }
 
 }  // namespace
+
+// spec_sampling.hip: categorical draws over strided rows with a scatter list.
+int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u, int64_t m,
+                         int64_t vocab, int64_t* out_index, const int64_t* scatter, int64_t n_out,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 extern "C" {
 
@@ -801,15 +814,15 @@ int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t 
   const int V = (int)vocab;
   switch (logits_dtype) {
     case RLT_F32:
-      dispatch_probs<RLT_F32>(n, logits, row_stride, V, temperature, top_k, top_p, mtk,
+      dispatch_probs<RLT_F32>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk,
                               apply_top_p != 0, out, out_stride, stream);
       break;
     case RLT_BF16:
-      dispatch_probs<RLT_BF16>(n, logits, row_stride, V, temperature, top_k, top_p, mtk,
+      dispatch_probs<RLT_BF16>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk,
                                apply_top_p != 0, out, out_stride, stream);
       break;
     case RLT_F16:
-      dispatch_probs<RLT_F16>(n, logits, row_stride, V, temperature, top_k, top_p, mtk,
+      dispatch_probs<RLT_F16>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk,
                               apply_top_p != 0, out, out_stride, stream);
       break;
     default:
@@ -850,6 +863,61 @@ int rlt_greedy_accept(const int64_t* draft_tokens, const int64_t* drafts, const 
                      dim3(threads), 0, stream, draft_tokens, drafts, targets, n, w1, accepted,
                      next_token);
   return rlt_launch_status();
+}
+
+int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_stride, int64_t m,
+                       int64_t vocab, const int64_t* random_rows, int64_t r,
+                       const float* temperature, const int64_t* top_k, const float* top_p,
+                       int64_t max_top_k, int32_t apply_top_p, const float* u, float* q_out,
+                       int64_t q_stride, int64_t* proposed, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  if (m < 0 || r < 0 || vocab < 1 || vocab > 0x7fffffff || row_stride < vocab ||
+      max_top_k < 0 || (r > 0 && q_stride < vocab))
+    return RLT_ERR_ARGUMENT;
+  if (m == 0 && r == 0) return RLT_OK;
+  if (!logits || !proposed) return RLT_ERR_ARGUMENT;
+  if (r > 0 && (!random_rows || !temperature || !top_k || !top_p || !u || !q_out))
+    return RLT_ERR_ARGUMENT;
+  if (vocab > (int64_t)kMaxStreamChunks * kThreads || m > 0x7fffffff || r > 0x7fffffff)
+    return RLT_ERR_UNSUPPORTED;
+  if (r > 0 && (!workspace || workspace_bytes < rlt_categorical_workspace_size(r, vocab)))
+    return RLT_ERR_WORKSPACE;
+  const int V = (int)vocab;
+  const int mtk = max_top_k > vocab ? V : (int)max_top_k;
+  // greedy proposals for every row, then the random rows' distributions and draws
+  switch (logits_dtype) {
+    case RLT_F32:
+      if (m > 0)
+        hipLaunchKernelGGL(rlt_argmax_rows_kernel<RLT_F32>, dim3((unsigned)m), dim3(kThreads), 0,
+                           stream, logits, row_stride, V, proposed);
+      if (r > 0)
+        dispatch_probs<RLT_F32>(r, logits, random_rows, m, row_stride, V, temperature, top_k,
+                                top_p, mtk, apply_top_p != 0, q_out, q_stride, stream);
+      break;
+    case RLT_BF16:
+      if (m > 0)
+        hipLaunchKernelGGL(rlt_argmax_rows_kernel<RLT_BF16>, dim3((unsigned)m), dim3(kThreads), 0,
+                           stream, logits, row_stride, V, proposed);
+      if (r > 0)
+        dispatch_probs<RLT_BF16>(r, logits, random_rows, m, row_stride, V, temperature, top_k,
+                                 top_p, mtk, apply_top_p != 0, q_out, q_stride, stream);
+      break;
+    case RLT_F16:
+      if (m > 0)
+        hipLaunchKernelGGL(rlt_argmax_rows_kernel<RLT_F16>, dim3((unsigned)m), dim3(kThreads), 0,
+                           stream, logits, row_stride, V, proposed);
+      if (r > 0)
+        dispatch_probs<RLT_F16>(r, logits, random_rows, m, row_stride, V, temperature, top_k,
+                                top_p, mtk, apply_top_p != 0, q_out, q_stride, stream);
+      break;
+    default:
+      return RLT_ERR_UNSUPPORTED;
+  }
+  if (r == 0) return rlt_launch_status();
+  const int st = rlt_launch_status();
+  if (st != RLT_OK) return st;
+  return rlt_categorical_rows(q_out, q_stride, u, r, vocab, proposed, random_rows, m, workspace,
+                              workspace_bytes, stream);
 }
 
 }  // extern "C"

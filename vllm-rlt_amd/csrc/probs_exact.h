@@ -360,10 +360,11 @@ __device__ __forceinline__ Cut select_cut(Shared& sh, const R& row, float m,
   return c;
 }
 
-// One row (block r = blockIdx.x) on the re-reading variant; sh is the caller's LDS.
+// One row (block r = blockIdx.x, logits row src_r) on the re-reading variant; sh is
+// the caller's LDS.
 template <int DT, int TC>
 __device__ __forceinline__ void exact_row(SharedT<TC>& sh, const void* __restrict__ logits,
-                                          int64_t row_stride, int V,
+                                          int64_t src_r, int64_t row_stride, int V,
                                           const float* __restrict__ temperature,
                                           const int64_t* __restrict__ top_k,
                                           const float* __restrict__ top_p, int max_top_k,
@@ -378,7 +379,7 @@ __device__ __forceinline__ void exact_row(SharedT<TC>& sh, const void* __restric
   Row<DT, NREG, NLDS> row;
   row.xl = xlds;
   row.V = V;
-  row.src = (const char*)logits + r * row_stride * (DT == RLT_F32 ? 4 : 2);
+  row.src = (const char*)logits + src_r * row_stride * (DT == RLT_F32 ? 4 : 2);
   row.temp = temperature[r];
   row.npt = NPT > 0 ? NPT : (V + kThreads - 1) / kThreads;
   float* dst = out + r * out_stride;

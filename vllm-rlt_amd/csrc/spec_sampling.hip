@@ -517,11 +517,13 @@ struct CatShared {
   uint32_t flags;
 };
 
-// grid (m), kDrawThreads threads: one row of raw weights per workgroup.
+// grid (m), kDrawThreads threads: one row of raw weights (row i at weights + i *
+// w_stride) per workgroup.  The index goes to out_index[i], or with a scatter list
+// to out_index[scatter[i]] when that lies in [0, n_out); out_valid may be null.
 __global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
-    const float* __restrict__ weights, int64_t V, const float* __restrict__ u,
+    const float* __restrict__ weights, int64_t V, int64_t w_stride, const float* __restrict__ u,
     int64_t* __restrict__ out_index, uint8_t* __restrict__ out_valid,
-    int32_t* __restrict__ slow_count) {
+    const int64_t* __restrict__ scatter, int64_t n_out, int32_t* __restrict__ slow_count) {
   __shared__ CatShared sh;
   const int64_t i = blockIdx.x;
   const int t = threadIdx.x;
@@ -529,7 +531,7 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
   const int lane = t & 63;
   if (t == 0) sh.flags = 0;
   WeightRow w;
-  w.a = weights + i * V;
+  w.a = weights + i * w_stride;
   w.b = nullptr;
   w.am = w.bm = 1.f;
   w.residual = false;
@@ -566,8 +568,13 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
   bool valid;
   draw_from_tiles(w, V, u[i], tiles, f, false, vec_ok, sh.ds, slow_count, &index, &valid);
   if (t == 0) {
-    out_index[i] = index;
-    out_valid[i] = valid;
+    if (!scatter) {
+      out_index[i] = index;
+    } else {
+      const int64_t d = scatter[i];
+      if (d >= 0 && d < n_out) out_index[d] = index;
+    }
+    if (out_valid) out_valid[i] = valid;
   }
 }
 
@@ -858,8 +865,8 @@ int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t voc
   const Layout l = layout_for(0, 0, vocab);
   if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
   int32_t* slow = (int32_t*)((char*)workspace + l.slow);
-  rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(weights, vocab, u, index, valid,
-                                                                  slow);
+  rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(weights, vocab, vocab, u, index,
+                                                                  valid, nullptr, m, slow);
   return rlt_launch_status();
 }
 
@@ -883,3 +890,18 @@ int rlt_row_mass_f32(const float* x, int64_t rows, int64_t vocab, float* out, vo
 }
 
 }  // extern "C"
+
+// Categorical draws over strided weight rows, scattered into out_index (used by the
+// draft proposal in probabilities.hip); the workspace is rlt_categorical's.
+int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u, int64_t m,
+                         int64_t vocab, int64_t* out_index, const int64_t* scatter, int64_t n_out,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (m < 0 || vocab < 1 || w_stride < vocab) return RLT_ERR_ARGUMENT;
+  if (m == 0) return RLT_OK;
+  const Layout l = layout_for(0, 0, vocab);
+  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
+  int32_t* slow = (int32_t*)((char*)workspace + l.slow);
+  rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(
+      weights, vocab, w_stride, u, out_index, nullptr, scatter, n_out, slow);
+  return rlt_launch_status();
+}

@@ -115,6 +115,58 @@ def greedy_accept_batched(draft_tokens, drafts, target_logits):
     return targets, accepted, next_token
 
 
+def propose_drafts(logits, random_rows, temperature, top_k, top_p, u, *, max_top_k, apply_top_p,
+                   q_out=None):
+    """Draft proposals of one draft offset: ``(proposed int64 [m], q_o float32 [r, V])``.
+
+    reference: vllm_rlt/worker/async_speculative.py:645-663 -- ``proposed =
+    logits.argmax(-1)``; for the random rows ``q_o = batched_probabilities(
+    logits[random_rows], temperature, top_k, top_p)``, ``proposed[random_rows] =
+    categorical(q_o, u)[0]``.  ``temperature`` / ``top_k`` / ``top_p`` / ``u`` are per
+    random row.  ``q_out`` (optional) is a ``[r, V]`` float32 view with unit column
+    stride to write q_o into (e.g. ``q[ranks, offset]`` when ranks are contiguous:
+    ``q[:, offset]``); otherwise a new tensor.
+    """
+    if logits.ndim != 2:
+        raise ValueError("logits must be a 2-D [m, V] tensor")
+    m, vocab = logits.shape
+    if random_rows is None:
+        random_rows = torch.empty(0, dtype=torch.int64, device=logits.device)
+    if random_rows.ndim != 1:
+        raise ValueError("random_rows must be 1-D")
+    r = random_rows.shape[0]
+    for name, value in (("temperature", temperature), ("top_k", top_k), ("top_p", top_p),
+                        ("u", u)):
+        if r and value.shape != (r,):
+            raise ValueError(f"{name} must have shape [{r}], got {tuple(value.shape)}")
+    if max_top_k < 0:
+        raise ValueError("max_top_k must be nonnegative")
+    _lib.require_gpu(logits, random_rows, *((temperature, top_k, top_p, u) if r else ()), q_out)
+    device = logits.device
+    proposed = torch.empty(m, dtype=torch.int64, device=device)
+    if q_out is None:
+        q_out = torch.empty((r, vocab), dtype=torch.float32, device=device)
+    elif q_out.shape != (r, vocab) or q_out.dtype != torch.float32 or q_out.stride(-1) != 1:
+        raise ValueError("q_out must be a float32 [r, V] view with unit column stride")
+    if m == 0 and r == 0:
+        return proposed, q_out
+    if vocab == 0:
+        raise ValueError("logits must have V >= 1")
+    x = logits if logits.dtype in _LOGIT_DTYPES else logits.float()
+    x = _rows(x)
+    rows = _i64(random_rows)
+    lib = _lib.library()
+    ws = _lib.workspace(lib.rlt_categorical_workspace_size(r, vocab) if r else 0, device)
+    args = (_f32(temperature), _i64(top_k), _f32(top_p), _f32(u)) if r else (None,) * 4
+    status = lib.rlt_propose_drafts(
+        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), m, vocab, _lib.ptr(rows), r,
+        *(_lib.ptr(a) for a in args[:3]), int(max_top_k), int(bool(apply_top_p)),
+        _lib.ptr(args[3]), _lib.ptr(q_out), q_out.stride(0) if r else vocab, _lib.ptr(proposed),
+        _lib.ptr(ws), ws.numel(), _lib.stream_of(device))
+    _lib.check(status, "rlt_propose_drafts")
+    return proposed, q_out
+
+
 def categorical(weights, u):
     """Inverse-CDF draw from ``[m, V]`` nonnegative weights with ``[m]`` uniforms.
 
