@@ -320,3 +320,44 @@ def test_more_rows_than_the_persistent_index_uses_grid_kernel(kernel, dev):
         assert torch.equal(alone[0], got[row])
     want = oatt.paged_attention(q[sel], k, v, tables[sel], ctx[sel])
     _close(got[sel], want, dtype)
+
+
+def _dense_packed(q, k_seq, v_seq, q_len, length, window=0):
+    """Closed form: fp32 SDPA of one sequence's q_len queries over its `length` keys,
+    query i at absolute position length - q_len + i (bottom-right causal), seeing the
+    last `window` keys when window > 0; GQA by kv head h // (Hq / Hkv)."""
+    hq, hkv = q.shape[1], k_seq.shape[1]
+    kk = k_seq.float().repeat_interleave(hq // hkv, 1).transpose(0, 1)
+    vv = v_seq.float().repeat_interleave(hq // hkv, 1).transpose(0, 1)
+    pos = torch.arange(length - q_len, length).view(-1, 1)
+    key = torch.arange(length).view(1, -1)
+    mask = key <= pos
+    if window:
+        mask &= key > pos - window
+    return torch.nn.functional.scaled_dot_product_attention(
+        q.float().transpose(0, 1), kk, vv, attn_mask=mask[None]).transpose(0, 1)
+
+
+@pytest.mark.parametrize("window", [0, 256])
+def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window):
+    """Prompt prefill on the same backend: a 1024-token prompt from scratch, a
+    512-token chunk after a 1536-token prefix, and a short window, packed together."""
+    _say("long prefill", window)
+    g = torch.Generator().manual_seed(21)
+    bs, hq, hkv, d, dtype = 16, 16, 4, 128, torch.bfloat16
+    seqs = [(1024, 1024), (2048, 512), (3000, 37)]
+    pages = sum(-(-n // bs) for n, _ in seqs) + 2
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables([n for n, _ in seqs], bs, pages, g)
+    total = sum(c for _, c in seqs)
+    q = torch.randn(total, hq, d, generator=g).to(dtype)
+    lengths = torch.tensor([n for n, _ in seqs], dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor([c for _, c in seqs]).cumsum(0)), dtype=torch.int32)
+    got = kernel.prefill(q.to(dev), k.to(dev), v.to(dev), tables.to(dev), lengths.to(dev),
+                         cu.to(dev), max(c for _, c in seqs), window=window).cpu()
+    for s, (n, c) in enumerate(seqs):
+        pages_s = tables[s, : -(-n // bs)].long()
+        k_seq = k[pages_s].reshape(-1, hkv, d)[:n]
+        v_seq = v[pages_s].reshape(-1, hkv, d)[:n]
+        want = _dense_packed(q[cu[s]:cu[s + 1]], k_seq, v_seq, c, n, window)
+        torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
