@@ -127,6 +127,47 @@ def measured_traffic():
         return None
 
 
+def config2_decode(pkg, dev):
+    """BASELINE.json configs[1] (the decode attention config the >=70%-of-HBM target names:
+    batch 64, ctx U[512, 4096]): one launch, its algorithmic bytes and bandwidth."""
+    g = torch.Generator().manual_seed(2)
+    n, planes, bs, h, d = 64, 4, 16, 16, 128
+    lengths = torch.randint(512, 4097, (n,), generator=g)
+    exit_depth = torch.randint(1, 5, (n,), generator=g)
+    width = 4096 // bs
+    pool = n * planes * width
+    gd = torch.Generator(device=dev).manual_seed(2)
+    k = torch.randn(pool, bs, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(pool, bs, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    tables = torch.randperm(pool, generator=g).int().view(n, planes, width)
+    rows = tables[torch.arange(n), exit_depth - 1].to(dev)
+    q = torch.randn(n, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    ctx = lengths.int().to(dev)
+    kern = pkg.MI355XPagedAttention()
+    for _ in range(3):
+        kern(q, k, v, rows, ctx)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(10):
+            kern(q, k, v, rows, ctx)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(5):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    t = a.elapsed_time(b) / 50 / 1e3
+    nbytes = int(lengths.sum()) * 2 * h * d * 2 + 2 * n * h * d * 2 + int(
+        sum(math.ceil(int(x) / bs) for x in lengths)) * 4
+    return {"workload": "config2 decode attention: batch 64, ctx U[512,4096], 16/16 heads, D=128, "
+                        "bf16, 4 LAST_EXITED planes, exit depth U{1..4}",
+            "us": round(t * 1e6, 1), "algorithmic_bytes": nbytes,
+            "GBps": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def cpu_baseline(w, repeats=1):
     """The torch-CPU oracle (restatement of the reference Torch path) on this host."""
     from oracle import attention as oatt
@@ -169,6 +210,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-config2", action="store_true",
+                    help="skip the secondary config-2 decode attention measurement")
     ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "copy"),
                     help="replay only this part K times and exit (for counter collection); "
                          "'copy' copies a 1 GiB buffer K times (counter calibration)")
@@ -353,6 +396,9 @@ def main():
             "algorithmic_bytes": a_bytes,
         },
     }
+    if not args.no_config2:
+        del g_kv, g_attn, g_probs, g_acc, g_step
+        result["config2_decode_attention"] = config2_decode(pkg, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
