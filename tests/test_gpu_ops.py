@@ -1,0 +1,60 @@
+"""torch.ops.rlt_mi355x operators on the GPU: same results as the package API, and
+torch.library.opcheck's schema and fake-tensor checks."""
+
+import pytest
+import torch
+
+from tests.attn_cases import make_pool, random_tables
+
+pytestmark = pytest.mark.gpu
+CHECKS = ("test_schema", "test_faketensor")
+
+
+def test_attention_and_sampling_ops_match_the_api(pkg, dev):
+    g = torch.Generator().manual_seed(1)
+    _, _, k, v = make_pool(40, 1, 16, 4, 128, torch.bfloat16, g)
+    lengths = torch.tensor([100, 37, 300], dtype=torch.int32)
+    tables = random_tables(lengths.tolist(), 16, 40, g)
+    q = torch.randn(15, 16, 128, generator=g).bfloat16()
+    cu = torch.tensor([0, 5, 10, 15], dtype=torch.int32)
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), lengths.to(dev), None, None,
+            cu.to(dev), 5, 0)
+    got = torch.ops.rlt_mi355x.paged_attention(*args)
+    want = pkg.MI355XPagedAttention().prefill(*args[:5], cu.to(dev), 5)
+    assert torch.equal(got, want)
+    torch.library.opcheck(torch.ops.rlt_mi355x.paged_attention, args, test_utils=CHECKS)
+
+    logits = torch.randn(6, 3000, generator=g).to(dev)
+    t, tk = torch.full((6,), 0.8, device=dev), torch.full((6,), -1, dtype=torch.int64, device=dev)
+    tp = torch.full((6,), 0.9, device=dev)
+    pa = (logits, t, tk, tp, 0, True)
+    probs = torch.ops.rlt_mi355x.spec_probs(*pa)
+    assert torch.equal(probs, pkg.batched_probabilities(logits, t, tk, tp, max_top_k=0,
+                                                        apply_top_p=True))
+    torch.library.opcheck(torch.ops.rlt_mi355x.spec_probs, pa, test_utils=CHECKS)
+
+    u = torch.rand(6, generator=g).to(dev)
+    idx, valid = torch.ops.rlt_mi355x.categorical(probs, u)
+    want_idx, want_valid = pkg.categorical(probs, u)
+    assert torch.equal(idx, want_idx) and torch.equal(valid, want_valid)
+
+    n, w1 = 2, 2
+    pq = probs[: n * (w1 + 1)].view(n, w1 + 1, -1).contiguous()
+    qq = probs[: n * w1].view(n, w1, -1).contiguous()
+    dt = torch.stack([pkg.categorical(qq[:, j].contiguous(), u[:n])[0] for j in range(w1)], 1)
+    drafts = torch.full((n,), w1, dtype=torch.int64, device=dev)
+    ua, uf = torch.rand(n, w1, generator=g).to(dev), torch.rand(n, generator=g).to(dev)
+    got = torch.ops.rlt_mi355x.spec_accept(dt, drafts, qq, pq, ua, uf)
+    want = pkg.speculative_accept(dt, drafts, qq, pq, ua, uf)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+
+
+def test_kv_write_op_mutates_the_pool(pkg, dev):
+    kc = torch.zeros(8, 16, 2, 64, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    k = torch.randn(3, 2, 64, device=dev).bfloat16()
+    blocks = torch.tensor([1, 5, 7], device=dev)
+    offsets = torch.tensor([0, 15, 3], device=dev)
+    torch.ops.rlt_mi355x.store_kv(kc, vc, k, -k, blocks, offsets, None, None)
+    assert torch.equal(kc[blocks, offsets], k) and torch.equal(vc[blocks, offsets], -k)

@@ -14,6 +14,8 @@ Drop-in host layer over ``librlt_mi355x.so`` (hand-written gfx950 HIP kernels):
   ``finalize_rows``, the KV writers the verify window's keys and values go through
   (vllm_rlt/kernels/routing.py:147-223, vllm_rlt/kernels/graph_kv.py:52-67,
   vllm_rlt/kernels/triton_attention.py:579-623).
+* ``ops``: the same entry points as ``torch.ops.rlt_mi355x.*`` operators (ROCm device
+  implementations and fake shape functions; the reference's torch_bindings pattern).
 * ``routing``: device metadata and request routing of the asynchronous verify step
   (vllm_rlt/kernels/routing.py:7-144, vllm_rlt/kernels/metadata.py:7-24, the depth-table
   gather of vllm_rlt/worker/async_speculative.py:449-466), graph-capturable.
@@ -22,7 +24,7 @@ The directory is named ``vllm-rlt_amd``; it is imported as ``vllm_rlt_amd``
 (see ``__graft_entry__.load_package``).
 """
 
-from . import attention, kv_write, routing, sampling  # noqa: F401
+from . import attention, kv_write, ops, routing, sampling  # noqa: F401
 from .attention import (  # noqa: F401
     AttentionBackend,
     BackendCapabilities,

@@ -1,0 +1,144 @@
+"""The hot path as torch operators in the ``rlt_mi355x`` namespace.
+
+The reference binds its native code as a ``TORCH_LIBRARY`` schema
+(csrc/torch_bindings.cpp:7-13) next to Python ``torch.library`` fragments
+(vllm_rlt/kernels/activation.py:34-39).  These operators are the same kind of binding
+for the gfx950 kernels: ``torch.ops.rlt_mi355x.<name>`` with a fixed schema, an
+implementation for ROCm device tensors only (a CPU tensor finds no kernel and raises:
+there is no fallback), and a fake (meta) implementation so that graph capture and
+``torch.compile`` can trace shapes without running them.  Every implementation calls
+the package's wrappers of ``librlt_mi355x.so``; the Python shims with the reference
+signatures stay in ``attention``, ``sampling`` and ``kv_write``.
+"""
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import kv_write as _kv
+from . import sampling as _samp
+from .attention import MI355XPagedAttention
+
+_ATTN = MI355XPagedAttention()
+
+
+@torch.library.custom_op("rlt_mi355x::paged_attention", mutates_args=(), device_types="cuda")
+def paged_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                    block_tables: torch.Tensor, context_lengths: torch.Tensor,
+                    key_scale: Optional[torch.Tensor], value_scale: Optional[torch.Tensor],
+                    cu_seqlens_q: Optional[torch.Tensor], max_seqlen_q: int,
+                    window: int) -> torch.Tensor:
+    """Per-row (cu_seqlens_q None) or packed causal-window paged attention;
+    reference: vllm_rlt/kernels/paged_attention.py:13-90, triton_attention.py:386-404."""
+    return _ATTN._run(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+                      max_seqlen_q, key_scale, value_scale, window)
+
+
+@paged_attention.register_fake
+def _(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value_scale,
+      cu_seqlens_q, max_seqlen_q, window):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("rlt_mi355x::spec_probs", mutates_args=(), device_types="cuda")
+def spec_probs(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.Tensor,
+               top_p: torch.Tensor, max_top_k: int, apply_top_p: bool) -> torch.Tensor:
+    """reference: vllm_rlt/worker/speculative_sampling.py:8-56 batched_probabilities."""
+    return _samp.batched_probabilities(logits, temperature, top_k, top_p, max_top_k=max_top_k,
+                                       apply_top_p=apply_top_p)
+
+
+@spec_probs.register_fake
+def _(logits, temperature, top_k, top_p, max_top_k, apply_top_p):
+    return logits.new_empty(logits.shape, dtype=torch.float32)
+
+
+@torch.library.custom_op("rlt_mi355x::categorical", mutates_args=(), device_types="cuda")
+def categorical(weights: torch.Tensor, u: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """reference: vllm_rlt/worker/speculative_sampling.py:59-85."""
+    return _samp.categorical(weights, u)
+
+
+@categorical.register_fake
+def _(weights, u):
+    m = weights.shape[0]
+    return (weights.new_empty((m,), dtype=torch.int64), weights.new_empty((m,), dtype=torch.bool))
+
+
+@torch.library.custom_op("rlt_mi355x::spec_accept", mutates_args=(), device_types="cuda")
+def spec_accept(draft_tokens: torch.Tensor, drafts: torch.Tensor, q: torch.Tensor,
+                p: torch.Tensor, u_accept: torch.Tensor, u_final: torch.Tensor
+                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(tokens, accepted, final, error); reference: speculative_sampling.py:88-181."""
+    return tuple(_samp.speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final))
+
+
+@spec_accept.register_fake
+def _(draft_tokens, drafts, q, p, u_accept, u_final):
+    n, w1 = draft_tokens.shape
+    i64 = dict(dtype=torch.int64)
+    return (p.new_empty((n, w1 + 1), **i64), p.new_empty((n,), **i64), p.new_empty((n,), **i64),
+            p.new_empty((n,), dtype=torch.bool))
+
+
+@torch.library.custom_op("rlt_mi355x::greedy_accept", mutates_args=(), device_types="cuda")
+def greedy_accept(draft_tokens: torch.Tensor, drafts: torch.Tensor, target_logits: torch.Tensor
+                  ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(targets, accepted, next_token); reference: vllm_rlt/worker/async_speculative.py:706-720."""
+    return _samp.greedy_accept_batched(draft_tokens, drafts, target_logits)
+
+
+@greedy_accept.register_fake
+def _(draft_tokens, drafts, target_logits):
+    n, w1 = draft_tokens.shape
+    i64 = dict(dtype=torch.int64)
+    return (target_logits.new_empty((n, w1 + 1), **i64), target_logits.new_empty((n,), **i64),
+            target_logits.new_empty((n,), **i64))
+
+
+@torch.library.custom_op("rlt_mi355x::propose_drafts", mutates_args=(), device_types="cuda")
+def propose_drafts(logits: torch.Tensor, random_rows: torch.Tensor, temperature: torch.Tensor,
+                   top_k: torch.Tensor, top_p: torch.Tensor, u: torch.Tensor, max_top_k: int,
+                   apply_top_p: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(proposed, q_o); reference: vllm_rlt/worker/async_speculative.py:645-663."""
+    return _samp.propose_drafts(logits, random_rows, temperature, top_k, top_p, u,
+                                max_top_k=max_top_k, apply_top_p=apply_top_p)
+
+
+@propose_drafts.register_fake
+def _(logits, random_rows, temperature, top_k, top_p, u, max_top_k, apply_top_p):
+    return (logits.new_empty((logits.shape[0],), dtype=torch.int64),
+            logits.new_empty((random_rows.shape[0], logits.shape[1]), dtype=torch.float32))
+
+
+@torch.library.custom_op("rlt_mi355x::store_kv", mutates_args=("key_cache", "value_cache"),
+                         device_types="cuda")
+def store_kv(key_cache: torch.Tensor, value_cache: torch.Tensor, k: torch.Tensor,
+             v: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor,
+             mask: Optional[torch.Tensor], active: Optional[torch.Tensor]) -> None:
+    """reference: vllm_rlt/kernels/routing.py:210-223, vllm_rlt/kernels/graph_kv.py:52-67."""
+    _kv.store_kv(key_cache, value_cache, k, v, blocks, offsets, mask=mask, active=active)
+
+
+@torch.library.custom_op("rlt_mi355x::store_fp8",
+                         mutates_args=("key_codes", "value_codes", "key_scale", "value_scale"),
+                         device_types="cuda")
+def store_fp8(k: torch.Tensor, v: torch.Tensor, key_codes: torch.Tensor,
+              value_codes: torch.Tensor, key_scale: torch.Tensor, value_scale: torch.Tensor,
+              blocks: torch.Tensor, offsets: torch.Tensor, mask: Optional[torch.Tensor],
+              active: Optional[torch.Tensor], fixed_scale: Optional[float]) -> None:
+    """reference: vllm_rlt/kernels/triton_attention.py:579-623."""
+    _kv.store_fp8(k, v, key_codes, value_codes, key_scale, value_scale, blocks, offsets,
+                  _kv.FP8_E4M3_MAX, mask=mask, active=active, fixed_scale=fixed_scale)
+
+
+@torch.library.custom_op("rlt_mi355x::finalize_rows", mutates_args=("key_pool", "value_pool"),
+                         device_types="cuda")
+def finalize_rows(descriptor: torch.Tensor, tables: torch.Tensor, key_pool: torch.Tensor,
+                  value_pool: torch.Tensor, block_size: int) -> None:
+    """reference: vllm_rlt/kernels/routing.py:147-180 finalize_kernel."""
+    _kv.finalize_rows(descriptor, tables, key_pool, value_pool, block_size)
+
+
+OPS = ("paged_attention", "spec_probs", "categorical", "spec_accept", "greedy_accept",
+       "propose_drafts", "store_kv", "store_fp8", "finalize_rows")
