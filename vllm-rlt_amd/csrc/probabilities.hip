@@ -389,16 +389,12 @@ __device__ __forceinline__ void admit_stages(Shared& sh, const R& row, int s0, i
 // Leaves the crossing bin's tokens sorted in sh.list[0, sh.list_n).
 template <bool kMass, class Shared, class R>
 __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long long limit,
-                                      int& stages, int first_stages, int mbin,
-                                      uint32_t mlist) {
+                                      int& stages, int mbin, uint32_t mlist) {
   const int t = threadIdx.x, lane = t & 63;
-  // admit tokens into the histogram by mass range until the criterion is crossed:
-  // e > 2^-8, then (2^-16, 2^-8], then the rest (each stage a prefix of the order,
-  // so a scan over the admitted bins is exact for the cuts they contain)
-  if (stages == 0) {
-    admit_stages(sh, row, 0, first_stages);
-    stages = first_stages;
-  }
+  // the histogram holds stages [0, stages); admit further tokens by mass range until
+  // the criterion is crossed: e > 2^-8 (admitted by the mass pass), then
+  // (2^-16, 2^-8], then the rest (each stage a prefix of the order, so a scan over
+  // the admitted bins is exact for the cuts they contain)
   scan_select<kMass>(sh, kBins, 0, 0, limit);
   while (sh.sel_bin < 0 && stages < 3) {
     __syncthreads();
@@ -515,19 +511,14 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
 template <class Shared, class R>
 __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __restrict__ dst,
                                            bool do_k, bool do_p, unsigned long long kk, float p,
-                                           double z, uint32_t c16) {
+                                           double z) {
   const int t = threadIdx.x;
-  clear_hist(sh, 0, kBins);
-  __syncthreads();
-  int stages = 0;  // histogram stages admitted so far
-  // first admission: stages 0 and 1 together when few tokens lie above 2^-16 (one
-  // pass instead of two when the cut lies below 2^-8), else stage 0 alone
-  const int first_stages = c16 <= 4096u ? 2 : 1;
+  int stages = 1;  // histogram stages admitted so far (stage 0 by the mass pass)
 
   Cut cut;
   if (do_k) {
     // top-k (reference: speculative_sampling.py:39-48): keeps min(k_eff, max_top_k)
-    cut = select<false>(sh, row, kk, stages, first_stages, kBins, 0u);
+    cut = select<false>(sh, row, kk, stages, kBins, 0u);
     if (cut.bin < 0) return false;
   }
   if (do_p) {
@@ -548,9 +539,9 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
       clear_hist(sh, ck.bin + 1, kBins);
       __syncthreads();
       stages = 3;  // bins up to the top-k bin are complete; later ones hold no survivor
-      cut = select<true>(sh, row, limit, stages, first_stages, ck.bin, ck.kept_in_bin);
+      cut = select<true>(sh, row, limit, stages, ck.bin, ck.kept_in_bin);
     } else {
-      cut = select<true>(sh, row, limit, stages, first_stages, kBins, 0u);
+      cut = select<true>(sh, row, limit, stages, kBins, 0u);
     }
     if (cut.bin < 0) return false;
   }
@@ -574,10 +565,10 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   return true;
 }
 
-template <int DT, int NREG, int NLDS>
 // Output row r (blockIdx.x) is the distribution of logits row rows[r] (rows ==
 // nullptr: row r) of n_src; temperature / top_k / top_p are indexed by r.  A source
 // row outside [0, n_src) gives an all-NaN output row.
+template <int DT, int NREG, int NLDS>
 __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     const void* __restrict__ logits, const int64_t* __restrict__ rows, int64_t n_src,
     int64_t row_stride, int V,
@@ -656,6 +647,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     sh.wave_f64[w] = lmax;
     sh.wave_u32[w] = nan_b != 0;
   }
+  clear_hist(sh, 0, kBins);  // stage 0 is admitted by the mass pass
   __syncthreads();
   lmax = -INFINITY;
   int bad = 0;
@@ -676,22 +668,22 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   const float p = top_p[r];
   const bool do_p = apply_top_p && p < 1.f;
 
-  // ---- mass pass: e in place of l, float64 total; then (filtered rows) the count
-  // and mass of the tokens above 2^-8 and 2^-16, which pick the histogram region
+  // ---- mass pass: e in place of l, the float64 total, and histogram stage 0 (the
+  // few tokens with e > 2^-8)
   double zs = 0.0;
-  uint32_t c16 = 0;  // tokens with e > 2^-16
   row.for_chunks([&](int j) {
     const float l = row.x(j);
     const float e = l == l ? row.mass(l) : 0.f;
     if (NPT > 0) row.set(j, l == l ? e : NAN);
     zs += (double)e;
-    c16 += __float_as_uint(e) > kFloor16;
+    const uint32_t bits = __float_as_uint(e);
+    if (bits > kFloor8) {
+      const int b = bin_of(bits);
+      atomicAdd(&sh.cnt[b], 1u);
+      atomicAdd(&sh.mass[b], fixed_mass(e));
+    }
   });
   const double z = block_sum_f64(sh, zs);
-  {
-    unsigned long long unused = 0;
-    block_sum2(sh, c16, unused);
-  }
   if (!do_k && !do_p) {
     const float inv = (float)(1.0 / z);
     row.for_chunks([&](int j) {
@@ -703,7 +695,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
 
   const unsigned long long kk =
       (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
-  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z, c16)) {
+  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z)) {
     __syncthreads();
     exact::exact_row<DT, kTC>(lds.ex, logits, src_r, row_stride, V, temperature, top_k, top_p,
                               max_top_k, apply_top_p, out, out_stride);
