@@ -392,9 +392,9 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
                                       int& stages, int mbin, uint32_t mlist) {
   const int t = threadIdx.x, lane = t & 63;
   // the histogram holds stages [0, stages); admit further tokens by mass range until
-  // the criterion is crossed: e > 2^-8 (admitted by the mass pass), then
-  // (2^-16, 2^-8], then the rest (each stage a prefix of the order, so a scan over
-  // the admitted bins is exact for the cuts they contain)
+  // the criterion is crossed: e > 2^-8 and (2^-16, 2^-8] (both admitted by the mass
+  // pass), then the rest (each stage a prefix of the order, so a scan over the
+  // admitted bins is exact for the cuts they contain)
   scan_select<kMass>(sh, kBins, 0, 0, limit);
   while (sh.sel_bin < 0 && stages < 3) {
     __syncthreads();
@@ -513,7 +513,7 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
                                            bool do_k, bool do_p, unsigned long long kk, float p,
                                            double z) {
   const int t = threadIdx.x;
-  int stages = 1;  // histogram stages admitted so far (stage 0 by the mass pass)
+  int stages = 2;  // histogram stages admitted so far (0 and 1 by the mass pass)
 
   Cut cut;
   if (do_k) {
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     sh.wave_f64[w] = lmax;
     sh.wave_u32[w] = nan_b != 0;
   }
-  clear_hist(sh, 0, kBins);  // stage 0 is admitted by the mass pass
+  clear_hist(sh, 0, kBins);  // stages 0 and 1 are admitted by the mass pass
   __syncthreads();
   lmax = -INFINITY;
   int bad = 0;
@@ -668,8 +668,9 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   const float p = top_p[r];
   const bool do_p = apply_top_p && p < 1.f;
 
-  // ---- mass pass: e in place of l, the float64 total, and histogram stage 0 (the
-  // few tokens with e > 2^-8)
+  // ---- mass pass: e in place of l, the float64 total, and histogram stages 0 and 1
+  // (the tokens with e > 2^-16: a few percent of a row; where top-p cuts the
+  // distributions of a verify step)
   double zs = 0.0;
   row.for_chunks([&](int j) {
     const float l = row.x(j);
@@ -677,7 +678,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     if (NPT > 0) row.set(j, l == l ? e : NAN);
     zs += (double)e;
     const uint32_t bits = __float_as_uint(e);
-    if (bits > kFloor8) {
+    if (bits > kFloor16) {
       const int b = bin_of(bits);
       atomicAdd(&sh.cnt[b], 1u);
       atomicAdd(&sh.mass[b], fixed_mass(e));
