@@ -78,6 +78,20 @@ __device__ __forceinline__ int bin_of(uint32_t b) {
   return b > kFloor16 ? (int)((kOneBits - b) >> 17) : kTopBins + (int)((kFloor16 - b) >> kTailShift);
 }
 
+// The float bits of the masses in bin b: [lo, hi] (the inverse of bin_of).
+__device__ __forceinline__ void bin_bits(int b, uint32_t& lo, uint32_t& hi) {
+  if (b < kTopBins) {
+    hi = kOneBits - ((uint32_t)b << 17);
+    lo = hi - (1u << 17) + 1u;
+  } else {
+    const int64_t k = b - kTopBins;
+    const int64_t h = (int64_t)kFloor16 - (k << kTailShift);
+    const int64_t l = h - (1ll << kTailShift) + 1;
+    hi = h < 0 ? 0u : (uint32_t)h;
+    lo = h < 0 ? 1u : l < 0 ? 0u : (uint32_t)l;  // bins past bin_of(0) are empty
+  }
+}
+
 // Order-preserving key of a float (NaN excluded by the callers); -0 maps to +0.
 __device__ __forceinline__ uint32_t order_key(float x) {
   uint32_t b = __float_as_uint(x);
@@ -423,9 +437,12 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
     // entry per thread, so no load waits inside the row loop
     if (t == 0) sh.list_n = 0;
     __syncthreads();
+    uint32_t blo, bhi;
+    bin_bits(bin, blo, bhi);
     row.for_chunks([&](int j) {
-      const float e = row.e(j);
-      const bool take = e == e && bin_of(__float_as_uint(e)) == bin;
+      // the bin's bit range (NaN padding lies above every bin's range)
+      const uint32_t bits = __float_as_uint(row.e(j));
+      const bool take = bits >= blo && bits <= bhi;
       const uint64_t m = __ballot(take);
       if (m == 0) return;
       uint32_t base = 0;
@@ -550,11 +567,15 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   // bins before the cut bin kept, later bins dropped, the cut bin's tokens written
   // from the sorted list (its first kept_in_bin kept)
   const float inv = (float)(kFixScale / (double)cut.kept);
+  uint32_t clo, chi;
+  bin_bits(cut.bin, clo, chi);
   row.for_chunks([&](int j) {
     const float e = row.e(j);
     if (e != e) return;
-    const int b = bin_of(__float_as_uint(e));
-    if (b != cut.bin) dst[(int64_t)j * kThreads + t] = b < cut.bin ? e * inv : 0.f;
+    // bins before the cut bin hold larger masses (kept), later bins smaller ones
+    const uint32_t bits = __float_as_uint(e);
+    if (bits > chi) dst[(int64_t)j * kThreads + t] = e * inv;
+    else if (bits < clo) dst[(int64_t)j * kThreads + t] = 0.f;
   });
   const int nl = min((int)sh.list_n, Shared::kCap);
   for (int i = t; i < nl; i += kThreads) {
