@@ -20,7 +20,8 @@
 //     the sequential cumsum on one lane (exact by construction); then tokens /
 //     accepted / final / error.
 //
-// ``categorical`` runs one workgroup per row on raw weights (tile totals + draw).
+// ``categorical`` runs the same tile totals and draw on raw weights: a (row, tile) grid
+// for the totals, then one draw workgroup per row.
 //
 // torch's fp32 row-sum order (what ``p.sum(-1, dtype=float32)`` computes on CPU):
 // 32 streams, stream s = 8k + l owns elements 32*i + s (8-lane vectors, 4 in
@@ -578,6 +579,83 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_categorical_kernel(
   }
 }
 
+// Two-launch categorical (V <= kMaxTiles tiles): grid (m, tiles) tile totals, then
+// grid (m) draws.  The tile totals are the single-workgroup kernel's bits (wave
+// partials summed in wave order), so both forms draw the same index.
+__global__ __launch_bounds__(kDrawThreads) void rlt_categorical_tiles_kernel(
+    const float* __restrict__ weights, int64_t V, int64_t w_stride, double* __restrict__ tile_sum,
+    uint32_t* __restrict__ tile_flags) {
+  __shared__ double wave_part[kDrawWaves];
+  __shared__ uint32_t wave_flags[kDrawWaves];
+  const int64_t i = blockIdx.x;
+  const int64_t k = blockIdx.y;
+  const int64_t tiles = gridDim.y;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  WeightRow w;
+  w.a = weights + i * w_stride;
+  w.b = nullptr;
+  w.am = w.bm = 1.f;
+  w.residual = false;
+  w.raw = true;
+  const bool vec_ok = (V % 4 == 0) && ((uintptr_t)w.a % 16 == 0);
+  float wv[kElems];
+  load_weights(w, V, k, t, vec_ok, wv);
+  uint32_t fl = 0;
+  const double part = tile_partial(wv, fl);
+  fl = wave_or_flags(fl);
+  if (lane == 0) {
+    wave_part[wave] = part;
+    wave_flags[wave] = fl;
+  }
+  __syncthreads();
+  if (t == 0) {
+    double tk = 0.0;
+    uint32_t f = 0;
+    for (int v = 0; v < kDrawWaves; ++v) {
+      tk += wave_part[v];
+      f |= wave_flags[v];
+    }
+    tile_sum[i * tiles + k] = tk;
+    tile_flags[i * tiles + k] = f;
+  }
+}
+
+__global__ __launch_bounds__(kDrawThreads) void rlt_categorical_draw_kernel(
+    const float* __restrict__ weights, int64_t V, int64_t w_stride, int64_t tiles,
+    const float* __restrict__ u, const double* __restrict__ tile_sum,
+    const uint32_t* __restrict__ tile_flags, int64_t* __restrict__ out_index,
+    uint8_t* __restrict__ out_valid, const int64_t* __restrict__ scatter, int64_t n_out,
+    int32_t* __restrict__ slow_count) {
+  __shared__ DrawScratch ds;
+  const int64_t i = blockIdx.x;
+  const int t = threadIdx.x;
+  for (int64_t k = t; k < tiles; k += kDrawThreads) {
+    ds.tile_total[k] = tile_sum[i * tiles + k];
+    ds.tile_flags[k] = tile_flags[i * tiles + k];
+  }
+  WeightRow w;
+  w.a = weights + i * w_stride;
+  w.b = nullptr;
+  w.am = w.bm = 1.f;
+  w.residual = false;
+  w.raw = true;
+  const bool vec_ok = (V % 4 == 0) && ((uintptr_t)w.a % 16 == 0);
+  __syncthreads();
+  int64_t index;
+  bool valid;
+  draw_from_tiles(w, V, u[i], tiles, 0u, true, vec_ok, ds, slow_count, &index, &valid);
+  if (t != 0) return;
+  if (!scatter) {
+    out_index[i] = index;
+  } else {
+    const int64_t d = scatter[i];
+    if (d >= 0 && d < n_out) out_index[d] = index;
+  }
+  if (out_valid) out_valid[i] = valid;
+}
+
 // ------------------------------------------------------------------ accept
 
 // Stop state of one request, written by its tile-0 workgroup for the draw kernel.
@@ -814,6 +892,33 @@ void launch_mass_groups(const float* p, const float* q, int64_t p_rows, int64_t 
                                                             geo.full_chunks, partials);
 }
 
+// Categorical draws of m weight rows (w_stride floats apart): tile totals over the
+// whole GPU, then one draw workgroup per row; rows of more than kMaxTiles tiles run
+// the single-workgroup kernel (its draw replays them exactly).
+int launch_categorical(const float* weights, int64_t w_stride, const float* u, int64_t m,
+                       int64_t vocab, int64_t* index, uint8_t* valid, const int64_t* scatter,
+                       int64_t n_out, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  const Layout l = layout_for(0, m, vocab);
+  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
+  char* ws = (char*)workspace;
+  int32_t* slow = (int32_t*)(ws + l.slow);
+  const int64_t tiles = (vocab + kTile - 1) / kTile;
+  if (tiles > kMaxTiles) {
+    rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(
+        weights, vocab, w_stride, u, index, valid, scatter, n_out, slow);
+    return rlt_launch_status();
+  }
+  double* tile_sum = (double*)(ws + l.tile_sum);
+  uint32_t* tile_flags = (uint32_t*)(ws + l.tile_flags);
+  rlt_categorical_tiles_kernel<<<dim3((unsigned)m, (unsigned)tiles), kDrawThreads, 0, stream>>>(
+      weights, vocab, w_stride, tile_sum, tile_flags);
+  rlt_categorical_draw_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(
+      weights, vocab, w_stride, tiles, u, tile_sum, tile_flags, index, valid, scatter, n_out,
+      slow);
+  return rlt_launch_status();
+}
+
 }  // namespace
 
 extern "C" {
@@ -823,8 +928,7 @@ size_t rlt_speculative_accept_workspace_size(int64_t n, int32_t w1, int64_t voca
 }
 
 size_t rlt_categorical_workspace_size(int64_t m, int64_t vocab) {
-  (void)m;
-  return layout_for(0, 0, vocab).total;
+  return layout_for(0, m, vocab).total;
 }
 
 int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
@@ -862,12 +966,8 @@ int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t voc
                     hipStream_t stream) {
   if (m < 0 || vocab < 1) return RLT_ERR_ARGUMENT;
   if (m == 0) return RLT_OK;
-  const Layout l = layout_for(0, 0, vocab);
-  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
-  int32_t* slow = (int32_t*)((char*)workspace + l.slow);
-  rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(weights, vocab, vocab, u, index,
-                                                                  valid, nullptr, m, slow);
-  return rlt_launch_status();
+  return launch_categorical(weights, vocab, u, m, vocab, index, valid, nullptr, m, workspace,
+                            workspace_bytes, stream);
 }
 
 size_t rlt_row_mass_workspace_size(int64_t rows, int64_t vocab) {
@@ -898,10 +998,6 @@ int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u,
                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (m < 0 || vocab < 1 || w_stride < vocab) return RLT_ERR_ARGUMENT;
   if (m == 0) return RLT_OK;
-  const Layout l = layout_for(0, 0, vocab);
-  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
-  int32_t* slow = (int32_t*)((char*)workspace + l.slow);
-  rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(
-      weights, vocab, w_stride, u, out_index, nullptr, scatter, n_out, slow);
-  return rlt_launch_status();
+  return launch_categorical(weights, w_stride, u, m, vocab, out_index, nullptr, scatter, n_out,
+                            workspace, workspace_bytes, stream);
 }
