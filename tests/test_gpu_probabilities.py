@@ -185,7 +185,7 @@ def test_config_shaped_parity(pkg, dev, name, n, vocab, temperature, top_p, dtyp
 
 
 @pytest.mark.parametrize("vocab", [1, 2, 17, 1000, 1024, 1025, 4096, 4097, 16384, 16385, 32768,
-                                   32769, 49152, 65536, 65537, 131072 + 3])
+                                   32769, 49152, 65536, 65537, 128256, 131072 + 3, 151936])
 def test_mixed_filters_across_vocab_sizes(pkg, dev, vocab):
     """Every row placement (registers, registers + LDS, re-reading) with a mix of
     temperatures, top-k (including k >= V and k <= 0) and top-p per row."""

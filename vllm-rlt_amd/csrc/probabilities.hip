@@ -59,7 +59,10 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / RLT_WAVE;
 constexpr int kMaxRegChunks = 64;       // V <= 65536 keeps the row on chip
-constexpr int kMaxStreamChunks = 256;   // V <= 262144 on the re-reading variant
+constexpr int kMaxStreamChunks = 256;   // V <= 262144: the first chunks on chip, the rest re-read
+// On-chip chunks of rows longer than kMaxRegChunks (the exact path then needs tie
+// tables for 256 chunks, which leaves room for 24 LDS chunks)
+constexpr int kTailReg = 16, kTailLds = 24;
 constexpr double kFixScale = 1099511627776.0;  // 2^40
 
 // Histogram bins over the float bits of e in [0, 1].
@@ -298,7 +301,7 @@ struct Cut {
 // Columns past V read as NaN: rows holding a real NaN are finished before any
 // pass that tests `v == v` for validity, which keeps per-chunk bounds masks out of
 // the scalar registers.
-template <int DT, int NREG, int NLDS>
+template <int DT, int NREG, int NLDS, bool kTail = false>
 struct Row {
   static constexpr int kNpt = NREG + NLDS;
   static constexpr int kDtype = DT;
@@ -312,16 +315,18 @@ struct Row {
   __device__ __forceinline__ bool valid(int j) const {
     return (int64_t)j * kThreads + threadIdx.x < V;
   }
+  // chunks past the on-chip ones (kTail: rows longer than kNpt chunks) are re-read
+  __device__ __forceinline__ bool on_chip(int j) const { return kNpt > 0 && (!kTail || j < kNpt); }
   __device__ __forceinline__ void set(int j, float v) {
     if (j < NREG) xr[j] = v;
-    else if (kNpt > 0) xl[(j - NREG) * kThreads + threadIdx.x] = v;
+    else if (on_chip(j)) xl[(j - NREG) * kThreads + threadIdx.x] = v;
   }
   // the on-chip value of chunk j (l before the mass pass, e after), or the logit
-  // re-read from memory on the re-reading variant
+  // re-read from memory (re-reading variant, and the tail of a kTail row)
   __device__ __forceinline__ float x(int j) const {
     float v;
     if (j < NREG) v = xr[j];
-    else if (kNpt > 0) v = xl[(j - NREG) * kThreads + threadIdx.x];
+    else if (on_chip(j)) v = xl[(j - NREG) * kThreads + threadIdx.x];
     else v = logit(j);
     // opaque copy: values derived from v are recomputed in each pass instead of
     // being kept live across passes, which would spill
@@ -336,7 +341,7 @@ struct Row {
   }
   // e of chunk j after the mass pass (NaN for padding)
   __device__ __forceinline__ float e(int j) const {
-    if (kNpt > 0) return x(j);
+    if (on_chip(j)) return x(j);
     const float l = x(j);
     return l == l ? mass(l) : NAN;
   }
@@ -349,9 +354,10 @@ struct Row {
     for (int j = 0; j < NREG; ++j) f(j);
     if (kNpt > 0) {
 #pragma unroll 1
-      for (int j = NREG; j < npt; ++j) f(j);
-    } else {
-      int j = 0;
+      for (int j = NREG; j < (kTail ? kNpt : npt); ++j) f(j);
+    }
+    if (kNpt == 0 || kTail) {
+      int j = kNpt;
 #pragma unroll 1
       for (; j + 4 <= npt; j += 4) {
 #pragma unroll
@@ -589,7 +595,7 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
 // Output row r (blockIdx.x) is the distribution of logits row rows[r] (rows ==
 // nullptr: row r) of n_src; temperature / top_k / top_p are indexed by r.  A source
 // row outside [0, n_src) gives an all-NaN output row.
-template <int DT, int NREG, int NLDS>
+template <int DT, int NREG, int NLDS, bool kTail>
 __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     const void* __restrict__ logits, const int64_t* __restrict__ rows, int64_t n_src,
     int64_t row_stride, int V,
@@ -599,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   constexpr int NPT = NREG + NLDS;
   // the exact path (crowded rows) reuses the fast path's LDS
   constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
-  constexpr int kTC = NPT > 0 ? NPT : kMaxStreamChunks;
+  constexpr int kTC = NPT > 0 && !kTail ? NPT : kMaxStreamChunks;
   union Lds {
     SharedT<kCapV> fast;
     exact::SharedT<kTC> ex;
@@ -610,12 +616,12 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   const int64_t r = blockIdx.x;
   const int64_t src_r = rows ? rows[r] : r;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  Row<DT, NREG, NLDS> row;
+  Row<DT, NREG, NLDS, kTail> row;
   row.xl = xlds;
   row.V = V;
   const bool src_ok = src_r >= 0 && src_r < n_src;
   row.src = (const char*)logits + (src_ok ? src_r : 0) * row_stride * (DT == RLT_F32 ? 4 : 2);
-  row.npt = NPT > 0 ? NPT : (V + kThreads - 1) / kThreads;
+  row.npt = NPT > 0 && !kTail ? NPT : (V + kThreads - 1) / kThreads;
   float* dst = out + r * out_stride;
   const float temp = temperature[r];
   row.c = 1.44269504088896341f / temp;  // log2(e) / T
@@ -654,6 +660,20 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
         if (j0 + u < NPT) take_raw(j0 + u, cur[u]);
 #pragma unroll
       for (int u = 0; u < kB; ++u) cur[u] = nxt[u];
+    }
+    if (kTail) {
+      // the re-read tail: maximum and NaN only (nothing stored)
+#pragma unroll 1
+      for (int j0 = NPT; j0 < row.npt; j0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = j0 + u < row.npt ? row.logit(j0 + u) : NAN;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          nan |= row.valid(j0 + u) && v[u] != v[u];
+          lmax = fmaxf(lmax, v[u]);  // padding reads NaN, which fmaxf ignores
+        }
+      }
     }
   } else {
     row.for_chunks([&](int j) {
@@ -774,18 +794,19 @@ __global__ void rlt_greedy_match_kernel(const int64_t* __restrict__ draft_tokens
   next_token[i] = targets[i * (w1 + 1) + a];
 }
 
-template <int DT, int NREG, int NLDS>
+template <int DT, int NREG, int NLDS, bool kTail = false>
 void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_src,
                   int64_t row_stride, int V, const float* temperature, const int64_t* top_k,
                   const float* top_p, int max_top_k, int apply_top_p, float* out,
                   int64_t out_stride, hipStream_t stream) {
-  hipLaunchKernelGGL((rlt_probs_kernel<DT, NREG, NLDS>), dim3((unsigned)n), dim3(kThreads), 0,
+  hipLaunchKernelGGL((rlt_probs_kernel<DT, NREG, NLDS, kTail>), dim3((unsigned)n), dim3(kThreads), 0,
                      stream, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,
                      max_top_k, apply_top_p, out, out_stride);
 }
 
 // Row placement by chunks per thread: registers first (at most 32, beyond which
-// the kernel spills), then LDS (at most 128 KiB), else the re-reading variant.
+// the kernel spills), then LDS (at most 128 KiB); longer rows keep their first 40
+// chunks on chip and re-read the rest on every pass.
 template <int DT>
 void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_src,
                     int64_t row_stride, int V,
@@ -801,7 +822,10 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
   else if (chunks <= 48) RLT_PROBS_CASE(16, 32);
   else if (chunks <= kMaxRegChunks) RLT_PROBS_CASE(30, 34);
-  else RLT_PROBS_CASE(0, 0);
+  else
+    launch_probs<DT, kTailReg, kTailLds, true>(n, logits, rows, n_src, row_stride, V,
+                                                       temperature, top_k, top_p, max_top_k,
+                                                       apply_top_p, out, out_stride, stream);
 #undef RLT_PROBS_CASE
 }
 
