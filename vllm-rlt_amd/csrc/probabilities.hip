@@ -757,12 +757,22 @@ __global__ __launch_bounds__(kThreads) void rlt_argmax_rows_kernel(const void* _
   const char* src = (const char*)logits + r * row_stride * (DT == RLT_F32 ? 4 : 2);
   // packed key: (order key of the value, NaN = all ones) << 32 | ~column
   unsigned long long best = 0;
-  for (int64_t i = t; i < V; i += kThreads) {
-    const float x = load_as_f32<DT>(src, i);
+  auto take = [&](float x, int64_t i) {
     const uint32_t key = x != x ? 0xffffffffu : order_key(x);
     const unsigned long long packed = ((unsigned long long)key << 32) | (0xffffffffu - (uint32_t)i);
     best = packed > best ? packed : best;
+  };
+  // eight loads in flight per thread, then the remainder
+  constexpr int kU = 8;
+  int64_t i0 = t;
+  for (; i0 + (kU - 1) * kThreads < V; i0 += kU * kThreads) {
+    float x[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) x[u] = load_as_f32<DT>(src, i0 + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) take(x[u], i0 + u * kThreads);
   }
+  for (; i0 < V; i0 += kThreads) take(load_as_f32<DT>(src, i0), i0);
   for (int off = 32; off >= 1; off >>= 1) {
     const unsigned long long o = __shfl_xor(best, off, RLT_WAVE);
     best = o > best ? o : best;
