@@ -592,6 +592,45 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   return true;
 }
 
+// First maximal column of logits row r (NaN counts as the maximum, torch's argmax
+// rule) into targets[r]; one 1024-thread workgroup.
+template <int DT>
+__device__ __forceinline__ void argmax_row(const void* __restrict__ logits, int64_t row_stride,
+                                           int V, int64_t r, int64_t* __restrict__ targets,
+                                           unsigned long long* wave_best) {
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const char* src = (const char*)logits + r * row_stride * (DT == RLT_F32 ? 4 : 2);
+  // packed key: (order key of the value, NaN = all ones) << 32 | ~column
+  unsigned long long best = 0;
+  auto take = [&](float x, int64_t i) {
+    const uint32_t key = x != x ? 0xffffffffu : order_key(x);
+    const unsigned long long packed = ((unsigned long long)key << 32) | (0xffffffffu - (uint32_t)i);
+    best = packed > best ? packed : best;
+  };
+  // eight loads in flight per thread, then the remainder
+  constexpr int kU = 8;
+  int64_t i0 = t;
+  for (; i0 + (kU - 1) * kThreads < V; i0 += kU * kThreads) {
+    float x[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) x[u] = load_as_f32<DT>(src, i0 + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) take(x[u], i0 + u * kThreads);
+  }
+  for (; i0 < V; i0 += kThreads) take(load_as_f32<DT>(src, i0), i0);
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(best, off, RLT_WAVE);
+    best = o > best ? o : best;
+  }
+  if (lane == 0) wave_best[w] = best;
+  __syncthreads();
+  if (t == 0) {
+    unsigned long long b = 0;
+    for (int i = 0; i < kWaves; ++i) b = wave_best[i] > b ? wave_best[i] : b;
+    targets[r] = (int64_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+  }
+}
+
 // Output row r (blockIdx.x) is the distribution of logits row rows[r] (rows ==
 // nullptr: row r) of n_src; temperature / top_k / top_p are indexed by r.  A source
 // row outside [0, n_src) gives an all-NaN output row.
@@ -601,7 +640,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     int64_t row_stride, int V,
     const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
     const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
-    int64_t out_stride) {
+    int64_t out_stride, int64_t* __restrict__ argmax_out, int64_t argmax_rows) {
   constexpr int NPT = NREG + NLDS;
   // the exact path (crowded rows) reuses the fast path's LDS
   constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
@@ -612,6 +651,14 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   };
   __shared__ Lds lds;
   SharedT<kCapV>& sh = lds.fast;
+  // blocks past the distribution rows take the argmax of logits rows 0..argmax_rows-1
+  // (the draft step's greedy proposals, run alongside the distributions)
+  const int64_t n_dist = (int64_t)gridDim.x - argmax_rows;
+  if ((int64_t)blockIdx.x >= n_dist) {
+    argmax_row<DT>(logits, row_stride, V, (int64_t)blockIdx.x - n_dist, argmax_out,
+                   reinterpret_cast<unsigned long long*>(&lds));
+    return;
+  }
   __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
   const int64_t r = blockIdx.x;
   const int64_t src_r = rows ? rows[r] : r;
@@ -752,38 +799,7 @@ __global__ __launch_bounds__(kThreads) void rlt_argmax_rows_kernel(const void* _
                                                                    int64_t row_stride, int V,
                                                                    int64_t* __restrict__ targets) {
   __shared__ unsigned long long wave_best[kWaves];
-  const int64_t r = blockIdx.x;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const char* src = (const char*)logits + r * row_stride * (DT == RLT_F32 ? 4 : 2);
-  // packed key: (order key of the value, NaN = all ones) << 32 | ~column
-  unsigned long long best = 0;
-  auto take = [&](float x, int64_t i) {
-    const uint32_t key = x != x ? 0xffffffffu : order_key(x);
-    const unsigned long long packed = ((unsigned long long)key << 32) | (0xffffffffu - (uint32_t)i);
-    best = packed > best ? packed : best;
-  };
-  // eight loads in flight per thread, then the remainder
-  constexpr int kU = 8;
-  int64_t i0 = t;
-  for (; i0 + (kU - 1) * kThreads < V; i0 += kU * kThreads) {
-    float x[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) x[u] = load_as_f32<DT>(src, i0 + u * kThreads);
-#pragma unroll
-    for (int u = 0; u < kU; ++u) take(x[u], i0 + u * kThreads);
-  }
-  for (; i0 < V; i0 += kThreads) take(load_as_f32<DT>(src, i0), i0);
-  for (int off = 32; off >= 1; off >>= 1) {
-    const unsigned long long o = __shfl_xor(best, off, RLT_WAVE);
-    best = o > best ? o : best;
-  }
-  if (lane == 0) wave_best[w] = best;
-  __syncthreads();
-  if (t == 0) {
-    unsigned long long b = 0;
-    for (int i = 0; i < kWaves; ++i) b = wave_best[i] > b ? wave_best[i] : b;
-    targets[r] = (int64_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
-  }
+  argmax_row<DT>(logits, row_stride, V, blockIdx.x, targets, wave_best);
 }
 
 // One lane per request: leading matches of draft j against target row j.
@@ -808,10 +824,12 @@ template <int DT, int NREG, int NLDS, bool kTail = false>
 void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_src,
                   int64_t row_stride, int V, const float* temperature, const int64_t* top_k,
                   const float* top_p, int max_top_k, int apply_top_p, float* out,
-                  int64_t out_stride, hipStream_t stream) {
-  hipLaunchKernelGGL((rlt_probs_kernel<DT, NREG, NLDS, kTail>), dim3((unsigned)n), dim3(kThreads), 0,
-                     stream, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,
-                     max_top_k, apply_top_p, out, out_stride);
+                  int64_t out_stride, hipStream_t stream, int64_t* argmax_out = nullptr,
+                  int64_t argmax_rows = 0) {
+  hipLaunchKernelGGL((rlt_probs_kernel<DT, NREG, NLDS, kTail>),
+                     dim3((unsigned)(n + argmax_rows)), dim3(kThreads), 0, stream, logits, rows,
+                     n_src, row_stride, V, temperature, top_k, top_p, max_top_k, apply_top_p, out,
+                     out_stride, argmax_out, argmax_rows);
 }
 
 // Row placement by chunks per thread: registers first (at most 32, beyond which
@@ -822,11 +840,12 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
                     int64_t row_stride, int V,
                     const float* temperature, const int64_t* top_k, const float* top_p,
                     int max_top_k, int apply_top_p, float* out, int64_t out_stride,
-                    hipStream_t stream) {
+                    hipStream_t stream, int64_t* argmax_out = nullptr, int64_t argmax_rows = 0) {
   const int chunks = (V + kThreads - 1) / kThreads;
 #define RLT_PROBS_CASE(R, L)                                                                  \
   launch_probs<DT, R, L>(n, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,     \
-                         max_top_k, apply_top_p, out, out_stride, stream)
+                         max_top_k, apply_top_p, out, out_stride, stream, argmax_out,         \
+                         argmax_rows)
   if (chunks <= 4) RLT_PROBS_CASE(4, 0);
   else if (chunks <= 16) RLT_PROBS_CASE(8, 8);
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
@@ -834,8 +853,9 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
   else if (chunks <= kMaxRegChunks) RLT_PROBS_CASE(30, 34);
   else
     launch_probs<DT, kTailReg, kTailLds, true>(n, logits, rows, n_src, row_stride, V,
-                                                       temperature, top_k, top_p, max_top_k,
-                                                       apply_top_p, out, out_stride, stream);
+                                               temperature, top_k, top_p, max_top_k,
+                                               apply_top_p, out, out_stride, stream, argmax_out,
+                                               argmax_rows);
 #undef RLT_PROBS_CASE
 }
 
@@ -932,35 +952,24 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
     return RLT_ERR_WORKSPACE;
   const int V = (int)vocab;
   const int mtk = max_top_k > vocab ? V : (int)max_top_k;
-  // greedy proposals for every row, then the random rows' distributions and draws
+  // greedy proposals for every row (extra workgroups of the distribution launch when
+  // there are random rows), then the random rows' draws
+#define RLT_PROPOSE(DT)                                                                       \
+  do {                                                                                        \
+    if (r == 0)                                                                               \
+      hipLaunchKernelGGL(rlt_argmax_rows_kernel<DT>, dim3((unsigned)m), dim3(kThreads), 0,    \
+                         stream, logits, row_stride, V, proposed);                            \
+    else                                                                                      \
+      dispatch_probs<DT>(r, logits, random_rows, m, row_stride, V, temperature, top_k, top_p, \
+                         mtk, apply_top_p != 0, q_out, q_stride, stream, proposed, m);        \
+  } while (0)
   switch (logits_dtype) {
-    case RLT_F32:
-      if (m > 0)
-        hipLaunchKernelGGL(rlt_argmax_rows_kernel<RLT_F32>, dim3((unsigned)m), dim3(kThreads), 0,
-                           stream, logits, row_stride, V, proposed);
-      if (r > 0)
-        dispatch_probs<RLT_F32>(r, logits, random_rows, m, row_stride, V, temperature, top_k,
-                                top_p, mtk, apply_top_p != 0, q_out, q_stride, stream);
-      break;
-    case RLT_BF16:
-      if (m > 0)
-        hipLaunchKernelGGL(rlt_argmax_rows_kernel<RLT_BF16>, dim3((unsigned)m), dim3(kThreads), 0,
-                           stream, logits, row_stride, V, proposed);
-      if (r > 0)
-        dispatch_probs<RLT_BF16>(r, logits, random_rows, m, row_stride, V, temperature, top_k,
-                                 top_p, mtk, apply_top_p != 0, q_out, q_stride, stream);
-      break;
-    case RLT_F16:
-      if (m > 0)
-        hipLaunchKernelGGL(rlt_argmax_rows_kernel<RLT_F16>, dim3((unsigned)m), dim3(kThreads), 0,
-                           stream, logits, row_stride, V, proposed);
-      if (r > 0)
-        dispatch_probs<RLT_F16>(r, logits, random_rows, m, row_stride, V, temperature, top_k,
-                                top_p, mtk, apply_top_p != 0, q_out, q_stride, stream);
-      break;
-    default:
-      return RLT_ERR_UNSUPPORTED;
+    case RLT_F32: RLT_PROPOSE(RLT_F32); break;
+    case RLT_BF16: RLT_PROPOSE(RLT_BF16); break;
+    case RLT_F16: RLT_PROPOSE(RLT_F16); break;
+    default: return RLT_ERR_UNSUPPORTED;
   }
+#undef RLT_PROPOSE
   if (r == 0) return rlt_launch_status();
   const int st = rlt_launch_status();
   if (st != RLT_OK) return st;
