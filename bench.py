@@ -11,9 +11,10 @@ uniforms.  Synthetic data, random values: there is no model or dataset.
 
 One step = the KV write of the 160 window rows' keys and values into the pool (the
 writer that precedes attention in every layer, vllm_rlt/kernels/graph_kv.py:52-67) +
-the attention call over all 160 verify rows + batched_probabilities of
-the 160 target-logit rows (fp32, T = 0.7, top-p 0.9: the reference's _verify,
-vllm_rlt/worker/async_speculative.py:694-704) + speculative_accept over the 32
+the attention call over all 160 verify rows + the verify side of the round (the
+argmax of every verify row and the distributions of the 160 target-logit rows, fp32,
+T = 0.7, top-p 0.9: the reference's _verify, vllm_rlt/worker/async_speculative.py:678-692,
+in one launch) + speculative_accept over the 32
 requests (draft distributions q are inputs, made in the draft step), all replayed
 from HIP graphs (the reference runs its recurrent core under graphs too).
 ``value`` = verified tokens (32 x 5) / step time.
@@ -260,9 +261,14 @@ def main():
     def attn():
         return backend.prefill(w["q"], kc, vc, tables, lengths, cu, w["window"])
 
+    all_rows = torch.arange(rows, device=dev)
+
     def probs():
-        pbuf["p"] = pkg.batched_probabilities(logits, temp, top_k, top_p, max_top_k=0,
-                                              apply_top_p=True).view(w["n"], w["window"], -1)
+        # _verify: argmax of every verify row and the distributions of the (all random)
+        # rows in one launch, async_speculative.py:678-692
+        pbuf["t"], p = pkg.verify_distributions(logits, all_rows, temp, top_k, top_p,
+                                                max_top_k=0, apply_top_p=True)
+        pbuf["p"] = p.view(w["n"], w["window"], -1)
         return pbuf["p"]
 
     def accept():
@@ -372,7 +378,7 @@ def main():
         "data": "synthetic (seeded random KV, q and logits; no model or dataset)",
         "config": {
             "workload": "config3 verify step: window KV write, packed q_len=5 causal window, 16q/4kv heads, D=128, "
-                        "bf16 SHARED KV, batch 32, ctx U[1024,8192]; target distributions from "
+                        "bf16 SHARED KV, batch 32, ctx U[1024,8192]; target argmax and distributions from "
                         "fp32 logits (T=0.7, top-p 0.9) and acceptance, V=49152",
             "batch": w["n"], "window": w["window"], "q_heads": w["hq"], "kv_heads": w["hkv"],
             "head_dim": w["d"], "block_size": w["bs"], "vocab": w["vocab"],

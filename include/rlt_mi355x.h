@@ -156,6 +156,22 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
                        size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * The verify side of a round: targets[i] = argmax of logits row i (i < m; first
+ * maximal column, NaN the maximum) and, for the random rows random_rows[j] (j < r),
+ * p_out row j = batched_probabilities of that logits row with temperature[j] /
+ * top_k[j] / top_p[j] (rows p_stride floats apart, e.g. a p[ranks, offsets] view when
+ * rows line up).  One launch: the argmax rows are extra workgroups of the
+ * distribution launch.  Replaces vllm_rlt/worker/async_speculative.py:678-692
+ * (target = logits.argmax(-1); p[v_ranks, v_offsets] = _probabilities(logits[v_rows],
+ * ...)).  No workspace.  A random row index outside [0, m) gives an all-NaN p row.
+ */
+int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t row_stride,
+                             int64_t m, int64_t vocab, const int64_t* random_rows, int64_t r,
+                             const float* temperature, const int64_t* top_k, const float* top_p,
+                             int64_t max_top_k, int32_t apply_top_p, float* p_out,
+                             int64_t p_stride, int64_t* targets, hipStream_t stream);
+
+/*
  * Greedy verify round: targets = argmax of every verify row (first maximal column,
  * NaN counts as the maximum), accepted = number of leading drafts j < drafts[r]
  * with draft_tokens[r, j] == targets[r, j], next_token = targets[r, accepted].

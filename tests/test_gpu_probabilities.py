@@ -373,3 +373,28 @@ def test_propose_drafts_greedy_only_and_bad_rows(pkg, dev):
     want = logits.argmax(-1)
     want[1] = osamp.categorical(q_o[:1].cpu(), torch.full((1,), 0.5))[0][0]
     assert torch.equal(proposed.cpu(), want)
+
+
+@pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 3001)])
+def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vocab):
+    """async_speculative.py:678-692: argmax of every verify row, distributions of the
+    random rows; bitwise what batched_probabilities gives for the gathered rows."""
+    _say("verify distributions", dtype, vocab)
+    g = torch.Generator().manual_seed(vocab + 1)
+    m = 10
+    logits = (torch.randn(m, vocab, generator=g) * 3).to(dtype)
+    logits[2, 5] = float("nan")
+    rows = torch.tensor([9, 0, 2, 4])
+    t = torch.tensor([0.7, 1.0, 0.9, 1.2])
+    k = torch.tensor([-1, 30, -1, 0])
+    p = torch.tensor([0.9, 1.0, 0.8, 0.95])
+    plan = _host_args(k.tolist(), p.tolist(), vocab)
+    ld = logits.to(dev)
+    out = torch.full((4, 3, vocab), -1.0, device=dev)
+    target, p_o = pkg.verify_distributions(ld, rows.to(dev), t.to(dev), k.to(dev), p.to(dev),
+                                           p_out=out[:, 1], **plan)
+    want_t = logits.float().argmax(-1)  # torch: first maximal column, NaN the maximum
+    assert torch.equal(target.cpu(), want_t)
+    want_p = pkg.batched_probabilities(ld[rows.to(dev)], t.to(dev), k.to(dev), p.to(dev), **plan)
+    assert torch.equal(out[:, 1].cpu().view(torch.int32), want_p.cpu().view(torch.int32))
+    assert bool((out[:, 0] == -1).all()) and bool((out[:, 2] == -1).all())

@@ -977,4 +977,40 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
                               workspace_bytes, stream);
 }
 
+int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t row_stride,
+                             int64_t m, int64_t vocab, const int64_t* random_rows, int64_t r,
+                             const float* temperature, const int64_t* top_k, const float* top_p,
+                             int64_t max_top_k, int32_t apply_top_p, float* p_out,
+                             int64_t p_stride, int64_t* targets, hipStream_t stream) {
+  if (m < 0 || r < 0 || vocab < 1 || vocab > 0x7fffffff || row_stride < vocab ||
+      max_top_k < 0 || (r > 0 && p_stride < vocab))
+    return RLT_ERR_ARGUMENT;
+  if (m == 0 && r == 0) return RLT_OK;
+  if (!logits || (m > 0 && !targets)) return RLT_ERR_ARGUMENT;
+  if (r > 0 && (!random_rows || !temperature || !top_k || !top_p || !p_out))
+    return RLT_ERR_ARGUMENT;
+  if (vocab > (int64_t)kMaxStreamChunks * kThreads || m > 0x7fffffff || r > 0x7fffffff)
+    return RLT_ERR_UNSUPPORTED;
+  const int V = (int)vocab;
+  const int mtk = max_top_k > vocab ? V : (int)max_top_k;
+  // targets of every row as extra workgroups of the distribution launch
+#define RLT_VERIFY(DT)                                                                        \
+  do {                                                                                        \
+    if (r == 0)                                                                               \
+      hipLaunchKernelGGL(rlt_argmax_rows_kernel<DT>, dim3((unsigned)m), dim3(kThreads), 0,    \
+                         stream, logits, row_stride, V, targets);                             \
+    else                                                                                      \
+      dispatch_probs<DT>(r, logits, random_rows, m, row_stride, V, temperature, top_k, top_p, \
+                         mtk, apply_top_p != 0, p_out, p_stride, stream, targets, m);         \
+  } while (0)
+  switch (logits_dtype) {
+    case RLT_F32: RLT_VERIFY(RLT_F32); break;
+    case RLT_BF16: RLT_VERIFY(RLT_BF16); break;
+    case RLT_F16: RLT_VERIFY(RLT_F16); break;
+    default: return RLT_ERR_UNSUPPORTED;
+  }
+#undef RLT_VERIFY
+  return rlt_launch_status();
+}
+
 }  // extern "C"

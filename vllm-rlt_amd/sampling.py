@@ -167,6 +167,51 @@ def propose_drafts(logits, random_rows, temperature, top_k, top_p, u, *, max_top
     return proposed, q_out
 
 
+def verify_distributions(logits, random_rows, temperature, top_k, top_p, *, max_top_k,
+                         apply_top_p, p_out=None):
+    """The verify side of a round: ``(target int64 [m], p float32 [r, V])``.
+
+    reference: vllm_rlt/worker/async_speculative.py:678-692 -- ``target =
+    logits.argmax(-1)`` over every verify row, and the distributions of the random
+    rows (``_probabilities(logits[v_rows], ...)``; ``temperature`` / ``top_k`` /
+    ``top_p`` per random row), read straight from ``logits`` through ``random_rows``.
+    ``p_out`` (optional): a ``[r, V]`` float32 view with unit column stride.
+    """
+    if logits.ndim != 2:
+        raise ValueError("logits must be a 2-D [m, V] tensor")
+    m, vocab = logits.shape
+    if random_rows is None:
+        random_rows = torch.empty(0, dtype=torch.int64, device=logits.device)
+    if random_rows.ndim != 1:
+        raise ValueError("random_rows must be 1-D")
+    r = random_rows.shape[0]
+    for name, value in (("temperature", temperature), ("top_k", top_k), ("top_p", top_p)):
+        if r and value.shape != (r,):
+            raise ValueError(f"{name} must have shape [{r}], got {tuple(value.shape)}")
+    if max_top_k < 0:
+        raise ValueError("max_top_k must be nonnegative")
+    _lib.require_gpu(logits, random_rows, *((temperature, top_k, top_p) if r else ()), p_out)
+    device = logits.device
+    target = torch.empty(m, dtype=torch.int64, device=device)
+    if p_out is None:
+        p_out = torch.empty((r, vocab), dtype=torch.float32, device=device)
+    elif p_out.shape != (r, vocab) or p_out.dtype != torch.float32 or p_out.stride(-1) != 1:
+        raise ValueError("p_out must be a float32 [r, V] view with unit column stride")
+    if m == 0 and r == 0:
+        return target, p_out
+    if vocab == 0:
+        raise ValueError("logits must have V >= 1")
+    x = logits if logits.dtype in _LOGIT_DTYPES else logits.float()
+    x = _rows(x)
+    args = (_f32(temperature), _i64(top_k), _f32(top_p)) if r else (None,) * 3
+    status = _lib.library().rlt_verify_distributions(
+        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), m, vocab, _lib.ptr(_i64(random_rows)),
+        r, *(_lib.ptr(a) for a in args), int(max_top_k), int(bool(apply_top_p)), _lib.ptr(p_out),
+        p_out.stride(0) if r else vocab, _lib.ptr(target), _lib.stream_of(device))
+    _lib.check(status, "rlt_verify_distributions")
+    return target, p_out
+
+
 def categorical(weights, u):
     """Inverse-CDF draw from ``[m, V]`` nonnegative weights with ``[m]`` uniforms.
 
