@@ -111,6 +111,21 @@ def _(logits, random_rows, temperature, top_k, top_p, u, max_top_k, apply_top_p)
             logits.new_empty((random_rows.shape[0], logits.shape[1]), dtype=torch.float32))
 
 
+@torch.library.custom_op("rlt_mi355x::verify_distributions", mutates_args=(), device_types="cuda")
+def verify_distributions(logits: torch.Tensor, random_rows: torch.Tensor,
+                         temperature: torch.Tensor, top_k: torch.Tensor, top_p: torch.Tensor,
+                         max_top_k: int, apply_top_p: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(target, p); reference: vllm_rlt/worker/async_speculative.py:678-692."""
+    return _samp.verify_distributions(logits, random_rows, temperature, top_k, top_p,
+                                      max_top_k=max_top_k, apply_top_p=apply_top_p)
+
+
+@verify_distributions.register_fake
+def _(logits, random_rows, temperature, top_k, top_p, max_top_k, apply_top_p):
+    return (logits.new_empty((logits.shape[0],), dtype=torch.int64),
+            logits.new_empty((random_rows.shape[0], logits.shape[1]), dtype=torch.float32))
+
+
 @torch.library.custom_op("rlt_mi355x::store_kv", mutates_args=("key_cache", "value_cache"),
                          device_types="cuda")
 def store_kv(key_cache: torch.Tensor, value_cache: torch.Tensor, k: torch.Tensor,
@@ -141,4 +156,4 @@ def finalize_rows(descriptor: torch.Tensor, tables: torch.Tensor, key_pool: torc
 
 
 OPS = ("paged_attention", "spec_probs", "categorical", "spec_accept", "greedy_accept",
-       "propose_drafts", "store_kv", "store_fp8", "finalize_rows")
+       "propose_drafts", "verify_distributions", "store_kv", "store_fp8", "finalize_rows")
