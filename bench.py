@@ -15,7 +15,9 @@ the attention call over all 160 verify rows + the verify side of the round (the
 argmax of every verify row and the distributions of the 160 target-logit rows, fp32,
 T = 0.7, top-p 0.9: the reference's _verify, vllm_rlt/worker/async_speculative.py:678-692,
 in one launch) + speculative_accept over the 32
-requests (draft distributions q are inputs, made in the draft step), all replayed
+requests (draft distributions q are inputs, made in the draft step); the verify side
+and the acceptance run as one ``verify_accept`` call, whose distribution launch also
+sums the draft rows for the acceptance.  All replayed
 from HIP graphs (the reference runs its recurrent core under graphs too).
 ``value`` = verified tokens (32 x 5) / step time.
 
@@ -213,7 +215,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-config2", action="store_true",
                     help="skip the secondary config-2 decode attention measurement")
-    ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "copy"),
+    ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "verify", "copy"),
                     help="replay only this part K times and exit (for counter collection); "
                          "'copy' copies a 1 GiB buffer K times (counter calibration)")
     ap.add_argument("--steps-per-graph", type=int, default=10,
@@ -274,11 +276,18 @@ def main():
     def accept():
         return pkg.speculative_accept(dt_tok, drafts, w["qprob"], pbuf["p"], ua, uf)
 
+    logits3 = logits.view(w["n"], w["window"], -1)
+
+    def verify():
+        # the two calls above in one (targets, distributions and the draft rows'
+        # row sums in one launch, then the acceptance); bitwise the same results
+        return pkg.verify_accept(logits3, temp, top_k, top_p, dt_tok, drafts, w["qprob"], ua, uf,
+                                 max_top_k=0, apply_top_p=True)
+
     def step():
         kv_write()
         attn()
-        probs()
-        accept()
+        verify()
 
     for _ in range(max(args.warmup, 1)):
         step()
@@ -294,7 +303,7 @@ def main():
     # so per-launch timings are not inflated by the per-replay launch overhead.
     spg = max(1, min(args.steps_per_graph, args.steps))
     g_kv, g_attn, g_probs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-    g_acc, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    g_acc, g_step, g_ver = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_kv):
         for _ in range(spg):
             kv_write()
@@ -307,6 +316,9 @@ def main():
     with torch.cuda.graph(g_acc):
         for _ in range(spg):
             out_acc = accept()
+    with torch.cuda.graph(g_ver):
+        for _ in range(spg):
+            out_ver = verify()
     with torch.cuda.graph(g_step):
         for _ in range(spg):
             step()
@@ -315,7 +327,7 @@ def main():
     torch.cuda.synchronize()
     if args.only:
         graph = {"kv_write": g_kv, "attention": g_attn, "probs": g_probs,
-                 "accept": g_acc}[args.only]
+                 "accept": g_acc, "verify": g_ver}[args.only]
         for _ in range(max(1, args.steps // spg)):
             graph.replay()
         torch.cuda.synchronize()
@@ -348,15 +360,21 @@ def main():
     t_attn = launch_time(g_attn, replays)
     t_probs = launch_time(g_probs, replays)
     t_acc = launch_time(g_acc, replays)
+    t_ver = launch_time(g_ver, replays)
 
     # ---- correctness of the measured outputs against an eager run
     eager_attn = attn()
     eager_probs = probs()
     eager_acc = accept()
+    eager_ver = verify()
     torch.cuda.synchronize()
     assert torch.equal(eager_attn, out_attn)
     assert torch.equal(eager_probs, out_probs)
     for a, b in zip(eager_acc, out_acc):
+        assert torch.equal(a, b)
+    # the fused verify round: bitwise the separate calls' results
+    assert torch.equal(out_ver[0], pbuf["t"]) and torch.equal(out_ver[1], eager_probs)
+    for a, b in zip(out_ver[2], eager_acc):
         assert torch.equal(a, b)
 
     a_bytes, p_bytes, c_bytes = attention_bytes(w), probs_bytes(w), accept_bytes(w)
@@ -389,6 +407,7 @@ def main():
         "attention_ms": round(t_attn * 1e3, 4),
         "probs_ms": round(t_probs * 1e3, 4),
         "accept_ms": round(t_acc * 1e3, 4),
+        "verify_accept_ms": round(t_ver * 1e3, 4),
         "steps_per_graph": spg,
         "roofline": {
             "kernel": "attention launch (rlt_attn_mfma_kernel + rlt_merge_kernel)",
@@ -403,7 +422,7 @@ def main():
         },
     }
     if not args.no_config2:
-        del g_kv, g_attn, g_probs, g_acc, g_step
+        del g_kv, g_attn, g_probs, g_acc, g_step, g_ver
         result["config2_decode_attention"] = config2_decode(pkg, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)

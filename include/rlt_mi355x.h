@@ -172,6 +172,25 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
                              int64_t p_stride, int64_t* targets, hipStream_t stream);
 
 /*
+ * The stochastic verify round in one call: targets = argmax of each of the
+ * n * (w1 + 1) target-logit rows, p_out [n, w1 + 1, V] = their batched_probabilities
+ * (temperature / top_k / top_p per row), then speculative_accept with p_out.  Bitwise
+ * the results of rlt_verify_distributions (all rows random) followed by
+ * rlt_speculative_accept; the draft rows' float32 row-sum partials are computed by
+ * otherwise idle workgroups of the distribution launch, so the acceptance then sums
+ * only p.  Replaces vllm_rlt/worker/async_speculative.py:678-692 (_verify) followed by
+ * :727-734 (speculative_accept).  Workspace: rlt_speculative_accept_workspace_size.
+ */
+int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t row_stride,
+                      const float* temperature, const int64_t* top_k, const float* top_p,
+                      int64_t max_top_k, int32_t apply_top_p, const int64_t* draft_tokens,
+                      const int64_t* drafts, const float* q, const float* u_accept,
+                      const float* u_final, int64_t n, int32_t w1, int64_t vocab,
+                      int64_t* targets, float* p_out, int64_t* tokens, int64_t* accepted,
+                      int64_t* final_token, uint8_t* error, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Greedy verify round: targets = argmax of every verify row (first maximal column,
  * NaN counts as the maximum), accepted = number of leading drafts j < drafts[r]
  * with draft_tokens[r, j] == targets[r, j], next_token = targets[r, accepted].

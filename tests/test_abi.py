@@ -202,3 +202,26 @@ def test_propose_drafts_checks_arguments(pkg):
     # q rows narrower than the vocabulary
     assert lib.rlt_propose_drafts(*base, fake, 2, fake, fake, fake, 0, 0, fake, fake, 50, fake,
                                   fake, 1 << 20, null) == 1
+
+
+def test_verify_accept_checks_arguments(pkg):
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null, fake = None, 0x1000
+    io = [fake] * 6  # targets, p_out, tokens, accepted, final_token, error
+    # nothing to do
+    assert lib.rlt_verify_accept(fake, 0, 100, fake, fake, fake, 0, 0, null, fake, null, null,
+                                 fake, 0, 4, 100, *io, null, 0, null) == 0
+    # row stride narrower than the vocabulary
+    assert lib.rlt_verify_accept(fake, 0, 50, fake, fake, fake, 0, 0, fake, fake, fake, fake,
+                                 fake, 2, 4, 100, *io, fake, 1 << 20, null) == 1
+    # drafts without draft tokens / q / uniforms
+    assert lib.rlt_verify_accept(fake, 0, 100, fake, fake, fake, 0, 0, null, fake, null, null,
+                                 fake, 2, 4, 100, *io, fake, 1 << 20, null) == 1
+    # more than 32 drafts per request
+    assert lib.rlt_verify_accept(fake, 0, 100, fake, fake, fake, 0, 0, fake, fake, fake, fake,
+                                 fake, 2, 33, 100, *io, fake, 1 << 30, null) == 2
+    # workspace too small
+    assert lib.rlt_verify_accept(fake, 0, 100, fake, fake, fake, 0, 0, fake, fake, fake, fake,
+                                 fake, 2, 4, 100, *io, fake, 1, null) == 3

@@ -49,6 +49,14 @@ def test_attention_and_sampling_ops_match_the_api(pkg, dev):
     for a, b in zip(got, want):
         assert torch.equal(a, b)
 
+    va = (logits[: n * (w1 + 1)].view(n, w1 + 1, -1), t[: n * (w1 + 1)], tk[: n * (w1 + 1)],
+          tp[: n * (w1 + 1)], dt, drafts, qq, ua, uf, 0, True)
+    got = torch.ops.rlt_mi355x.verify_accept(*va)
+    want_t, want_p, want_r = pkg.verify_accept(*va[:9], max_top_k=0, apply_top_p=True)
+    for a, b in zip(got, (want_t, want_p) + tuple(want_r)):
+        assert torch.equal(a, b)
+    torch.library.opcheck(torch.ops.rlt_mi355x.verify_accept, va, test_utils=CHECKS)
+
 
 def test_kv_write_op_mutates_the_pool(pkg, dev):
     kc = torch.zeros(8, 16, 2, 64, dtype=torch.bfloat16, device=dev)

@@ -398,3 +398,37 @@ def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vo
     want_p = pkg.batched_probabilities(ld[rows.to(dev)], t.to(dev), k.to(dev), p.to(dev), **plan)
     assert torch.equal(out[:, 1].cpu().view(torch.int32), want_p.cpu().view(torch.int32))
     assert bool((out[:, 0] == -1).all()) and bool((out[:, 2] == -1).all())
+
+
+@pytest.mark.parametrize("dtype,vocab,n,w1", [(torch.bfloat16, 32000, 6, 4),
+                                              (torch.float32, 1000, 3, 1),
+                                              (torch.float16, 151936, 2, 3),
+                                              (torch.bfloat16, 5000, 40, 8)])
+def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1):
+    """verify_accept (distributions, argmax targets and the draft rows' partial sums in
+    one launch, then the acceptance) is bitwise verify_distributions over every row
+    followed by speculative_accept."""
+    _say("verify accept", dtype, vocab, n, w1)
+    g = torch.Generator().manual_seed(vocab + n)
+    rows = n * (w1 + 1)
+    logits = (torch.randn(n, w1 + 1, vocab, generator=g) * 3).to(dtype)
+    t = torch.rand(rows, generator=g) + 0.5
+    k = torch.where(torch.rand(rows, generator=g) < 0.3, 40, -1)
+    p = torch.where(torch.rand(rows, generator=g) < 0.5, 0.9, 1.0)
+    plan = _host_args(k.tolist(), p.tolist(), vocab)
+    q = (torch.randn(n, w1, vocab, generator=g) * 2).softmax(-1)
+    u = torch.rand(n, 2 * w1 + 1, generator=g)
+    draft_tok = torch.stack([osamp.categorical(q[:, j], u[:, j])[0] for j in range(w1)], 1)
+    drafts = torch.randint(0, w1 + 1, (n,), generator=g)
+    args = [x.to(dev) for x in (logits, t, k, p, draft_tok, drafts, q,
+                                u[:, w1:2 * w1].contiguous(), u[:, 2 * w1].contiguous())]
+    target, p_o, res = pkg.verify_accept(*args, **plan)
+    want_t, want_p = pkg.verify_distributions(args[0].view(rows, vocab),
+                                              torch.arange(rows, device=dev), args[1], args[2],
+                                              args[3], **plan)
+    want = pkg.speculative_accept(args[4], args[5], args[6], want_p.view(n, w1 + 1, vocab),
+                                  args[7], args[8])
+    assert torch.equal(target.cpu(), want_t.cpu())
+    assert torch.equal(p_o.cpu().view(torch.int32), want_p.view(n, w1 + 1, vocab).cpu().view(torch.int32))
+    for a, b, name in zip(res, want, want._fields):
+        assert torch.equal(a.cpu(), b.cpu()), name

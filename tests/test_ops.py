@@ -43,3 +43,9 @@ def test_fake_implementations_give_output_shapes(pkg):
             torch.empty(7, 300), torch.empty(2, dtype=torch.int64), torch.empty(2),
             torch.empty(2, dtype=torch.int64), torch.empty(2), torch.empty(2), 0, False)
         assert prop.shape == (7,) and q_o.shape == (2, 300)
+        out = torch.ops.rlt_mi355x.verify_accept(
+            torch.empty(3, 5, 80), torch.empty(15), torch.empty(15, dtype=torch.int64),
+            torch.empty(15), torch.empty(3, 4, dtype=torch.int64),
+            torch.empty(3, dtype=torch.int64), torch.empty(3, 4, 80), torch.empty(3, 4),
+            torch.empty(3), 0, True)
+        assert [tuple(x.shape) for x in out] == [(15,), (3, 5, 80), (3, 5), (3,), (3,), (3,)]

@@ -39,6 +39,7 @@ from .sampling import (  # noqa: F401
     greedy_accept_batched,
     propose_drafts,
     speculative_accept,
+    verify_accept,
     verify_distributions,
 )
 from .kv_write import (  # noqa: F401

@@ -58,6 +58,9 @@ _SIGNATURES = {
         _p]),
     "rlt_verify_distributions": (ctypes.c_int, [
         _p, _i32, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _p, _i64, _p, _p]),
+    "rlt_verify_accept": (ctypes.c_int, [
+        _p, _i32, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _i64, _i32, _i64, _p, _p, _p,
+        _p, _p, _p, _p, _sz, _p]),
     "rlt_greedy_accept": (ctypes.c_int, [
         _p, _p, _p, _i32, _i64, _i64, _i32, _i64, _p, _p, _p, _p]),
     "rlt_kv_store": (ctypes.c_int, [

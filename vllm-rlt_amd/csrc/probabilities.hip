@@ -47,6 +47,7 @@
 // with the host rule of vllm_rlt/worker/speculative.py:41-53.  argmax takes the first
 // maximal column; NaN counts as the maximum (torch's argmax rule).
 
+#include "cascade.h"
 #include "common.h"
 #include "rlt_mi355x.h"
 
@@ -640,7 +641,9 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     int64_t row_stride, int V,
     const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
     const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
-    int64_t out_stride, int64_t* __restrict__ argmax_out, int64_t argmax_rows) {
+    int64_t out_stride, int64_t* __restrict__ argmax_out, int64_t argmax_rows,
+    const float* __restrict__ qm_src, int64_t qm_rows, float* __restrict__ qm_out,
+    int64_t qm_blocks) {
   constexpr int NPT = NREG + NLDS;
   // the exact path (crowded rows) reuses the fast path's LDS
   constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
@@ -652,8 +655,34 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   __shared__ Lds lds;
   SharedT<kCapV>& sh = lds.fast;
   // blocks past the distribution rows take the argmax of logits rows 0..argmax_rows-1
-  // (the draft step's greedy proposals, run alongside the distributions)
-  const int64_t n_dist = (int64_t)gridDim.x - argmax_rows;
+  // (greedy proposals and targets, run alongside the distributions), then the float32
+  // row-sum partials of the qm_rows draft rows for the acceptance sampler, eight
+  // 8192-float groups per workgroup, on CUs the distributions leave idle
+  const int64_t n_dist = (int64_t)gridDim.x - argmax_rows - qm_blocks;
+  if ((int64_t)blockIdx.x >= n_dist + argmax_rows) {
+    static_assert(sizeof(Lds) >= 8 * sizeof(cascade::ChunkSums), "group staging");
+    cascade::ChunkSums* cs = reinterpret_cast<cascade::ChunkSums*>(&lds);
+    const cascade::RowGeom geo = cascade::row_geom(V);
+    const int t = threadIdx.x;
+    const int sub = t / cascade::kGroupThreads, st = t % cascade::kGroupThreads;
+    const int64_t task = ((int64_t)blockIdx.x - n_dist - argmax_rows) *
+                             (kThreads / cascade::kGroupThreads) + sub;
+    const int64_t qrow = geo.groups > 0 ? task / geo.groups : qm_rows;
+    const int64_t g = geo.groups > 0 ? task % geo.groups : 0;
+    const bool live = qrow < qm_rows;
+    const float* x = qm_src + qrow * V;
+    if (live) {
+      if (V % 4 == 0 && (uintptr_t)qm_src % 16 == 0)
+        cascade::group_chunk_sums<true>(x, g, geo.full_chunks, st, cs[sub]);
+      else
+        cascade::group_chunk_sums<false>(x, g, geo.full_chunks, st, cs[sub]);
+    }
+    __syncthreads();
+    if (live)
+      cascade::group_stream_sums(g, geo.full_chunks, st, cs[sub],
+                                 qm_out + (qrow * geo.groups + g) * cascade::kStreams);
+    return;
+  }
   if ((int64_t)blockIdx.x >= n_dist) {
     argmax_row<DT>(logits, row_stride, V, (int64_t)blockIdx.x - n_dist, argmax_out,
                    reinterpret_cast<unsigned long long*>(&lds));
@@ -825,11 +854,16 @@ void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_
                   int64_t row_stride, int V, const float* temperature, const int64_t* top_k,
                   const float* top_p, int max_top_k, int apply_top_p, float* out,
                   int64_t out_stride, hipStream_t stream, int64_t* argmax_out = nullptr,
-                  int64_t argmax_rows = 0) {
+                  int64_t argmax_rows = 0, const float* qm_src = nullptr, int64_t qm_rows = 0,
+                  float* qm_out = nullptr) {
+  const cascade::RowGeom geo = cascade::row_geom(V);
+  const int64_t per_block = kThreads / cascade::kGroupThreads;
+  const int64_t qm_blocks = qm_src ? (qm_rows * geo.groups + per_block - 1) / per_block : 0;
   hipLaunchKernelGGL((rlt_probs_kernel<DT, NREG, NLDS, kTail>),
-                     dim3((unsigned)(n + argmax_rows)), dim3(kThreads), 0, stream, logits, rows,
-                     n_src, row_stride, V, temperature, top_k, top_p, max_top_k, apply_top_p, out,
-                     out_stride, argmax_out, argmax_rows);
+                     dim3((unsigned)(n + argmax_rows + qm_blocks)), dim3(kThreads), 0, stream,
+                     logits, rows, n_src, row_stride, V, temperature, top_k, top_p, max_top_k,
+                     apply_top_p, out, out_stride, argmax_out, argmax_rows, qm_src, qm_rows,
+                     qm_out, qm_blocks);
 }
 
 // Row placement by chunks per thread: registers first (at most 32, beyond which
@@ -840,12 +874,14 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
                     int64_t row_stride, int V,
                     const float* temperature, const int64_t* top_k, const float* top_p,
                     int max_top_k, int apply_top_p, float* out, int64_t out_stride,
-                    hipStream_t stream, int64_t* argmax_out = nullptr, int64_t argmax_rows = 0) {
+                    hipStream_t stream, int64_t* argmax_out = nullptr, int64_t argmax_rows = 0,
+                    const float* qm_src = nullptr, int64_t qm_rows = 0,
+                    float* qm_out = nullptr) {
   const int chunks = (V + kThreads - 1) / kThreads;
 #define RLT_PROBS_CASE(R, L)                                                                  \
   launch_probs<DT, R, L>(n, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,     \
                          max_top_k, apply_top_p, out, out_stride, stream, argmax_out,         \
-                         argmax_rows)
+                         argmax_rows, qm_src, qm_rows, qm_out)
   if (chunks <= 4) RLT_PROBS_CASE(4, 0);
   else if (chunks <= 16) RLT_PROBS_CASE(8, 8);
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
@@ -855,11 +891,20 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
     launch_probs<DT, kTailReg, kTailLds, true>(n, logits, rows, n_src, row_stride, V,
                                                temperature, top_k, top_p, max_top_k,
                                                apply_top_p, out, out_stride, stream, argmax_out,
-                                               argmax_rows);
+                                               argmax_rows, qm_src, qm_rows, qm_out);
 #undef RLT_PROBS_CASE
 }
 
 }  // namespace
+
+// spec_sampling.hip: the acceptance workspace's q-row partials, and the acceptance
+// launches that use them instead of summing q again.
+float* rlt_accept_q_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab);
+int rlt_accept_after_q_partials(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
+                                const float* p, const float* u_accept, const float* u_final,
+                                int64_t n, int32_t w1, int64_t vocab, int64_t* tokens,
+                                int64_t* accepted, int64_t* final_token, uint8_t* error,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // spec_sampling.hip: categorical draws over strided rows with a scatter list.
 int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u, int64_t m,
@@ -1011,6 +1056,50 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
   }
 #undef RLT_VERIFY
   return rlt_launch_status();
+}
+
+int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t row_stride,
+                      const float* temperature, const int64_t* top_k, const float* top_p,
+                      int64_t max_top_k, int32_t apply_top_p, const int64_t* draft_tokens,
+                      const int64_t* drafts, const float* q, const float* u_accept,
+                      const float* u_final, int64_t n, int32_t w1, int64_t vocab,
+                      int64_t* targets, float* p_out, int64_t* tokens, int64_t* accepted,
+                      int64_t* final_token, uint8_t* error, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
+  if (n < 0 || w1 < 0 || vocab < 1 || row_stride < vocab || max_top_k < 0) return RLT_ERR_ARGUMENT;
+  if (n == 0) return RLT_OK;
+  if (!target_logits || !temperature || !top_k || !top_p || !drafts || !u_final || !targets ||
+      !p_out || !tokens || !accepted || !final_token || !error ||
+      (w1 > 0 && (!draft_tokens || !q || !u_accept)))
+    return RLT_ERR_ARGUMENT;
+  const int64_t rows = n * (w1 + 1);
+  if (vocab > (int64_t)kMaxStreamChunks * kThreads || rows > 0x7fffffff || w1 > 32 ||
+      vocab >= ((int64_t)1 << 25))
+    return RLT_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < rlt_speculative_accept_workspace_size(n, w1, vocab))
+    return RLT_ERR_WORKSPACE;
+  float* qm_out = rlt_accept_q_partials(workspace, n, w1, vocab);
+  const int64_t q_rows = n * (int64_t)w1;
+  const int V = (int)vocab;
+  const int mtk = max_top_k > vocab ? V : (int)max_top_k;
+  // one launch: distributions of every verify row, their argmax targets, and the
+  // draft rows' row-sum partials; then the acceptance sums only p
+#define RLT_VERIFY_ACCEPT(DT)                                                                 \
+  dispatch_probs<DT>(rows, target_logits, nullptr, rows, row_stride, V, temperature, top_k,    \
+                     top_p, mtk, apply_top_p != 0, p_out, vocab, stream, targets, rows,        \
+                     q_rows > 0 ? q : nullptr, q_rows, qm_out)
+  switch (logits_dtype) {
+    case RLT_F32: RLT_VERIFY_ACCEPT(RLT_F32); break;
+    case RLT_BF16: RLT_VERIFY_ACCEPT(RLT_BF16); break;
+    case RLT_F16: RLT_VERIFY_ACCEPT(RLT_F16); break;
+    default: return RLT_ERR_UNSUPPORTED;
+  }
+#undef RLT_VERIFY_ACCEPT
+  const int st = rlt_launch_status();
+  if (st != RLT_OK) return st;
+  return rlt_accept_after_q_partials(draft_tokens, drafts, q, p_out, u_accept, u_final, n, w1,
+                                     vocab, tokens, accepted, final_token, error, workspace,
+                                     workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -30,6 +30,7 @@
 // (one "group" = 16 chunks = 8192 floats of the row), level 2 flushed to level 3
 // every 16 groups; leftovers per the final combine in rlt_row_mass_finish().
 
+#include "cascade.h"
 #include "common.h"
 #include "rlt_mi355x.h"
 
@@ -37,10 +38,12 @@
 
 namespace {
 
-constexpr int kStreams = 32;          // 8 lanes x ILP 4
-constexpr int kChunkSteps = 16;       // stream steps per level-0 chunk
-constexpr int kGroupChunks = 16;      // chunks per level-1 group
-constexpr int kGroupFloats = kStreams * kChunkSteps * kGroupChunks;  // 8192
+using cascade::kChunkSteps;
+using cascade::kGroupChunks;
+using cascade::kGroupFloats;
+using cascade::kStreams;
+using cascade::row_geom;
+using cascade::RowGeom;
 constexpr int kDrawThreads = 512;
 constexpr int kDrawWaves = kDrawThreads / 64;
 constexpr int kElems = 8;                           // weights per thread per tile
@@ -48,21 +51,6 @@ constexpr int kTile = kDrawThreads * kElems;        // 4096 tokens
 constexpr int kMaxTiles = 512;                      // V <= 2M on the fast path
 constexpr int kMaxW1 = 32;
 
-struct RowGeom {
-  int64_t vs;  // whole 8-lane vectors
-  int64_t si;  // steps per stream
-  int64_t full_chunks;
-  int64_t groups;  // level-1 groups holding >= 1 full chunk
-};
-
-__host__ __device__ inline RowGeom row_geom(int64_t V) {
-  RowGeom g;
-  g.vs = V / 8;
-  g.si = g.vs / 4;
-  g.full_chunks = g.si / kChunkSteps;
-  g.groups = (g.full_chunks + kGroupChunks - 1) / kGroupChunks;
-  return g;
-}
 
 // ------------------------------------------------------------------ kernel 1
 
@@ -75,45 +63,14 @@ __global__ __launch_bounds__(128) void rlt_mass_groups_kernel(const float* __res
                                                               int64_t p_rows, int64_t V,
                                                               int64_t groups, int64_t full_chunks,
                                                               float* __restrict__ out) {
-  __shared__ float chunk_sum[kGroupChunks][kStreams + 1];
+  __shared__ cascade::ChunkSums chunk_sum;
   const int64_t row = blockIdx.y;
   const int64_t g = blockIdx.x;
   const float* x = row < p_rows ? p + row * V : q + (row - p_rows) * V;
   const int t = threadIdx.x;
-  const int cc = t >> 3;
-  const int quad = t & 7;
-  const int64_t chunks_here = min<int64_t>(kGroupChunks, full_chunks - g * kGroupChunks);
-  if (cc < chunks_here) {
-    const float* base = x + g * kGroupFloats + (int64_t)cc * (kStreams * kChunkSteps) + quad * 4;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    if (kVec4) {
-      float4 v[kChunkSteps];
-#pragma unroll
-      for (int e = 0; e < kChunkSteps; ++e) v[e] = *(const float4*)(base + e * kStreams);
-#pragma unroll
-      for (int e = 0; e < kChunkSteps; ++e) {
-        a0 += v[e].x; a1 += v[e].y; a2 += v[e].z; a3 += v[e].w;
-      }
-    } else {
-#pragma unroll 4
-      for (int e = 0; e < kChunkSteps; ++e) {
-        a0 += base[e * kStreams + 0];
-        a1 += base[e * kStreams + 1];
-        a2 += base[e * kStreams + 2];
-        a3 += base[e * kStreams + 3];
-      }
-    }
-    chunk_sum[cc][quad * 4 + 0] = a0;
-    chunk_sum[cc][quad * 4 + 1] = a1;
-    chunk_sum[cc][quad * 4 + 2] = a2;
-    chunk_sum[cc][quad * 4 + 3] = a3;
-  }
+  cascade::group_chunk_sums<kVec4>(x, g, full_chunks, t, chunk_sum);
   __syncthreads();
-  if (t < kStreams && chunks_here > 0) {
-    float acc1 = 0.f;
-    for (int c = 0; c < chunks_here; ++c) acc1 += chunk_sum[c][t];
-    out[(row * groups + g) * kStreams + t] = acc1;
-  }
+  cascade::group_stream_sums(g, full_chunks, t, chunk_sum, out + (row * groups + g) * kStreams);
 }
 
 // Exact torch-CPU fp32 row sum of x[0..V) from the group partials (nullptr when
@@ -919,7 +876,62 @@ int launch_categorical(const float* weights, int64_t w_stride, const float* u, i
   return rlt_launch_status();
 }
 
+// speculative_accept; with q_partials_ready the workspace already holds the mass
+// partials of the q rows (written alongside the target distributions) and only the
+// p rows are summed here.
+int accept_launch(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
+                  const float* p, const float* u_accept, const float* u_final, int64_t n,
+                  int32_t w1, int64_t vocab, int64_t* tokens, int64_t* accepted,
+                  int64_t* final_token, uint8_t* error, void* workspace, size_t workspace_bytes,
+                  bool q_partials_ready, hipStream_t stream) {
+  if (n < 0 || w1 < 0 || w1 > kMaxW1 || vocab < 1) return RLT_ERR_ARGUMENT;
+  if (vocab >= ((int64_t)1 << 25)) return RLT_ERR_UNSUPPORTED;
+  if (n == 0) return RLT_OK;
+  const int64_t rows = n * (2 * (int64_t)w1 + 1);
+  const Layout l = layout_for(rows, n, vocab);
+  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
+  char* ws = (char*)workspace;
+  float* partials = (float*)(ws + l.partials);
+  double* tile_sum = (double*)(ws + l.tile_sum);
+  uint32_t* tile_flags = (uint32_t*)(ws + l.tile_flags);
+  StopState* stop = (StopState*)(ws + l.stop);
+  int32_t* slow = (int32_t*)(ws + l.slow);
+  const RowGeom geo = row_geom(vocab);
+  const int64_t tiles = (vocab + kTile - 1) / kTile;
+  if (tiles > 65535) return RLT_ERR_UNSUPPORTED;  // grid.y of the tile kernel
+  const int64_t p_rows = n * (w1 + 1);
+  if (q_partials_ready)
+    launch_mass_groups(p, nullptr, p_rows, p_rows, vocab, partials, stream);
+  else
+    launch_mass_groups(p, w1 > 0 ? q : nullptr, p_rows, rows, vocab, partials, stream);
+  rlt_accept_tiles_kernel<<<dim3((unsigned)n, (unsigned)tiles), kDrawThreads, 0, stream>>>(
+      p, q, w1, vocab, n, geo.groups > 0 ? partials : nullptr, geo.groups, draft_tokens, drafts,
+      u_accept, tile_sum, tile_flags, stop);
+  rlt_accept_draw_kernel<<<(unsigned)n, kDrawThreads, 0, stream>>>(
+      p, q, w1, vocab, tiles, u_final, tile_sum, tile_flags, stop, final_token, tokens, accepted,
+      error, slow);
+  return rlt_launch_status();
+}
+
 }  // namespace
+
+// The mass partials of the q rows inside an acceptance workspace (q row r at
+// partials + r * groups * 32), for a launch that computes them.
+float* rlt_accept_q_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab) {
+  const Layout l = layout_for(n * (2 * (int64_t)w1 + 1), n, vocab);
+  return (float*)((char*)workspace + l.partials) +
+         n * (w1 + 1) * row_geom(vocab).groups * kStreams;
+}
+
+// speculative_accept after the q rows' partials were written into the workspace.
+int rlt_accept_after_q_partials(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
+                                const float* p, const float* u_accept, const float* u_final,
+                                int64_t n, int32_t w1, int64_t vocab, int64_t* tokens,
+                                int64_t* accepted, int64_t* final_token, uint8_t* error,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
+                       accepted, final_token, error, workspace, workspace_bytes, true, stream);
+}
 
 extern "C" {
 
@@ -936,29 +948,8 @@ int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, c
                            int32_t w1, int64_t vocab, int64_t* tokens, int64_t* accepted,
                            int64_t* final_token, uint8_t* error, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-  if (n < 0 || w1 < 0 || w1 > kMaxW1 || vocab < 1) return RLT_ERR_ARGUMENT;
-  if (vocab >= ((int64_t)1 << 25)) return RLT_ERR_UNSUPPORTED;
-  if (n == 0) return RLT_OK;
-  const int64_t rows = n * (2 * (int64_t)w1 + 1);
-  const Layout l = layout_for(rows, n, vocab);
-  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
-  char* ws = (char*)workspace;
-  float* partials = (float*)(ws + l.partials);
-  double* tile_sum = (double*)(ws + l.tile_sum);
-  uint32_t* tile_flags = (uint32_t*)(ws + l.tile_flags);
-  StopState* stop = (StopState*)(ws + l.stop);
-  int32_t* slow = (int32_t*)(ws + l.slow);
-  const RowGeom geo = row_geom(vocab);
-  const int64_t tiles = (vocab + kTile - 1) / kTile;
-  if (tiles > 65535) return RLT_ERR_UNSUPPORTED;  // grid.y of the tile kernel
-  launch_mass_groups(p, w1 > 0 ? q : nullptr, n * (w1 + 1), rows, vocab, partials, stream);
-  rlt_accept_tiles_kernel<<<dim3((unsigned)n, (unsigned)tiles), kDrawThreads, 0, stream>>>(
-      p, q, w1, vocab, n, geo.groups > 0 ? partials : nullptr, geo.groups, draft_tokens, drafts,
-      u_accept, tile_sum, tile_flags, stop);
-  rlt_accept_draw_kernel<<<(unsigned)n, kDrawThreads, 0, stream>>>(
-      p, q, w1, vocab, tiles, u_final, tile_sum, tile_flags, stop, final_token, tokens, accepted,
-      error, slow);
-  return rlt_launch_status();
+  return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
+                       accepted, final_token, error, workspace, workspace_bytes, false, stream);
 }
 
 int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t vocab,

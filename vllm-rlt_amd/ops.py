@@ -126,6 +126,31 @@ def _(logits, random_rows, temperature, top_k, top_p, max_top_k, apply_top_p):
             logits.new_empty((random_rows.shape[0], logits.shape[1]), dtype=torch.float32))
 
 
+@torch.library.custom_op("rlt_mi355x::verify_accept", mutates_args=(), device_types="cuda")
+def verify_accept(target_logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.Tensor,
+                  top_p: torch.Tensor, draft_tokens: torch.Tensor, drafts: torch.Tensor,
+                  q: torch.Tensor, u_accept: torch.Tensor, u_final: torch.Tensor, max_top_k: int,
+                  apply_top_p: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                              torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(target, p, tokens, accepted, final, error); reference:
+    vllm_rlt/worker/async_speculative.py:678-692 then :727-734."""
+    target, p, res = _samp.verify_accept(target_logits, temperature, top_k, top_p, draft_tokens,
+                                         drafts, q, u_accept, u_final, max_top_k=max_top_k,
+                                         apply_top_p=apply_top_p)
+    return (target, p) + tuple(res)
+
+
+@verify_accept.register_fake
+def _(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept, u_final,
+      max_top_k, apply_top_p):
+    n, w1 = draft_tokens.shape
+    i64 = dict(dtype=torch.int64)
+    x = target_logits
+    return (x.new_empty((n * (w1 + 1),), **i64), x.new_empty(x.shape, dtype=torch.float32),
+            x.new_empty((n, w1 + 1), **i64), x.new_empty((n,), **i64), x.new_empty((n,), **i64),
+            x.new_empty((n,), dtype=torch.bool))
+
+
 @torch.library.custom_op("rlt_mi355x::store_kv", mutates_args=("key_cache", "value_cache"),
                          device_types="cuda")
 def store_kv(key_cache: torch.Tensor, value_cache: torch.Tensor, k: torch.Tensor,
@@ -156,4 +181,4 @@ def finalize_rows(descriptor: torch.Tensor, tables: torch.Tensor, key_pool: torc
 
 
 OPS = ("paged_attention", "spec_probs", "categorical", "spec_accept", "greedy_accept",
-       "propose_drafts", "verify_distributions", "store_kv", "store_fp8", "finalize_rows")
+       "propose_drafts", "verify_distributions", "verify_accept", "store_kv", "store_fp8", "finalize_rows")

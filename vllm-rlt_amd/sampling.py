@@ -266,6 +266,61 @@ def speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final):
     return AcceptResult(tokens, accepted, final, error)
 
 
+def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
+                  u_final, *, max_top_k, apply_top_p):
+    """The stochastic verify round in one call: ``(target, p, AcceptResult)``.
+
+    ``target, p = verify_distributions(target_logits.view(-1, V), all rows, ...)`` and
+    ``speculative_accept(draft_tokens, drafts, q, p.view(n, W1 + 1, V), u_accept,
+    u_final)``, bitwise (reference: vllm_rlt/worker/async_speculative.py:678-692 then
+    :727-734).  The draft rows' row sums are computed by otherwise idle workgroups of
+    the distribution launch.  ``temperature`` / ``top_k`` / ``top_p`` are per verify row
+    ``[n * (W1 + 1)]``; ``target`` is ``[n * (W1 + 1)]``.
+    """
+    n, w1 = draft_tokens.shape
+    if target_logits.ndim != 3 or target_logits.shape[:2] != (n, w1 + 1):
+        raise ValueError("target_logits must be [n, W1 + 1, V]")
+    vocab = target_logits.shape[-1]
+    rows = n * (w1 + 1)
+    for name, value in (("temperature", temperature), ("top_k", top_k), ("top_p", top_p)):
+        if value.shape != (rows,):
+            raise ValueError(f"{name} must have shape [{rows}], got {tuple(value.shape)}")
+    if drafts.shape != (n,) or u_final.shape != (n,) or u_accept.shape != (n, w1):
+        raise ValueError("drafts, u_accept and u_final must match draft_tokens [n, W1]")
+    if q.shape != (n, w1, vocab):
+        raise ValueError("q must be [n, W1, V]")
+    if max_top_k < 0:
+        raise ValueError("max_top_k must be nonnegative")
+    if w1 > 32:
+        raise ValueError("at most 32 draft tokens per request are supported")
+    _lib.require_gpu(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
+                     u_final)
+    device = target_logits.device
+    target = torch.empty(rows, dtype=torch.int64, device=device)
+    p = torch.empty((n, w1 + 1, vocab), dtype=torch.float32, device=device)
+    tokens = torch.empty((n, w1 + 1), dtype=torch.int64, device=device)
+    accepted = torch.empty(n, dtype=torch.int64, device=device)
+    final = torch.empty(n, dtype=torch.int64, device=device)
+    error = torch.empty(n, dtype=torch.bool, device=device)
+    if n == 0:
+        return target, p, AcceptResult(tokens, accepted, final, error)
+    x = target_logits.reshape(rows, vocab)
+    if x.dtype not in _LOGIT_DTYPES:
+        x = x.float()
+    x = _rows(x)
+    lib = _lib.library()
+    ws = _lib.workspace(lib.rlt_speculative_accept_workspace_size(n, w1, vocab), device)
+    status = lib.rlt_verify_accept(
+        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), _lib.ptr(_f32(temperature)),
+        _lib.ptr(_i64(top_k)), _lib.ptr(_f32(top_p)), int(max_top_k), int(bool(apply_top_p)),
+        _lib.ptr(_i64(draft_tokens)), _lib.ptr(_i64(drafts)), _lib.ptr(_f32(q)),
+        _lib.ptr(_f32(u_accept)), _lib.ptr(_f32(u_final)), n, w1, vocab, _lib.ptr(target),
+        _lib.ptr(p), _lib.ptr(tokens), _lib.ptr(accepted), _lib.ptr(final), _lib.ptr(error),
+        _lib.ptr(ws), ws.numel(), _lib.stream_of(device))
+    _lib.check(status, "rlt_verify_accept")
+    return target, p, AcceptResult(tokens, accepted, final, error)
+
+
 def row_mass(x):
     """``x.sum(-1, dtype=float32)`` of a 2-D fp32 tensor in torch-CPU summation order."""
     if x.ndim != 2:
