@@ -185,7 +185,7 @@ def test_config_shaped_parity(pkg, dev, name, n, vocab, temperature, top_p, dtyp
 
 
 @pytest.mark.parametrize("vocab", [1, 2, 17, 1000, 1024, 1025, 4096, 4097, 16384, 16385, 32768,
-                                   32769, 49152, 65536, 65537, 128256, 131072 + 3, 151936])
+                                   32769, 49152, 49153, 57344, 59000, 61440, 65536, 65537, 128256, 131072 + 3, 151936])
 def test_mixed_filters_across_vocab_sizes(pkg, dev, vocab):
     """Every row placement (registers, registers + LDS, re-reading) with a mix of
     temperatures, top-k (including k >= V and k <= 0) and top-p per row."""
@@ -293,7 +293,7 @@ def test_greedy_round_bit_exact(pkg, dev, dtype, vocab):
     assert got[0][7, 2].item() == vocab // 2
 
 
-@pytest.mark.parametrize("vocab", [3000, 49152, 65536, 100003])
+@pytest.mark.parametrize("vocab", [3000, 49152, 57000, 59000, 61000, 65536, 100003])
 def test_crowded_rows_use_the_exact_path(pkg, dev, vocab):
     """Near-flat rows put thousands of tokens into one mass bin, more than the fast
     kernel's sorted list holds: those rows are recomputed by the exact path, the

@@ -886,6 +886,9 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
   else if (chunks <= 16) RLT_PROBS_CASE(8, 8);
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
   else if (chunks <= 48) RLT_PROBS_CASE(16, 32);
+  else if (chunks <= 56) RLT_PROBS_CASE(24, 32);
+  else if (chunks <= 58) RLT_PROBS_CASE(26, 32);
+  else if (chunks <= 60) RLT_PROBS_CASE(28, 32);
   else if (chunks <= kMaxRegChunks) RLT_PROBS_CASE(30, 34);
   else
     launch_probs<DT, kTailReg, kTailLds, true>(n, logits, rows, n_src, row_stride, V,
