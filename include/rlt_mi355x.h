@@ -71,6 +71,15 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
 /* 1 when (q dtype, kv dtype, head_dim) runs on the MFMA kernel, else 0 (vector kernel). */
 int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim);
 
+/* 1 when a packed call with this longest q window takes the long-prompt prefill
+ * tiling (bf16 / fp16 q with KV of the same type, head_dim 64 or 128, max_q_len >= 64):
+ * 128-row groups, K / V tiles shared through LDS, normalized in one launch.  Rows of
+ * such a call match the per-row form within floating-point tolerance; every other
+ * call (all verify windows) equals the per-row form bit for bit.  The reference's
+ * prefill kernel is a separate tiling too: vllm_rlt/kernels/triton_attention.py:250-383. */
+int rlt_paged_attention_uses_prefill(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim,
+                                     int32_t max_q_len);
+
 /* ---------------------------------------------------------------- sampler */
 
 /*

@@ -97,7 +97,21 @@ def test_packed_window_matches_oracle_and_per_row_bitwise(kernel, dev, dtype, he
     seq_of_row, row_len = oatt.packed_row_layout(lengths, cu)
     per_row = kernel(q.to(dev), kd, vd, tables[torch.tensor(seq_of_row)].to(dev),
                      torch.tensor(row_len, dtype=torch.int32).to(dev))
-    assert torch.equal(per_row, packed), "packed window differs from per-row decode"
+    if kernel.uses_prefill_tiling(dtype, dtype, head_dim, max(c for _, c in seqs)):
+        # windows of 64+ rows take the prefill tiling: equal within tolerance
+        _close(packed, per_row.cpu().float(), dtype)
+    else:
+        assert torch.equal(per_row, packed), "packed window differs from per-row decode"
+    # verify-length windows (at most 33 rows) equal per-row decode bit for bit
+    short = torch.tensor([0, 5, 38, 41, 58, 91, 96, 101], dtype=torch.int32)
+    assert not kernel.uses_prefill_tiling(dtype, dtype, head_dim, 33)
+    qs = q[: int(short[-1])]
+    packed_s = kernel.prefill(qs.to(dev), kd, vd, tables.to(dev), lengths.to(dev), short.to(dev),
+                              33)
+    seq_of_row, row_len = oatt.packed_row_layout(lengths, short)
+    per_row_s = kernel(qs.to(dev), kd, vd, tables[torch.tensor(seq_of_row)].to(dev),
+                       torch.tensor(row_len, dtype=torch.int32).to(dev))
+    assert torch.equal(per_row_s, packed_s), "packed verify window differs from per-row decode"
 
 
 @pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float32])
@@ -339,13 +353,19 @@ def _dense_packed(q, k_seq, v_seq, q_len, length, window=0):
 
 
 @pytest.mark.parametrize("window", [0, 256])
-def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window):
+@pytest.mark.parametrize("dtype,d,hq,hkv", [(torch.bfloat16, 128, 16, 4),
+                                            (torch.float16, 64, 8, 8),
+                                            (torch.bfloat16, 64, 4, 1),
+                                            (torch.float16, 128, 6, 2),
+                                            (torch.bfloat16, 96, 8, 2)])
+def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d, hq, hkv):
     """Prompt prefill on the same backend: a 1024-token prompt from scratch, a
-    512-token chunk after a 1536-token prefix, and a short window, packed together."""
-    _say("long prefill", window)
+    512-token chunk after a 1536-token prefix, ragged windows (64, 97 and 129 rows,
+    one shorter than its 128-row group), and a short window, packed together."""
+    _say("long prefill", window, dtype, d, hq, hkv)
     g = torch.Generator().manual_seed(21)
-    bs, hq, hkv, d, dtype = 16, 16, 4, 128, torch.bfloat16
-    seqs = [(1024, 1024), (2048, 512), (3000, 37)]
+    bs = 16
+    seqs = [(1024, 1024), (2048, 512), (3000, 37), (64, 64), (300, 97), (129, 129)]
     pages = sum(-(-n // bs) for n, _ in seqs) + 2
     _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
     tables = random_tables([n for n, _ in seqs], bs, pages, g)

@@ -32,6 +32,7 @@ _i32, _i64, _sz, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_
 _SIGNATURES = {
     "rlt_paged_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "rlt_paged_attention_uses_mfma": (ctypes.c_int, [_i32, _i32, _i32]),
+    "rlt_paged_attention_uses_prefill": (ctypes.c_int, [_i32, _i32, _i32, _i32]),
     "rlt_paged_attention": (ctypes.c_int, [
         _p, _i64, _i64,                 # q
         _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,  # k, v, strides

@@ -196,6 +196,13 @@ class MI355XPagedAttention:
         return bool(lib.rlt_paged_attention_uses_mfma(_lib.dtype_code(q_dtype),
                                                       _lib.dtype_code(kv_dtype), head_dim))
 
+    def uses_prefill_tiling(self, q_dtype, kv_dtype, head_dim, max_seqlen_q):
+        """True when ``prefill`` calls with this longest window take the long-prompt
+        tiling (equal to the per-row form within tolerance, not bit for bit)."""
+        lib = _lib.library()
+        return bool(lib.rlt_paged_attention_uses_prefill(
+            _lib.dtype_code(q_dtype), _lib.dtype_code(kv_dtype), head_dim, max_seqlen_q))
+
 
 _BACKEND_NAMES = ("auto", "mi355x")
 

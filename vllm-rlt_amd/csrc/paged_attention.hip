@@ -1231,6 +1231,259 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
   }
 }
 
+// ============================================================ long-prompt prefill
+//
+// Calls whose longest q window reaches kPfMinQ rows (prompt prefill, long chunks)
+// take a tiling built for many rows per sequence: one 256-thread workgroup per
+// (sequence, 128-row group, kv head), each wave owning 32 rows (two 16-row MFMA
+// tiles).  64-position K and V tiles are staged once per workgroup in LDS (K as
+// [position][dim], V transposed to [dim][position] while it is stored) and shared
+// by the four waves, double-buffered with the next tile's global loads in
+// registers.  The math is the verify kernel's (S^T = K Q^T, online softmax in the
+// log2 domain, O^T = V^T P^T), with both products on v_mfma_f32_16x16x32: the
+// P^T operand of a key-tile pair is the two S^T accumulators of the lane, and the
+// contraction order over the pair's 32 positions is permuted to match.  The
+// output is normalized in the kernel (no split, no merge launch).  Rows of such a
+// call are equal to the per-row form within floating-point tolerance, not bit for
+// bit (the tile boundaries differ).
+constexpr int kPfRows = 128;    // q rows per workgroup
+constexpr int kPfKeys = 64;     // key positions per LDS tile
+constexpr int kPfThreads = 256;
+constexpr int kPfMinQ = 64;     // q window length from which a call takes this path
+
+template <int D>
+struct PrefillLds {
+  static constexpr int kKRow = D * 2 + 16;            // bytes per K position row
+  static constexpr int kVRowW = kPfKeys / 2 + 1;      // dwords per V^T dim row (odd: fewer conflicts)
+  uint8_t k[2][kPfKeys * kKRow];
+  uint32_t vt[2][D * kVRowW];
+};
+
+template <int QT, int D>
+__global__ __launch_bounds__(kPfThreads, 2) void rlt_prefill_kernel(AttnParams P) {
+  using M = Mfma<QT>;
+  using L = PrefillLds<D>;
+  constexpr int NT = 2;             // 16-row tiles per wave
+  constexpr int NQS = D / 32;       // 32-wide contraction slices of S^T
+  constexpr int ND = D / 16;        // 16-wide dim tiles of O^T
+  constexpr int KCH = D / 8;        // 16-byte pieces per position row
+  constexpr int KSTEP = kPfThreads / KCH;          // K rows one pass of the workgroup loads
+  constexpr int KPT = kPfKeys / KSTEP;             // K pieces per thread per tile
+  constexpr int VPAIRS = kPfThreads / KCH;         // V position pairs per pass
+  constexpr int VPT = kPfKeys / (2 * VPAIRS);      // V passes per tile (two pieces each)
+  __shared__ L sh;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
+
+  // heaviest row-groups (latest positions) first
+  const int64_t id = blockIdx.x;
+  const int kvh = (int)(id % P.hkv);
+  const int64_t sr = id / P.hkv;
+  const int rg = P.rowgroups - 1 - (int)(sr % P.rowgroups);
+  const int seq = (int)(sr / P.rowgroups);
+  const SeqView sv = seq_view(P, seq);
+  const int rows_total = sv.q_len * P.group;
+  const int rg_begin = rg * kPfRows;
+  if (rg_begin >= rows_total) return;  // uniform over the workgroup
+  const int rg_rows = min(kPfRows, rows_total - rg_begin);
+  int lo_first, hi_first, lo_last, hi_last;
+  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
+  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+
+  // this lane's rows (one per 16-row tile): B operand of S^T = K Q^T
+  uint4 qreg[NT][NQS];
+  int row_lo[NT], row_hi[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int local = w * 32 + nt * 16 + l16;
+    if (local < rg_rows) {
+      const int rho = rg_begin + local;
+      const int qi = rho / P.group;
+      const int head = kvh * P.group + rho % P.group;
+      row_range(P, sv, qi, row_lo[nt], row_hi[nt]);
+      const uint16_t* qp = (const uint16_t*)P.q + (int64_t)(sv.q_begin + qi) * P.q_row_stride +
+                           (int64_t)head * P.q_head_stride + grp * 8;
+#pragma unroll
+      for (int s = 0; s < NQS; ++s) qreg[nt][s] = *(const uint4*)(qp + 32 * s);
+    } else {
+      row_lo[nt] = row_hi[nt] = 0;
+#pragma unroll
+      for (int s = 0; s < NQS; ++s) qreg[nt][s] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  f32x4 oacc[NT][ND];
+  float m_run[NT], l_run[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- global -> registers -> LDS staging of one 64-position tile
+  const int piece = t % KCH;
+  const int krow = t / KCH;  // K: rows krow + KSTEP j;  V: pairs (2 krow, 2 krow + 1) + 2 VPAIRS h
+  const int64_t k_head = (int64_t)kvh * P.k_head_stride + piece * 8;
+  const int64_t v_head = (int64_t)kvh * P.v_head_stride + piece * 8;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 kr[KPT], vr[2 * VPT];
+  auto token = [&](int pos, int64_t block_stride, int64_t token_stride) {
+    const int idx = min(pos / P.block_size, P.table_width - 1);
+    const int32_t e = P.tables[(int64_t)seq * P.table_stride + idx];
+    const int64_t blk = (e >= 0 && e < P.num_blocks) ? e : 0;
+    return blk * block_stride + (int64_t)(pos % P.block_size) * token_stride;
+  };
+  auto load = [&](int tile) {
+    const int base = tile * kPfKeys;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int pos = base + krow + KSTEP * j;
+      kr[j] = *(const u32x4*)((const uint16_t*)P.k + token(pos, P.k_block_stride, P.k_token_stride) +
+                               k_head);
+    }
+#pragma unroll
+    for (int h = 0; h < VPT; ++h)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int pos = base + 2 * krow + 2 * VPAIRS * h + e;
+        const u32x4 v = *(const u32x4*)((const uint16_t*)P.v +
+                                        token(pos, P.v_block_stride, P.v_token_stride) + v_head);
+        // positions past the sequence may hold any bits (NaN included): zero them,
+        // since their weight 0 times NaN would not vanish
+        vr[2 * h + e] = pos < hi_last ? v : u32x4{0u, 0u, 0u, 0u};
+      }
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+      *(u32x4*)(sh.k[b] + (krow + KSTEP * j) * L::kKRow + piece * 16) = kr[j];
+#pragma unroll
+    for (int h = 0; h < VPT; ++h) {
+      const u32x4 av = vr[2 * h], cv = vr[2 * h + 1];
+      const int col = krow + VPAIRS * h;  // dword column: positions 2 col, 2 col + 1
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // dims piece*8 + 2q (low halves) and + 2q + 1 (high halves)
+        const uint32_t lo = (av[q] & 0xffffu) | (cv[q] << 16);
+        const uint32_t hi = (av[q] >> 16) | (cv[q] & 0xffff0000u);
+        sh.vt[b][(piece * 8 + 2 * q) * L::kVRowW + col] = lo;
+        sh.vt[b][(piece * 8 + 2 * q + 1) * L::kVRowW + col] = hi;
+      }
+    }
+  };
+
+  const float qk_scale = P.qk_scale_log2;
+  auto compute = [&](int tile, int b) {
+    const int base = tile * kPfKeys;
+    const uint8_t* kb = sh.k[b];
+    const uint32_t* vb = sh.vt[b];
+    // ---- S^T = K Q^T for the tile's four 16-position sub-tiles
+    f32x4 sc[4][NT];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) sc[kt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NQS; ++s)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const uint4 a = *(const uint4*)(kb + (kt * 16 + l16) * L::kKRow + (s * 32 + grp * 8) * 2);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) sc[kt][nt] = M::qk(a, qreg[nt][s], sc[kt][nt]);
+      }
+    // ---- online softmax (log2 domain); lane holds positions base + 16 kt + 4 grp + i
+    uint4 pop[2][NT];
+    bool rescale = false;
+    float corr[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float x[4][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int pos = base + kt * 16 + 4 * grp + i;
+          const float v = sc[kt][nt][i] * qk_scale;
+          x[kt][i] = (pos >= row_lo[nt] && pos < row_hi[nt]) ? v : -INFINITY;
+          mx = fmaxf(mx, x[kt][i]);
+        }
+      mx = group_max(mx);
+      const float m_new = fmaxf(m_run[nt], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      corr[nt] = m_new == m_run[nt] ? 1.f : __builtin_amdgcn_exp2f(m_run[nt] - m_use);
+      rescale |= corr[nt] != 1.f;
+      float rs = 0.f;
+      float pr[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[kt][i] = __builtin_amdgcn_exp2f(x[kt][i] - m_use);
+          rs += pr[kt][i];
+        }
+      l_run[nt] = l_run[nt] * corr[nt] + group_sum(rs);
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        pop[c][nt] = make_uint4(M::pack2(pr[2 * c][0], pr[2 * c][1]),
+                                M::pack2(pr[2 * c][2], pr[2 * c][3]),
+                                M::pack2(pr[2 * c + 1][0], pr[2 * c + 1][1]),
+                                M::pack2(pr[2 * c + 1][2], pr[2 * c + 1][3]));
+    }
+    if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] *= corr[nt];
+    }
+    // ---- O^T += V^T P^T over the sub-tile pairs (2c, 2c + 1): contraction slot
+    // 8 grp + j is position 16 (2c) + 4 grp + j for j < 4, else 16 (2c + 1) + 4 grp + j - 4
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const uint32_t* row = vb + (dt * 16 + l16) * L::kVRowW + 16 * c + 2 * grp;
+        const uint4 a = make_uint4(row[0], row[1], row[8], row[9]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::qk(a, pop[c][nt], oacc[nt][dt]);
+      }
+  };
+
+  const int kt0 = lo_first / kPfKeys;
+  const int kt1 = (hi_last + kPfKeys - 1) / kPfKeys;
+  if (kt0 < kt1) {
+    load(kt0);
+    store(0);
+    __syncthreads();
+    for (int tile = kt0; tile < kt1; ++tile) {
+      const int b = (tile - kt0) & 1;
+      const bool more = tile + 1 < kt1;
+      if (more) load(tile + 1);
+      compute(tile, b);
+      // buffer b ^ 1 was last read in the previous iteration, before its barrier
+      if (more) store(b ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- normalized output: lane holds dims 16 dt + 4 grp + i of its rows
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int local = w * 32 + nt * 16 + l16;
+    if (local >= rg_rows) continue;
+    const int rho = rg_begin + local;
+    const int qi = rho / P.group;
+    const int head = kvh * P.group + rho % P.group;
+    const int64_t off = (int64_t)(sv.q_begin + qi) * P.out_row_stride + (int64_t)head * P.out_head_stride;
+    const float inv = 1.f / fmaxf(l_run[nt], 1.0e-30f);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store_from_f32<QT>(P.out, off + dt * 16 + 4 * grp + i, oacc[nt][dt][i] * inv);
+  }
+}
+
 // ============================================================ dispatch
 
 template <int QT, int KVT, int D, int SM, bool UB, int NT>
@@ -1323,6 +1576,12 @@ int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t hea
   return qok && kvok && mfma_head_dim(head_dim);
 }
 
+int rlt_paged_attention_uses_prefill(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim,
+                                     int32_t max_q_len) {
+  return rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) && kv_dtype == q_dtype &&
+         (head_dim == 64 || head_dim == 128) && max_q_len >= kPfMinQ;
+}
+
 size_t rlt_paged_attention_workspace_size(int32_t num_q_rows, int32_t num_q_heads, int32_t head_dim,
                                           int32_t table_width, int32_t block_size) {
   const int64_t slots = (int64_t)num_q_rows * num_q_heads * max_chunks_for(table_width, block_size);
@@ -1413,6 +1672,22 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
         (k_head_stride * kv_elt) % kv_align == 0 && (v_block_stride * kv_elt) % kv_align == 0 &&
         (v_token_stride * kv_elt) % kv_align == 0 && (v_head_stride * kv_elt) % kv_align == 0;
     if (!aligned) return RLT_ERR_ARGUMENT;
+    if (cu_seqlens_q && rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len)) {
+      // long q windows: the prefill tiling, normalized in one launch
+      P.rows_per_rg = kPfRows;
+      P.rowgroups = (rows_per_seq + kPfRows - 1) / kPfRows;
+      const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads;
+      if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
+      const dim3 grid((unsigned)wgs);
+      if (q_dtype == RLT_BF16) {
+        if (head_dim == 64) rlt_prefill_kernel<RLT_BF16, 64><<<grid, kPfThreads, 0, stream>>>(P);
+        else rlt_prefill_kernel<RLT_BF16, 128><<<grid, kPfThreads, 0, stream>>>(P);
+      } else {
+        if (head_dim == 64) rlt_prefill_kernel<RLT_F16, 64><<<grid, kPfThreads, 0, stream>>>(P);
+        else rlt_prefill_kernel<RLT_F16, 128><<<grid, kPfThreads, 0, stream>>>(P);
+      }
+      return rlt_launch_status();
+    }
     const int nt = (rows_per_seq > 16 && head_dim <= 128) ? 2 : 1;
     P.rows_per_rg = 16 * nt;
     P.rowgroups = (rows_per_seq + P.rows_per_rg - 1) / P.rows_per_rg;
