@@ -25,9 +25,11 @@
 // boundaries and its own q vector -- never on which other rows share its
 // workgroup -- so packed verify equals per-row decode bit for bit and results are
 // batch invariant (the reference's ``packed_matches_decode`` contract,
-// vllm_rlt/attention/backend.py:25-27).
+// vllm_rlt/attention/backend.py:25-27).  The one exception is a packed call whose
+// longest window reaches kPfMinQ = 64 rows (prompt prefill: no verify window is that
+// long), which takes the prefill tiling further down (rlt_prefill_kernel).
 //
-// Math paths (chosen by dtype and head_dim only, never by row count):
+// Math paths of the split kernels (chosen by dtype and head_dim only, never by row count):
 //  * MFMA (q bf16/fp16, KV same type or fp8-e4m3, head_dim % 32 == 0, <= 256):
 //    S^T = K Q^T with v_mfma_f32_16x16x32_{bf16,f16} straight from global memory
 //    (the contraction order is permuted so that each lane's eight elements per
