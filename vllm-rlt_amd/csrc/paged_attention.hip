@@ -1248,7 +1248,8 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
 // output is normalized in the kernel (no split, no merge launch).  Rows of such a
 // call are equal to the per-row form within floating-point tolerance, not bit for
 // bit (the tile boundaries differ).
-constexpr int kPfRows = 128;    // q rows per workgroup
+constexpr int kPfNT = 2;        // 16-row MFMA tiles per wave
+constexpr int kPfRows = 4 * 16 * kPfNT;  // q rows per workgroup (4 waves)
 constexpr int kPfKeys = 64;     // key positions per LDS tile
 constexpr int kPfThreads = 256;
 constexpr int kPfMinQ = 64;     // q window length from which a call takes this path
@@ -1262,10 +1263,10 @@ struct PrefillLds {
 };
 
 template <int QT, int D>
-__global__ __launch_bounds__(kPfThreads, 2) void rlt_prefill_kernel(AttnParams P) {
+__global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_kernel(AttnParams P) {
   using M = Mfma<QT>;
   using L = PrefillLds<D>;
-  constexpr int NT = 2;             // 16-row tiles per wave
+  constexpr int NT = kPfNT;
   constexpr int NQS = D / 32;       // 32-wide contraction slices of S^T
   constexpr int ND = D / 16;        // 16-wide dim tiles of O^T
   constexpr int KCH = D / 8;        // 16-byte pieces per position row
@@ -1296,7 +1297,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void rlt_prefill_kernel(AttnParams P
   int row_lo[NT], row_hi[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int local = w * 32 + nt * 16 + l16;
+    const int local = w * 16 * NT + nt * 16 + l16;
     if (local < rg_rows) {
       const int rho = rg_begin + local;
       const int qi = rho / P.group;
@@ -1472,7 +1473,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void rlt_prefill_kernel(AttnParams P
   // ---- normalized output: lane holds dims 16 dt + 4 grp + i of its rows
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int local = w * 32 + nt * 16 + l16;
+    const int local = w * 16 * NT + nt * 16 + l16;
     if (local >= rg_rows) continue;
     const int rho = rg_begin + local;
     const int qi = rho / P.group;
