@@ -171,6 +171,167 @@ def config2_decode(pkg, dev):
             "GBps": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def _graph_time(fn, reps=3, per_graph=10):
+    """Average launch time of ``fn`` replayed from a HIP graph of ``per_graph`` calls,
+    HIP events on the current stream, queue pre-filled."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            out = fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    torch.cuda._sleep(50_000_000)
+    for a, b in ev:
+        a.record(s)
+        graph.replay()
+        b.record(s)
+    torch.cuda.synchronize()
+    t = sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3 / per_graph
+    eager = fn()
+    torch.cuda.synchronize()
+    same = all(torch.equal(x, y) for x, y in zip(_flat(eager), _flat(out)))
+    del graph
+    return t, same
+
+
+def _flat(x):
+    if isinstance(x, torch.Tensor):
+        return [x]
+    out = []
+    for y in x:
+        out.extend(_flat(y))
+    return out
+
+
+def _fp8_pool(shape, dev, gd):
+    """Random finite float8_e4m3fn bytes (0x7f / 0xff are NaN), filled in 1 GiB pieces."""
+    buf = torch.empty(shape, dtype=torch.uint8, device=dev)
+    flat = buf.view(-1)
+    step = 1 << 30
+    for i in range(0, flat.numel(), step):
+        c = flat[i:i + step]
+        c.random_(0, 255, generator=gd)
+        c.masked_fill_(c == 0x7F, 0x7E)
+    return buf.view(torch.float8_e4m3fn)
+
+
+def _accept_part(pkg, dev, gd, n, window, vocab):
+    """The verify round at T = 1, no truncation (configs 4 and 5 name no truncation):
+    target argmax, distributions and acceptance in one ``verify_accept`` call."""
+    k = window - 1
+    draft_logits = torch.randn(n, k, vocab, generator=gd, device=dev) * 3.0
+    target_logits = torch.cat([draft_logits, draft_logits[:, :1]], 1) + torch.randn(
+        n, window, vocab, generator=gd, device=dev)
+    qprob = draft_logits.softmax(-1).contiguous()
+    u = torch.rand(n, 2 * k + 1, generator=gd, device=dev)
+    drafts_tok = torch.stack([pkg.categorical(qprob[:, j].contiguous(), u[:, j].contiguous())[0]
+                              for j in range(k)], 1)
+    drafts = torch.full((n,), k, dtype=torch.int64, device=dev)
+    rows = n * window
+    temp = torch.ones(rows, device=dev)
+    top_k = torch.full((rows,), -1, dtype=torch.int64, device=dev)
+    top_p = torch.ones(rows, device=dev)
+    ua, uf = u[:, k:2 * k].contiguous(), u[:, 2 * k].contiguous()
+
+    def verify():
+        return pkg.verify_accept(target_logits, temp, top_k, top_p, drafts_tok, drafts, qprob, ua, uf,
+                                 max_top_k=0, apply_top_p=False)
+
+    t, same = _graph_time(verify)
+    nbytes = 2 * 4 * rows * vocab + 4 * n * k * vocab + 4 * n * (2 * k + 1) + 8 * n * (k + 1) + 8 * rows
+    return t, same, nbytes
+
+
+def _kv_bytes_distinct(tables, lengths, req_of_row, kv_heads, head_dim, elt, bs):
+    """Each needed KV byte once per (request, block table): the longest row reading it."""
+    longest = {}
+    for r in range(tables.shape[0]):
+        key = (int(req_of_row[r]), tuple(tables[r, :4].tolist()))
+        longest[key] = max(longest.get(key, 0), int(lengths[r]))
+    toks = sum(longest.values())
+    return toks * 2 * kv_heads * head_dim * elt + sum(-(-x // bs) for x in longest.values()) * 4
+
+
+def config4_step(pkg, dev):
+    """55 q / kv heads, head_dim 96, 32 LAST_EXITED planes with exit
+    depth U{8..32}, batch 16, ctx 2048, verify window 5 (packed form), acceptance at V = 65536."""
+    g = torch.Generator().manual_seed(4)
+    gd = torch.Generator(device=dev).manual_seed(4)
+    n, w, planes, bs, h, d, ctx_len, vocab = 16, 5, 32, 16, 55, 96, 2048, 65536
+    per = ctx_len // bs
+    pool = n * planes * per
+    k = torch.randn(pool, bs, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(pool, bs, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    tables = torch.randperm(pool, generator=g).int().view(n, planes, per)
+    exit_depth = torch.randint(8, 33, (n,), generator=g)
+    seq_tables = tables[torch.arange(n), exit_depth - 1].to(dev)
+    lengths = torch.full((n,), ctx_len, dtype=torch.int32, device=dev)
+    q = torch.randn(n * w, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    cu = torch.arange(0, n * w + 1, w, dtype=torch.int32, device=dev)
+    kern = pkg.MI355XPagedAttention()
+    t_attn, same_attn = _graph_time(lambda: kern.prefill(q, k, v, seq_tables, lengths, cu, w))
+    a_bytes = n * ctx_len * 2 * h * d * 2 + 2 * n * w * h * d * 2 + n * per * 4
+    del k, v
+    t_acc, same_acc, c_bytes = _accept_part(pkg, dev, gd, n, w, vocab)
+    return _secondary("config4: 55/55 heads, D=96, bf16, 32 LAST_EXITED planes (exit depth U{8..32}), "
+                      "batch 16, ctx 2048, packed q_len=5; verify_accept V=65536, T=1, no truncation",
+                      n * w, t_attn, a_bytes, t_acc, c_bytes, same_attn and same_acc)
+
+
+def config5_step(pkg, dev):
+    """fp8-e4m3 KV with per-tensor fp32 scales, batch 256, ctx
+    U[16384, 32768], q_len 5 with window row j at plane (d0 + j) mod 4 (per-row form, one
+    table and length per row), 16 q / 8 kv heads, D = 128; acceptance at V = 65536."""
+    g = torch.Generator().manual_seed(5)
+    gd = torch.Generator(device=dev).manual_seed(5)
+    n, w, planes, bs, hq, hkv, d, vocab = 256, 5, 4, 16, 16, 8, 128, 65536
+    max_len = 32768 + w
+    per = -(-max_len // bs)
+    pool = n * planes * per
+    kc = _fp8_pool((pool, bs, hkv, d), dev, gd)
+    vc = _fp8_pool((pool, bs, hkv, d), dev, gd)
+    tables = torch.randperm(pool, generator=g).int().view(n, planes, per)
+    start = torch.randint(16384 - w, 32768 - w + 1, (n,), generator=g)
+    d0 = torch.randint(0, planes, (n,), generator=g)
+    j = torch.arange(w)
+    plane = (d0.view(n, 1) + j.view(1, w)) % planes
+    row_tables = tables[torch.arange(n).view(n, 1), plane].reshape(n * w, per)
+    row_len = (start.view(n, 1) + j.view(1, w) + 1).reshape(-1).int()
+    req = torch.arange(n).repeat_interleave(w)
+    q = torch.randn(n * w, hq, d, generator=gd, device=dev, dtype=torch.bfloat16)
+    sk = torch.tensor(0.03, device=dev)
+    sv = torch.tensor(0.05, device=dev)
+    rt, rl = row_tables.to(dev), row_len.to(dev)
+    kern = pkg.MI355XPagedAttention()
+    t_attn, same_attn = _graph_time(lambda: kern(q, kc, vc, rt, rl, sk, sv), reps=2, per_graph=4)
+    a_bytes = _kv_bytes_distinct(row_tables, row_len, req, hkv, d, 1, bs) + 2 * n * w * hq * d * 2
+    row_bytes = int(row_len.sum()) * 2 * hkv * d
+    del kc, vc
+    t_acc, same_acc, c_bytes = _accept_part(pkg, dev, gd, n, w, vocab)
+    out = _secondary("config5: fp8-e4m3 KV, per-tensor scales, batch 256, ctx U[16384,32768], 16/8 heads, "
+                     "D=128, window row j at plane (d0+j) mod 4 (per-row form); verify_accept V=65536, "
+                     "T=1, no truncation", n * w, t_attn, a_bytes, t_acc, c_bytes, same_attn and same_acc)
+    out["attention_row_bytes_GBps"] = round(row_bytes / t_attn / 1e9, 1)
+    return out
+
+
+def _secondary(workload, tokens, t_attn, a_bytes, t_acc, c_bytes, replay_equal):
+    return {"workload": workload,
+            "verified_tokens_per_s": round(tokens / (t_attn + t_acc), 1),
+            "attention_us": round(t_attn * 1e6, 1), "attention_algorithmic_bytes": a_bytes,
+            "attention_GBps": round(a_bytes / t_attn / 1e9, 1),
+            "attention_frac": round(a_bytes / t_attn / 1e9 / PEAK_HBM_GBS, 4),
+            "verify_accept_us": round(t_acc * 1e6, 1), "verify_accept_algorithmic_bytes": c_bytes,
+            "verify_accept_GBps": round(c_bytes / t_acc / 1e9, 1),
+            "graph_replays_equal_eager": replay_equal}
+
+
 def cpu_baseline(w, repeats=1):
     """The torch-CPU oracle (restatement of the reference Torch path) on this host."""
     from oracle import attention as oatt
@@ -215,6 +376,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-config2", action="store_true",
                     help="skip the secondary config-2 decode attention measurement")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the config-4 and config-5 attention + verify_accept measurements")
     ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "verify", "copy"),
                     help="replay only this part K times and exit (for counter collection); "
                          "'copy' copies a 1 GiB buffer K times (counter calibration)")
@@ -424,6 +587,11 @@ def main():
     if not args.no_config2:
         del g_kv, g_attn, g_probs, g_acc, g_step, g_ver
         result["config2_decode_attention"] = config2_decode(pkg, dev)
+    if not args.no_secondary:
+        result["config4_verify"] = config4_step(pkg, dev)
+        torch.cuda.empty_cache()
+        result["config5_verify"] = config5_step(pkg, dev)
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
