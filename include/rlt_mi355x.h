@@ -68,6 +68,36 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
                         void* out, int64_t out_row_stride, int64_t out_head_stride,
                         void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * rlt_paged_attention with explicit per-row key counts for the packed form:
+ * query i of sequence s sees keys < row_lengths[cu_seqlens_q[s] + i] (int32
+ * [num_q_rows]; with window > 0, the last `window` of them) instead of the causal
+ * window's context_lengths[s] - q_len(s) + i + 1.  Rows of one sequence must be
+ * ordered by nondecreasing length (not checked on the device: another order gives
+ * wrong but in-bounds results).  It lets rows that read one block table share each
+ * KV byte although their positions are not consecutive: the pipelined verify of
+ * vllm_rlt/worker/async_speculative.py:449-470, where window row j reads loop-depth
+ * plane (d0 + j) mod planes and rows d0 and d0 + planes fall on the same plane.  The
+ * reference runs such rows through the per-row call (kernels/paged_attention.py:13-47,
+ * one gathered table per row); every row here equals that per-row result bit for bit.
+ * Never takes the long-prompt prefill tiling.  row_lengths == NULL is
+ * rlt_paged_attention; row_lengths without cu_seqlens_q is RLT_ERR_ARGUMENT.
+ */
+int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                             const void* key_cache, const void* value_cache, int64_t k_block_stride,
+                             int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                             int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                             const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                             const int32_t* context_lengths, const int32_t* row_lengths,
+                             const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                             int32_t num_q_rows, const float* key_scale, const float* value_scale,
+                             int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
+                             int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
+                             int32_t window, void* out, int64_t out_row_stride,
+                             int64_t out_head_stride, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
 /* 1 when (q dtype, kv dtype, head_dim) runs on the MFMA kernel, else 0 (vector kernel). */
 int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim);
 

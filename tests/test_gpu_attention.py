@@ -381,3 +381,90 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
         v_seq = v[pages_s].reshape(-1, hkv, d)[:n]
         want = _dense_packed(q[cu[s]:cu[s + 1]], k_seq, v_seq, c, n, window)
         torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
+
+
+# ------------------------------------------ packed rows with explicit row lengths
+
+def _group_rows_by_plane(n, w, planes, d0, row_len):
+    """Pipelined verify rows: row j of request i reads plane (d0[i] + j) % planes.  One
+    packed sequence per (request, plane), its rows by nondecreasing length."""
+    perm, cu, seq_req, seq_plane = [], [0], [], []
+    for i in range(n):
+        for pl in range(planes):
+            rows = [i * w + j for j in range(w) if (int(d0[i]) + j) % planes == pl]
+            if not rows:
+                continue
+            rows.sort(key=lambda r: int(row_len[r]))
+            perm += rows
+            cu.append(len(perm))
+            seq_req.append(i)
+            seq_plane.append(pl)
+    return (torch.tensor(perm), torch.tensor(cu, dtype=torch.int32), torch.tensor(seq_req),
+            torch.tensor(seq_plane))
+
+
+@pytest.mark.parametrize("q_dtype,kv,planes,hq,hkv,d,window", [
+    (torch.bfloat16, "fp8", 4, 16, 8, 128, 0),     # config 5 shape: rows 0 and 4 share d0
+    (torch.bfloat16, "bf16", 2, 16, 2, 128, 0),    # 3 rows x GQA 8 = 24 rows: two row tiles
+    (torch.float16, "fp16", 4, 8, 8, 64, 300),     # windowed
+    (torch.float32, "fp32", 3, 4, 2, 32, 0),       # vector path
+])
+def test_packed_rows_with_row_lengths_equal_per_row_bitwise(kernel, dev, q_dtype, kv, planes, hq,
+                                                            hkv, d, window):
+    _say("row_lengths", q_dtype, kv, planes, hq, hkv, d, window)
+    g = torch.Generator().manual_seed(11)
+    n, w, bs = 5, 5, 16
+    max_len = 3000 + w
+    per = -(-max_len // bs)
+    pool = n * planes * per
+    if kv == "fp8":
+        kc = (torch.randn(pool, bs, hkv, d, generator=g) * 8).to(torch.float8_e4m3fn)
+        vc = (torch.randn(pool, bs, hkv, d, generator=g) * 8).to(torch.float8_e4m3fn)
+        sk, sv = torch.tensor(0.03), torch.tensor(0.05)
+    else:
+        kv_dtype = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[kv]
+        kc = torch.randn(pool, bs, hkv, d, generator=g).to(kv_dtype)
+        vc = torch.randn(pool, bs, hkv, d, generator=g).to(kv_dtype)
+        sk = sv = None
+    tables = torch.randperm(pool, generator=g)[: n * planes * per].view(n, planes, per).int()
+    start = torch.randint(1, 3000, (n,), generator=g)
+    start[0] = 507  # the window straddles a 512-position chunk boundary
+    d0 = torch.randint(0, planes, (n,), generator=g)
+    j = torch.arange(w)
+    plane = (d0.view(n, 1) + j.view(1, w)) % planes
+    row_tables = tables[torch.arange(n).view(n, 1), plane].reshape(n * w, per)
+    row_len = (start.view(n, 1) + j.view(1, w) + 1).reshape(-1).int()
+    q = torch.randn(n * w, hq, d, generator=g).to(q_dtype)
+    perm, cu, seq_req, seq_plane = _group_rows_by_plane(n, w, planes, d0, row_len)
+    seq_tables = tables[seq_req, seq_plane]
+    seq_len = torch.stack([row_len[perm[cu[s]:cu[s + 1]]].max() for s in range(len(cu) - 1)])
+    max_q = int((cu[1:] - cu[:-1]).max())
+    kd, vd = kc.to(dev), vc.to(dev)
+    skd = sk.to(dev) if sk is not None else None
+    svd = sv.to(dev) if sv is not None else None
+    if window:
+        per_row = kernel.windowed(q.to(dev), kd, vd, row_tables.to(dev), row_len.to(dev), window,
+                                  skd, svd)
+    else:
+        per_row = kernel(q.to(dev), kd, vd, row_tables.to(dev), row_len.to(dev), skd, svd)
+    packed = kernel.prefill(q[perm].contiguous().to(dev), kd, vd, seq_tables.to(dev),
+                            seq_len.int().to(dev), cu.to(dev), max_q, skd, svd, window=window,
+                            row_lengths=row_len[perm].to(dev))
+    assert torch.equal(packed.cpu(), per_row.cpu()[perm])
+    if window:
+        want = oatt.paged_attention(q, kc, vc, row_tables, row_len, sk, sv, window)
+    else:
+        want = oatt.paged_attention(q, kc, vc, row_tables, row_len, sk, sv)
+    _close(packed.cpu(), want[perm], q_dtype)
+
+
+def test_row_lengths_need_the_packed_form(kernel, dev):
+    q = torch.zeros(2, 4, 64, device=dev, dtype=torch.bfloat16)
+    k = torch.zeros(4, 16, 4, 64, device=dev, dtype=torch.bfloat16)
+    t = torch.zeros(2, 2, device=dev, dtype=torch.int32)
+    ln = torch.full((2,), 8, device=dev, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        kernel._run(q, k, k, t, ln, None, 1, None, None, 0, ln)
+    cu = torch.tensor([0, 2], device=dev, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        kernel.prefill(q, k, k, t[:1], ln[:1], cu, 2, row_lengths=ln[:1])

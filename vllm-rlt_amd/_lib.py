@@ -45,6 +45,19 @@ _SIGNATURES = {
         _p, _i64, _i64,                 # out
         _p, _sz, _p,                    # workspace, bytes, stream
     ]),
+    "rlt_paged_attention_rows": (ctypes.c_int, [
+        _p, _i64, _i64,                 # q
+        _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,  # k, v, strides
+        _i32,                           # num_blocks
+        _p, _i64, _i32,                 # tables
+        _p, _p,                         # lengths, row lengths
+        _p, _i32, _i32, _i32,           # cu, num_seqs, max_q_len, num_q_rows
+        _p, _p, _i32, _i64, _i64, _i64,  # scales
+        _i32, _i32, _i32, _i32,         # hq, hkv, head_dim, block_size
+        _i32, _i32, _i32,               # q dtype, kv dtype, window
+        _p, _i64, _i64,                 # out
+        _p, _sz, _p,                    # workspace, bytes, stream
+    ]),
     "rlt_speculative_accept_workspace_size": (_sz, [_i64, _i32, _i64]),
     "rlt_speculative_accept": (ctypes.c_int, [
         _p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _p, _p, _p, _p, _p, _sz, _p]),

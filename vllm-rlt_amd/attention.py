@@ -107,11 +107,11 @@ class MI355XPagedAttention:
     generation = None
 
     def _run(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-             max_seqlen_q, key_scale, value_scale, window):
+             max_seqlen_q, key_scale, value_scale, window, row_lengths=None):
         if type(window) is not int or window < 0:
             raise ValueError("window must be a nonnegative integer")
         _lib.require_gpu(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-                         key_scale, value_scale)
+                         key_scale, value_scale, row_lengths)
         if q.ndim != 3 or key_cache.ndim != 4 or value_cache.ndim != 4:
             raise ValueError("q must be [rows, heads, dim] and caches [block, token, kv_head, dim]")
         head_dim = q.shape[-1]
@@ -150,19 +150,26 @@ class MI355XPagedAttention:
             if cu.shape[0] != num_seqs + 1 or lengths.shape[0] != num_seqs:
                 raise ValueError("cu_seqlens_q must be [sequences + 1] and lengths [sequences]")
             max_q = int(max_seqlen_q)
+        if row_lengths is not None:
+            if cu_seqlens_q is None:
+                raise ValueError("row_lengths needs the packed form (cu_seqlens_q)")
+            if row_lengths.dim() != 1 or row_lengths.shape[0] != rows:
+                raise ValueError("row_lengths must be [q rows]")
+            row_lengths = (row_lengths if row_lengths.dtype == torch.int32
+                           else row_lengths.int()).contiguous()
         lib = _lib.library()
         heads = q.shape[1]
         width = tables.shape[1]
         nbytes = lib.rlt_paged_attention_workspace_size(rows, heads, head_dim, width, block_size)
         ws = _lib.workspace(nbytes, q.device)
-        status = lib.rlt_paged_attention(
+        status = lib.rlt_paged_attention_rows(
             _lib.ptr(q), q.stride(0), q.stride(1),
             _lib.ptr(key_cache), _lib.ptr(value_cache),
             key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
             value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
             num_blocks,
             _lib.ptr(tables), tables.stride(0), width,
-            _lib.ptr(lengths), _lib.ptr(cu), num_seqs, max_q, rows,
+            _lib.ptr(lengths), _lib.ptr(row_lengths), _lib.ptr(cu), num_seqs, max_q, rows,
             _lib.ptr(ks), _lib.ptr(vs), mode, *s_strides,
             heads, kv_heads, head_dim, block_size,
             _lib.dtype_code(q.dtype), _lib.dtype_code(key_cache.dtype), window,
@@ -186,10 +193,18 @@ class MI355XPagedAttention:
                          key_scale, value_scale, window)
 
     def prefill(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-                max_seqlen_q, key_scale=None, value_scale=None, *, window=0):
-        """Packed causal window, bottom-right aligned; reference: triton_attention.py:386-404."""
+                max_seqlen_q, key_scale=None, value_scale=None, *, window=0, row_lengths=None):
+        """Packed causal window, bottom-right aligned; reference: triton_attention.py:386-404.
+
+        ``row_lengths`` (int32 ``[q rows]``, optional, not in the reference signature): row i
+        of a sequence sees ``row_lengths[cu_seqlens_q[s] + i]`` keys instead of the causal
+        window's ``context_lengths[s] - q_len + i + 1``; a sequence's rows must be ordered by
+        nondecreasing length.  Rows that read one block table at non-consecutive positions
+        (pipelined verify rows at the same loop-depth plane) then share each KV byte, and
+        every row equals the per-row ``__call__`` bit for bit.
+        """
         return self._run(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-                         max_seqlen_q, key_scale, value_scale, window)
+                         max_seqlen_q, key_scale, value_scale, window, row_lengths)
 
     def uses_mfma(self, q_dtype, kv_dtype, head_dim):
         lib = _lib.library()

@@ -69,6 +69,7 @@ struct AttnParams {
   int32_t num_blocks;  // physical blocks in the pool: out-of-range table entries read block 0
   const int32_t* lengths;
   const int32_t* cu_q;  // nullptr: per-row form
+  const int32_t* row_len;  // packed form: explicit key count of each q row (nullptr: causal window)
   const float* k_scale;
   const float* v_scale;
   int64_t s_block_stride, s_token_stride, s_head_stride;
@@ -130,7 +131,7 @@ __device__ __forceinline__ SeqView seq_view(const AttnParams& P, int seq) {
 // Row (window index qi) of a sequence: visible key range [lo, hi).
 __device__ __forceinline__ void row_range(const AttnParams& P, const SeqView& s, int qi, int& lo,
                                           int& hi) {
-  hi = s.kv_len - s.q_len + 1 + qi;
+  hi = P.row_len ? P.row_len[s.q_begin + qi] : s.kv_len - s.q_len + 1 + qi;
   if (hi < 0) hi = 0;
   // Never read past the row's block table (a length beyond it is a caller error).
   const int cap = P.table_width * P.block_size;
@@ -1591,19 +1592,20 @@ size_t rlt_paged_attention_workspace_size(int32_t num_q_rows, int32_t num_q_head
   return rlt_align_up(sizeof(float) * slots * 2, 256) + rlt_align_up(sizeof(float) * slots * head_dim, 256);
 }
 
-int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
-                        const void* key_cache, const void* value_cache, int64_t k_block_stride,
-                        int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
-                        int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
-                        const int32_t* block_tables, int64_t table_stride, int32_t table_width,
-                        const int32_t* context_lengths,
-                        const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
-                        int32_t num_q_rows, const float* key_scale, const float* value_scale,
-                        int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
-                        int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
-                        int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
-                        int32_t window, void* out, int64_t out_row_stride, int64_t out_head_stride,
-                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                             const void* key_cache, const void* value_cache, int64_t k_block_stride,
+                             int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                             int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                             const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                             const int32_t* context_lengths, const int32_t* row_lengths,
+                             const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                             int32_t num_q_rows, const float* key_scale, const float* value_scale,
+                             int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
+                             int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
+                             int32_t window, void* out, int64_t out_row_stride,
+                             int64_t out_head_stride, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return RLT_ERR_ARGUMENT;
   if (head_dim <= 0 || head_dim > 256 || block_size <= 0 || window < 0) return RLT_ERR_ARGUMENT;
   if (num_seqs < 0 || num_q_rows < 0 || max_q_len < 0 || table_width < 0) return RLT_ERR_ARGUMENT;
@@ -1615,6 +1617,7 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
   if (num_q_rows == 0 || num_seqs == 0) return RLT_OK;
   if (!cu_seqlens_q && num_seqs != num_q_rows) return RLT_ERR_ARGUMENT;
   if (cu_seqlens_q && max_q_len <= 0) return RLT_ERR_ARGUMENT;
+  if (row_lengths && !cu_seqlens_q) return RLT_ERR_ARGUMENT;
   const size_t need = rlt_paged_attention_workspace_size(num_q_rows, num_q_heads, head_dim,
                                                          table_width, block_size);
   if (!workspace || workspace_bytes < need) return RLT_ERR_WORKSPACE;
@@ -1637,6 +1640,7 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
   P.num_blocks = num_blocks;
   P.lengths = context_lengths;
   P.cu_q = cu_seqlens_q;
+  P.row_len = row_lengths;
   P.k_scale = key_scale;
   P.v_scale = value_scale;
   P.s_block_stride = s_block_stride;
@@ -1675,7 +1679,7 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
         (k_head_stride * kv_elt) % kv_align == 0 && (v_block_stride * kv_elt) % kv_align == 0 &&
         (v_token_stride * kv_elt) % kv_align == 0 && (v_head_stride * kv_elt) % kv_align == 0;
     if (!aligned) return RLT_ERR_ARGUMENT;
-    if (cu_seqlens_q && rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len)) {
+    if (cu_seqlens_q && !row_lengths && rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len)) {
       // long q windows: the prefill tiling, normalized in one launch
       P.rows_per_rg = kPfRows;
       P.rowgroups = (rows_per_seq + kPfRows - 1) / kPfRows;
@@ -1736,6 +1740,28 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
     case RLT_BF16: launch_merge<RLT_BF16>(P, mgrid, stream); break;
   }
   return rlt_launch_status();
+}
+
+int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                        const void* key_cache, const void* value_cache, int64_t k_block_stride,
+                        int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                        int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                        const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                        const int32_t* context_lengths,
+                        const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                        int32_t num_q_rows, const float* key_scale, const float* value_scale,
+                        int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
+                        int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
+                        int32_t window, void* out, int64_t out_row_stride, int64_t out_head_stride,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return rlt_paged_attention_rows(
+      q, q_row_stride, q_head_stride, key_cache, value_cache, k_block_stride, k_token_stride,
+      k_head_stride, v_block_stride, v_token_stride, v_head_stride, num_blocks, block_tables,
+      table_stride, table_width, context_lengths, nullptr, cu_seqlens_q, num_seqs, max_q_len,
+      num_q_rows, key_scale, value_scale, scale_mode, s_block_stride, s_token_stride,
+      s_head_stride, num_q_heads, num_kv_heads, head_dim, block_size, q_dtype, kv_dtype, window,
+      out, out_row_stride, out_head_stride, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"
