@@ -27,16 +27,18 @@ def paged_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch
                     block_tables: torch.Tensor, context_lengths: torch.Tensor,
                     key_scale: Optional[torch.Tensor], value_scale: Optional[torch.Tensor],
                     cu_seqlens_q: Optional[torch.Tensor], max_seqlen_q: int,
-                    window: int) -> torch.Tensor:
+                    window: int, row_lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Per-row (cu_seqlens_q None) or packed causal-window paged attention;
-    reference: vllm_rlt/kernels/paged_attention.py:13-90, triton_attention.py:386-404."""
+    reference: vllm_rlt/kernels/paged_attention.py:13-90, triton_attention.py:386-404.
+    ``row_lengths`` (packed form only): each row's key count, rows of a sequence by
+    nondecreasing length."""
     return _ATTN._run(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-                      max_seqlen_q, key_scale, value_scale, window)
+                      max_seqlen_q, key_scale, value_scale, window, row_lengths)
 
 
 @paged_attention.register_fake
 def _(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value_scale,
-      cu_seqlens_q, max_seqlen_q, window):
+      cu_seqlens_q, max_seqlen_q, window, row_lengths=None):
     return torch.empty_like(q)
 
 
