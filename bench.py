@@ -284,7 +284,7 @@ def config4_step(pkg, dev):
                       n * w, t_attn, a_bytes, t_acc, c_bytes, same_attn and same_acc)
 
 
-def config5_step(pkg, dev):
+def config5_step(pkg, dev, attention_only=False):
     """fp8-e4m3 KV with per-tensor fp32 scales, batch 256, ctx
     U[16384, 32768], q_len 5 with window row j at plane (d0 + j) mod 4, 16 q / 8 kv heads,
     D = 128; acceptance at V = 65536.  Attention is timed twice: the reference's per-row form
@@ -311,7 +311,6 @@ def config5_step(pkg, dev):
     sv = torch.tensor(0.05, device=dev)
     rt, rl = row_tables.to(dev), row_len.to(dev)
     kern = pkg.MI355XPagedAttention()
-    t_row, same_row = _graph_time(lambda: kern(q, kc, vc, rt, rl, sk, sv), reps=2, per_graph=4)
     # the same rows as one packed sequence per (request, plane) with explicit row lengths:
     # rows j = 0 and j = 4 read plane d0 once between them
     perm, cu = [], [0]
@@ -329,6 +328,14 @@ def config5_step(pkg, dev):
     cu_d = torch.tensor(cu, dtype=torch.int32, device=dev)
     max_q = max(cu[s + 1] - cu[s] for s in range(len(cu) - 1))
     qp, rlp = q[perm_d].contiguous(), row_len.to(dev)[perm_d].contiguous()
+    if attention_only:  # counter collection: two per-row launches, then two packed launches
+        for _ in range(2):
+            kern(q, kc, vc, rt, rl, sk, sv)
+        for _ in range(2):
+            kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sv, row_lengths=rlp)
+        torch.cuda.synchronize()
+        return {"only": "config5_attention", "launches": 4}
+    t_row, same_row = _graph_time(lambda: kern(q, kc, vc, rt, rl, sk, sv), reps=2, per_graph=4)
     t_attn, same_attn = _graph_time(
         lambda: kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sv, row_lengths=rlp),
         reps=2, per_graph=4)
@@ -406,9 +413,12 @@ def main():
                     help="skip the secondary config-2 decode attention measurement")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the config-4 and config-5 attention + verify_accept measurements")
-    ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "verify", "copy"),
+    ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "verify", "copy",
+                                       "config5_attention"),
                     help="replay only this part K times and exit (for counter collection); "
-                         "'copy' copies a 1 GiB buffer K times (counter calibration)")
+                         "'copy' copies a 1 GiB buffer K times (counter calibration); "
+                         "'config5_attention' runs the config-5 attention twice per-row, then "
+                         "twice packed with row lengths")
     ap.add_argument("--steps-per-graph", type=int, default=10,
                     help="verify steps captured back to back in one HIP graph")
     args = ap.parse_args()
@@ -426,6 +436,9 @@ def main():
             dst_buf.copy_(src_buf)
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_launch": 1 << 30, "steps": args.steps}), flush=True)
+        return
+    if args.only == "config5_attention":
+        print(json.dumps(config5_step(pkg, dev, attention_only=True)), flush=True)
         return
     w = build_workload(dev)
     backend = pkg.create_backend("auto", dev, torch.bfloat16, w["d"], w["bs"])
