@@ -57,11 +57,14 @@ def probabilities(logits, temperature, top_p):
     return x.softmax(-1)
 
 
-def build_workload(dev, seed=0):
-    n, window, hq, hkv, d, bs, layers, vocab = 32, 5, 16, 4, 128, 16, 2, 49152
+def build_workload(dev, seed=0, n=32, ctx=None):
+    """Config 3 (n = 32, ctx U[1024, 8192]); ``ctx`` fixes every context length instead."""
+    window, hq, hkv, d, bs, layers, vocab = 5, 16, 4, 128, 16, 2, 49152
     k_drafts = window - 1
     g = torch.Generator().manual_seed(seed)
     lengths = torch.randint(1024, 8193, (n,), generator=g, dtype=torch.int64)
+    if ctx is not None:
+        lengths = torch.full((n,), ctx, dtype=torch.int64)
     width = 8192 // bs
     pool = n * width
     tables = torch.randperm(pool, generator=g)[: n * width].view(n, width).int()
@@ -356,6 +359,45 @@ def config5_step(pkg, dev, attention_only=False):
     return out
 
 
+
+def target_step(pkg, dev):
+    """The shape the north-star target names: the verify step at batch 64, ctx 4096 (config 3's
+    heads, window and sampling otherwise).  Reports attention + speculative_accept (the
+    acceptance from p and q, the bit-exact contract) and attention + verify_accept (the
+    distributions from logits too), each as algorithmic bytes over summed launch times."""
+    w = build_workload(dev, seed=7, n=64, ctx=4096)
+    k = w["k"]
+    kc, vc = w["key_pool"][:, w["layer"]], w["value_pool"][:, w["layer"]]
+    tables, lengths, cu = w["tables"].to(dev), w["lengths"].int().to(dev), w["cu"].to(dev)
+    u = w["u"].to(dev)
+    ua, uf = u[:, k:2 * k].contiguous(), u[:, 2 * k].contiguous()
+    drafts = torch.full((w["n"],), k, dtype=torch.int64, device=dev)
+    dt_tok = torch.stack([pkg.categorical(w["qprob"][:, j].contiguous(), u[:, j].contiguous())[0]
+                          for j in range(k)], 1)
+    rows = w["n"] * w["window"]
+    temp = torch.full((rows,), w["temperature"], device=dev)
+    top_k = torch.full((rows,), -1, dtype=torch.int64, device=dev)
+    top_p = torch.full((rows,), w["top_p"], device=dev)
+    kern = pkg.MI355XPagedAttention()
+    logits3 = w["target_logits"].view(w["n"], w["window"], -1)
+    t_attn, s1 = _graph_time(lambda: kern.prefill(w["q"], kc, vc, tables, lengths, cu, w["window"]))
+    t_acc, s2 = _graph_time(lambda: pkg.speculative_accept(dt_tok, drafts, w["qprob"], w["pprob"], ua, uf))
+    t_ver, s3 = _graph_time(lambda: pkg.verify_accept(logits3, temp, top_k, top_p, dt_tok, drafts,
+                                                      w["qprob"], ua, uf, max_top_k=0,
+                                                      apply_top_p=True))
+    a, c, pb = attention_bytes(w), accept_bytes(w), probs_bytes(w)
+    frac = lambda b, t: round(b / t / 1e9 / PEAK_HBM_GBS, 4)
+    return {"workload": "verify step at batch 64, ctx 4096: packed q_len=5, 16q/4kv heads, D=128, bf16 "
+                        "SHARED KV; acceptance V=49152, T=0.7, top-p 0.9",
+            "attention_us": round(t_attn * 1e6, 1), "attention_algorithmic_bytes": a,
+            "attention_frac": frac(a, t_attn),
+            "accept_us": round(t_acc * 1e6, 1), "accept_algorithmic_bytes": c,
+            "attention_plus_accept_frac": frac(a + c, t_attn + t_acc),
+            "verify_accept_us": round(t_ver * 1e6, 1),
+            "attention_plus_verify_accept_frac": frac(a + c + pb, t_attn + t_ver),
+            "verified_tokens_per_s": round(rows / (t_attn + t_ver), 1),
+            "graph_replays_equal_eager": s1 and s2 and s3}
+
 def _secondary(workload, tokens, t_attn, a_bytes, t_acc, c_bytes, replay_equal):
     return {"workload": workload,
             "verified_tokens_per_s": round(tokens / (t_attn + t_acc), 1),
@@ -629,6 +671,8 @@ def main():
         del g_kv, g_attn, g_probs, g_acc, g_step, g_ver
         result["config2_decode_attention"] = config2_decode(pkg, dev)
     if not args.no_secondary:
+        result["batch64_ctx4096_verify"] = target_step(pkg, dev)
+        torch.cuda.empty_cache()
         result["config4_verify"] = config4_step(pkg, dev)
         torch.cuda.empty_cache()
         result["config5_verify"] = config5_step(pkg, dev)

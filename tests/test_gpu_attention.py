@@ -468,3 +468,31 @@ def test_row_lengths_need_the_packed_form(kernel, dev):
     cu = torch.tensor([0, 2], device=dev, dtype=torch.int32)
     with pytest.raises(ValueError):
         kernel.prefill(q, k, k, t[:1], ln[:1], cu, 2, row_lengths=ln[:1])
+
+
+def test_row_lengths_on_the_grid_kernel(kernel, dev):
+    # 8200 packed sequences of two rows (more than 8192 pairs: the grid kernel); row 0
+    # of each sequence sees a key count a few positions below row 1's, as pipelined
+    # rows on one plane do.  Every row equals its per-row launch bit for bit.
+    _say("row_lengths grid kernel")
+    g = torch.Generator().manual_seed(13)
+    bs, hq, hkv, d, dtype = 16, 2, 1, 64, torch.bfloat16
+    n = 8200
+    hi = torch.randint(5, 41, (n,), generator=g)
+    lo = hi - torch.randint(0, 5, (n,), generator=g)
+    lengths = hi.tolist()
+    pages = sum(-(-x // bs) for x in lengths)
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables(lengths, bs, pages, g)
+    q = torch.randn(2 * n, hq, d, generator=g).to(dtype)
+    row_len = torch.stack([lo, hi], 1).reshape(-1).int()
+    row_tables = tables.repeat_interleave(2, 0)
+    cu = torch.arange(0, 2 * n + 1, 2, dtype=torch.int32)
+    kd, vd, qd = k.to(dev), v.to(dev), q.to(dev)
+    got = kernel.prefill(qd, kd, vd, tables.to(dev), hi.int().to(dev), cu.to(dev), 2,
+                         row_lengths=row_len.to(dev))
+    per_row = kernel(qd, kd, vd, row_tables.to(dev), row_len.to(dev))
+    assert torch.equal(got, per_row)
+    sel = [0, 1, 8198, 16399]
+    want = oatt.paged_attention(q[sel], k, v, row_tables[sel], row_len[sel])
+    _close(got[sel].cpu(), want, dtype)
