@@ -384,6 +384,29 @@ int rlt_depth_tables(const int32_t* tables, int64_t row_stride, int64_t plane_st
                      int32_t* out_table, int64_t out_stride, int64_t* blocks, int64_t* offsets,
                      int32_t* lengths, int64_t n, hipStream_t stream);
 
+/* Random-round merge: overlay the random requests' speculative_accept outcome on
+ * the greedy round, in one launch with no host reads.  Replaces
+ * vllm_rlt/worker/async_speculative.py:162-198 merge_random_round (RandomRoundMerge
+ * :152-159).  target int64 [num_rows] (argmax per request-major verify row),
+ * accepted / next_tokens / starts / input_tokens int64 [n]; the outcome of the r random
+ * requests: tokens int64 [r, width], r_accepted / r_final int64 [r], r_error bool [r];
+ * random_requests int64 [r]; verify_rows / verify_ranks / verify_offsets int64
+ * [num_verify].  Outputs: rows_out [num_rows], accepted_out / next_tokens_out /
+ * next_positions_out / error_out [n] (error as 0 / 1), next_values_out [n, 2]
+ * (token, position): a failed request keeps (input_token, start).  Index tensors must
+ * not repeat an index (the reference's scatters leave the winner unspecified then);
+ * indices outside their ranges are skipped (the reference raises a device assert). */
+int rlt_merge_random_round(const int64_t* target, int64_t num_rows, const int64_t* accepted,
+                           const int64_t* next_tokens, const int64_t* starts,
+                           const int64_t* input_tokens, int64_t n, const int64_t* tokens,
+                           int32_t width, const int64_t* r_accepted, const int64_t* r_final,
+                           const uint8_t* r_error, const int64_t* random_requests, int64_t r,
+                           const int64_t* verify_rows, const int64_t* verify_ranks,
+                           const int64_t* verify_offsets, int64_t num_verify, int64_t* rows_out,
+                           int64_t* accepted_out, int64_t* next_tokens_out,
+                           int64_t* next_positions_out, int64_t* next_values_out,
+                           int64_t* error_out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

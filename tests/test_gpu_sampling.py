@@ -162,3 +162,63 @@ def test_inputs_are_not_modified(pkg, dev):
     torch.cuda.synchronize()
     for a, b in zip(args, before):
         assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------ random-round merge
+
+def _merge_on_gpu(pkg, dev, args, res):
+    target, accepted, next_tokens, starts, inputs, req, vrow, vrank, voff = args
+    gres = pkg.AcceptResult(*(x.to(dev) for x in res))
+    out = pkg.merge_random_round(target.to(dev), accepted.to(dev), next_tokens.to(dev),
+                                 starts.to(dev), inputs.to(dev), gres, req.to(dev), vrow.to(dev),
+                                 vrank.to(dev), voff.to(dev))
+    return [x.cpu() for x in out]
+
+
+def test_merge_random_round_known_answer(pkg, dev):
+    # reference: tests/test_async_speculative_sampling_plan.py:127-161
+    _say("merge KAT")
+    res = osamp.AcceptResult(tokens=torch.tensor([[77, 66, 55], [9, 0, 0]]),
+                             accepted=torch.tensor([2, 0]), final=torch.tensor([55, 0]),
+                             error=torch.tensor([False, True]))
+    args = (torch.tensor([10, 11, 12, 20, 21, 30, 31]), torch.tensor([0, 1, 0]),
+            torch.tensor([10, 21, 30]), torch.tensor([5, 8, 12]), torch.tensor([1, 2, 3]),
+            torch.tensor([0, 2]), torch.tensor([0, 1, 2, 5, 6]), torch.tensor([0, 0, 0, 1, 1]),
+            torch.tensor([0, 1, 2, 0, 1]))
+    rows, acc, nxt, pos, values, err = _merge_on_gpu(pkg, dev, args, res)
+    assert rows.tolist() == [77, 66, 55, 20, 21, 9, 0]
+    assert acc.tolist() == [2, 1, 0] and nxt.tolist() == [55, 21, 0]
+    assert pos.tolist() == [8, 10, 13]
+    assert values.tolist() == [[55, 8], [21, 10], [3, 12]]
+    assert err.tolist() == [0, 0, 1] and err.dtype == torch.int64
+
+
+@pytest.mark.parametrize("n,seed", [(1, 0), (7, 1), (300, 2), (2500, 3)])
+def test_merge_random_round_matches_oracle(pkg, dev, n, seed):
+    _say("merge", n, seed)
+    g = torch.Generator().manual_seed(seed)
+    k = 4
+    temps = (torch.rand(n, generator=g) < 0.6).float() * 0.7
+    counts = torch.randint(1, k + 2, (n,), generator=g).tolist()
+    plan = osamp.plan_random_rows(temps.tolist(), counts, k)
+    total = sum(counts)
+    target = torch.randint(0, 50000, (total,), generator=g)
+    accepted = torch.randint(0, k + 1, (n,), generator=g)
+    next_tokens = torch.randint(0, 50000, (n,), generator=g)
+    starts = torch.randint(0, 10000, (n,), generator=g)
+    inputs = torch.randint(0, 50000, (n,), generator=g)
+    if plan is None:
+        req = vrow = vrank = voff = torch.zeros(0, dtype=torch.int64)
+    else:
+        req, vrow, vrank, voff = (torch.as_tensor(x, dtype=torch.int64) for x in plan)
+    r = req.shape[0]
+    res = osamp.AcceptResult(tokens=torch.randint(0, 50000, (r, k + 1), generator=g),
+                             accepted=torch.randint(0, k + 1, (r,), generator=g),
+                             final=torch.randint(0, 50000, (r,), generator=g),
+                             error=torch.rand(r, generator=g) < 0.2)
+    args = (target, accepted, next_tokens, starts, inputs, req, vrow, vrank, voff)
+    got = _merge_on_gpu(pkg, dev, args, res)
+    want = osamp.merge_random_round(target, accepted, next_tokens, starts, inputs, res, req, vrow,
+                                    vrank, voff)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b.reshape(a.shape).to(a.dtype))

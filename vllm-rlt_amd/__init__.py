@@ -37,7 +37,9 @@ from .sampling import (  # noqa: F401
     categorical,
     greedy_accept,
     greedy_accept_batched,
+    merge_random_round,
     propose_drafts,
+    RandomRoundMerge,
     speculative_accept,
     verify_accept,
     verify_distributions,

@@ -58,6 +58,12 @@ _SIGNATURES = {
         _p, _i64, _i64,                 # out
         _p, _sz, _p,                    # workspace, bytes, stream
     ]),
+    "rlt_merge_random_round": (ctypes.c_int, [
+        _p, _i64, _p, _p, _p, _p, _i64,  # target, rows, accepted, next, starts, inputs, n
+        _p, _i32, _p, _p, _p, _p, _i64,  # tokens, width, accepted, final, error, requests, r
+        _p, _p, _p, _i64,                # verify rows, ranks, offsets, count
+        _p, _p, _p, _p, _p, _p, _p,      # outputs, stream
+    ]),
     "rlt_speculative_accept_workspace_size": (_sz, [_i64, _i32, _i64]),
     "rlt_speculative_accept": (ctypes.c_int, [
         _p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _p, _p, _p, _p, _p, _sz, _p]),

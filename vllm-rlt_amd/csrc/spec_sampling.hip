@@ -992,3 +992,79 @@ int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u,
   return launch_categorical(weights, w_stride, u, m, vocab, out_index, nullptr, scatter, n_out,
                             workspace, workspace_bytes, stream);
 }
+
+// ============================================================ random-round merge
+
+namespace {
+
+constexpr int kMergeThreads = 1024;
+
+// One workgroup, three phases separated by workgroup barriers (global writes are
+// visible to the whole workgroup after __syncthreads): copy the greedy round's
+// values, overlay the random requests' outcomes, then form the slot values.
+// Indices outside their ranges are skipped.
+__global__ __launch_bounds__(kMergeThreads) void rlt_merge_random_round_kernel(
+    const int64_t* __restrict__ target, int64_t num_rows, const int64_t* __restrict__ accepted,
+    const int64_t* __restrict__ next_tokens, const int64_t* __restrict__ starts,
+    const int64_t* __restrict__ input_tokens, int64_t n, const int64_t* __restrict__ tokens,
+    int32_t width, const int64_t* __restrict__ r_accepted, const int64_t* __restrict__ r_final,
+    const uint8_t* __restrict__ r_error, const int64_t* __restrict__ random_requests, int64_t r,
+    const int64_t* __restrict__ verify_rows, const int64_t* __restrict__ verify_ranks,
+    const int64_t* __restrict__ verify_offsets, int64_t num_verify, int64_t* rows_out,
+    int64_t* accepted_out, int64_t* next_tokens_out, int64_t* next_positions_out,
+    int64_t* next_values_out, int64_t* error_out) {
+  const int t = threadIdx.x;
+  for (int64_t i = t; i < num_rows; i += kMergeThreads) rows_out[i] = target[i];
+  for (int64_t i = t; i < n; i += kMergeThreads) {
+    accepted_out[i] = accepted[i];
+    next_tokens_out[i] = next_tokens[i];
+    error_out[i] = 0;
+  }
+  __syncthreads();
+  for (int64_t k = t; k < num_verify; k += kMergeThreads) {
+    const int64_t row = verify_rows[k], rank = verify_ranks[k], off = verify_offsets[k];
+    if (row >= 0 && row < num_rows && rank >= 0 && rank < r && off >= 0 && off < width)
+      rows_out[row] = tokens[rank * width + off];
+  }
+  for (int64_t k = t; k < r; k += kMergeThreads) {
+    const int64_t req = random_requests[k];
+    if (req >= 0 && req < n) {
+      accepted_out[req] = r_accepted[k];
+      next_tokens_out[req] = r_final[k];
+      error_out[req] = r_error[k] ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  for (int64_t i = t; i < n; i += kMergeThreads) {
+    const int64_t pos = starts[i] + accepted_out[i] + 1;
+    next_positions_out[i] = pos;
+    const bool failed = error_out[i] != 0;
+    next_values_out[2 * i] = failed ? input_tokens[i] : next_tokens_out[i];
+    next_values_out[2 * i + 1] = failed ? starts[i] : pos;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int rlt_merge_random_round(const int64_t* target, int64_t num_rows, const int64_t* accepted,
+                           const int64_t* next_tokens, const int64_t* starts,
+                           const int64_t* input_tokens, int64_t n, const int64_t* tokens,
+                           int32_t width, const int64_t* r_accepted, const int64_t* r_final,
+                           const uint8_t* r_error, const int64_t* random_requests, int64_t r,
+                           const int64_t* verify_rows, const int64_t* verify_ranks,
+                           const int64_t* verify_offsets, int64_t num_verify, int64_t* rows_out,
+                           int64_t* accepted_out, int64_t* next_tokens_out,
+                           int64_t* next_positions_out, int64_t* next_values_out,
+                           int64_t* error_out, hipStream_t stream) {
+  if (num_rows < 0 || n < 0 || r < 0 || num_verify < 0 || width < 0) return RLT_ERR_ARGUMENT;
+  if (num_rows == 0 && n == 0) return RLT_OK;
+  rlt_merge_random_round_kernel<<<1, kMergeThreads, 0, stream>>>(
+      target, num_rows, accepted, next_tokens, starts, input_tokens, n, tokens, width, r_accepted,
+      r_final, r_error, random_requests, r, verify_rows, verify_ranks, verify_offsets, num_verify,
+      rows_out, accepted_out, next_tokens_out, next_positions_out, next_values_out, error_out);
+  return rlt_launch_status();
+}
+
+}  // extern "C"

@@ -351,3 +351,61 @@ def greedy_accept(candidates, targets):
             break
         accepted += 1
     return list(targets[: accepted + 1]), accepted
+
+
+class RandomRoundMerge(NamedTuple):
+    """reference: vllm_rlt/worker/async_speculative.py:152-159."""
+
+    rows: torch.Tensor  # [R] result rows (committed sequences for random requests)
+    accepted: torch.Tensor  # [n]
+    next_tokens: torch.Tensor  # [n]
+    next_positions: torch.Tensor  # [n] starts + accepted + 1
+    next_values: torch.Tensor  # [n, 2] (token, position) to scatter into the slot table
+    error: torch.Tensor  # [n] int64 0/1 flags
+
+
+def merge_random_round(target, accepted, next_tokens, starts, input_tokens, result,
+                       random_requests, verify_rows, verify_ranks, verify_offsets):
+    """Overlay the random requests' outcome on the greedy round in one launch, no host reads.
+
+    reference: vllm_rlt/worker/async_speculative.py:162-198.  ``random_requests`` and the
+    ``verify_*`` index arrays may be device tensors or host arrays (copied to the device);
+    an index must not repeat, and indices outside their ranges are skipped.
+    """
+    device = target.device
+    _lib.require_gpu(target, accepted, next_tokens, starts, input_tokens, *result)
+
+    def idx(x):
+        return _i64(torch.as_tensor(x, dtype=torch.int64, device=device))
+
+    req, vrow, vrank, voff = (idx(x) for x in (random_requests, verify_rows, verify_ranks,
+                                               verify_offsets))
+    n, num_rows = starts.shape[0], target.shape[0]
+    if accepted.shape != (n,) or next_tokens.shape != (n,) or input_tokens.shape != (n,):
+        raise ValueError("accepted, next_tokens, starts and input_tokens must be [n]")
+    r = req.shape[0]
+    tokens = _i64(result.tokens)
+    if tokens.dim() != 2 or tokens.shape[0] != r or result.accepted.shape != (r,) \
+            or result.final.shape != (r,) or result.error.shape != (r,):
+        raise ValueError("result must hold one row per random request")
+    if not (vrow.shape == vrank.shape == voff.shape) or vrow.dim() != 1:
+        raise ValueError("verify_rows, verify_ranks and verify_offsets must be equal-length 1-D")
+    err_in = result.error if result.error.dtype == torch.bool else result.error != 0
+    err_in = err_in.contiguous()
+    rows = torch.empty(num_rows, dtype=torch.int64, device=device)
+    acc = torch.empty(n, dtype=torch.int64, device=device)
+    nxt = torch.empty(n, dtype=torch.int64, device=device)
+    pos = torch.empty(n, dtype=torch.int64, device=device)
+    values = torch.empty((n, 2), dtype=torch.int64, device=device)
+    error = torch.empty(n, dtype=torch.int64, device=device)
+    tg, ac, nt, st, it = (_i64(x) for x in (target, accepted, next_tokens, starts, input_tokens))
+    ra, rf = _i64(result.accepted), _i64(result.final)
+    lib = _lib.library()
+    status = lib.rlt_merge_random_round(
+        _lib.ptr(tg), num_rows, _lib.ptr(ac), _lib.ptr(nt), _lib.ptr(st), _lib.ptr(it), n,
+        _lib.ptr(tokens), tokens.shape[1], _lib.ptr(ra), _lib.ptr(rf), _lib.ptr(err_in),
+        _lib.ptr(req), r, _lib.ptr(vrow), _lib.ptr(vrank), _lib.ptr(voff), vrow.shape[0],
+        _lib.ptr(rows), _lib.ptr(acc), _lib.ptr(nxt), _lib.ptr(pos), _lib.ptr(values),
+        _lib.ptr(error), _lib.stream_of(device))
+    _lib.check(status, "rlt_merge_random_round")
+    return RandomRoundMerge(rows, acc, nxt, pos, values, error)
