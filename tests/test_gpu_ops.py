@@ -66,3 +66,16 @@ def test_kv_write_op_mutates_the_pool(pkg, dev):
     offsets = torch.tensor([0, 15, 3], device=dev)
     torch.ops.rlt_mi355x.store_kv(kc, vc, k, -k, blocks, offsets, None, None)
     assert torch.equal(kc[blocks, offsets], k) and torch.equal(vc[blocks, offsets], -k)
+
+
+def test_merge_random_round_op(pkg, dev):
+    # reference KAT: tests/test_async_speculative_sampling_plan.py:127-161
+    t = lambda x, **kw: torch.tensor(x, device=dev, **kw)  # noqa: E731
+    args = (t([10, 11, 12, 20, 21, 30, 31]), t([0, 1, 0]), t([10, 21, 30]), t([5, 8, 12]),
+            t([1, 2, 3]), t([[77, 66, 55], [9, 0, 0]]), t([2, 0]), t([55, 0]),
+            t([False, True]), t([0, 2]), t([0, 1, 2, 5, 6]), t([0, 0, 0, 1, 1]), t([0, 1, 2, 0, 1]))
+    rows, acc, nxt, pos, values, err = torch.ops.rlt_mi355x.merge_random_round(*args)
+    assert rows.tolist() == [77, 66, 55, 20, 21, 9, 0]
+    assert acc.tolist() == [2, 1, 0] and nxt.tolist() == [55, 21, 0] and pos.tolist() == [8, 10, 13]
+    assert values.tolist() == [[55, 8], [21, 10], [3, 12]] and err.tolist() == [0, 0, 1]
+    torch.library.opcheck(torch.ops.rlt_mi355x.merge_random_round, args, test_utils=CHECKS)

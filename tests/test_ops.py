@@ -12,6 +12,8 @@ def test_operators_are_registered_with_reference_shaped_schemas(pkg):
     assert names["spec_accept"].endswith("-> (Tensor, Tensor, Tensor, Tensor)")
     assert "Tensor(a0!) key_cache" in names["store_kv"]
     assert "float? fixed_scale" in names["store_fp8"]
+    assert "Tensor? row_lengths=None" in names["paged_attention"]
+    assert names["merge_random_round"].endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
 
 
 def test_cpu_tensors_find_no_kernel(pkg):

@@ -153,6 +153,33 @@ def _(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accep
             x.new_empty((n,), dtype=torch.bool))
 
 
+
+@torch.library.custom_op("rlt_mi355x::merge_random_round", mutates_args=(), device_types="cuda")
+def merge_random_round(target: torch.Tensor, accepted: torch.Tensor, next_tokens: torch.Tensor,
+                       starts: torch.Tensor, input_tokens: torch.Tensor, tokens: torch.Tensor,
+                       result_accepted: torch.Tensor, result_final: torch.Tensor,
+                       result_error: torch.Tensor, random_requests: torch.Tensor,
+                       verify_rows: torch.Tensor, verify_ranks: torch.Tensor,
+                       verify_offsets: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor,
+                                                              torch.Tensor, torch.Tensor,
+                                                              torch.Tensor, torch.Tensor]:
+    """(rows, accepted, next_tokens, next_positions, next_values, error); reference:
+    vllm_rlt/worker/async_speculative.py:162-198."""
+    res = _samp.AcceptResult(tokens, result_accepted, result_final, result_error)
+    return tuple(_samp.merge_random_round(target, accepted, next_tokens, starts, input_tokens,
+                                          res, random_requests, verify_rows, verify_ranks,
+                                          verify_offsets))
+
+
+@merge_random_round.register_fake
+def _(target, accepted, next_tokens, starts, input_tokens, tokens, result_accepted, result_final,
+      result_error, random_requests, verify_rows, verify_ranks, verify_offsets):
+    n = starts.shape[0]
+    i64 = dict(dtype=torch.int64)
+    return (target.new_empty(target.shape, **i64), starts.new_empty((n,), **i64),
+            starts.new_empty((n,), **i64), starts.new_empty((n,), **i64),
+            starts.new_empty((n, 2), **i64), starts.new_empty((n,), **i64))
+
 @torch.library.custom_op("rlt_mi355x::store_kv", mutates_args=("key_cache", "value_cache"),
                          device_types="cuda")
 def store_kv(key_cache: torch.Tensor, value_cache: torch.Tensor, k: torch.Tensor,
@@ -183,4 +210,5 @@ def finalize_rows(descriptor: torch.Tensor, tables: torch.Tensor, key_pool: torc
 
 
 OPS = ("paged_attention", "spec_probs", "categorical", "spec_accept", "greedy_accept",
-       "propose_drafts", "verify_distributions", "verify_accept", "store_kv", "store_fp8", "finalize_rows")
+       "propose_drafts", "verify_distributions", "verify_accept", "merge_random_round", "store_kv",
+       "store_fp8", "finalize_rows")
