@@ -623,6 +623,19 @@ def main():
     for a, b in zip(out_ver[2], eager_acc):
         assert torch.equal(a, b)
 
+    # the round's bookkeeping after the acceptance: the random requests' outcome merged
+    # into the (here all-random) round, async_speculative.py:735-746
+    n_req, win = w["n"], w["window"]
+    m_req = torch.arange(n_req, device=dev)
+    m_rows = torch.arange(n_req * win, device=dev)
+    m_ranks = m_req.repeat_interleave(win)
+    m_offs = torch.arange(win, device=dev).repeat(n_req)
+    m_zero = torch.zeros(n_req, dtype=torch.int64, device=dev)
+    m_starts = lengths.long() - win
+    t_merge, _ = _graph_time(lambda: pkg.merge_random_round(
+        out_ver[0], m_zero, m_zero, m_starts, dt_tok[:, 0], out_ver[2], m_req, m_rows, m_ranks,
+        m_offs))
+
     a_bytes, p_bytes, c_bytes = attention_bytes(w), probs_bytes(w), accept_bytes(w)
     kv_bytes = kv_write_bytes(w)
     achieved = a_bytes / t_attn / 1e9
@@ -654,6 +667,7 @@ def main():
         "probs_ms": round(t_probs * 1e3, 4),
         "accept_ms": round(t_acc * 1e3, 4),
         "verify_accept_ms": round(t_ver * 1e3, 4),
+        "merge_random_round_ms": round(t_merge * 1e3, 4),
         "steps_per_graph": spg,
         "roofline": {
             "kernel": "attention launch (rlt_attn_mfma_kernel + rlt_merge_kernel)",
