@@ -1679,7 +1679,8 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
         (k_head_stride * kv_elt) % kv_align == 0 && (v_block_stride * kv_elt) % kv_align == 0 &&
         (v_token_stride * kv_elt) % kv_align == 0 && (v_head_stride * kv_elt) % kv_align == 0;
     if (!aligned) return RLT_ERR_ARGUMENT;
-    if (cu_seqlens_q && !row_lengths && rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len)) {
+    if (cu_seqlens_q && !row_lengths &&
+        rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len)) {
       // long q windows: the prefill tiling, normalized in one launch
       P.rows_per_rg = kPfRows;
       P.rowgroups = (rows_per_seq + kPfRows - 1) / kPfRows;
