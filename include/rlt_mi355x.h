@@ -72,9 +72,8 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
  * rlt_paged_attention with explicit per-row key counts for the packed form:
  * query i of sequence s sees keys < row_lengths[cu_seqlens_q[s] + i] (int32
  * [num_q_rows]; with window > 0, the last `window` of them) instead of the causal
- * window's context_lengths[s] - q_len(s) + i + 1.  Rows of one sequence must be
- * ordered by nondecreasing length (not checked on the device: another order gives
- * wrong but in-bounds results).  It lets rows that read one block table share each
+ * window's context_lengths[s] - q_len(s) + i + 1.  The rows of a sequence may come
+ * in any order (each unit takes the bounds over all of its rows).  It lets rows that read one block table share each
  * KV byte although their positions are not consecutive: the pipelined verify of
  * vllm_rlt/worker/async_speculative.py:449-470, where window row j reads loop-depth
  * plane (d0 + j) mod planes and rows d0 and d0 + planes fall on the same plane.  The

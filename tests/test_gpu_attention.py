@@ -385,16 +385,19 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
 
 # ------------------------------------------ packed rows with explicit row lengths
 
-def _group_rows_by_plane(n, w, planes, d0, row_len):
+def _group_rows_by_plane(n, w, planes, d0, row_len, order="ascending"):
     """Pipelined verify rows: row j of request i reads plane (d0[i] + j) % planes.  One
-    packed sequence per (request, plane), its rows by nondecreasing length."""
+    packed sequence per (request, plane), its rows by length (``order`` ascending or
+    descending) or in a mixed order (``rotated``: the longest row first)."""
     perm, cu, seq_req, seq_plane = [], [0], [], []
     for i in range(n):
         for pl in range(planes):
             rows = [i * w + j for j in range(w) if (int(d0[i]) + j) % planes == pl]
             if not rows:
                 continue
-            rows.sort(key=lambda r: int(row_len[r]))
+            rows.sort(key=lambda r: int(row_len[r]), reverse=order == "descending")
+            if order == "rotated":
+                rows = rows[-1:] + rows[:-1]
             perm += rows
             cu.append(len(perm))
             seq_req.append(i)
@@ -403,15 +406,20 @@ def _group_rows_by_plane(n, w, planes, d0, row_len):
             torch.tensor(seq_plane))
 
 
-@pytest.mark.parametrize("q_dtype,kv,planes,hq,hkv,d,window", [
-    (torch.bfloat16, "fp8", 4, 16, 8, 128, 0),     # config 5 shape: rows 0 and 4 share d0
-    (torch.bfloat16, "bf16", 2, 16, 2, 128, 0),    # 3 rows x GQA 8 = 24 rows: two row tiles
-    (torch.float16, "fp16", 4, 8, 8, 64, 300),     # windowed
-    (torch.float32, "fp32", 3, 4, 2, 32, 0),       # vector path
+@pytest.mark.parametrize("q_dtype,kv,planes,hq,hkv,d,window,order", [
+    (torch.bfloat16, "fp8", 4, 16, 8, 128, 0, "ascending"),   # config 5: rows 0 and 4 share d0
+    (torch.bfloat16, "bf16", 2, 16, 2, 128, 0, "ascending"),  # 3 rows x GQA 8: two row tiles
+    (torch.float16, "fp16", 4, 8, 8, 64, 300, "ascending"),   # windowed
+    (torch.float32, "fp32", 3, 4, 2, 32, 0, "ascending"),     # vector path
+    # rows of a sequence in any order (each unit bounds over all of its rows)
+    (torch.bfloat16, "fp8", 4, 16, 8, 128, 0, "descending"),
+    (torch.bfloat16, "bf16", 2, 16, 2, 128, 0, "rotated"),
+    (torch.float16, "fp16", 4, 8, 8, 64, 300, "descending"),
+    (torch.float32, "fp32", 3, 4, 2, 32, 0, "rotated"),
 ])
 def test_packed_rows_with_row_lengths_equal_per_row_bitwise(kernel, dev, q_dtype, kv, planes, hq,
-                                                            hkv, d, window):
-    _say("row_lengths", q_dtype, kv, planes, hq, hkv, d, window)
+                                                            hkv, d, window, order):
+    _say("row_lengths", q_dtype, kv, planes, hq, hkv, d, window, order)
     g = torch.Generator().manual_seed(11)
     n, w, bs = 5, 5, 16
     max_len = 3000 + w
@@ -435,7 +443,7 @@ def test_packed_rows_with_row_lengths_equal_per_row_bitwise(kernel, dev, q_dtype
     row_tables = tables[torch.arange(n).view(n, 1), plane].reshape(n * w, per)
     row_len = (start.view(n, 1) + j.view(1, w) + 1).reshape(-1).int()
     q = torch.randn(n * w, hq, d, generator=g).to(q_dtype)
-    perm, cu, seq_req, seq_plane = _group_rows_by_plane(n, w, planes, d0, row_len)
+    perm, cu, seq_req, seq_plane = _group_rows_by_plane(n, w, planes, d0, row_len, order)
     seq_tables = tables[seq_req, seq_plane]
     seq_len = torch.stack([row_len[perm[cu[s]:cu[s + 1]]].max() for s in range(len(cu) - 1)])
     max_q = int((cu[1:] - cu[:-1]).max())

@@ -104,6 +104,19 @@ def _assert_match(got, want, logits, t, k, p, plan):
             tb = sm.cumsum(-1) - sm
             lo, hi = min(gc, wc), max(gc, wc)
             assert ((tb[lo:hi] - top_p).abs() <= band).all(), f"row {i}: {gc} vs torch {wc}"
+            # torch's kept set is a top set too, so the two differ only by tail positions
+            # lo..hi of the order (tied tokens may be swapped, which leaves the values).
+            assert torch.equal(x[ws].sort(descending=True).values, sx[:wc]), \
+                f"row {i}: torch's kept set is not a top set"
+            # Values: both rows renormalised over the common support agree token by token.
+            common = gs & ws
+            gn = g[common].double() / g[common].double().sum()
+            wn = w[common].double() / w[common].double().sum()
+            torch.testing.assert_close(gn, wn, atol=ATOL, rtol=RTOL)
+            # And before renormalising, each side's kept mass over the common support is
+            # 1 minus its extra tail tokens' mass.
+            torch.testing.assert_close(g[common].double().sum() + g[gs & ~ws].double().sum(),
+                                       torch.tensor(1.0, dtype=torch.float64), atol=1e-5, rtol=0)
             continue
         torch.testing.assert_close(g.sort().values, w.sort().values, atol=ATOL, rtol=RTOL)
 

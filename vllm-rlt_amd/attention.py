@@ -198,8 +198,7 @@ class MI355XPagedAttention:
 
         ``row_lengths`` (int32 ``[q rows]``, optional, not in the reference signature): row i
         of a sequence sees ``row_lengths[cu_seqlens_q[s] + i]`` keys instead of the causal
-        window's ``context_lengths[s] - q_len + i + 1``; a sequence's rows must be ordered by
-        nondecreasing length.  Rows that read one block table at non-consecutive positions
+        window's ``context_lengths[s] - q_len + i + 1``, in any order.  Rows that read one block table at non-consecutive positions
         (pipelined verify rows at the same loop-depth plane) then share each KV byte, and
         every row equals the per-row ``__call__`` bit for bit.
         """

@@ -139,6 +139,35 @@ __device__ __forceinline__ void row_range(const AttnParams& P, const SeqView& s,
   lo = P.window > 0 ? max(0, hi - P.window) : 0;
 }
 
+// Bounds over the rows [rg_begin, rg_begin + rg_rows) of a sequence (row rho is
+// window index rho / group): every row's visible range lies in [lo_min, hi_max),
+// and positions in [lo_max, hi_min) are visible to every row.  The causal window's
+// ranges grow with the window index, so its first and last rows give the bounds;
+// explicit row lengths may come in any order and every row is visited.
+__device__ __forceinline__ void group_range(const AttnParams& P, const SeqView& s, int rg_begin,
+                                            int rg_rows, int& lo_min, int& hi_min, int& lo_max,
+                                            int& hi_max) {
+  const int q0 = rg_begin / P.group, q1 = (rg_begin + rg_rows - 1) / P.group;
+  row_range(P, s, q0, lo_min, hi_min);
+  row_range(P, s, q1, lo_max, hi_max);
+  if (P.row_len) {
+    if (lo_max < lo_min) {
+      const int t = lo_min; lo_min = lo_max; lo_max = t;
+    }
+    if (hi_max < hi_min) {
+      const int t = hi_min; hi_min = hi_max; hi_max = t;
+    }
+    for (int qi = q0 + 1; qi < q1; ++qi) {
+      int lo, hi;
+      row_range(P, s, qi, lo, hi);
+      lo_min = min(lo_min, lo);
+      lo_max = max(lo_max, lo);
+      hi_min = min(hi_min, hi);
+      hi_max = max(hi_max, hi);
+    }
+  }
+}
+
 // Physical block of key position `pos`; entries outside the pool read block 0
 // so that a corrupt table can never address memory outside the KV pool.
 __device__ __forceinline__ int64_t block_of(const AttnParams& P, int seq, int pos) {
@@ -448,8 +477,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
   if (rg_begin >= rows_total) return;
   const int rg_rows = min(P.rows_per_rg, rows_total - rg_begin);
   int lo_first, hi_first, lo_last, hi_last;
-  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
-  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  group_range(P, sv, rg_begin, rg_rows, lo_first, hi_first, lo_last, hi_last);
   if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
   st.active = true;
   st.rg_begin = rg_begin;
@@ -752,8 +780,7 @@ __device__ __forceinline__ void pair_chunks(const AttnParams& P, int p, int& c0,
   if (rg_begin >= rows_total) return;
   const int rg_rows = min(P.rows_per_rg, rows_total - rg_begin);
   int lo_first, hi_first, lo_last, hi_last;
-  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
-  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  group_range(P, sv, rg_begin, rg_rows, lo_first, hi_first, lo_last, hi_last);
   if (hi_last <= lo_first) return;
   c0 = lo_first / kChunk;
   c1 = (hi_last + kChunk - 1) / kChunk;
@@ -919,8 +946,7 @@ __global__ __launch_bounds__(256) void rlt_attn_vec_kernel(AttnParams P) {
   if (rg_begin >= rows_total) return;
   const int rg_rows = min(kVecRows, rows_total - rg_begin);
   int lo_first, hi_first, lo_last, hi_last;
-  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
-  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  group_range(P, sv, rg_begin, rg_rows, lo_first, hi_first, lo_last, hi_last);
   const int c_begin = chunk * kChunk;
   if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
 
@@ -1290,8 +1316,7 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   if (rg_begin >= rows_total) return;  // uniform over the workgroup
   const int rg_rows = min(kPfRows, rows_total - rg_begin);
   int lo_first, hi_first, lo_last, hi_last;
-  row_range(P, sv, rg_begin / P.group, lo_first, hi_first);
-  row_range(P, sv, (rg_begin + rg_rows - 1) / P.group, lo_last, hi_last);
+  group_range(P, sv, rg_begin, rg_rows, lo_first, hi_first, lo_last, hi_last);
 
   // this lane's rows (one per 16-row tile): B operand of S^T = K Q^T
   uint4 qreg[NT][NQS];

@@ -30,8 +30,7 @@ def paged_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch
                     window: int, row_lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Per-row (cu_seqlens_q None) or packed causal-window paged attention;
     reference: vllm_rlt/kernels/paged_attention.py:13-90, triton_attention.py:386-404.
-    ``row_lengths`` (packed form only): each row's key count, rows of a sequence by
-    nondecreasing length."""
+    ``row_lengths`` (packed form only): each row's key count, rows in any order."""
     return _ATTN._run(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
                       max_seqlen_q, key_scale, value_scale, window, row_lengths)
 
