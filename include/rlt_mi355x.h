@@ -131,6 +131,27 @@ int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, c
                            size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * rlt_speculative_accept without a workspace argument and without any allocation:
+ * the workspace is a file-scope device array of
+ * rlt_speculative_accept_noalloc_max_bytes() bytes (8 MiB) per GPU, held until the
+ * process ends.  No counterpart in the reference: this is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, outputs and results as
+ * rlt_speculative_accept.  Returns RLT_ERR_WORKSPACE when the call needs more than
+ * that maximum (rlt_speculative_accept_workspace_size(n, w1, V) bytes; e.g. n = 256,
+ * w1 = 4, V = 65536 needs about 2.5 MiB).  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (on different streams, or from different
+ * threads) race and must be serialized by the caller.
+ */
+size_t rlt_speculative_accept_noalloc_max_bytes(void);
+
+int rlt_speculative_accept_noalloc(const int64_t* draft_tokens, const int64_t* drafts,
+                                   const float* q, const float* p, const float* u_accept,
+                                   const float* u_final, int64_t n, int32_t w1, int64_t vocab,
+                                   int64_t* tokens, int64_t* accepted, int64_t* final_token,
+                                   uint8_t* error, hipStream_t stream);
+
+/*
  * Inverse-CDF draw from nonnegative, possibly unnormalized fp32 weights [m, V]
  * (contiguous) with uniforms u [m]: float64 cumulative sum, threshold
  * min(u * mass, nextafter(mass, 0)), right-bisect; invalid rows (mass not finite

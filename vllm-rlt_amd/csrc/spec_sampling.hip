@@ -36,6 +36,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace {
 
 using cascade::kChunkSteps;
@@ -933,6 +935,37 @@ int rlt_accept_after_q_partials(const int64_t* draft_tokens, const int64_t* draf
                        accepted, final_token, error, workspace, workspace_bytes, true, stream);
 }
 
+// ------------------------------------------------------------ no-allocation form
+
+namespace {
+
+// The acceptance workspace of rlt_speculative_accept_noalloc: one copy per GPU,
+// held until the process ends.  Host code never passes this name to a kernel (on
+// the host it is only a stand-in for the symbol); it passes the device address
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up once per device with that device
+// current; nullptr on failure.
+void* scratch_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
 extern "C" {
 
 size_t rlt_speculative_accept_workspace_size(int64_t n, int32_t w1, int64_t vocab) {
@@ -950,6 +983,25 @@ int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, c
                            size_t workspace_bytes, hipStream_t stream) {
   return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
                        accepted, final_token, error, workspace, workspace_bytes, false, stream);
+}
+
+size_t rlt_speculative_accept_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+int rlt_speculative_accept_noalloc(const int64_t* draft_tokens, const int64_t* drafts,
+                                   const float* q, const float* p, const float* u_accept,
+                                   const float* u_final, int64_t n, int32_t w1, int64_t vocab,
+                                   int64_t* tokens, int64_t* accepted, int64_t* final_token,
+                                   uint8_t* error, hipStream_t stream) {
+  if (n < 0 || w1 < 0 || w1 > kMaxW1 || vocab < 1) return RLT_ERR_ARGUMENT;
+  if (n == 0) return RLT_OK;
+  // Every kernel writes the parts of the workspace it later reads (the one counter
+  // it only increments is diagnostic), so the array needs no clearing between calls.
+  const size_t need = layout_for(n * (2 * (int64_t)w1 + 1), n, vocab).total;
+  if (need > kNoAllocScratchBytes) return RLT_ERR_WORKSPACE;
+  void* ws = scratch_for_current_device();
+  if (!ws) return RLT_ERR_LAUNCH;
+  return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
+                       accepted, final_token, error, ws, kNoAllocScratchBytes, false, stream);
 }
 
 int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t vocab,
