@@ -415,7 +415,8 @@ int rlt_depth_tables(const int32_t* tables, int64_t row_stride, int64_t plane_st
  * next_positions_out / error_out [n] (error as 0 / 1), next_values_out [n, 2]
  * (token, position): a failed request keeps (input_token, start).  Index tensors must
  * not repeat an index (the reference's scatters leave the winner unspecified then);
- * indices outside their ranges are skipped (the reference raises a device assert). */
+ * an index outside its range (the reference raises) is skipped and fails the whole
+ * round: error_out is 1 for every request, whose slot values stay (input_token, start). */
 int rlt_merge_random_round(const int64_t* target, int64_t num_rows, const int64_t* accepted,
                            const int64_t* next_tokens, const int64_t* starts,
                            const int64_t* input_tokens, int64_t n, const int64_t* tokens,

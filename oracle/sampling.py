@@ -92,8 +92,8 @@ def speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final):
         raise ValueError("drafts, u_accept and u_final must match draft_tokens [n, W1]")
     if q.shape != (n, w1, vocab) or p.shape != (n, w1 + 1, vocab):
         raise ValueError("q must be [n, W1, V] and p must be [n, W1 + 1, V]")
-    rows = torch.arange(n)
-    pos = torch.arange(w1 + 1)
+    rows = torch.arange(n, device=p.device)
+    pos = torch.arange(w1 + 1, device=p.device)
     p_mass = p.sum(-1, dtype=torch.float32)
     p_ok = torch.isfinite(p_mass) & (p_mass > 0)
     d = drafts.clamp(0, w1)

@@ -222,3 +222,108 @@ def test_merge_random_round_matches_oracle(pkg, dev, n, seed):
                                     vrank, voff)
     for a, b in zip(got, want):
         assert torch.equal(a, b.reshape(a.shape).to(a.dtype))
+
+
+@pytest.mark.parametrize("corrupt", ["row", "rank", "offset", "request"])
+def test_merge_random_round_corrupt_plan_fails_the_round(pkg, dev, corrupt):
+    """An index outside its range: the reference's indexing raises; the device merge
+    skips it and reports every request failed, each keeping its slot values."""
+    _say("merge corrupt", corrupt)
+    res = osamp.AcceptResult(tokens=torch.tensor([[77, 66, 55], [9, 0, 0]]),
+                             accepted=torch.tensor([2, 0]), final=torch.tensor([55, 0]),
+                             error=torch.tensor([False, False]))
+    vrow, vrank = torch.tensor([0, 1, 2, 5, 6]), torch.tensor([0, 0, 0, 1, 1])
+    voff, req = torch.tensor([0, 1, 2, 0, 1]), torch.tensor([0, 2])
+    if corrupt == "row":
+        vrow[3] = 7
+    elif corrupt == "rank":
+        vrank[4] = 2
+    elif corrupt == "offset":
+        voff[2] = 3
+    else:
+        req[1] = 3
+    args = (torch.tensor([10, 11, 12, 20, 21, 30, 31]), torch.tensor([0, 1, 0]),
+            torch.tensor([10, 21, 30]), torch.tensor([5, 8, 12]), torch.tensor([1, 2, 3]),
+            req, vrow, vrank, voff)
+    with pytest.raises(IndexError):
+        osamp.merge_random_round(*args[:5], res, *args[5:])
+    rows, acc, nxt, pos, values, err = _merge_on_gpu(pkg, dev, args, res)
+    assert err.tolist() == [1, 1, 1]
+    assert values.tolist() == [[1, 5], [2, 8], [3, 12]]
+
+
+# ------------------------------------- against the reference formula on the device
+
+def _margins(q, p, u, dt, w1):
+    """Per request: the smallest relative margin of any decision the reference takes
+    (each accept test u*qx < px up to the stop point, and the final inverse-CDF
+    threshold against the cumulative values around the drawn index), in torch-CPU
+    arithmetic."""
+    ua, uf = u[:, w1:2 * w1], u[:, 2 * w1]
+    res = osamp.speculative_accept(dt, torch.full((dt.shape[0],), w1), q, p, ua, uf)
+    pm, qm = p.sum(-1, dtype=torch.float32), q.sum(-1, dtype=torch.float32)
+    out = []
+    for i in range(dt.shape[0]):
+        s = int(res.accepted[i])
+        m = float("inf")
+        for j in range(min(s + 1, w1)):
+            x = int(dt[i, j])
+            px, qx = float(p[i, j, x] / pm[i, j]), float(q[i, j, x] / qm[i, j])
+            m = min(m, abs(float(ua[i, j]) * qx - px) / max(px, 1e-30), abs(px - qx) / max(px, 1e-30))
+        pr = p[i, s].double() / float(pm[i, s])
+        w = pr if s == w1 else (pr - q[i, s].double() / float(qm[i, s])).clamp_min(0)
+        c = w.cumsum(0)
+        t = float(uf[i]) * float(c[-1])
+        k = int(res.final[i])
+        lo = float(c[k - 1]) if k > 0 else 0.0
+        m = min(m, abs(t - lo) / float(c[-1]), abs(float(c[k]) - t) / float(c[-1]))
+        out.append(m)
+    return out
+
+
+@pytest.mark.parametrize("name,n,vocab,temperature,top_p", [
+    ("config1", 8, 49152, 1.0, 1.0),
+    ("config3", 32, 49152, 0.7, 0.9),
+    ("config5", 256, 65536, 1.0, 1.0),
+])
+def test_accept_against_reference_formula_run_on_the_gpu(pkg, dev, name, n, vocab, temperature,
+                                                         top_p):
+    """The reference's own async path runs speculative_accept on device tensors
+    (vllm_rlt/worker/async_speculative.py:727-734), so its row sums and float64 cumsum
+    follow torch-ROCm's reduction orders, not torch-CPU's that this kernel reproduces.
+    Every request where the two disagree must hinge on a decision whose margin is
+    within float32 rounding of the masses (relative 1e-5); on these seeds they agree."""
+    _say("accept vs device reference", name)
+    g = torch.Generator().manual_seed(1000 + n)
+    w1 = 4
+    q, p, u, dt = _verify_inputs(n, w1, vocab, g, temperature, top_p)
+    drafts = torch.full((n,), w1, dtype=torch.int64)
+    ua, uf = u[:, w1:2 * w1].contiguous(), u[:, 2 * w1].contiguous()
+    args = [a.to(dev) for a in (dt, drafts, q, p, ua, uf)]
+    ours = pkg.speculative_accept(*args)
+    dev_ref = osamp.speculative_accept(*args)
+    cpu_ref = osamp.speculative_accept(dt, drafts, q, p, ua, uf)
+    assert torch.equal(ours.tokens.cpu(), cpu_ref.tokens)
+    differ = [i for i in range(n)
+              if not (torch.equal(ours.tokens[i].cpu(), dev_ref.tokens[i].cpu())
+                      and int(ours.accepted[i]) == int(dev_ref.accepted[i]))]
+    if differ:
+        margins = _margins(q, p, u, dt, w1)
+        assert all(margins[i] <= 1e-5 for i in differ), [(i, margins[i]) for i in differ]
+    # the masses themselves: torch-ROCm's fp32 row sums are within a few ulps of ours
+    gm = p.to(dev).sum(-1, dtype=torch.float32).cpu()
+    cm = p.sum(-1, dtype=torch.float32)
+    assert ((gm - cm).abs() <= 8 * torch.finfo(torch.float32).eps * cm.abs()).all()
+    print(f"[case] {name}: {len(differ)} of {n} requests differ from the device reference",
+          flush=True)
+
+
+def test_order_fixture_sums_are_the_kernels(pkg, dev):
+    """The constants the import-time guard compares the host's torch with are the
+    kernels' own sums of the fixture rows."""
+    from vllm_rlt_amd import sampling
+
+    for vocab, bits in sampling.ORDER_FIXTURE_SUMS.items():
+        x = torch.from_numpy(sampling.order_fixture(vocab)).view(1, vocab).repeat(3, 1)
+        got = pkg.sampling.row_mass(x.to(dev)).cpu()
+        assert all((int(v) & 0xFFFFFFFF) == bits for v in got.view(torch.int32)), vocab

@@ -91,3 +91,15 @@ def test_categorical_model_negative_weights_follow_torch_bisect():
     want_i, _ = _torch_categorical(w, u)
     got_i, _ = order.categorical(w.numpy(), u.numpy())
     assert np.array_equal(want_i.numpy(), got_i)
+
+
+def test_import_guard_fixture_matches_torch_and_the_model(pkg):
+    """The package's import-time sum-order guard: the committed fixture sums equal the C
+    order model's and this host's torch's (the guard then reports a match)."""
+    from vllm_rlt_amd import sampling
+
+    assert sampling.CPU_SUM_ORDER_MATCHES
+    for vocab, bits in sampling.ORDER_FIXTURE_SUMS.items():
+        x = sampling.order_fixture(vocab)[None]
+        got = order.row_sums(x)
+        assert (int(got.view(np.int32)[0]) & 0xFFFFFFFF) == bits, vocab

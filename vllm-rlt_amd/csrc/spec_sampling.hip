@@ -1054,7 +1054,7 @@ constexpr int kMergeThreads = 1024;
 // One workgroup, three phases separated by workgroup barriers (global writes are
 // visible to the whole workgroup after __syncthreads): copy the greedy round's
 // values, overlay the random requests' outcomes, then form the slot values.
-// Indices outside their ranges are skipped.
+// Indices outside their ranges are skipped and fail the whole round.
 __global__ __launch_bounds__(kMergeThreads) void rlt_merge_random_round_kernel(
     const int64_t* __restrict__ target, int64_t num_rows, const int64_t* __restrict__ accepted,
     const int64_t* __restrict__ next_tokens, const int64_t* __restrict__ starts,
@@ -1065,7 +1065,9 @@ __global__ __launch_bounds__(kMergeThreads) void rlt_merge_random_round_kernel(
     const int64_t* __restrict__ verify_offsets, int64_t num_verify, int64_t* rows_out,
     int64_t* accepted_out, int64_t* next_tokens_out, int64_t* next_positions_out,
     int64_t* next_values_out, int64_t* error_out) {
+  __shared__ int bad_plan;
   const int t = threadIdx.x;
+  if (t == 0) bad_plan = 0;
   for (int64_t i = t; i < num_rows; i += kMergeThreads) rows_out[i] = target[i];
   for (int64_t i = t; i < n; i += kMergeThreads) {
     accepted_out[i] = accepted[i];
@@ -1077,6 +1079,8 @@ __global__ __launch_bounds__(kMergeThreads) void rlt_merge_random_round_kernel(
     const int64_t row = verify_rows[k], rank = verify_ranks[k], off = verify_offsets[k];
     if (row >= 0 && row < num_rows && rank >= 0 && rank < r && off >= 0 && off < width)
       rows_out[row] = tokens[rank * width + off];
+    else
+      bad_plan = 1;
   }
   for (int64_t k = t; k < r; k += kMergeThreads) {
     const int64_t req = random_requests[k];
@@ -1084,12 +1088,18 @@ __global__ __launch_bounds__(kMergeThreads) void rlt_merge_random_round_kernel(
       accepted_out[req] = r_accepted[k];
       next_tokens_out[req] = r_final[k];
       error_out[req] = r_error[k] ? 1 : 0;
+    } else {
+      bad_plan = 1;
     }
   }
   __syncthreads();
+  // An index outside its range (where the reference's indexing raises) fails the
+  // whole round: every request reports an error and keeps its slot values.
+  const bool bad = bad_plan != 0;
   for (int64_t i = t; i < n; i += kMergeThreads) {
     const int64_t pos = starts[i] + accepted_out[i] + 1;
     next_positions_out[i] = pos;
+    if (bad) error_out[i] = 1;
     const bool failed = error_out[i] != 0;
     next_values_out[2 * i] = failed ? input_tokens[i] : next_tokens_out[i];
     next_values_out[2 * i + 1] = failed ? starts[i] : pos;

@@ -5,16 +5,63 @@ vllm_rlt/worker/speculative_sampling.py (``batched_probabilities`` :8-56,
 ``categorical`` :59-85, ``AcceptResult`` :88-101, ``speculative_accept``
 :104-181), plus the device greedy round of vllm_rlt/worker/async_speculative.py:706-720
 (``greedy_accept_batched``).  Acceptance and categorical results are
-bit-exact with the reference's torch-CPU arithmetic when fed identical fp32
-probabilities and uniforms.  Every call enqueues gfx950 kernels on the current
+bit-exact with the reference formula computed by torch on the CPU when fed
+identical fp32 probabilities and uniforms (the import-time guard below checks
+that this host's torch sums in that order); against the formula computed by
+torch on the GPU they can differ only at decisions within float32 rounding of
+the masses.  Every call enqueues gfx950 kernels on the current
 stream without host synchronization; inputs are never modified.
 """
 
+import warnings
 from typing import NamedTuple
 
+import numpy as np
 import torch
 
 from . import _lib
+
+
+# ------------------------------------------------------- torch-CPU sum-order guard
+#
+# The acceptance kernels reproduce the summation order of torch's CPU
+# ``Tensor.sum(-1, dtype=float32)`` (32 streams of a 4-level cascade over 8-lane
+# vectors, 4 in flight), which is what makes them bit-exact with the reference run
+# on the CPU.  Another torch build or CPU dispatch (e.g. 16-lane vectors) would
+# sum in another order, and the bit-exact claim would silently stop holding.  At
+# import the host's torch sums order-sensitive rows and compares the bits with the
+# values the kernels produce (pinned by a GPU test); a mismatch warns and is
+# recorded in CPU_SUM_ORDER_MATCHES.
+
+def order_fixture(vocab):
+    """Deterministic float32 row whose float32 sum depends on the summation order
+    (values spread over 2^-11 .. 2^11)."""
+    i = np.arange(vocab, dtype=np.uint64)
+    frac = ((i * np.uint64(2654435761)) % np.uint64(1 << 32)).astype(np.float64) / 2.0**32
+    scale = np.exp2(((i * np.uint64(7)) % np.uint64(23)).astype(np.int64) - 11)
+    return (frac * scale).astype(np.float32)
+
+
+# float32 bits of order_fixture(V).sum() in the kernels' order, per V
+ORDER_FIXTURE_SUMS = {7: 0x4484407F, 1000: 0x47AB9584, 49152: 0x4A8587B4, 65536: 0x4AB1FE4C,
+                      151936: 0x4B4E6A2B}
+
+
+def _host_sum_order_matches():
+    for vocab, bits in ORDER_FIXTURE_SUMS.items():
+        x = torch.from_numpy(order_fixture(vocab)).view(1, vocab)
+        got = int(x.sum(-1, dtype=torch.float32).view(torch.int32)[0]) & 0xFFFFFFFF
+        if got != bits:
+            return False
+    return True
+
+
+CPU_SUM_ORDER_MATCHES = _host_sum_order_matches()
+if not CPU_SUM_ORDER_MATCHES:
+    warnings.warn(
+        "this host's torch sums float32 rows in another order than the one the MI355X "
+        "acceptance kernels reproduce: their results are not bit-exact with the reference "
+        "run on this host's CPU (they still follow the reference's formula)", RuntimeWarning)
 
 
 class AcceptResult(NamedTuple):
@@ -370,7 +417,9 @@ def merge_random_round(target, accepted, next_tokens, starts, input_tokens, resu
 
     reference: vllm_rlt/worker/async_speculative.py:162-198.  ``random_requests`` and the
     ``verify_*`` index arrays may be device tensors or host arrays (copied to the device);
-    an index must not repeat, and indices outside their ranges are skipped.
+    an index must not repeat.  An index outside its range (where the reference's
+    indexing raises) is skipped and fails the whole round: ``error`` is 1 for every
+    request, and every request keeps its ``(input_token, start)`` slot values.
     """
     device = target.device
     _lib.require_gpu(target, accepted, next_tokens, starts, input_tokens, *result)
