@@ -404,6 +404,35 @@ int rlt_depth_tables(const int32_t* tables, int64_t row_stride, int64_t plane_st
                      int32_t* out_table, int64_t out_stride, int64_t* blocks, int64_t* offsets,
                      int32_t* lengths, int64_t n, hipStream_t stream);
 
+/*
+ * Sync-mode rejection sampling of a batch of requests: the device part of
+ * vllm_rlt/worker/speculative.py:56-72 rejection_sample as its caller _collect_round
+ * (:574-625) runs it, draft after draft.  For request i with counts[i] = d <= k drafts
+ * candidates[i, :d] (int64 [n, k]), target p fp32 [n, k + 1, V] (row j verifies draft
+ * j), proposal q fp32 [n, k, V] and uniforms u fp32 [n, k] (the generator's draws, in
+ * order), draft j is taken in order until the first event:
+ *   candidate outside [-V, V)  -> status 4 (the reference raises IndexError),
+ *   q[j, x] not > 0            -> status 2 (ValueError; u[j] is not consumed),
+ *   u[j] * q[j, x] < p[j, x]   -> accepted, next draft,
+ *   otherwise                  -> rejected: residual[i] = clamp_min(p[j] - q[j], 0)
+ *                                 divided by its float32 total, summed in torch's order
+ *                                 for a whole 1-D tensor on `sum_threads` CPU threads;
+ *                                 status 1, or 3 if that total is not finite and > 0
+ *                                 (RuntimeError).
+ * All d accepted -> status 0 (the bonus draw comes from p[d]).  accepted[i] = drafts
+ * accepted before the event.  status int32 [n], accepted int64 [n], residual fp32
+ * [n, V] (rows of requests whose status is not 1 are unspecified).  The residual draw
+ * itself (torch.multinomial on the request's generator) stays with the caller.
+ * 1 <= sum_threads <= 256, V < 2^31.
+ */
+size_t rlt_rejection_sample_workspace_size(int64_t n, int64_t vocab, int32_t sum_threads);
+
+int rlt_rejection_sample(const int64_t* candidates, const int64_t* counts, const float* target,
+                         const float* proposal, const float* uniforms, int64_t n, int32_t k,
+                         int64_t vocab, int32_t sum_threads, int32_t* status, int64_t* accepted,
+                         float* residual, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
 /* Random-round merge: overlay the random requests' speculative_accept outcome on
  * the greedy round, in one launch with no host reads.  Replaces
  * vllm_rlt/worker/async_speculative.py:162-198 merge_random_round (RandomRoundMerge

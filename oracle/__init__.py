@@ -12,6 +12,7 @@ Contents (each function cites the reference file:line it restates):
   vllm_rlt/kernels/triton_attention.py:386-404 for the packed form).
 * ``sampling``   -- ``batched_probabilities``, ``Sampler.probabilities``,
   ``categorical``, ``speculative_accept``, greedy prefix accept, the
+  synchronous runner's ``rejection_sample`` / random-request round, the
   per-request uniform protocol and the random-round merge
   (vllm_rlt/worker/speculative_sampling.py, worker/sampler.py:28-62,
   worker/speculative.py:41-72, worker/async_speculative.py:101-198,567-586,
@@ -20,8 +21,8 @@ Contents (each function cites the reference file:line it restates):
   (vllm_rlt/core/kv_cache_manager.py:40-65).
 * ``order``      -- ctypes binding of ``order.c``, an independent C model of
   the two torch-CPU summation orders the acceptance contract depends on:
-  the fp32 ``Tensor.sum(-1)`` cascade and the sequential fp64 ``cumsum``
-  feeding ``searchsorted``.  Tests pin it bit-for-bit against torch itself.
+  the fp32 ``Tensor.sum(-1)`` cascade (and a whole 1-D tensor's ``sum()`` over
+  thread chunks) and the sequential fp64 ``cumsum`` feeding ``searchsorted``.  Tests pin it bit-for-bit against torch itself.
 
 Pinning (what fixes each function beyond restating it):
 
@@ -36,4 +37,8 @@ Pinning (what fixes each function beyond restating it):
   top-k tie counts, top_p == 1 softmax identity.
 * greedy accept: reference KAT tests/test_speculative.py:277-285 and brute
   force over tiny vocabularies.
+* rejection_sample / collect_stochastic: the reference's recovery test
+  (tests/test_speculative.py:455-471: the accepted-or-resampled token follows p)
+  on CPU generators, exact residual closed forms, the error cases, and the C
+  model of the 1-D sum order.
 """

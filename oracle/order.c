@@ -18,7 +18,9 @@
  *    lane-wise, then a scalar starts at 0, adds the leftover scalar tail in
  *    order and then the 8 lanes in order.  Rows shorter than 8 take the
  *    scalar form of the same ILP-4 cascade.
- * 2. categorical draw (speculative_sampling.py:74-84): sequential float64
+ * 2. fp32 sum of a whole 1-D tensor (``oracle_sum_1d_f32``): the same row
+ *    cascade over thread chunks, then over the per-thread partials.
+ * 3. categorical draw (speculative_sampling.py:74-84): sequential float64
  *    cumsum from 0, mass = last entry, valid = finite and > 0,
  *    t = min(u * mass, nextafter(mass, 0)), index = torch's upper_bound
  *    binary search over the cdf, 0 when invalid, clamped to [0, V - 1].
@@ -83,6 +85,31 @@ float oracle_row_sum_f32(const float *x, int64_t n) {
     for (int64_t e = vs * 8; e < n; ++e) f += x[e];
     for (int l = 0; l < 8; ++l) f += lanes[l];
     return f;
+}
+
+/* fp32 sum of a whole 1-D tensor, ``x.sum()`` (the residual total at
+ * vllm_rlt/worker/speculative.py:66).  torch reduces a contiguous tensor to one
+ * value serially when it has fewer than 32768 elements or one thread; otherwise
+ * it splits it into c = min(threads, ceil(n / 32768)) chunks of ceil(n / c)
+ * elements, sums each chunk with the row cascade into its own slot of a
+ * `threads`-long zero buffer, and reduces that buffer with the row cascade.
+ * The output starts at 0 and accumulates (0 + sum). */
+float oracle_sum_1d_f32(const float *x, int64_t n, int threads) {
+    const int64_t grain = 32768;
+    if (n < grain || threads <= 1) return 0.0f + oracle_row_sum_f32(x, n);
+    int64_t chunks = (n + grain - 1) / grain;
+    if (chunks > threads) chunks = threads;
+    const int64_t size = (n + chunks - 1) / chunks;
+    float buf[1024];
+    if (threads > 1024) return NAN;
+    for (int i = 0; i < threads; ++i) buf[i] = 0.0f;
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int64_t b = c * size;
+        if (b >= n) break;
+        const int64_t e = b + size < n ? b + size : n;
+        buf[c] = 0.0f + oracle_row_sum_f32(x + b, e - b);
+    }
+    return 0.0f + oracle_row_sum_f32(buf, threads);
 }
 
 void oracle_row_sums_f32(const float *x, int64_t rows, int64_t n, float *out) {

@@ -22,6 +22,8 @@ def _load():
             build()
         lib = ctypes.CDLL(_LIB)
         lib.oracle_row_sums_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+        lib.oracle_sum_1d_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+        lib.oracle_sum_1d_f32.restype = ctypes.c_float
         lib.oracle_categorical_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         _lib = lib
@@ -34,6 +36,12 @@ def row_sums(x):
     out = np.empty(x.shape[0], dtype=np.float32)
     _load().oracle_row_sums_f32(x.ctypes.data, x.shape[0], x.shape[1], out.ctypes.data)
     return out
+
+
+def sum_1d(x, threads):
+    """fp32 ``x.sum()`` of a 1-D array as torch-CPU computes it with ``threads`` threads."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return np.float32(_load().oracle_sum_1d_f32(x.ctypes.data, x.shape[0], int(threads)))
 
 
 def categorical(w, u):

@@ -210,3 +210,63 @@ def plan_random_rows(temperatures, token_counts, num_speculative_tokens):
     verify_ranks = np.repeat(np.arange(len(requests)), rc)
     verify_offsets = np.concatenate([np.arange(c) for c in rc])
     return requests, verify_rows, verify_ranks, verify_offsets
+
+
+def rejection_sample(candidate, target, proposal, generator):
+    """One draft of the synchronous runner, on whatever device the rows live.
+
+    reference: vllm_rlt/worker/speculative.py:56-72 (Sampler.draw:
+    vllm_rlt/worker/sampler.py:57-60).
+    """
+    mass = proposal[candidate]
+    if not bool(mass > 0):
+        raise ValueError("candidate has zero proposal probability")
+    uniform = torch.rand((), device=target.device, generator=generator)
+    if bool(uniform * mass < target[candidate]):
+        return candidate, True
+    residual = (target - proposal).clamp_min(0)
+    total = residual.sum()
+    if not bool(torch.isfinite(total) & (total > 0)):
+        raise RuntimeError("invalid speculative residual probability mass")
+    return int(torch.multinomial(residual / total, 1, generator=generator).squeeze(0).item()), False
+
+
+def rejection_step(candidate, target, proposal, uniform):
+    """The same decision with the uniform given: ``(accepted, normalized residual or None)``.
+
+    Raises as the reference raises.  CPU float32 rows; the residual total is torch's
+    ``residual.sum()`` on this process's threads.
+    """
+    mass = proposal[candidate]
+    if not bool(mass > 0):
+        raise ValueError("candidate has zero proposal probability")
+    if bool(uniform * mass < target[candidate]):
+        return True, None
+    residual = (target - proposal).clamp_min(0)
+    total = residual.sum()
+    if not bool(torch.isfinite(total) & (total > 0)):
+        raise RuntimeError("invalid speculative residual probability mass")
+    return False, residual / total
+
+
+def collect_stochastic(candidates, target, proposal, generators):
+    """The random-request branch of the synchronous round, request by request.
+
+    reference: vllm_rlt/worker/speculative.py:601-624 (``_collect_round``); ``target[i]``
+    holds request i's verify-row distributions (row ``len(candidates[i])`` is the bonus
+    row), ``proposal[i]`` its draft distributions.
+    """
+    results = []
+    for i, cands in enumerate(candidates):
+        tokens, accepted = [], 0
+        for offset, cand in enumerate(cands):
+            token, ok = rejection_sample(cand, target[i, offset], proposal[i, offset], generators[i])
+            tokens.append(token)
+            if not ok:
+                break
+            accepted += 1
+        else:
+            tokens.append(int(torch.multinomial(target[i, len(cands)], 1,
+                                                generator=generators[i]).squeeze(0).item()))
+        results.append((tokens, accepted))
+    return results

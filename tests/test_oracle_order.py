@@ -103,3 +103,30 @@ def test_import_guard_fixture_matches_torch_and_the_model(pkg):
         x = sampling.order_fixture(vocab)[None]
         got = order.row_sums(x)
         assert (int(got.view(np.int32)[0]) & 0xFFFFFFFF) == bits, vocab
+
+
+@pytest.mark.parametrize("threads", [1, 2, 3, 5, 8])
+def test_sum_1d_model_matches_torch_cpu_bitwise(threads):
+    """``x.sum()`` of a whole 1-D tensor (the residual total of the synchronous runner,
+    vllm_rlt/worker/speculative.py:66): serial below 32768 elements, else thread chunks."""
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        for V in (100, 32767, 32768, 32769, 49152, 65536, 65537, 151936, 300001):
+            g = torch.Generator().manual_seed(V + threads)
+            x = torch.rand(V, generator=g) ** 8
+            want = x.sum()
+            got = order.sum_1d(x.numpy(), threads)
+            assert np.float32(want.item()).view(np.int32) == got.view(np.int32), V
+    finally:
+        torch.set_num_threads(prev)
+
+
+def test_sum_1d_thread_chunks_change_the_bits():
+    """The chunked order is not the row order: the model would catch a dropped chunking."""
+    g = torch.Generator().manual_seed(5)
+    differ = 0
+    for _ in range(20):
+        x = (torch.rand(151936, generator=g) ** 8).numpy()
+        differ += order.sum_1d(x, 8).view(np.int32) != order.sum_1d(x, 1).view(np.int32)
+    assert differ > 0

@@ -3,6 +3,7 @@
 import types
 
 import pytest
+import numpy as np
 import torch
 
 from oracle import sampling as osamp
@@ -147,3 +148,52 @@ def test_accept_shape_errors():
                                  torch.zeros(2, 3, 4), torch.zeros(2, 4, 4), torch.zeros(2, 3), torch.zeros(2))
     with pytest.raises(ValueError):
         osamp.categorical(torch.zeros(3), torch.zeros(3))
+
+
+# ------------------------------------------------ synchronous runner's rejection sampling
+
+@pytest.mark.parametrize("p,q", [
+    ([0.1, 0.6, 0.3], [0.7, 0.2, 0.1]),
+    ([0.0, 1.0, 0.0], [1.0, 0.0, 0.0]),
+    ([0.2, 0.3, 0.5], [0.2, 0.3, 0.5]),
+])
+def test_rejection_sample_recovers_target_distribution(p, q):
+    # reference known answer: tests/test_speculative.py:455-471
+    p, q = torch.tensor(p), torch.tensor(q)
+    g = torch.Generator().manual_seed(431)
+    counts = torch.zeros(3)
+    for _ in range(12000):
+        candidate = int(torch.multinomial(q, 1, generator=g))
+        token, _ = osamp.rejection_sample(candidate, p, q, g)
+        counts[token] += 1
+    torch.testing.assert_close(counts / counts.sum(), p, atol=0.016, rtol=0)
+
+
+def test_rejection_step_closed_form_and_errors():
+    p = torch.tensor([0.1, 0.6, 0.3])
+    q = torch.tensor([0.7, 0.2, 0.1])
+    assert osamp.rejection_step(1, p, q, torch.tensor(0.99))[0]  # p >= q: always accepted
+    ok, r = osamp.rejection_step(0, p, q, torch.tensor(0.5))  # 0.35 >= 0.1: rejected
+    assert not ok
+    p32, q32 = p.numpy(), q.numpy()
+    diff = np.maximum(p32 - q32, np.float32(0))
+    want = diff / ((diff[0] + diff[1]) + diff[2])
+    assert np.array_equal(r.numpy(), want)
+    with pytest.raises(ValueError):
+        osamp.rejection_step(0, p, torch.tensor([0.0, 0.5, 0.5]), torch.tensor(0.1))
+    with pytest.raises(RuntimeError):
+        osamp.rejection_step(0, torch.tensor([0.1, float("nan"), 0.3]), q, torch.tensor(0.5))
+
+
+def test_collect_stochastic_consumes_the_generator_like_the_loop():
+    """One uniform per examined draft, then one multinomial draw: the generator of a
+    request that accepts everything advances by K uniforms and the bonus draw."""
+    p = torch.tensor([[[0.0, 1.0], [0.0, 1.0], [0.5, 0.5]]])
+    q = torch.tensor([[[0.0, 1.0], [0.0, 1.0]]])
+    g = torch.Generator().manual_seed(3)
+    res = osamp.collect_stochastic([[1, 1]], p, q, [g])
+    assert res[0][1] == 2 and res[0][0][:2] == [1, 1]
+    h = torch.Generator().manual_seed(3)
+    torch.rand((), generator=h), torch.rand((), generator=h)
+    torch.multinomial(p[0, 2], 1, generator=h)
+    assert torch.equal(g.get_state(), h.get_state())

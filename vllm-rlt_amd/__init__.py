@@ -9,7 +9,9 @@ Drop-in host layer over ``librlt_mi355x.so`` (hand-written gfx950 HIP kernels):
 * ``sampling``: ``batched_probabilities``, ``categorical``, ``speculative_accept`` /
   ``AcceptResult``, ``greedy_accept`` and the device greedy round
   ``greedy_accept_batched`` (vllm_rlt/worker/speculative_sampling.py,
-  vllm_rlt/worker/speculative.py:41-53, vllm_rlt/worker/async_speculative.py:706-720).
+  vllm_rlt/worker/speculative.py:41-53, vllm_rlt/worker/async_speculative.py:706-720),
+  and the synchronous runner's ``rejection_sample`` / ``rejection_round``
+  (vllm_rlt/worker/speculative.py:56-72,574-625).
 * ``kv_write``: ``store_kv``, ``masked_kv_store``, ``write_graph_kv``, ``store_fp8`` and
   ``finalize_rows``, the KV writers the verify window's keys and values go through
   (vllm_rlt/kernels/routing.py:147-223, vllm_rlt/kernels/graph_kv.py:52-67,
@@ -40,6 +42,9 @@ from .sampling import (  # noqa: F401
     merge_random_round,
     propose_drafts,
     RandomRoundMerge,
+    rejection_round,
+    rejection_rows,
+    rejection_sample,
     speculative_accept,
     verify_accept,
     verify_distributions,

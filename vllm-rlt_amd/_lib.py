@@ -70,6 +70,9 @@ _SIGNATURES = {
     "rlt_speculative_accept_noalloc_max_bytes": (_sz, []),
     "rlt_speculative_accept_noalloc": (ctypes.c_int, [
         _p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _p, _p, _p, _p, _p]),
+    "rlt_rejection_sample_workspace_size": (_sz, [_i64, _i64, _i32]),
+    "rlt_rejection_sample": (ctypes.c_int, [
+        _p, _p, _p, _p, _p, _i64, _i32, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
     "rlt_categorical_workspace_size": (_sz, [_i64, _i64]),
     "rlt_categorical": (ctypes.c_int, [_p, _p, _i64, _i64, _p, _p, _p, _sz, _p]),
     "rlt_row_mass_workspace_size": (_sz, [_i64, _i64]),

@@ -1130,3 +1130,246 @@ int rlt_merge_random_round(const int64_t* target, int64_t num_rows, const int64_
 }
 
 }  // extern "C"
+
+// ============================================================ sync-mode rejection
+
+// Per-token rejection sampling of the synchronous runner
+// (vllm_rlt/worker/speculative.py:56-72 rejection_sample, driven by _collect_round
+// :574-625), for a batch of requests in three launches:
+//
+//  1. rlt_reject_chain_kernel -- grid (n, tiles): every workgroup walks its
+//     request's drafts in order (candidate range, q[x] > 0, u * q[x] < p[x]) up to
+//     the first event, and on a rejection writes its tile of the residual
+//     clamp_min(p - q, 0) of that draft's rows; tile 0 records the event.
+//  2. rlt_reject_groups_kernel -- grid (groups, chunks, n): the float32 cascade
+//     partials of the residual rows, per summation chunk.
+//  3. rlt_reject_scale_kernel -- grid (n, tiles): the residual total in torch's
+//     order for a whole 1-D tensor (`residual.sum()`), its validity, and the
+//     residual divided by it; tile 0 writes status and accepted.
+//
+// torch sums a contiguous 1-D float32 tensor serially (the row cascade) when it
+// has fewer than 32768 elements or runs on one thread; otherwise in
+// c = min(threads, ceil(V / 32768)) chunks of ceil(V / c), each summed with the
+// row cascade into a `threads`-long zero buffer that is then summed the same way.
+
+namespace {
+
+constexpr int kRejThreads = 256;
+constexpr int kRejTile = kRejThreads * 4;  // residual elements per workgroup
+constexpr int64_t kSumGrain = 32768;
+constexpr int kMaxSumThreads = 256;
+
+enum RejectStatus : int32_t {
+  kRejAllAccepted = 0,  // every draft accepted: the bonus comes from p[count]
+  kRejRejected = 1,     // rejected at `accepted`: the residual row is normalized
+  kRejZeroMass = 2,     // q[x] is not > 0 at `accepted` (the reference raises ValueError)
+  kRejBadResidual = 3,  // residual total not finite and > 0 (RuntimeError)
+  kRejBadToken = 4,     // candidate outside [-V, V) at `accepted` (IndexError)
+};
+
+struct RejectState {
+  int32_t status;
+  int32_t s;  // drafts accepted before the event
+};
+
+struct SumGeom {
+  int64_t chunks, size;  // summation chunks of the row and their length
+};
+
+SumGeom sum_geom(int64_t V, int threads) {
+  SumGeom g;
+  if (V < kSumGrain || threads <= 1) {
+    g.chunks = 1;
+    g.size = V;
+  } else {
+    g.chunks = min((V + kSumGrain - 1) / kSumGrain, (int64_t)threads);
+    g.size = (V + g.chunks - 1) / g.chunks;
+  }
+  return g;
+}
+
+// The reference's draft loop for request i up to its first event.
+__device__ RejectState reject_chain(const int64_t* cand, int64_t K, int64_t d, const float* p,
+                                    const float* q, const float* u, int64_t i, int64_t V) {
+  RejectState r;
+  for (int64_t j = 0; j < d; ++j) {
+    const int64_t c = cand[i * K + j];
+    r.s = (int32_t)j;
+    if (c < -V || c >= V) {
+      r.status = kRejBadToken;
+      return r;
+    }
+    const int64_t x = c < 0 ? c + V : c;
+    const float mass = q[(i * K + j) * V + x];
+    if (!(mass > 0.f)) {
+      r.status = kRejZeroMass;
+      return r;
+    }
+    const float prod = u[i * K + j] * mass;
+    if (!(prod < p[(i * (K + 1) + j) * V + x])) {
+      r.status = kRejRejected;
+      return r;
+    }
+  }
+  r.status = kRejAllAccepted;
+  r.s = (int32_t)d;
+  return r;
+}
+
+__global__ __launch_bounds__(kRejThreads) void rlt_reject_chain_kernel(
+    const int64_t* __restrict__ cand, const int64_t* __restrict__ counts, const float* __restrict__ p,
+    const float* __restrict__ q, const float* __restrict__ u, int64_t K, int64_t V,
+    float* __restrict__ residual, RejectState* __restrict__ state) {
+  __shared__ RejectState sh;
+  const int64_t i = blockIdx.x;
+  if (threadIdx.x == 0) {
+    const int64_t dc = counts[i];
+    sh = reject_chain(cand, K, dc < 0 ? 0 : (dc > K ? K : dc), p, q, u, i, V);
+    if (blockIdx.y == 0) state[i] = sh;
+  }
+  __syncthreads();
+  if (sh.status != kRejRejected) return;
+  const float* pr = p + (i * (K + 1) + sh.s) * V;
+  const float* qr = q + (i * K + sh.s) * V;
+  float* out = residual + i * V;
+  const int64_t base = (int64_t)blockIdx.y * kRejTile;
+  for (int e = threadIdx.x; e < kRejTile; e += kRejThreads) {
+    const int64_t k = base + e;
+    if (k < V) {
+      const float r = pr[k] - qr[k];
+      out[k] = r < 0.f ? 0.f : r;  // clamp_min(0): NaN stays NaN
+    }
+  }
+}
+
+// grid (groups of the longest chunk, chunks, n), 128 threads.
+template <bool kVec4>
+__global__ __launch_bounds__(128) void rlt_reject_groups_kernel(
+    const float* __restrict__ residual, const RejectState* __restrict__ state, int64_t V,
+    int64_t size, int64_t gmax, float* __restrict__ partials) {
+  __shared__ cascade::ChunkSums chunk_sum;
+  const int64_t i = blockIdx.z, c = blockIdx.y, g = blockIdx.x;
+  if (state[i].status != kRejRejected) return;
+  const int64_t b = c * size;
+  const int64_t len = min(size, V - b);
+  const RowGeom geo = row_geom(len);
+  if (g >= geo.groups) return;
+  const int t = threadIdx.x;
+  cascade::group_chunk_sums<kVec4>(residual + i * V + b, g, geo.full_chunks, t, chunk_sum);
+  __syncthreads();
+  cascade::group_stream_sums(g, geo.full_chunks, t, chunk_sum,
+                             partials + ((i * gridDim.y + c) * gmax + g) * kStreams);
+}
+
+__global__ __launch_bounds__(kRejThreads) void rlt_reject_scale_kernel(
+    float* __restrict__ residual, const RejectState* __restrict__ state, int64_t V, int64_t chunks,
+    int64_t size, int64_t gmax, const float* __restrict__ partials, int threads,
+    int32_t* __restrict__ status_out, int64_t* __restrict__ accepted_out) {
+  __shared__ float buf[kMaxSumThreads];
+  __shared__ float total_sh;
+  const int64_t i = blockIdx.x;
+  const RejectState st = state[i];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  if (st.status != kRejRejected) {
+    if (blockIdx.y == 0 && t == 0) {
+      status_out[i] = st.status;
+      accepted_out[i] = st.s;
+    }
+    return;
+  }
+  float* row = residual + i * V;
+  const float* part = partials + i * chunks * gmax * kStreams;
+  if (chunks == 1) {
+    if (wave == 0) {
+      const float s = rlt_row_mass_finish(row, V, row_geom(V).groups > 0 ? part : nullptr);
+      if (lane == 0) total_sh = 0.f + s;
+    }
+  } else {
+    for (int c = t; c < threads; c += kRejThreads) buf[c] = 0.f;
+    __syncthreads();
+    for (int64_t c = wave; c < chunks; c += kRejThreads / 64) {
+      const int64_t b = c * size;
+      const int64_t len = min(size, V - b);
+      const float s = rlt_row_mass_finish(row + b, len,
+                                          row_geom(len).groups > 0 ? part + c * gmax * kStreams : nullptr);
+      if (lane == 0) buf[c] = 0.f + s;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const float s = rlt_row_mass_finish(buf, threads, nullptr);
+      if (lane == 0) total_sh = 0.f + s;
+    }
+  }
+  __syncthreads();
+  const float total = total_sh;
+  const bool ok = isfinite(total) && total > 0.f;
+  if (blockIdx.y == 0 && t == 0) {
+    status_out[i] = ok ? kRejRejected : kRejBadResidual;
+    accepted_out[i] = st.s;
+  }
+  const int64_t base = (int64_t)blockIdx.y * kRejTile;
+  for (int e = t; e < kRejTile; e += kRejThreads) {
+    const int64_t k = base + e;
+    if (k < V) row[k] = __fdiv_rn(row[k], total);
+  }
+}
+
+struct RejectLayout {
+  size_t state, partials, total;
+};
+
+RejectLayout reject_layout(int64_t n, int64_t V, int threads) {
+  const SumGeom sg = sum_geom(V, threads);
+  const int64_t gmax = row_geom(sg.size).groups;
+  RejectLayout l;
+  l.state = 0;
+  size_t off = rlt_align_up(sizeof(RejectState) * n, 256);
+  l.partials = off;
+  off = rlt_align_up(off + sizeof(float) * n * sg.chunks * gmax * kStreams, 256);
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t rlt_rejection_sample_workspace_size(int64_t n, int64_t vocab, int32_t sum_threads) {
+  return reject_layout(n, vocab, sum_threads).total;
+}
+
+int rlt_rejection_sample(const int64_t* candidates, const int64_t* counts, const float* target,
+                         const float* proposal, const float* uniforms, int64_t n, int32_t k,
+                         int64_t vocab, int32_t sum_threads, int32_t* status, int64_t* accepted,
+                         float* residual, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  if (n < 0 || k < 0 || vocab < 1 || sum_threads < 1) return RLT_ERR_ARGUMENT;
+  if (sum_threads > kMaxSumThreads || vocab >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
+  if (n == 0) return RLT_OK;
+  const RejectLayout l = reject_layout(n, vocab, sum_threads);
+  if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
+  const int64_t tiles = (vocab + kRejTile - 1) / kRejTile;
+  if (n >= ((int64_t)1 << 31) || tiles > 65535) return RLT_ERR_UNSUPPORTED;
+  RejectState* state = (RejectState*)((char*)workspace + l.state);
+  float* partials = (float*)((char*)workspace + l.partials);
+  const SumGeom sg = sum_geom(vocab, sum_threads);
+  const int64_t gmax = row_geom(sg.size).groups;
+  rlt_reject_chain_kernel<<<dim3((unsigned)n, (unsigned)tiles), kRejThreads, 0, stream>>>(
+      candidates, counts, target, proposal, uniforms, k, vocab, residual, state);
+  if (gmax > 0) {
+    if (n > 65535) return RLT_ERR_UNSUPPORTED;  // grid.z
+    const dim3 grid((unsigned)gmax, (unsigned)sg.chunks, (unsigned)n);
+    const bool vec = vocab % 4 == 0 && sg.size % 4 == 0 && (uintptr_t)residual % 16 == 0;
+    if (vec)
+      rlt_reject_groups_kernel<true><<<grid, 128, 0, stream>>>(residual, state, vocab, sg.size,
+                                                               gmax, partials);
+    else
+      rlt_reject_groups_kernel<false><<<grid, 128, 0, stream>>>(residual, state, vocab, sg.size,
+                                                                gmax, partials);
+  }
+  rlt_reject_scale_kernel<<<dim3((unsigned)n, (unsigned)tiles), kRejThreads, 0, stream>>>(
+      residual, state, vocab, sg.chunks, sg.size, gmax, partials, sum_threads, status, accepted);
+  return rlt_launch_status();
+}
+
+}  // extern "C"

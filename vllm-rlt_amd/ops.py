@@ -179,6 +179,23 @@ def _(target, accepted, next_tokens, starts, input_tokens, tokens, result_accept
             starts.new_empty((n,), **i64), starts.new_empty((n,), **i64),
             starts.new_empty((n, 2), **i64), starts.new_empty((n,), **i64))
 
+@torch.library.custom_op("rlt_mi355x::rejection_rows", mutates_args=(), device_types="cuda")
+def rejection_rows(candidates: torch.Tensor, counts: torch.Tensor, target: torch.Tensor,
+                   proposal: torch.Tensor, uniforms: torch.Tensor,
+                   sum_threads: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """reference: vllm_rlt/worker/speculative.py:56-72 rejection_sample (device part)."""
+    return _samp.rejection_rows(candidates, counts, target, proposal, uniforms,
+                                sum_threads=sum_threads)
+
+
+@rejection_rows.register_fake
+def _(candidates, counts, target, proposal, uniforms, sum_threads):
+    n = candidates.shape[0]
+    return (candidates.new_empty((n,), dtype=torch.int32),
+            candidates.new_empty((n,), dtype=torch.int64),
+            target.new_empty((n, target.shape[-1]), dtype=torch.float32))
+
+
 @torch.library.custom_op("rlt_mi355x::store_kv", mutates_args=("key_cache", "value_cache"),
                          device_types="cuda")
 def store_kv(key_cache: torch.Tensor, value_cache: torch.Tensor, k: torch.Tensor,
@@ -209,5 +226,6 @@ def finalize_rows(descriptor: torch.Tensor, tables: torch.Tensor, key_pool: torc
 
 
 OPS = ("paged_attention", "spec_probs", "categorical", "spec_accept", "greedy_accept",
-       "propose_drafts", "verify_distributions", "verify_accept", "merge_random_round", "store_kv",
+       "propose_drafts", "verify_distributions", "verify_accept", "merge_random_round",
+       "rejection_rows", "store_kv",
        "store_fp8", "finalize_rows")

@@ -368,6 +368,165 @@ def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts
     return target, p, AcceptResult(tokens, accepted, final, error)
 
 
+# ------------------------------------------------------------ sync-mode rejection
+
+REJECT_ALL_ACCEPTED, REJECT_REJECTED, REJECT_ZERO_MASS, REJECT_BAD_RESIDUAL, REJECT_BAD_TOKEN = range(5)
+
+
+def rejection_rows(candidates, counts, target, proposal, uniforms, *, sum_threads=None):
+    """Device part of sync-mode rejection sampling for a batch: ``(status int32 [n],
+    accepted int64 [n], residual float32 [n, V])``.
+
+    reference: vllm_rlt/worker/speculative.py:56-72 (``rejection_sample``) as
+    ``_collect_round`` (:574-625) applies it draft after draft.  ``candidates`` int64
+    ``[n, K]``, ``counts`` ``[n]`` (drafts per request), ``target`` float32
+    ``[n, K + 1, V]``, ``proposal`` ``[n, K, V]``, ``uniforms`` ``[n, K]``.  Status:
+    0 all drafts accepted, 1 rejected at ``accepted`` (``residual`` row = the normalized
+    residual), 2 zero proposal mass, 3 invalid residual mass, 4 candidate out of range.
+    The residual total follows torch's CPU order for ``residual.sum()`` with
+    ``sum_threads`` threads (default ``torch.get_num_threads()``).
+    """
+    if candidates.ndim != 2:
+        raise ValueError("candidates must be [n, K]")
+    n, k = candidates.shape
+    if target.ndim != 3 or target.shape[:2] != (n, k + 1):
+        raise ValueError("target must be [n, K + 1, V]")
+    vocab = target.shape[-1]
+    if proposal.shape != (n, k, vocab) or uniforms.shape != (n, k) or counts.shape != (n,):
+        raise ValueError("proposal must be [n, K, V], uniforms [n, K] and counts [n]")
+    return _launch_rejection(candidates, counts, target, proposal, uniforms, k, sum_threads)
+
+
+def _launch_rejection(candidates, counts, target, proposal, uniforms, k, sum_threads):
+    """rlt_rejection_sample on rows whose layout the caller has checked (target rows
+    j > count of a request are never read, so one verified draft may pass a [1, 1, V]
+    target)."""
+    n, vocab = candidates.shape[0], target.shape[-1]
+    threads = int(torch.get_num_threads() if sum_threads is None else sum_threads)
+    _lib.require_gpu(candidates, counts, target, proposal, uniforms)
+    device = target.device
+    status = torch.empty(n, dtype=torch.int32, device=device)
+    accepted = torch.empty(n, dtype=torch.int64, device=device)
+    residual = torch.empty((n, vocab), dtype=torch.float32, device=device)
+    if n == 0:
+        return status, accepted, residual
+    lib = _lib.library()
+    ws = _lib.workspace(lib.rlt_rejection_sample_workspace_size(n, vocab, threads), device)
+    st = lib.rlt_rejection_sample(
+        _lib.ptr(_i64(candidates)), _lib.ptr(_i64(counts)), _lib.ptr(_f32(target)),
+        _lib.ptr(_f32(proposal)), _lib.ptr(_f32(uniforms)), n, k, vocab, threads,
+        _lib.ptr(status), _lib.ptr(accepted), _lib.ptr(residual), _lib.ptr(ws), ws.numel(),
+        _lib.stream_of(device))
+    _lib.check(st, "rlt_rejection_sample")
+    return status, accepted, residual
+
+
+def _raise_for(status, what=""):
+    if status == REJECT_ZERO_MASS:
+        raise ValueError("candidate has zero proposal probability" + what)
+    if status == REJECT_BAD_TOKEN:
+        raise IndexError("candidate is outside the vocabulary" + what)
+    if status == REJECT_BAD_RESIDUAL:
+        raise RuntimeError("invalid speculative residual probability mass" + what)
+
+
+def rejection_sample(candidate, target, proposal, generator):
+    """Return ``(token, accepted)`` for one draft; reference:
+    vllm_rlt/worker/speculative.py:56-72.
+
+    ``target`` / ``proposal`` are the normalized float32 ``[V]`` rows of p and q on the
+    device, ``generator`` the request's generator on that device.  The generator is
+    consumed exactly as the reference consumes it: one ``torch.rand(())`` unless the
+    candidate has no proposal mass, then one ``torch.multinomial`` draw on a rejection.
+    One host read of the outcome instead of the reference's three to four.
+    """
+    device = target.device
+    vocab = target.shape[-1]
+    if target.shape != (vocab,) or proposal.shape != (vocab,):
+        raise ValueError("target and proposal must be [V] rows")
+    before = generator.get_state()
+    u = torch.rand((), device=device, generator=generator)
+    cand = torch.tensor([[int(candidate)]], dtype=torch.int64).to(device, non_blocking=True)
+    counts = torch.ones(1, dtype=torch.int64, device=device)
+    # one draft: row 0 of the target is all the kernel reads
+    status, _, residual = _launch_rejection(cand, counts, target.view(1, 1, vocab),
+                                            proposal.view(1, 1, vocab), u.view(1, 1), 1, None)
+    code = int(status[0])
+    if code in (REJECT_ZERO_MASS, REJECT_BAD_TOKEN):
+        generator.set_state(before)  # the reference raises before drawing u
+    _raise_for(code)
+    if code == REJECT_ALL_ACCEPTED:
+        return candidate, True
+    return int(torch.multinomial(residual[0], 1, generator=generator).squeeze(0).item()), False
+
+
+def rejection_round(candidates, target, proposal, generators, *, sum_threads=None):
+    """The stochastic branch of the synchronous runner's round for a batch of requests:
+    a list of ``(tokens, accepted)`` per request.
+
+    reference: vllm_rlt/worker/speculative.py:574-625 (``_collect_round``, requests with
+    temperature > 0).  ``candidates[i]``: request i's draft ids (host ints, at most K);
+    ``target`` float32 ``[n, K + 1, V]``: p of each verify row (row ``len(candidates[i])``
+    is the bonus row); ``proposal`` ``[n, K, V]``: the draft distributions q;
+    ``generators[i]``: request i's generator on the device.  Every generator ends in the
+    state the reference leaves it in and every token equals the reference's given the
+    same p and q rows: each request's uniforms are drawn in the reference's order before
+    one batched launch decides every request, and the generator is then rewound to just
+    after the uniforms the reference would have drawn before its residual or bonus
+    ``torch.multinomial``.  Errors are raised as the reference raises them, for the
+    first failing request, with the generators of later requests untouched.  Requests
+    must have distinct generators (a shared one is handled one request at a time).
+    """
+    n = len(candidates)
+    if len(generators) != n or target.shape[0] != n or proposal.shape[0] != n:
+        raise ValueError("candidates, target, proposal and generators must cover n requests")
+    if len({id(g) for g in generators}) != n:
+        return [rejection_round([candidates[i]], target[i:i + 1], proposal[i:i + 1],
+                                [generators[i]], sum_threads=sum_threads)[0] for i in range(n)]
+    k = proposal.shape[1]
+    device = target.device
+    counts = [len(c) for c in candidates]
+    if any(c > k for c in counts):
+        raise ValueError("a request has more candidates than proposal rows")
+    states, uniforms = [], []
+    for gen, d in zip(generators, counts):
+        st = [gen.get_state()]
+        row = []
+        for _ in range(d):
+            row.append(torch.rand((), device=device, generator=gen))
+            st.append(gen.get_state())
+        row += [torch.zeros((), device=device)] * (k - d)
+        uniforms.append(torch.stack(row) if row else torch.zeros(0, device=device))
+        states.append(st)
+    u = torch.stack(uniforms) if n else torch.zeros((0, k), device=device)
+    cand = torch.tensor([c + [0] * (k - len(c)) for c in candidates], dtype=torch.int64)
+    cand = cand.view(n, k).to(device, non_blocking=True)
+    cnt = torch.tensor(counts, dtype=torch.int64).to(device, non_blocking=True)
+    status, accepted, residual = rejection_rows(cand, cnt, target, proposal, u,
+                                                sum_threads=sum_threads)
+    outcome = torch.stack((status.long(), accepted)).tolist()  # the one host read
+    draws = []
+    for i, gen in enumerate(generators):
+        code, a = outcome[0][i], outcome[1][i]
+        if code != REJECT_ALL_ACCEPTED and code != REJECT_REJECTED:
+            consumed = a + 1 if code == REJECT_BAD_RESIDUAL else a
+            gen.set_state(states[i][consumed])
+            for j in range(i + 1, n):
+                generators[j].set_state(states[j][0])
+            _raise_for(code, f" (request {i}, draft {a})")
+        if code == REJECT_REJECTED:
+            gen.set_state(states[i][a + 1])
+            draws.append(torch.multinomial(residual[i], 1, generator=gen))
+        else:
+            draws.append(torch.multinomial(target[i, counts[i]], 1, generator=gen))
+    drawn = torch.cat(draws).tolist() if draws else []
+    results = []
+    for i in range(n):
+        a = outcome[1][i]
+        results.append((list(candidates[i][:a]) + [int(drawn[i])], a))
+    return results
+
+
 def row_mass(x):
     """``x.sum(-1, dtype=float32)`` of a 2-D fp32 tensor in torch-CPU summation order."""
     if x.ndim != 2:
