@@ -150,22 +150,7 @@ def config2_decode(pkg, dev):
     q = torch.randn(n, h, d, generator=gd, device=dev, dtype=torch.bfloat16)
     ctx = lengths.int().to(dev)
     kern = pkg.MI355XPagedAttention()
-    for _ in range(3):
-        kern(q, k, v, rows, ctx)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(10):
-            kern(q, k, v, rows, ctx)
-    graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(5):
-        graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    t = a.elapsed_time(b) / 50 / 1e3
+    t, _ = _graph_time(lambda: kern(q, k, v, rows, ctx))
     nbytes = int(lengths.sum()) * 2 * h * d * 2 + 2 * n * h * d * 2 + int(
         sum(math.ceil(int(x) / bs) for x in lengths)) * 4
     return {"workload": "config2 decode attention: batch 64, ctx U[512,4096], 16/16 heads, D=128, "
@@ -174,9 +159,9 @@ def config2_decode(pkg, dev):
             "GBps": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
 
 
-def _graph_time(fn, reps=3, per_graph=10):
-    """Average launch time of ``fn`` replayed from a HIP graph of ``per_graph`` calls,
-    HIP events on the current stream, queue pre-filled."""
+def _graph_time(fn, reps=21, per_graph=10):
+    """Median launch time of ``fn`` over ``reps`` replays of a HIP graph of ``per_graph``
+    calls, HIP events on the current stream, queue pre-filled."""
     for _ in range(2):
         fn()
     torch.cuda.synchronize()
@@ -195,7 +180,8 @@ def _graph_time(fn, reps=3, per_graph=10):
         graph.replay()
         b.record(s)
     torch.cuda.synchronize()
-    t = sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3 / per_graph
+    times = sorted(a.elapsed_time(b) for a, b in ev)
+    t = times[len(times) // 2] / 1e3 / per_graph
     eager = fn()
     torch.cuda.synchronize()
     same = all(torch.equal(x, y) for x, y in zip(_flat(eager), _flat(out)))
@@ -338,10 +324,10 @@ def config5_step(pkg, dev, attention_only=False):
             kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sv, row_lengths=rlp)
         torch.cuda.synchronize()
         return {"only": "config5_attention", "launches": 4}
-    t_row, same_row = _graph_time(lambda: kern(q, kc, vc, rt, rl, sk, sv), reps=2, per_graph=4)
+    t_row, same_row = _graph_time(lambda: kern(q, kc, vc, rt, rl, sk, sv), reps=5, per_graph=4)
     t_attn, same_attn = _graph_time(
         lambda: kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sv, row_lengths=rlp),
-        reps=2, per_graph=4)
+        reps=5, per_graph=4)
     packed_equal = torch.equal(kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sv, row_lengths=rlp),
                                kern(q, kc, vc, rt, rl, sk, sv)[perm_d])
     a_bytes = _kv_bytes_distinct(row_tables, row_len, req, hkv, d, 1, bs) + 2 * n * w * hq * d * 2
@@ -485,8 +471,10 @@ def main():
     w = build_workload(dev)
     backend = pkg.create_backend("auto", dev, torch.bfloat16, w["d"], w["bs"])
     k = w["k"]
-    kc = w["key_pool"][:, w["layer"]]
-    vc = w["value_pool"][:, w["layer"]]
+    # Consecutive steps alternate between the pool's two layers (354 MB of KV each), so a
+    # step never finds the previous step's KV in the 256 MB MALL.
+    kcs = [w["key_pool"][:, layer] for layer in range(2)]
+    vcs = [w["value_pool"][:, layer] for layer in range(2)]
     tables, lengths, cu = w["tables"].to(dev), w["lengths"].int().to(dev), w["cu"].to(dev)
     u = w["u"].to(dev)
     ua, uf = u[:, k:2 * k].contiguous(), u[:, 2 * k].contiguous()
@@ -503,11 +491,12 @@ def main():
     top_p = torch.full((rows,), w["top_p"], device=dev)
     pbuf = {}
 
-    def kv_write():
-        pkg.store_kv(kc, vc, w["k_new"], w["v_new"], w["w_blocks"], w["w_offsets"])
+    def kv_write(layer=1):
+        pkg.store_kv(kcs[layer], vcs[layer], w["k_new"], w["v_new"], w["w_blocks"],
+                     w["w_offsets"])
 
-    def attn():
-        return backend.prefill(w["q"], kc, vc, tables, lengths, cu, w["window"])
+    def attn(layer=1):
+        return backend.prefill(w["q"], kcs[layer], vcs[layer], tables, lengths, cu, w["window"])
 
     all_rows = torch.arange(rows, device=dev)
 
@@ -530,9 +519,9 @@ def main():
         return pkg.verify_accept(logits3, temp, top_k, top_p, dt_tok, drafts, w["qprob"], ua, uf,
                                  max_top_k=0, apply_top_p=True)
 
-    def step():
-        kv_write()
-        attn()
+    def step(layer=1):
+        kv_write(layer)
+        attn(layer)
         verify()
 
     for _ in range(max(args.warmup, 1)):
@@ -551,11 +540,11 @@ def main():
     g_kv, g_attn, g_probs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     g_acc, g_step, g_ver = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_kv):
-        for _ in range(spg):
-            kv_write()
+        for i in range(spg):
+            kv_write(i % 2)
     with torch.cuda.graph(g_attn):
-        for _ in range(spg):
-            out_attn = attn()
+        for i in range(spg):
+            out_attn = attn(i % 2)
     with torch.cuda.graph(g_probs):
         for _ in range(spg):
             out_probs = probs()
@@ -566,8 +555,8 @@ def main():
         for _ in range(spg):
             out_ver = verify()
     with torch.cuda.graph(g_step):
-        for _ in range(spg):
-            step()
+        for i in range(spg):
+            step(i % 2)
     for _ in range(max(1, args.warmup // spg)):
         g_step.replay()
     torch.cuda.synchronize()
@@ -589,8 +578,9 @@ def main():
     torch.cuda.synchronize()
     step_s = (time.perf_counter() - t0) / steps
 
-    # ---- per-launch durations with HIP events on the launch stream, queue pre-filled
-    def launch_time(graph, reps):
+    # ---- per-launch durations with HIP events on the launch stream, queue pre-filled:
+    # the median over `reps` graph replays of spg launches each
+    def launch_time(graph, reps=50):
         s = torch.cuda.current_stream()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(reps)]
@@ -600,16 +590,17 @@ def main():
             graph.replay()
             b.record(s)
         torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in ev) / reps / 1e3 / spg
+        times = sorted(a.elapsed_time(b) for a, b in ev)
+        return times[len(times) // 2] / 1e3 / spg
 
-    t_kv = launch_time(g_kv, replays)
-    t_attn = launch_time(g_attn, replays)
-    t_probs = launch_time(g_probs, replays)
-    t_acc = launch_time(g_acc, replays)
-    t_ver = launch_time(g_ver, replays)
+    t_kv = launch_time(g_kv)
+    t_attn = launch_time(g_attn)
+    t_probs = launch_time(g_probs)
+    t_acc = launch_time(g_acc)
+    t_ver = launch_time(g_ver)
 
     # ---- correctness of the measured outputs against an eager run
-    eager_attn = attn()
+    eager_attn = attn((spg - 1) % 2)
     eager_probs = probs()
     eager_acc = accept()
     eager_ver = verify()
@@ -669,6 +660,8 @@ def main():
         "verify_accept_ms": round(t_ver * 1e3, 4),
         "merge_random_round_ms": round(t_merge * 1e3, 4),
         "steps_per_graph": spg,
+        "part_times": "median of 50 graph replays of steps_per_graph launches; steps and "
+                      "attention launches alternate between two 354 MB KV layers (> the 256 MB MALL)",
         "roofline": {
             "kernel": "attention launch (rlt_attn_mfma_kernel + rlt_merge_kernel)",
             "bound": "hbm",
