@@ -10,10 +10,24 @@ def test_operators_are_registered_with_reference_shaped_schemas(pkg):
     names = {op: str(getattr(torch.ops.rlt_mi355x, op).default._schema) for op in pkg.ops.OPS}
     assert "Tensor? cu_seqlens_q" in names["paged_attention"]
     assert names["spec_accept"].endswith("-> (Tensor, Tensor, Tensor, Tensor)")
-    assert "Tensor(a0!) key_cache" in names["store_kv"]
+    assert "!) key_cache" in names["store_kv"]
     assert "float? fixed_scale" in names["store_fp8"]
     assert "Tensor? row_lengths=None" in names["paged_attention"]
     assert names["merge_random_round"].endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+
+
+def test_per_step_operators_are_cpp(pkg):
+    """The per-step entry points are the C++ operators of _C.so (TORCH_LIBRARY in
+    csrc/torch_bindings.cpp), not Python custom ops."""
+    import os
+
+    from vllm_rlt_amd import _lib
+
+    assert os.path.exists(_lib.OPS_PATH)
+    for op in ("paged_attention", "store_kv", "spec_probs", "categorical", "spec_accept",
+               "greedy_accept", "verify_distributions", "verify_accept"):
+        kernels = torch._C._dispatch_dump(f"rlt_mi355x::{op}")
+        assert "CUDA: registered at" in kernels and "torch_bindings.cpp" in kernels, op
 
 
 def test_cpu_tensors_find_no_kernel(pkg):

@@ -1,6 +1,7 @@
-"""ctypes binding of librlt_mi355x.so (the C ABI declared in include/rlt_mi355x.h).
+"""ctypes binding of librlt_mi355x.so (the C ABI declared in include/rlt_mi355x.h),
+and the loader of the C++ torch operators over it (``_C.so``, ``ops()``).
 
-There is no fallback: if the library is missing or the device is not a ROCm
+There is no fallback: if a library is missing or the device is not a ROCm
 GPU, every op raises.  Build it with ``python vllm-rlt_amd/build.py`` (or
 ``__graft_entry__.build()``).
 """
@@ -12,6 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "librlt_mi355x.so")
+OPS_PATH = os.path.join(HERE, "_C.so")
 
 RLT_F32, RLT_F16, RLT_BF16, RLT_FP8_E4M3 = 0, 1, 2, 3
 _DTYPE_CODE = {
@@ -136,6 +138,24 @@ def library():
             fn.argtypes = args
         _lib = lib
     return _lib
+
+
+_ops_loaded = False
+
+
+def ops():
+    """``torch.ops.rlt_mi355x`` with the C++ operators of ``_C.so`` (csrc/torch_bindings.cpp)
+    registered; raise if the extension is absent."""
+    global _ops_loaded
+    if not _ops_loaded:
+        if not os.path.exists(OPS_PATH):
+            raise RuntimeError(
+                f"{OPS_PATH} is missing: build it with `python vllm-rlt_amd/build.py`; "
+                "there is no fallback implementation")
+        library()  # the C ABI it links against, from this directory
+        torch.ops.load_library(OPS_PATH)
+        _ops_loaded = True
+    return torch.ops.rlt_mi355x
 
 
 def dtype_code(dtype):

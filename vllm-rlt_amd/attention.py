@@ -7,8 +7,9 @@ protocol of vllm_rlt/kernels/paged_attention.py (``__call__`` / ``windowed`` /
 (vllm_rlt/core/kv_cache_manager.py:993-1018) and the graph-time call site
 (vllm_rlt/worker/cuda_graph.py:161-167) drive it unchanged.
 
-Every call launches the gfx950 kernels of librlt_mi355x.so on the current HIP
-stream: no host synchronization, no fallback, static grids (capturable in HIP
+Every call goes through the C++ operator ``torch.ops.rlt_mi355x.paged_attention``
+(csrc/torch_bindings.cpp), which launches the gfx950 kernels of librlt_mi355x.so
+on the current HIP stream: no host synchronization, no fallback, static grids (capturable in HIP
 graphs).  The per-row, windowed and packed forms share one kernel whose per-row
 arithmetic is independent of batch composition, which is why this backend can
 declare ``packed_matches_decode``.
@@ -85,22 +86,6 @@ MI355X_CAPABILITIES = BackendCapabilities(
 )
 
 
-def _scale_args(key_scale, value_scale):
-    """(mode, key ptr tensor, value ptr tensor, strides) of the FP8 scale arguments."""
-    if key_scale is None and value_scale is None:
-        return 0, None, None, (0, 0, 0)
-    if key_scale is None or value_scale is None:
-        raise ValueError("key_scale and value_scale must be given together")
-    for s in (key_scale, value_scale):
-        if s.dtype != torch.float32:
-            raise ValueError("FP8 scales must be float32")
-    if key_scale.dim() == 0 and value_scale.dim() == 0:
-        return 1, key_scale, value_scale, (0, 0, 0)
-    if key_scale.dim() != 3 or key_scale.stride() != value_scale.stride():
-        raise ValueError("per-vector FP8 scales must be [block, token, kv_head] views sharing strides")
-    return 2, key_scale, value_scale, tuple(key_scale.stride())
-
-
 class MI355XPagedAttention:
     """Split-KV paged GQA attention on gfx950 (per-row, windowed and packed forms)."""
 
@@ -112,71 +97,12 @@ class MI355XPagedAttention:
             raise ValueError("window must be a nonnegative integer")
         _lib.require_gpu(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
                          key_scale, value_scale, row_lengths)
-        if q.ndim != 3 or key_cache.ndim != 4 or value_cache.ndim != 4:
-            raise ValueError("q must be [rows, heads, dim] and caches [block, token, kv_head, dim]")
-        head_dim = q.shape[-1]
-        if head_dim > 256:
-            raise ValueError("the MI355X attention backend supports head_dim <= 256")
-        if key_cache.shape != value_cache.shape or key_cache.dtype != value_cache.dtype:
-            raise ValueError("key and value caches must share shape and dtype")
-        num_blocks, block_size, kv_heads, kdim = key_cache.shape
-        if kdim != head_dim or q.shape[1] % kv_heads:
-            raise ValueError("q heads must be a positive multiple of KV heads with equal head_dim")
-        if key_cache.stride(3) != 1 or value_cache.stride(3) != 1:
-            raise ValueError("paged attention requires a contiguous head dimension")
-        output = torch.empty_like(q)
-        rows = q.shape[0]
-        if rows == 0 or block_tables.shape[0] == 0:
-            return output
-        if q.stride(2) != 1:
-            q = q.contiguous()
-        mode, ks, vs, s_strides = _scale_args(key_scale, value_scale)
-        if key_cache.dtype == torch.float8_e4m3fn and mode == 0:
-            raise ValueError("an FP8 KV pool needs key_scale / value_scale")
-        tables = block_tables if block_tables.dtype == torch.int32 else block_tables.int()
-        lengths = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.int()
-        if tables.stride(1) != 1:
-            tables = tables.contiguous()
-        lengths = lengths.contiguous()
-        num_seqs = tables.shape[0]
-        if cu_seqlens_q is None:
-            if num_seqs != rows or lengths.shape[0] != rows:
-                raise ValueError("per-row attention needs one block table and length per q row")
-            cu = None
-            max_q = 1
-        else:
-            cu = cu_seqlens_q if cu_seqlens_q.dtype == torch.int32 else cu_seqlens_q.int()
-            cu = cu.contiguous()
-            if cu.shape[0] != num_seqs + 1 or lengths.shape[0] != num_seqs:
-                raise ValueError("cu_seqlens_q must be [sequences + 1] and lengths [sequences]")
-            max_q = int(max_seqlen_q)
-        if row_lengths is not None:
-            if cu_seqlens_q is None:
-                raise ValueError("row_lengths needs the packed form (cu_seqlens_q)")
-            if row_lengths.dim() != 1 or row_lengths.shape[0] != rows:
-                raise ValueError("row_lengths must be [q rows]")
-            row_lengths = (row_lengths if row_lengths.dtype == torch.int32
-                           else row_lengths.int()).contiguous()
-        lib = _lib.library()
-        heads = q.shape[1]
-        width = tables.shape[1]
-        nbytes = lib.rlt_paged_attention_workspace_size(rows, heads, head_dim, width, block_size)
-        ws = _lib.workspace(nbytes, q.device)
-        status = lib.rlt_paged_attention_rows(
-            _lib.ptr(q), q.stride(0), q.stride(1),
-            _lib.ptr(key_cache), _lib.ptr(value_cache),
-            key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
-            value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
-            num_blocks,
-            _lib.ptr(tables), tables.stride(0), width,
-            _lib.ptr(lengths), _lib.ptr(row_lengths), _lib.ptr(cu), num_seqs, max_q, rows,
-            _lib.ptr(ks), _lib.ptr(vs), mode, *s_strides,
-            heads, kv_heads, head_dim, block_size,
-            _lib.dtype_code(q.dtype), _lib.dtype_code(key_cache.dtype), window,
-            _lib.ptr(output), output.stride(0), output.stride(1),
-            _lib.ptr(ws), ws.numel(), _lib.stream_of(q.device))
-        _lib.check(status, "rlt_paged_attention")
-        return output
+        # argument checks, workspace and launch: torch.ops.rlt_mi355x.paged_attention
+        # (csrc/torch_bindings.cpp), ValueError on a bad argument
+        return _lib.ops().paged_attention(q, key_cache, value_cache, block_tables,
+                                          context_lengths, key_scale, value_scale, cu_seqlens_q,
+                                          int(max_seqlen_q) if cu_seqlens_q is not None else 1,
+                                          window, row_lengths)
 
     def __call__(self, q, key_cache, value_cache, block_tables, context_lengths,
                  key_scale=None, value_scale=None):

@@ -1,0 +1,438 @@
+// torch operators over the C ABI of librlt_mi355x.so: the hot-path entry points as
+// ``torch.ops.rlt_mi355x.<name>`` with a fixed schema and a ROCm (CUDA dispatch key)
+// implementation, the way the reference binds its native code
+// (csrc/torch_bindings.cpp:7-13: TORCH_LIBRARY schema + implementation).  Argument
+// checks raise ValueError (TORCH_CHECK_VALUE) with the Python wrappers' messages; a
+// kernel status other than RLT_OK raises RuntimeError.  Every operator launches on
+// the tensor device's current stream, allocates its workspace from torch's caching
+// allocator and never synchronizes the host.  Fake (shape) implementations are
+// registered from Python (vllm-rlt_amd/ops.py).
+
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <optional>
+#include <tuple>
+
+#include "rlt_mi355x.h"
+
+namespace {
+
+using at::Tensor;
+using OptTensor = std::optional<Tensor>;
+
+hipStream_t stream_of(const Tensor& t) {
+  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+void check_status(int status, const char* what) {
+  static const char* kNames[] = {"ok", "invalid argument", "unsupported configuration",
+                                 "workspace too small", "kernel launch failed"};
+  TORCH_CHECK(status == 0, what, ": ",
+              (status > 0 && status < 5) ? kNames[status] : "unknown status");
+}
+
+int32_t dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return 0;
+    case at::kHalf: return 1;
+    case at::kBFloat16: return 2;
+    case at::kFloat8_e4m3fn: return 3;
+    default: TORCH_CHECK_VALUE(false, "unsupported dtype ", t);
+  }
+  return -1;
+}
+
+Tensor workspace(size_t bytes, const Tensor& like) {
+  return at::empty({(int64_t)std::max<size_t>(bytes, 1)},
+                   like.options().dtype(at::kByte));
+}
+
+void* ptr(const Tensor& t) { return t.data_ptr(); }
+void* ptr(const OptTensor& t) { return t.has_value() ? t->data_ptr() : nullptr; }
+
+Tensor as(const Tensor& t, at::ScalarType dt) {
+  Tensor r = t.scalar_type() == dt ? t : t.to(dt);
+  return r.is_contiguous() ? r : r.contiguous();
+}
+
+bool logit_dtype(at::ScalarType t) {
+  return t == at::kFloat || t == at::kBFloat16 || t == at::kHalf;
+}
+
+// Rows with unit column stride (row stride free) in a supported logits dtype.
+Tensor logit_rows(const Tensor& t) {
+  Tensor r = logit_dtype(t.scalar_type()) ? t : t.to(at::kFloat);
+  return r.stride(-1) == 1 ? r : r.contiguous();
+}
+
+// ---------------------------------------------------------------- attention
+
+// reference: vllm_rlt/kernels/paged_attention.py:13-90 (per-row, windowed),
+// vllm_rlt/kernels/triton_attention.py:386-404 (packed window).
+Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& value_cache,
+                       const Tensor& block_tables, const Tensor& context_lengths,
+                       const OptTensor& key_scale, const OptTensor& value_scale,
+                       const OptTensor& cu_seqlens_q, int64_t max_seqlen_q, int64_t window,
+                       const OptTensor& row_lengths) {
+  TORCH_CHECK_VALUE(window >= 0, "window must be a nonnegative integer");
+  TORCH_CHECK_VALUE(q.dim() == 3 && key_cache.dim() == 4 && value_cache.dim() == 4,
+                    "q must be [rows, heads, dim] and caches [block, token, kv_head, dim]");
+  const int64_t head_dim = q.size(2);
+  TORCH_CHECK_VALUE(head_dim <= 256, "the MI355X attention backend supports head_dim <= 256");
+  TORCH_CHECK_VALUE(key_cache.sizes() == value_cache.sizes() &&
+                        key_cache.scalar_type() == value_cache.scalar_type(),
+                    "key and value caches must share shape and dtype");
+  const int64_t num_blocks = key_cache.size(0), block_size = key_cache.size(1);
+  const int64_t kv_heads = key_cache.size(2);
+  TORCH_CHECK_VALUE(key_cache.size(3) == head_dim && q.size(1) % kv_heads == 0,
+                    "q heads must be a positive multiple of KV heads with equal head_dim");
+  TORCH_CHECK_VALUE(key_cache.stride(3) == 1 && value_cache.stride(3) == 1,
+                    "paged attention requires a contiguous head dimension");
+  Tensor output = at::empty_like(q);
+  const int64_t rows = q.size(0);
+  if (rows == 0 || block_tables.size(0) == 0) return output;
+  const Tensor qq = q.stride(2) == 1 ? q : q.contiguous();
+  int32_t mode = 0;
+  int64_t s_strides[3] = {0, 0, 0};
+  TORCH_CHECK_VALUE(key_scale.has_value() == value_scale.has_value(),
+                    "key_scale and value_scale must be given together");
+  if (key_scale.has_value()) {
+    TORCH_CHECK_VALUE(key_scale->scalar_type() == at::kFloat &&
+                          value_scale->scalar_type() == at::kFloat,
+                      "FP8 scales must be float32");
+    if (key_scale->dim() == 0 && value_scale->dim() == 0) {
+      mode = 1;
+    } else {
+      TORCH_CHECK_VALUE(key_scale->dim() == 3 && key_scale->strides() == value_scale->strides(),
+                        "per-vector FP8 scales must be [block, token, kv_head] views sharing "
+                        "strides");
+      mode = 2;
+      for (int i = 0; i < 3; ++i) s_strides[i] = key_scale->stride(i);
+    }
+  }
+  TORCH_CHECK_VALUE(!(key_cache.scalar_type() == at::kFloat8_e4m3fn && mode == 0),
+                    "an FP8 KV pool needs key_scale / value_scale");
+  Tensor tables = block_tables.scalar_type() == at::kInt ? block_tables : block_tables.to(at::kInt);
+  if (tables.stride(1) != 1) tables = tables.contiguous();
+  const Tensor lengths = as(context_lengths, at::kInt);
+  const int64_t num_seqs = tables.size(0);
+  OptTensor cu;
+  int64_t max_q = 1;
+  if (!cu_seqlens_q.has_value()) {
+    TORCH_CHECK_VALUE(num_seqs == rows && lengths.size(0) == rows,
+                      "per-row attention needs one block table and length per q row");
+  } else {
+    cu = as(*cu_seqlens_q, at::kInt);
+    TORCH_CHECK_VALUE(cu->size(0) == num_seqs + 1 && lengths.size(0) == num_seqs,
+                      "cu_seqlens_q must be [sequences + 1] and lengths [sequences]");
+    max_q = max_seqlen_q;
+  }
+  OptTensor rl;
+  if (row_lengths.has_value()) {
+    TORCH_CHECK_VALUE(cu_seqlens_q.has_value(), "row_lengths needs the packed form (cu_seqlens_q)");
+    TORCH_CHECK_VALUE(row_lengths->dim() == 1 && row_lengths->size(0) == rows,
+                      "row_lengths must be [q rows]");
+    rl = as(*row_lengths, at::kInt);
+  }
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int64_t heads = q.size(1), width = tables.size(1);
+  const Tensor ws = workspace(
+      rlt_paged_attention_workspace_size((int32_t)rows, (int32_t)heads, (int32_t)head_dim,
+                                         (int32_t)width, (int32_t)block_size),
+      q);
+  const int status = rlt_paged_attention_rows(
+      ptr(qq), qq.stride(0), qq.stride(1), ptr(key_cache), ptr(value_cache), key_cache.stride(0),
+      key_cache.stride(1), key_cache.stride(2), value_cache.stride(0), value_cache.stride(1),
+      value_cache.stride(2), (int32_t)num_blocks, (const int32_t*)ptr(tables), tables.stride(0),
+      (int32_t)width, (const int32_t*)ptr(lengths), (const int32_t*)ptr(rl),
+      (const int32_t*)ptr(cu), (int32_t)num_seqs, (int32_t)max_q, (int32_t)rows,
+      (const float*)ptr(key_scale), (const float*)ptr(value_scale), mode, s_strides[0],
+      s_strides[1], s_strides[2], (int32_t)heads, (int32_t)kv_heads, (int32_t)head_dim,
+      (int32_t)block_size, dtype_code(q.scalar_type()), dtype_code(key_cache.scalar_type()),
+      (int32_t)window, ptr(output), output.stride(0), output.stride(1), ptr(ws), ws.numel(),
+      stream_of(q));
+  check_status(status, "rlt_paged_attention");
+  return output;
+}
+
+// ---------------------------------------------------------------- KV writes
+
+void check_view(const Tensor& cache, const char* name) {
+  TORCH_CHECK_VALUE(cache.dim() == 4 && cache.stride(-1) == 1, name,
+                    " must be a [block, token, kv_head, dim] view with unit dim stride");
+}
+
+Tensor rows3(const Tensor& x, const char* name) {
+  TORCH_CHECK_VALUE(x.dim() == 3, name, " must be [rows, kv_heads, head_dim]");
+  return x.stride(-1) == 1 ? x : x.contiguous();
+}
+
+Tensor index_of(const Tensor& t, int64_t rows, const char* name) {
+  TORCH_CHECK_VALUE(t.dim() == 1 && t.size(0) == rows, name, " must have shape [", rows, "]");
+  return as(t, at::kLong);
+}
+
+// reference: vllm_rlt/kernels/routing.py:210-223, vllm_rlt/kernels/graph_kv.py:52-67.
+void store_kv(const Tensor& key_cache, const Tensor& value_cache, const Tensor& k_in, const Tensor& v_in,
+              const Tensor& blocks, const Tensor& offsets, const OptTensor& mask,
+              const OptTensor& active) {
+  check_view(key_cache, "key_cache");
+  check_view(value_cache, "value_cache");
+  TORCH_CHECK_VALUE(key_cache.strides() == value_cache.strides() &&
+                        key_cache.sizes() == value_cache.sizes(),
+                    "key and value pools must share a layout");
+  const Tensor k = rows3(k_in, "k"), v = rows3(v_in, "v");
+  const int64_t rows = k.size(0);
+  TORCH_CHECK_VALUE(v.sizes() == k.sizes() && k.size(1) == key_cache.size(2) &&
+                        k.size(2) == key_cache.size(3),
+                    "k, v must be [rows, kv_heads, head_dim] of the pool");
+  TORCH_CHECK_VALUE(k.scalar_type() == key_cache.scalar_type() &&
+                        v.scalar_type() == key_cache.scalar_type(),
+                    "rows must have the pool's dtype");
+  if (rows == 0) return;
+  const Tensor b = index_of(blocks, rows, "blocks"), o = index_of(offsets, rows, "offsets");
+  OptTensor m, a;
+  if (mask.has_value()) {
+    TORCH_CHECK_VALUE(mask->dim() == 1 && mask->size(0) == rows, "mask must have shape [", rows,
+                      "]");
+    const auto mt = mask->scalar_type();
+    m = (mt == at::kBool || mt == at::kByte) ? mask->contiguous() : mask->to(at::kBool).contiguous();
+  }
+  if (active.has_value()) {
+    TORCH_CHECK_VALUE(active->numel() == 1, "active must be one int32 row count");
+    a = active->reshape({}).to(at::kInt).contiguous();
+  }
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
+  const int status = rlt_kv_store(
+      ptr(k), ptr(v), k.stride(0), k.stride(1), v.stride(0), v.stride(1), ptr(key_cache),
+      ptr(value_cache), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+      key_cache.size(0), key_cache.size(1), (const int64_t*)ptr(b), (const int64_t*)ptr(o),
+      (const uint8_t*)ptr(m), (const int32_t*)ptr(a), rows, (int32_t)k.size(1),
+      (int32_t)k.size(2), dtype_code(k.scalar_type()), stream_of(k));
+  check_status(status, "rlt_kv_store");
+}
+
+// ---------------------------------------------------------------- sampling
+
+void check_vec(const Tensor& t, int64_t n, const char* name) {
+  TORCH_CHECK_VALUE(t.dim() == 1 && t.size(0) == n, name, " must have shape [", n, "], got ",
+                    t.sizes());
+}
+
+// reference: vllm_rlt/worker/speculative_sampling.py:8-56.
+Tensor spec_probs(const Tensor& logits, const Tensor& temperature, const Tensor& top_k,
+                  const Tensor& top_p, int64_t max_top_k, bool apply_top_p) {
+  TORCH_CHECK_VALUE(logits.dim() == 2, "logits must be a 2-D [n, V] tensor");
+  const int64_t n = logits.size(0), vocab = logits.size(1);
+  check_vec(temperature, n, "temperature");
+  check_vec(top_k, n, "top_k");
+  check_vec(top_p, n, "top_p");
+  TORCH_CHECK_VALUE(max_top_k >= 0, "max_top_k must be nonnegative");
+  Tensor out = at::empty({n, vocab}, logits.options().dtype(at::kFloat));
+  if (n == 0 || vocab == 0) return out;
+  const Tensor x = logit_rows(logits);
+  const Tensor t = as(temperature, at::kFloat), k = as(top_k, at::kLong), p = as(top_p, at::kFloat);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const int status = rlt_batched_probabilities(
+      ptr(x), dtype_code(x.scalar_type()), x.stride(0), n, vocab, (const float*)ptr(t),
+      (const int64_t*)ptr(k), (const float*)ptr(p), max_top_k, apply_top_p ? 1 : 0,
+      (float*)ptr(out), out.stride(0), stream_of(x));
+  check_status(status, "rlt_batched_probabilities");
+  return out;
+}
+
+// reference: vllm_rlt/worker/speculative_sampling.py:59-85.
+std::tuple<Tensor, Tensor> categorical(const Tensor& weights, const Tensor& u) {
+  TORCH_CHECK_VALUE(weights.dim() == 2 && weights.size(1) >= 1,
+                    "weights must be a 2-D [m, V] tensor with V >= 1");
+  const int64_t m = weights.size(0), vocab = weights.size(1);
+  check_vec(u, m, "u");
+  Tensor index = at::empty({m}, weights.options().dtype(at::kLong));
+  Tensor valid = at::empty({m}, weights.options().dtype(at::kBool));
+  if (m == 0) return {index, valid};
+  const Tensor w = as(weights, at::kFloat), uu = as(u, at::kFloat);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(w.device());
+  const Tensor ws = workspace(rlt_categorical_workspace_size(m, vocab), w);
+  const int status = rlt_categorical((const float*)ptr(w), (const float*)ptr(uu), m, vocab,
+                                     (int64_t*)ptr(index), (uint8_t*)ptr(valid), ptr(ws),
+                                     ws.numel(), stream_of(w));
+  check_status(status, "rlt_categorical");
+  return {index, valid};
+}
+
+// reference: vllm_rlt/worker/speculative_sampling.py:104-181.
+std::tuple<Tensor, Tensor, Tensor, Tensor> spec_accept(const Tensor& draft_tokens,
+                                                       const Tensor& drafts, const Tensor& q,
+                                                       const Tensor& p, const Tensor& u_accept,
+                                                       const Tensor& u_final) {
+  TORCH_CHECK_VALUE(draft_tokens.dim() == 2, "draft_tokens must be [n, W1]");
+  const int64_t n = draft_tokens.size(0), w1 = draft_tokens.size(1);
+  const int64_t vocab = p.size(-1);
+  TORCH_CHECK_VALUE(drafts.sizes() == at::IntArrayRef{n} && u_final.sizes() == at::IntArrayRef{n} &&
+                        u_accept.sizes() == at::IntArrayRef({n, w1}),
+                    "drafts, u_accept and u_final must match draft_tokens [n, W1]");
+  TORCH_CHECK_VALUE(q.sizes() == at::IntArrayRef({n, w1, vocab}) &&
+                        p.sizes() == at::IntArrayRef({n, w1 + 1, vocab}),
+                    "q must be [n, W1, V] and p must be [n, W1 + 1, V]");
+  Tensor tokens = at::empty({n, w1 + 1}, p.options().dtype(at::kLong));
+  Tensor accepted = at::empty({n}, p.options().dtype(at::kLong));
+  Tensor final_token = at::empty({n}, p.options().dtype(at::kLong));
+  Tensor error = at::empty({n}, p.options().dtype(at::kBool));
+  if (n == 0) return {tokens, accepted, final_token, error};
+  TORCH_CHECK_VALUE(w1 <= 32, "at most 32 draft tokens per request are supported");
+  const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
+  const Tensor qq = as(q, at::kFloat), pp = as(p, at::kFloat);
+  const Tensor ua = as(u_accept, at::kFloat), uf = as(u_final, at::kFloat);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(p.device());
+  const Tensor ws = workspace(rlt_speculative_accept_workspace_size(n, (int32_t)w1, vocab), p);
+  const int status = rlt_speculative_accept(
+      (const int64_t*)ptr(dt), (const int64_t*)ptr(dr), (const float*)ptr(qq),
+      (const float*)ptr(pp), (const float*)ptr(ua), (const float*)ptr(uf), n, (int32_t)w1, vocab,
+      (int64_t*)ptr(tokens), (int64_t*)ptr(accepted), (int64_t*)ptr(final_token),
+      (uint8_t*)ptr(error), ptr(ws), ws.numel(), stream_of(p));
+  check_status(status, "rlt_speculative_accept");
+  return {tokens, accepted, final_token, error};
+}
+
+// reference: vllm_rlt/worker/async_speculative.py:706-720.
+std::tuple<Tensor, Tensor, Tensor> greedy_accept(const Tensor& draft_tokens, const Tensor& drafts,
+                                                 const Tensor& target_logits) {
+  TORCH_CHECK_VALUE(draft_tokens.dim() == 2, "draft_tokens must be [n, W1]");
+  const int64_t n = draft_tokens.size(0), w1 = draft_tokens.size(1);
+  TORCH_CHECK_VALUE(drafts.sizes() == at::IntArrayRef{n}, "drafts must have shape [n]");
+  TORCH_CHECK_VALUE(target_logits.dim() == 3 && target_logits.size(0) == n &&
+                        target_logits.size(1) == w1 + 1,
+                    "target_logits must be [n, W1 + 1, V]");
+  const int64_t vocab = target_logits.size(2);
+  Tensor targets = at::empty({n, w1 + 1}, target_logits.options().dtype(at::kLong));
+  Tensor accepted = at::empty({n}, target_logits.options().dtype(at::kLong));
+  Tensor next_token = at::empty({n}, target_logits.options().dtype(at::kLong));
+  if (n == 0) return {targets, accepted, next_token};
+  TORCH_CHECK_VALUE(vocab >= 1, "target_logits must have V >= 1");
+  Tensor x = logit_dtype(target_logits.scalar_type()) ? target_logits : target_logits.to(at::kFloat);
+  if (!(x.stride(2) == 1 && x.stride(0) == (w1 + 1) * x.stride(1))) x = x.contiguous();
+  const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const int status = rlt_greedy_accept(
+      (const int64_t*)ptr(dt), (const int64_t*)ptr(dr), ptr(x), dtype_code(x.scalar_type()),
+      x.stride(1), n, (int32_t)w1, vocab, (int64_t*)ptr(targets), (int64_t*)ptr(accepted),
+      (int64_t*)ptr(next_token), stream_of(x));
+  check_status(status, "rlt_greedy_accept");
+  return {targets, accepted, next_token};
+}
+
+// reference: vllm_rlt/worker/async_speculative.py:678-692.
+std::tuple<Tensor, Tensor> verify_distributions(const Tensor& logits, const Tensor& random_rows,
+                                                const Tensor& temperature, const Tensor& top_k,
+                                                const Tensor& top_p, int64_t max_top_k,
+                                                bool apply_top_p) {
+  TORCH_CHECK_VALUE(logits.dim() == 2, "logits must be a 2-D [m, V] tensor");
+  TORCH_CHECK_VALUE(random_rows.dim() == 1, "random_rows must be 1-D");
+  const int64_t m = logits.size(0), vocab = logits.size(1), r = random_rows.size(0);
+  if (r) {
+    check_vec(temperature, r, "temperature");
+    check_vec(top_k, r, "top_k");
+    check_vec(top_p, r, "top_p");
+  }
+  TORCH_CHECK_VALUE(max_top_k >= 0, "max_top_k must be nonnegative");
+  Tensor target = at::empty({m}, logits.options().dtype(at::kLong));
+  Tensor p_out = at::empty({r, vocab}, logits.options().dtype(at::kFloat));
+  if (m == 0 && r == 0) return {target, p_out};
+  TORCH_CHECK_VALUE(vocab >= 1, "logits must have V >= 1");
+  const Tensor x = logit_rows(logits);
+  const Tensor rows = as(random_rows, at::kLong);
+  OptTensor t, k, p;
+  if (r) {
+    t = as(temperature, at::kFloat);
+    k = as(top_k, at::kLong);
+    p = as(top_p, at::kFloat);
+  }
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const int status = rlt_verify_distributions(
+      ptr(x), dtype_code(x.scalar_type()), x.stride(0), m, vocab, (const int64_t*)ptr(rows), r,
+      (const float*)ptr(t), (const int64_t*)ptr(k), (const float*)ptr(p), max_top_k,
+      apply_top_p ? 1 : 0, (float*)ptr(p_out), r ? p_out.stride(0) : vocab,
+      (int64_t*)ptr(target), stream_of(x));
+  check_status(status, "rlt_verify_distributions");
+  return {target, p_out};
+}
+
+// reference: vllm_rlt/worker/async_speculative.py:678-692 then :727-734.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> verify_accept(
+    const Tensor& target_logits, const Tensor& temperature, const Tensor& top_k,
+    const Tensor& top_p, const Tensor& draft_tokens, const Tensor& drafts, const Tensor& q,
+    const Tensor& u_accept, const Tensor& u_final, int64_t max_top_k, bool apply_top_p) {
+  TORCH_CHECK_VALUE(draft_tokens.dim() == 2, "draft_tokens must be [n, W1]");
+  const int64_t n = draft_tokens.size(0), w1 = draft_tokens.size(1);
+  TORCH_CHECK_VALUE(target_logits.dim() == 3 && target_logits.size(0) == n &&
+                        target_logits.size(1) == w1 + 1,
+                    "target_logits must be [n, W1 + 1, V]");
+  const int64_t vocab = target_logits.size(2), rows = n * (w1 + 1);
+  check_vec(temperature, rows, "temperature");
+  check_vec(top_k, rows, "top_k");
+  check_vec(top_p, rows, "top_p");
+  TORCH_CHECK_VALUE(drafts.sizes() == at::IntArrayRef{n} && u_final.sizes() == at::IntArrayRef{n} &&
+                        u_accept.sizes() == at::IntArrayRef({n, w1}),
+                    "drafts, u_accept and u_final must match draft_tokens [n, W1]");
+  TORCH_CHECK_VALUE(q.sizes() == at::IntArrayRef({n, w1, vocab}), "q must be [n, W1, V]");
+  TORCH_CHECK_VALUE(max_top_k >= 0, "max_top_k must be nonnegative");
+  TORCH_CHECK_VALUE(w1 <= 32, "at most 32 draft tokens per request are supported");
+  const auto i64 = target_logits.options().dtype(at::kLong);
+  Tensor target = at::empty({rows}, i64);
+  Tensor p = at::empty({n, w1 + 1, vocab}, target_logits.options().dtype(at::kFloat));
+  Tensor tokens = at::empty({n, w1 + 1}, i64);
+  Tensor accepted = at::empty({n}, i64), final_token = at::empty({n}, i64);
+  Tensor error = at::empty({n}, target_logits.options().dtype(at::kBool));
+  if (n == 0) return {target, p, tokens, accepted, final_token, error};
+  const Tensor x = logit_rows(target_logits.reshape({rows, vocab}));
+  const Tensor t = as(temperature, at::kFloat), k = as(top_k, at::kLong), pp = as(top_p, at::kFloat);
+  const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
+  const Tensor qq = as(q, at::kFloat), ua = as(u_accept, at::kFloat), uf = as(u_final, at::kFloat);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const Tensor ws = workspace(rlt_speculative_accept_workspace_size(n, (int32_t)w1, vocab), x);
+  const int status = rlt_verify_accept(
+      ptr(x), dtype_code(x.scalar_type()), x.stride(0), (const float*)ptr(t),
+      (const int64_t*)ptr(k), (const float*)ptr(pp), max_top_k, apply_top_p ? 1 : 0,
+      (const int64_t*)ptr(dt), (const int64_t*)ptr(dr), (const float*)ptr(qq),
+      (const float*)ptr(ua), (const float*)ptr(uf), n, (int32_t)w1, vocab, (int64_t*)ptr(target),
+      (float*)ptr(p), (int64_t*)ptr(tokens), (int64_t*)ptr(accepted), (int64_t*)ptr(final_token),
+      (uint8_t*)ptr(error), ptr(ws), ws.numel(), stream_of(x));
+  check_status(status, "rlt_verify_accept");
+  return {target, p, tokens, accepted, final_token, error};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(rlt_mi355x, m) {
+  m.def("paged_attention(Tensor q, Tensor key_cache, Tensor value_cache, Tensor block_tables, "
+        "Tensor context_lengths, Tensor? key_scale, Tensor? value_scale, Tensor? cu_seqlens_q, "
+        "int max_seqlen_q, int window, Tensor? row_lengths=None) -> Tensor");
+  m.def("store_kv(Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor k, Tensor v, "
+        "Tensor blocks, Tensor offsets, Tensor? mask, Tensor? active) -> ()");
+  m.def("spec_probs(Tensor logits, Tensor temperature, Tensor top_k, Tensor top_p, "
+        "int max_top_k, bool apply_top_p) -> Tensor");
+  m.def("categorical(Tensor weights, Tensor u) -> (Tensor, Tensor)");
+  m.def("spec_accept(Tensor draft_tokens, Tensor drafts, Tensor q, Tensor p, Tensor u_accept, "
+        "Tensor u_final) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("greedy_accept(Tensor draft_tokens, Tensor drafts, Tensor target_logits) "
+        "-> (Tensor, Tensor, Tensor)");
+  m.def("verify_distributions(Tensor logits, Tensor random_rows, Tensor temperature, "
+        "Tensor top_k, Tensor top_p, int max_top_k, bool apply_top_p) -> (Tensor, Tensor)");
+  m.def("verify_accept(Tensor target_logits, Tensor temperature, Tensor top_k, Tensor top_p, "
+        "Tensor draft_tokens, Tensor drafts, Tensor q, Tensor u_accept, Tensor u_final, "
+        "int max_top_k, bool apply_top_p) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(rlt_mi355x, CUDA, m) {
+  m.impl("paged_attention", &paged_attention);
+  m.impl("store_kv", &store_kv);
+  m.impl("spec_probs", &spec_probs);
+  m.impl("categorical", &categorical);
+  m.impl("spec_accept", &spec_accept);
+  m.impl("greedy_accept", &greedy_accept);
+  m.impl("verify_distributions", &verify_distributions);
+  m.impl("verify_accept", &verify_accept);
+}

@@ -74,16 +74,8 @@ def store_kv(key_cache, value_cache, k, v, blocks, offsets, *, mask=None, active
     _lib.require_gpu(key_cache, value_cache, k, v, blocks, offsets, mask, active)
     if rows == 0:
         return
-    b, o = _index(blocks, rows, "blocks"), _index(offsets, rows, "offsets")
-    m, a = _mask(mask, rows), _active(active)
-    lib = _lib.library()
-    status = lib.rlt_kv_store(
-        _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
-        _lib.ptr(key_cache), _lib.ptr(value_cache), key_cache.stride(0), key_cache.stride(1),
-        key_cache.stride(2), key_cache.shape[0], key_cache.shape[1], _lib.ptr(b), _lib.ptr(o),
-        _lib.ptr(m), _lib.ptr(a), rows, k.shape[1], k.shape[2], _lib.dtype_code(k.dtype),
-        _lib.stream_of(k.device))
-    _lib.check(status, "rlt_kv_store")
+    # index / mask conversions and the launch: torch.ops.rlt_mi355x.store_kv
+    _lib.ops().store_kv(key_cache, value_cache, k, v, blocks, offsets, mask, active)
 
 
 def masked_kv_store(keys, values, k, v, metadata):

@@ -2,79 +2,48 @@
 
 The reference binds its native code as a ``TORCH_LIBRARY`` schema
 (csrc/torch_bindings.cpp:7-13) next to Python ``torch.library`` fragments
-(vllm_rlt/kernels/activation.py:34-39).  These operators are the same kind of binding
-for the gfx950 kernels: ``torch.ops.rlt_mi355x.<name>`` with a fixed schema, an
-implementation for ROCm device tensors only (a CPU tensor finds no kernel and raises:
-there is no fallback), and a fake (meta) implementation so that graph capture and
-``torch.compile`` can trace shapes without running them.  Every implementation calls
-the package's wrappers of ``librlt_mi355x.so``; the Python shims with the reference
-signatures stay in ``attention``, ``sampling`` and ``kv_write``.
+(vllm_rlt/kernels/activation.py:34-39).  This package does the same for the gfx950
+kernels: the per-step entry points -- ``paged_attention``, ``store_kv``,
+``spec_probs``, ``categorical``, ``spec_accept``, ``greedy_accept``,
+``verify_distributions``, ``verify_accept`` -- are C++ operators
+(``csrc/torch_bindings.cpp`` -> ``_C.so``: schema, argument checks, workspace and
+launch, one dispatcher call per step); the rest are Python ``torch.library``
+custom ops over the same library.  Every operator has an implementation for ROCm
+device tensors only (a CPU tensor finds no kernel and raises: there is no
+fallback) and a fake (meta) implementation registered here, so that graph capture
+and ``torch.compile`` can trace shapes without running them.  The Python shims with
+the reference signatures stay in ``attention``, ``sampling`` and ``kv_write``.
 """
 
 from typing import Optional, Tuple
 
 import torch
 
+from . import _lib
 from . import kv_write as _kv
 from . import sampling as _samp
-from .attention import MI355XPagedAttention
 
-_ATTN = MI355XPagedAttention()
-
-
-@torch.library.custom_op("rlt_mi355x::paged_attention", mutates_args=(), device_types="cuda")
-def paged_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
-                    block_tables: torch.Tensor, context_lengths: torch.Tensor,
-                    key_scale: Optional[torch.Tensor], value_scale: Optional[torch.Tensor],
-                    cu_seqlens_q: Optional[torch.Tensor], max_seqlen_q: int,
-                    window: int, row_lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Per-row (cu_seqlens_q None) or packed causal-window paged attention;
-    reference: vllm_rlt/kernels/paged_attention.py:13-90, triton_attention.py:386-404.
-    ``row_lengths`` (packed form only): each row's key count, rows in any order."""
-    return _ATTN._run(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-                      max_seqlen_q, key_scale, value_scale, window, row_lengths)
+_lib.ops()  # registers the C++ operators (raises if _C.so is missing)
 
 
-@paged_attention.register_fake
+@torch.library.register_fake("rlt_mi355x::paged_attention")
 def _(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value_scale,
       cu_seqlens_q, max_seqlen_q, window, row_lengths=None):
     return torch.empty_like(q)
 
 
-@torch.library.custom_op("rlt_mi355x::spec_probs", mutates_args=(), device_types="cuda")
-def spec_probs(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.Tensor,
-               top_p: torch.Tensor, max_top_k: int, apply_top_p: bool) -> torch.Tensor:
-    """reference: vllm_rlt/worker/speculative_sampling.py:8-56 batched_probabilities."""
-    return _samp.batched_probabilities(logits, temperature, top_k, top_p, max_top_k=max_top_k,
-                                       apply_top_p=apply_top_p)
-
-
-@spec_probs.register_fake
+@torch.library.register_fake("rlt_mi355x::spec_probs")
 def _(logits, temperature, top_k, top_p, max_top_k, apply_top_p):
     return logits.new_empty(logits.shape, dtype=torch.float32)
 
 
-@torch.library.custom_op("rlt_mi355x::categorical", mutates_args=(), device_types="cuda")
-def categorical(weights: torch.Tensor, u: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """reference: vllm_rlt/worker/speculative_sampling.py:59-85."""
-    return _samp.categorical(weights, u)
-
-
-@categorical.register_fake
+@torch.library.register_fake("rlt_mi355x::categorical")
 def _(weights, u):
     m = weights.shape[0]
     return (weights.new_empty((m,), dtype=torch.int64), weights.new_empty((m,), dtype=torch.bool))
 
 
-@torch.library.custom_op("rlt_mi355x::spec_accept", mutates_args=(), device_types="cuda")
-def spec_accept(draft_tokens: torch.Tensor, drafts: torch.Tensor, q: torch.Tensor,
-                p: torch.Tensor, u_accept: torch.Tensor, u_final: torch.Tensor
-                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(tokens, accepted, final, error); reference: speculative_sampling.py:88-181."""
-    return tuple(_samp.speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final))
-
-
-@spec_accept.register_fake
+@torch.library.register_fake("rlt_mi355x::spec_accept")
 def _(draft_tokens, drafts, q, p, u_accept, u_final):
     n, w1 = draft_tokens.shape
     i64 = dict(dtype=torch.int64)
@@ -82,14 +51,7 @@ def _(draft_tokens, drafts, q, p, u_accept, u_final):
             p.new_empty((n,), dtype=torch.bool))
 
 
-@torch.library.custom_op("rlt_mi355x::greedy_accept", mutates_args=(), device_types="cuda")
-def greedy_accept(draft_tokens: torch.Tensor, drafts: torch.Tensor, target_logits: torch.Tensor
-                  ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(targets, accepted, next_token); reference: vllm_rlt/worker/async_speculative.py:706-720."""
-    return _samp.greedy_accept_batched(draft_tokens, drafts, target_logits)
-
-
-@greedy_accept.register_fake
+@torch.library.register_fake("rlt_mi355x::greedy_accept")
 def _(draft_tokens, drafts, target_logits):
     n, w1 = draft_tokens.shape
     i64 = dict(dtype=torch.int64)
@@ -112,36 +74,13 @@ def _(logits, random_rows, temperature, top_k, top_p, u, max_top_k, apply_top_p)
             logits.new_empty((random_rows.shape[0], logits.shape[1]), dtype=torch.float32))
 
 
-@torch.library.custom_op("rlt_mi355x::verify_distributions", mutates_args=(), device_types="cuda")
-def verify_distributions(logits: torch.Tensor, random_rows: torch.Tensor,
-                         temperature: torch.Tensor, top_k: torch.Tensor, top_p: torch.Tensor,
-                         max_top_k: int, apply_top_p: bool) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(target, p); reference: vllm_rlt/worker/async_speculative.py:678-692."""
-    return _samp.verify_distributions(logits, random_rows, temperature, top_k, top_p,
-                                      max_top_k=max_top_k, apply_top_p=apply_top_p)
-
-
-@verify_distributions.register_fake
+@torch.library.register_fake("rlt_mi355x::verify_distributions")
 def _(logits, random_rows, temperature, top_k, top_p, max_top_k, apply_top_p):
     return (logits.new_empty((logits.shape[0],), dtype=torch.int64),
             logits.new_empty((random_rows.shape[0], logits.shape[1]), dtype=torch.float32))
 
 
-@torch.library.custom_op("rlt_mi355x::verify_accept", mutates_args=(), device_types="cuda")
-def verify_accept(target_logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.Tensor,
-                  top_p: torch.Tensor, draft_tokens: torch.Tensor, drafts: torch.Tensor,
-                  q: torch.Tensor, u_accept: torch.Tensor, u_final: torch.Tensor, max_top_k: int,
-                  apply_top_p: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor,
-                                              torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(target, p, tokens, accepted, final, error); reference:
-    vllm_rlt/worker/async_speculative.py:678-692 then :727-734."""
-    target, p, res = _samp.verify_accept(target_logits, temperature, top_k, top_p, draft_tokens,
-                                         drafts, q, u_accept, u_final, max_top_k=max_top_k,
-                                         apply_top_p=apply_top_p)
-    return (target, p) + tuple(res)
-
-
-@verify_accept.register_fake
+@torch.library.register_fake("rlt_mi355x::verify_accept")
 def _(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept, u_final,
       max_top_k, apply_top_p):
     n, w1 = draft_tokens.shape
@@ -196,13 +135,9 @@ def _(candidates, counts, target, proposal, uniforms, sum_threads):
             target.new_empty((n, target.shape[-1]), dtype=torch.float32))
 
 
-@torch.library.custom_op("rlt_mi355x::store_kv", mutates_args=("key_cache", "value_cache"),
-                         device_types="cuda")
-def store_kv(key_cache: torch.Tensor, value_cache: torch.Tensor, k: torch.Tensor,
-             v: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor,
-             mask: Optional[torch.Tensor], active: Optional[torch.Tensor]) -> None:
-    """reference: vllm_rlt/kernels/routing.py:210-223, vllm_rlt/kernels/graph_kv.py:52-67."""
-    _kv.store_kv(key_cache, value_cache, k, v, blocks, offsets, mask=mask, active=active)
+@torch.library.register_fake("rlt_mi355x::store_kv")
+def _(key_cache, value_cache, k, v, blocks, offsets, mask, active):
+    return None
 
 
 @torch.library.custom_op("rlt_mi355x::store_fp8",

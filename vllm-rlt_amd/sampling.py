@@ -99,29 +99,12 @@ def batched_probabilities(logits, temperature, top_k, top_p, *, max_top_k, apply
     reference: vllm_rlt/worker/speculative_sampling.py:8-56.  ``max_top_k`` and
     ``apply_top_p`` come from the host plan (no host synchronization happens here).
     Tokens tied at a top-k or top-p cut survive in column order (the reference
-    leaves the surviving index of a tie unspecified).
+    leaves the surviving index of a tie unspecified).  Runs the C++ operator
+    ``torch.ops.rlt_mi355x.spec_probs``.
     """
-    if logits.ndim != 2:
-        raise ValueError("logits must be a 2-D [n, V] tensor")
-    n, vocab = logits.shape
-    for name, value in (("temperature", temperature), ("top_k", top_k), ("top_p", top_p)):
-        if value.shape != (n,):
-            raise ValueError(f"{name} must have shape [{n}], got {tuple(value.shape)}")
-    if max_top_k < 0:
-        raise ValueError("max_top_k must be nonnegative")
     _lib.require_gpu(logits, temperature, top_k, top_p)
-    out = torch.empty((n, vocab), dtype=torch.float32, device=logits.device)
-    if n == 0 or vocab == 0:
-        return out
-    x = _rows(logits)
-    temp, tk, tp = _f32(temperature), _i64(top_k), _f32(top_p)
-    lib = _lib.library()
-    status = lib.rlt_batched_probabilities(
-        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), n, vocab, _lib.ptr(temp), _lib.ptr(tk),
-        _lib.ptr(tp), int(max_top_k), int(bool(apply_top_p)), _lib.ptr(out), out.stride(0),
-        _lib.stream_of(x.device))
-    _lib.check(status, "rlt_batched_probabilities")
-    return out
+    return _lib.ops().spec_probs(logits, temperature, top_k, top_p, int(max_top_k),
+                                 bool(apply_top_p))
 
 
 def greedy_accept_batched(draft_tokens, drafts, target_logits):
@@ -131,35 +114,10 @@ def greedy_accept_batched(draft_tokens, drafts, target_logits):
     vllm_rlt/worker/speculative.py:41-53).  ``target_logits`` is ``[n, W1 + 1, V]``;
     returns ``(targets int64 [n, W1 + 1], accepted int64 [n], next_token int64 [n])``
     where draft j is checked against target row j and only ``drafts[r]`` drafts count.
+    Runs ``torch.ops.rlt_mi355x.greedy_accept``.
     """
-    n, w1 = draft_tokens.shape
-    if drafts.shape != (n,):
-        raise ValueError("drafts must have shape [n]")
-    if target_logits.ndim != 3 or target_logits.shape[:2] != (n, w1 + 1):
-        raise ValueError("target_logits must be [n, W1 + 1, V]")
     _lib.require_gpu(draft_tokens, drafts, target_logits)
-    device = target_logits.device
-    vocab = target_logits.shape[-1]
-    targets = torch.empty((n, w1 + 1), dtype=torch.int64, device=device)
-    accepted = torch.empty(n, dtype=torch.int64, device=device)
-    next_token = torch.empty(n, dtype=torch.int64, device=device)
-    if n == 0:
-        return targets, accepted, next_token
-    if vocab == 0:
-        raise ValueError("target_logits must have V >= 1")
-    x = target_logits
-    if x.dtype not in _LOGIT_DTYPES:
-        x = x.float()
-    if not (x.stride(-1) == 1 and x.stride(0) == (w1 + 1) * x.stride(1)):
-        x = x.contiguous()
-    dt, dr = _i64(draft_tokens), _i64(drafts)
-    lib = _lib.library()
-    status = lib.rlt_greedy_accept(
-        _lib.ptr(dt), _lib.ptr(dr), _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(1), n, w1,
-        vocab, _lib.ptr(targets), _lib.ptr(accepted), _lib.ptr(next_token),
-        _lib.stream_of(device))
-    _lib.check(status, "rlt_greedy_accept")
-    return targets, accepted, next_token
+    return _lib.ops().greedy_accept(draft_tokens, drafts, target_logits)
 
 
 def propose_drafts(logits, random_rows, temperature, top_k, top_p, u, *, max_top_k, apply_top_p,
@@ -238,6 +196,10 @@ def verify_distributions(logits, random_rows, temperature, top_k, top_p, *, max_
     if max_top_k < 0:
         raise ValueError("max_top_k must be nonnegative")
     _lib.require_gpu(logits, random_rows, *((temperature, top_k, top_p) if r else ()), p_out)
+    if p_out is None and r:
+        # new output rows: the C++ operator torch.ops.rlt_mi355x.verify_distributions
+        return tuple(_lib.ops().verify_distributions(logits, random_rows, temperature, top_k,
+                                                     top_p, int(max_top_k), bool(apply_top_p)))
     device = logits.device
     target = torch.empty(m, dtype=torch.int64, device=device)
     if p_out is None:
@@ -263,54 +225,17 @@ def categorical(weights, u):
     """Inverse-CDF draw from ``[m, V]`` nonnegative weights with ``[m]`` uniforms.
 
     Returns ``(index int64 [m], valid bool [m])``; reference: speculative_sampling.py:59-85.
+    Runs ``torch.ops.rlt_mi355x.categorical``.
     """
-    if weights.ndim != 2 or weights.shape[-1] < 1:
-        raise ValueError("weights must be a 2-D [m, V] tensor with V >= 1")
-    if u.shape != weights.shape[:1]:
-        raise ValueError(f"u must have shape [{weights.shape[0]}], got {tuple(u.shape)}")
     _lib.require_gpu(weights, u)
-    m, vocab = weights.shape
-    index = torch.empty(m, dtype=torch.int64, device=weights.device)
-    valid = torch.empty(m, dtype=torch.bool, device=weights.device)
-    if m == 0:
-        return index, valid
-    w, uu = _f32(weights), _f32(u)
-    lib = _lib.library()
-    ws = _lib.workspace(lib.rlt_categorical_workspace_size(m, vocab), w.device)
-    status = lib.rlt_categorical(_lib.ptr(w), _lib.ptr(uu), m, vocab, _lib.ptr(index),
-                                 _lib.ptr(valid), _lib.ptr(ws), ws.numel(), _lib.stream_of(w.device))
-    _lib.check(status, "rlt_categorical")
-    return index, valid
+    return _lib.ops().categorical(weights, u)
 
 
 def speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final):
-    """Batched speculative rejection sampling; reference: speculative_sampling.py:104-181."""
-    n, w1 = draft_tokens.shape
-    vocab = p.shape[-1]
-    if drafts.shape != (n,) or u_final.shape != (n,) or u_accept.shape != (n, w1):
-        raise ValueError("drafts, u_accept and u_final must match draft_tokens [n, W1]")
-    if q.shape != (n, w1, vocab) or p.shape != (n, w1 + 1, vocab):
-        raise ValueError("q must be [n, W1, V] and p must be [n, W1 + 1, V]")
+    """Batched speculative rejection sampling; reference: speculative_sampling.py:104-181.
+    Runs ``torch.ops.rlt_mi355x.spec_accept``."""
     _lib.require_gpu(draft_tokens, drafts, q, p, u_accept, u_final)
-    device = p.device
-    tokens = torch.empty((n, w1 + 1), dtype=torch.int64, device=device)
-    accepted = torch.empty(n, dtype=torch.int64, device=device)
-    final = torch.empty(n, dtype=torch.int64, device=device)
-    error = torch.empty(n, dtype=torch.bool, device=device)
-    if n == 0:
-        return AcceptResult(tokens, accepted, final, error)
-    if w1 > 32:
-        raise ValueError("at most 32 draft tokens per request are supported")
-    dt, dr = _i64(draft_tokens), _i64(drafts)
-    qq, pp, ua, uf = _f32(q), _f32(p), _f32(u_accept), _f32(u_final)
-    lib = _lib.library()
-    ws = _lib.workspace(lib.rlt_speculative_accept_workspace_size(n, w1, vocab), device)
-    status = lib.rlt_speculative_accept(
-        _lib.ptr(dt), _lib.ptr(dr), _lib.ptr(qq), _lib.ptr(pp), _lib.ptr(ua), _lib.ptr(uf),
-        n, w1, vocab, _lib.ptr(tokens), _lib.ptr(accepted), _lib.ptr(final), _lib.ptr(error),
-        _lib.ptr(ws), ws.numel(), _lib.stream_of(device))
-    _lib.check(status, "rlt_speculative_accept")
-    return AcceptResult(tokens, accepted, final, error)
+    return AcceptResult(*_lib.ops().spec_accept(draft_tokens, drafts, q, p, u_accept, u_final))
 
 
 def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
@@ -322,50 +247,14 @@ def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts
     u_final)``, bitwise (reference: vllm_rlt/worker/async_speculative.py:678-692 then
     :727-734).  The draft rows' row sums are computed by otherwise idle workgroups of
     the distribution launch.  ``temperature`` / ``top_k`` / ``top_p`` are per verify row
-    ``[n * (W1 + 1)]``; ``target`` is ``[n * (W1 + 1)]``.
+    ``[n * (W1 + 1)]``; ``target`` is ``[n * (W1 + 1)]``.  Runs
+    ``torch.ops.rlt_mi355x.verify_accept``.
     """
-    n, w1 = draft_tokens.shape
-    if target_logits.ndim != 3 or target_logits.shape[:2] != (n, w1 + 1):
-        raise ValueError("target_logits must be [n, W1 + 1, V]")
-    vocab = target_logits.shape[-1]
-    rows = n * (w1 + 1)
-    for name, value in (("temperature", temperature), ("top_k", top_k), ("top_p", top_p)):
-        if value.shape != (rows,):
-            raise ValueError(f"{name} must have shape [{rows}], got {tuple(value.shape)}")
-    if drafts.shape != (n,) or u_final.shape != (n,) or u_accept.shape != (n, w1):
-        raise ValueError("drafts, u_accept and u_final must match draft_tokens [n, W1]")
-    if q.shape != (n, w1, vocab):
-        raise ValueError("q must be [n, W1, V]")
-    if max_top_k < 0:
-        raise ValueError("max_top_k must be nonnegative")
-    if w1 > 32:
-        raise ValueError("at most 32 draft tokens per request are supported")
     _lib.require_gpu(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
                      u_final)
-    device = target_logits.device
-    target = torch.empty(rows, dtype=torch.int64, device=device)
-    p = torch.empty((n, w1 + 1, vocab), dtype=torch.float32, device=device)
-    tokens = torch.empty((n, w1 + 1), dtype=torch.int64, device=device)
-    accepted = torch.empty(n, dtype=torch.int64, device=device)
-    final = torch.empty(n, dtype=torch.int64, device=device)
-    error = torch.empty(n, dtype=torch.bool, device=device)
-    if n == 0:
-        return target, p, AcceptResult(tokens, accepted, final, error)
-    x = target_logits.reshape(rows, vocab)
-    if x.dtype not in _LOGIT_DTYPES:
-        x = x.float()
-    x = _rows(x)
-    lib = _lib.library()
-    ws = _lib.workspace(lib.rlt_speculative_accept_workspace_size(n, w1, vocab), device)
-    status = lib.rlt_verify_accept(
-        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), _lib.ptr(_f32(temperature)),
-        _lib.ptr(_i64(top_k)), _lib.ptr(_f32(top_p)), int(max_top_k), int(bool(apply_top_p)),
-        _lib.ptr(_i64(draft_tokens)), _lib.ptr(_i64(drafts)), _lib.ptr(_f32(q)),
-        _lib.ptr(_f32(u_accept)), _lib.ptr(_f32(u_final)), n, w1, vocab, _lib.ptr(target),
-        _lib.ptr(p), _lib.ptr(tokens), _lib.ptr(accepted), _lib.ptr(final), _lib.ptr(error),
-        _lib.ptr(ws), ws.numel(), _lib.stream_of(device))
-    _lib.check(status, "rlt_verify_accept")
-    return target, p, AcceptResult(tokens, accepted, final, error)
+    out = _lib.ops().verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts,
+                                   q, u_accept, u_final, int(max_top_k), bool(apply_top_p))
+    return out[0], out[1], AcceptResult(*out[2:])
 
 
 # ------------------------------------------------------------ sync-mode rejection
