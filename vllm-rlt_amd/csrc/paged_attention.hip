@@ -283,10 +283,29 @@ struct RawSlice {
   static constexpr int kElt = KVT == QT ? 2 : 1;
   static constexpr int kSteps = D / 32;
   static constexpr int kWords = kSteps * 2 * kElt;  // 8 elements per step
+  // fp8 keys with an even step count load 16 bytes per lane: steps 2j and 2j + 1 of
+  // lane group g take elements [64 j + 16 g, + 16), so one load instruction reads
+  // 64 contiguous bytes of each position (8-byte loads read 32)
+  static constexpr bool kWide = kElt == 1 && kSteps % 2 == 0;
+  static constexpr int kGroupElems = kWide ? 16 : 8;  // elements between lane groups
   uint32_t w[kWords];
 
-  // p: element 8 g of the position's head vector
+  // Element of step s, lane group g, slot e (0..7) in the head vector: the
+  // contraction order q must follow too.
+  __device__ static constexpr int element(int s, int g) {
+    return kWide ? 64 * (s / 2) + 16 * g + 8 * (s % 2) : 32 * s + 8 * g;
+  }
+
+  // p: element kGroupElems * g of the position's head vector
   __device__ __forceinline__ void load(const uint8_t* p) {
+    if (kWide) {
+#pragma unroll
+      for (int j = 0; j < kSteps / 2; ++j) {
+        const uint4 v = *(const uint4*)(p + j * 64);
+        w[4 * j] = v.x; w[4 * j + 1] = v.y; w[4 * j + 2] = v.z; w[4 * j + 3] = v.w;
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
       if (kElt == 2) {
@@ -503,9 +522,9 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
       const int head = kvh * P.group + rho % P.group;
       row_range(P, sv, qi, row_lo[nt], row_hi[nt]);
       const uint16_t* qp = (const uint16_t*)P.q + (int64_t)(sv.q_begin + qi) * P.q_row_stride +
-                           (int64_t)head * P.q_head_stride + grp * 8;
+                           (int64_t)head * P.q_head_stride;
 #pragma unroll
-      for (int s = 0; s < NQS; ++s) qreg[nt][s] = *(const uint4*)(qp + 32 * s);
+      for (int s = 0; s < NQS; ++s) qreg[nt][s] = *(const uint4*)(qp + Raw::element(s, grp));
     } else {
       row_lo[nt] = 0;
       row_hi[nt] = 0;
@@ -527,7 +546,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
     float ksc[kStages][4], vsc[kStages][4];
     bool okk[kStages];
     uint32_t okv[kStages];  // bit i: value position 4 * grp + i is inside the sequence
-    const int64_t k_head = (int64_t)kvh * P.k_head_stride + grp * 8;
+    const int64_t k_head = (int64_t)kvh * P.k_head_stride + grp * Raw::kGroupElems;
     const int64_t v_head = (int64_t)kvh * P.v_head_stride + l16 * ND;
     const int32_t* tbl = tbl_lds - c_begin;  // tbl[pos] for pos in the chunk
     // Loads of tile t into stage b.  Branch-free: every address is inside the
@@ -664,7 +683,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
     };
     // Measurement variant (build with -DRLT_DOT_NT1): one-row units on VALU dot products
     // instead of a 16-row MFMA tile with one real row.  Config-2 decode (batch 64, 16/16
-    // heads, D = 128): 213.6 us against 213.4 us for MFMA, both within bf16 rounding of the
+    // heads, D = 128): 216.4 us against 213.1 us for MFMA, both within tolerance of the
     // oracle; the launch is bound by the KV stream either way.  It is off by default:
     // choosing the math path by row count would make a one-row decode and the packed
     // window differ in arithmetic, and packed == per-row bit for bit would no longer hold.
@@ -1824,7 +1843,8 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
   if (mfma) {
     // 16-byte vector loads of q and of every lane's KV slice.
     const int64_t kv_elt = kv_dtype == RLT_FP8_E4M3 ? 1 : 2;
-    const int64_t kv_align = kv_dtype == RLT_FP8_E4M3 ? 8 : 16;
+    // (fp8 keys with head_dim % 64 == 0 are read 16 bytes per lane: RawSlice::kWide)
+    const int64_t kv_align = kv_dtype == RLT_FP8_E4M3 && head_dim % 64 != 0 ? 8 : 16;
     const bool aligned =
         ((uintptr_t)q % 16 == 0) && (q_row_stride * 2) % 16 == 0 && (q_head_stride * 2) % 16 == 0 &&
         ((uintptr_t)key_cache % 16 == 0) && ((uintptr_t)value_cache % 16 == 0) &&
