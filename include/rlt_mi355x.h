@@ -187,13 +187,21 @@ int rlt_row_mass_f32(const float* x, int64_t rows, int64_t vocab, float* out, vo
  * the softmax mass before them is <= top_p[i] (the token crossing the threshold is
  * kept); then softmax over the kept set.  max_top_k and apply_top_p are the host
  * plan's values, as in the reference.  Rows holding NaN (or with a non-finite
- * max) are written as NaN.  No workspace; V <= 262144.
+ * max) are written as NaN.  V <= 262144.
+ * Workspace (optional): with rlt_probabilities_workspace_size(n, 0, vocab) bytes, a
+ * call that filters no row (max_top_k == 0, apply_top_p == 0) runs the row-split
+ * form: each row spread over several workgroups (slice max and mass, then the
+ * normalized slices; two launches).  Otherwise (filtering calls, workspace == NULL)
+ * one workgroup per row in one launch.  Both forms give the same values up to the
+ * order of the float64 total's summation.
  */
+size_t rlt_probabilities_workspace_size(int64_t rows, int64_t argmax_rows, int64_t vocab);
+
 int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t row_stride,
                               int64_t n, int64_t vocab, const float* temperature,
                               const int64_t* top_k, const float* top_p, int64_t max_top_k,
                               int32_t apply_top_p, float* out, int64_t out_stride,
-                              hipStream_t stream);
+                              void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
  * Draft proposals of one draft offset: proposed[i] = argmax of logits row i
@@ -204,9 +212,13 @@ int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t 
  * of vllm_rlt/worker/async_speculative.py:645-663 (argmax, _probabilities on
  * logits[random_rows], categorical, proposed[random_rows] = sampled) in three
  * launches without host synchronization.  q_out rows are q_stride floats apart (pass
- * the q[:, offset] view).  Workspace: rlt_categorical_workspace_size(r, vocab).
+ * the q[:, offset] view).  Workspace: rlt_propose_drafts_workspace_size(m, r, vocab)
+ * (row-split distributions when no row is filtered), or at least
+ * rlt_categorical_workspace_size(r, vocab) (one workgroup per row).
  * A random row index outside [0, m) gives an all-NaN q_out row and proposes nothing.
  */
+size_t rlt_propose_drafts_workspace_size(int64_t m, int64_t r, int64_t vocab);
+
 int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_stride, int64_t m,
                        int64_t vocab, const int64_t* random_rows, int64_t r,
                        const float* temperature, const int64_t* top_k, const float* top_p,
@@ -222,13 +234,17 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
  * rows line up).  One launch: the argmax rows are extra workgroups of the
  * distribution launch.  Replaces vllm_rlt/worker/async_speculative.py:678-692
  * (target = logits.argmax(-1); p[v_ranks, v_offsets] = _probabilities(logits[v_rows],
- * ...)).  No workspace.  A random row index outside [0, m) gives an all-NaN p row.
+ * ...)).  A random row index outside [0, m) gives an all-NaN p row.  Workspace:
+ * rlt_probabilities_workspace_size(r, m, vocab) bytes (row-split form for calls
+ * that filter no row, the argmax rows as extra slices), or NULL (one workgroup per
+ * row).
  */
 int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t row_stride,
                              int64_t m, int64_t vocab, const int64_t* random_rows, int64_t r,
                              const float* temperature, const int64_t* top_k, const float* top_p,
                              int64_t max_top_k, int32_t apply_top_p, float* p_out,
-                             int64_t p_stride, int64_t* targets, hipStream_t stream);
+                             int64_t p_stride, int64_t* targets, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
 
 /*
  * The stochastic verify round in one call: targets = argmax of each of the
@@ -238,8 +254,13 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
  * rlt_speculative_accept; the draft rows' float32 row-sum partials are computed by
  * otherwise idle workgroups of the distribution launch, so the acceptance then sums
  * only p.  Replaces vllm_rlt/worker/async_speculative.py:678-692 (_verify) followed by
- * :727-734 (speculative_accept).  Workspace: rlt_speculative_accept_workspace_size.
+ * :727-734 (speculative_accept).  Workspace: rlt_verify_accept_workspace_size
+ * (row-split distributions when no row is filtered, the draft rows' partials as
+ * extra workgroups of its first launch), or at least
+ * rlt_speculative_accept_workspace_size (one workgroup per row).
  */
+size_t rlt_verify_accept_workspace_size(int64_t n, int32_t w1, int64_t vocab);
+
 int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t row_stride,
                       const float* temperature, const int64_t* top_k, const float* top_p,
                       int64_t max_top_k, int32_t apply_top_p, const int64_t* draft_tokens,

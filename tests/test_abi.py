@@ -32,6 +32,16 @@ def test_workspace_queries_are_host_only(pkg):
     lib = _lib.library()
     assert lib.rlt_speculative_accept_workspace_size(32, 4, 49152) > 0
     assert lib.rlt_categorical_workspace_size(8, 65536) > 0
+    # the row-split distributions: workspace for V up to 16 slices of 16384 columns
+    assert lib.rlt_probabilities_workspace_size(160, 0, 49152) > 0
+    assert lib.rlt_probabilities_workspace_size(160, 160, 49152) > \
+        lib.rlt_probabilities_workspace_size(160, 0, 49152)
+    assert lib.rlt_probabilities_workspace_size(8, 0, 262144) > 0
+    assert lib.rlt_probabilities_workspace_size(8, 0, 262145) == 0
+    assert lib.rlt_verify_accept_workspace_size(32, 4, 49152) > \
+        lib.rlt_speculative_accept_workspace_size(32, 4, 49152)
+    assert lib.rlt_propose_drafts_workspace_size(256, 32, 49152) > \
+        lib.rlt_categorical_workspace_size(32, 49152)
     # 160 rows x 16 heads x (512 blocks x 16 / 512 chunks) x (2 + 128) floats
     n = lib.rlt_paged_attention_workspace_size(160, 16, 128, 512, 16)
     assert n >= 160 * 16 * 16 * 130 * 4
@@ -89,20 +99,23 @@ def test_probability_and_greedy_entry_points_check_arguments(pkg):
     null, fake = ctypes.c_void_p(0), ctypes.c_void_p(16)
     # negative rows / row stride below V -> RLT_ERR_ARGUMENT (1)
     assert lib.rlt_batched_probabilities(null, 0, 10, -1, 10, null, null, null, 0, 0, null, 10,
-                                         null) == 1
+                                         null, 0, null) == 1
     assert lib.rlt_batched_probabilities(fake, 0, 5, 2, 10, fake, fake, fake, 0, 0, fake, 10,
-                                         null) == 1
+                                         null, 0, null) == 1
     # zero rows: nothing to launch
     assert lib.rlt_batched_probabilities(null, 0, 10, 0, 10, null, null, null, 0, 0, null, 10,
-                                         null) == 0
+                                         null, 0, null) == 0
     # missing pointers -> 1; V above 262144 -> RLT_ERR_UNSUPPORTED (2); fp8 logits -> 2
     assert lib.rlt_batched_probabilities(null, 0, 10, 2, 10, fake, fake, fake, 0, 0, fake, 10,
-                                         null) == 1
+                                         null, 0, null) == 1
     big = 262144 + 1
     assert lib.rlt_batched_probabilities(fake, 0, big, 2, big, fake, fake, fake, 0, 0, fake, big,
-                                         null) == 2
+                                         null, 0, null) == 2
     assert lib.rlt_batched_probabilities(fake, 3, 10, 2, 10, fake, fake, fake, 0, 0, fake, 10,
-                                         null) == 2
+                                         null, 0, null) == 2
+    # a workspace smaller than the row-split form's query -> RLT_ERR_WORKSPACE (3)
+    assert lib.rlt_batched_probabilities(fake, 0, 10, 2, 10, fake, fake, fake, 0, 0, fake, 10,
+                                         fake, 1, null) == 3
     assert lib.rlt_greedy_accept(null, null, null, 0, 10, -1, 4, 10, null, null, null, null) == 1
     assert lib.rlt_greedy_accept(fake, fake, fake, 0, 5, 2, 4, 10, fake, fake, fake, null) == 1
     assert lib.rlt_greedy_accept(fake, fake, fake, 3, 10, 2, 4, 10, fake, fake, fake, null) == 2

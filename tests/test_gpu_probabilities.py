@@ -445,3 +445,93 @@ def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1):
     assert torch.equal(p_o.cpu().view(torch.int32), want_p.view(n, w1 + 1, vocab).cpu().view(torch.int32))
     for a, b, name in zip(res, want, want._fields):
         assert torch.equal(a.cpu(), b.cpu()), name
+
+
+# ------------------------------------------------------------ row-split form
+
+def _probs_abi(dev, logits, t, k, p, plan, split, out=None):
+    """rlt_batched_probabilities through the C ABI: the row-split form (workspace of the
+    queried size) or the single-workgroup form (no workspace)."""
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    n, vocab = logits.shape
+    out = torch.full((n, vocab), -7.0, device=dev) if out is None else out
+    nbytes = lib.rlt_probabilities_workspace_size(n, 0, vocab) if split else 0
+    assert nbytes > 0 or not split
+    ws = _lib.workspace(nbytes, dev) if split else None
+    status = lib.rlt_batched_probabilities(
+        _lib.ptr(logits), _lib.dtype_code(logits.dtype), logits.stride(0), n, vocab,
+        _lib.ptr(t), _lib.ptr(k), _lib.ptr(p), plan["max_top_k"], int(plan["apply_top_p"]),
+        _lib.ptr(out), out.stride(0), _lib.ptr(ws), nbytes, _lib.stream_of(dev))
+    _lib.check(status, "rlt_batched_probabilities")
+    torch.cuda.synchronize(dev)
+    return out
+
+
+@pytest.mark.parametrize("name,n,vocab,dtype,stride_pad", [
+    ("config4-rows", 80, 65536, torch.float32, 0),    # 64 columns per thread
+    ("config5-rows", 1280, 65536, torch.float32, 0),
+    ("config1-q", 128, 49152, torch.float32, 0),       # 16 per thread
+    ("few-rows", 8, 65536, torch.bfloat16, 0),
+    ("tiny", 5, 1, torch.float32, 0),
+    ("small", 7, 17, torch.float16, 0),
+    ("odd-vocab", 24, 4097, torch.float32, 0),        # scalar loads (V % 4 != 0)
+    ("odd-stride", 24, 3000, torch.float16, 3),       # scalar loads (row stride % 4 != 0)
+    ("big-vocab", 6, 151936, torch.float32, 0),
+    ("max-vocab", 3, 262144, torch.bfloat16, 0),
+])
+def test_split_form_matches_single_workgroup_form(pkg, dev, name, n, vocab, dtype, stride_pad):
+    """Calls that filter no row run the row-split form when given a workspace: the same
+    values as the single-workgroup form (their float64 totals are summed in different
+    orders: 1e-6 relative), NaN rows alike, and the oracle's values."""
+    _say("split vs single", name)
+    g = torch.Generator().manual_seed(zlib.crc32(name.encode()))
+    scale = torch.tensor([3.0, 0.5, 6.0, 1e-3, 2.0, 30.0])[torch.arange(n) % 6][:, None]
+    base = torch.randn(n, vocab + stride_pad, generator=g) * scale
+    logits = base.to(dtype).to(dev)[:, :vocab]
+    tt = torch.tensor([0.7, 1.0, 0.5, 1.0, 1.3, 0.9])[torch.arange(n) % 6]
+    tk = torch.full((n,), -1, dtype=torch.int64)
+    tp = torch.ones(n)
+    if n > 2:
+        logits[2, vocab // 3] = float("nan")  # a NaN row
+    if n > 4:
+        logits[4] = -torch.inf                # no finite logit: NaN row
+    plan = {"max_top_k": 0, "apply_top_p": False}
+    args = [x.to(dev) for x in (tt, tk, tp)]
+    a = _probs_abi(dev, logits, *args, plan, split=True).cpu()
+    b = _probs_abi(dev, logits, *args, plan, split=False).cpu()
+    assert torch.equal(a.isnan(), b.isnan())
+    torch.testing.assert_close(a, b, atol=0, rtol=1e-6, equal_nan=True)
+    # against float64 softmax(l / T) (torch's float32 total drifts past 1e-5 at these
+    # widths), and against the oracle where its own total is accurate
+    sel = [i for i in range(min(n, 6)) if i not in (2, 4)]
+    x64 = logits[sel].double().cpu() / tt[sel].double()[:, None]
+    torch.testing.assert_close(a[sel].double(), x64.softmax(-1), atol=ATOL, rtol=RTOL)
+    if vocab <= 65536:
+        want = osamp.batched_probabilities(logits[sel].float().cpu(), tt[sel], tk[sel], tp[sel], **plan)
+        torch.testing.assert_close(a[sel], want, atol=ATOL, rtol=RTOL)
+    if n > 4:
+        assert torch.isnan(a[2]).all() and torch.isnan(a[4]).all()
+
+
+def test_split_form_output_stride_and_filtered_calls(pkg, dev):
+    """Output rows wider than V keep their columns past V; a filtering call ignores the
+    workspace and runs the single-workgroup form (bitwise equal)."""
+    _say("split output stride")
+    g = torch.Generator().manual_seed(5)
+    n, vocab = 10, 12000
+    logits = (torch.randn(n, vocab, generator=g) * 3).to(dev)
+    t = torch.full((n,), 0.8, device=dev)
+    k = torch.full((n,), -1, dtype=torch.int64, device=dev)
+    p = torch.full((n,), 0.9, device=dev)
+    plan = {"max_top_k": 0, "apply_top_p": False}
+    wide = torch.full((n, vocab + 5), -7.0, device=dev)
+    a = _probs_abi(dev, logits, t, k, p, plan, split=True, out=wide)
+    assert bool((a[:, vocab:] == -7.0).all())
+    b = _probs_abi(dev, logits, t, k, p, plan, split=False)
+    torch.testing.assert_close(a[:, :vocab], b, atol=0, rtol=1e-6)
+    plan = {"max_top_k": 0, "apply_top_p": True}
+    a = _probs_abi(dev, logits, t, k, p, plan, split=True)
+    b = _probs_abi(dev, logits, t, k, p, plan, split=False)
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))

@@ -79,13 +79,17 @@ _SIGNATURES = {
     "rlt_categorical": (ctypes.c_int, [_p, _p, _i64, _i64, _p, _p, _p, _sz, _p]),
     "rlt_row_mass_workspace_size": (_sz, [_i64, _i64]),
     "rlt_row_mass_f32": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _sz, _p]),
+    "rlt_probabilities_workspace_size": (_sz, [_i64, _i64, _i64]),
     "rlt_batched_probabilities": (ctypes.c_int, [
-        _p, _i32, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _i64, _p]),
+        _p, _i32, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
+    "rlt_propose_drafts_workspace_size": (_sz, [_i64, _i64, _i64]),
     "rlt_propose_drafts": (ctypes.c_int, [
         _p, _i32, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _i64, _p, _p, _sz,
         _p]),
     "rlt_verify_distributions": (ctypes.c_int, [
-        _p, _i32, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _p, _i64, _p, _p]),
+        _p, _i32, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _p, _i64, _p, _p, _sz,
+        _p]),
+    "rlt_verify_accept_workspace_size": (_sz, [_i64, _i32, _i64]),
     "rlt_verify_accept": (ctypes.c_int, [
         _p, _i32, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _i64, _i32, _i64, _p, _p, _p,
         _p, _p, _p, _p, _sz, _p]),

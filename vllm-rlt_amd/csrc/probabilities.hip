@@ -52,6 +52,7 @@
 #include "rlt_mi355x.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace {
 
@@ -131,6 +132,8 @@ __device__ __forceinline__ T wave_sum(T v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, RLT_WAVE);
   return v;
 }
+
+#include "probs_split.h"
 
 template <int CAP>
 struct SharedT {
@@ -853,9 +856,8 @@ template <int DT, int NREG, int NLDS, bool kTail = false>
 void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_src,
                   int64_t row_stride, int V, const float* temperature, const int64_t* top_k,
                   const float* top_p, int max_top_k, int apply_top_p, float* out,
-                  int64_t out_stride, hipStream_t stream, int64_t* argmax_out = nullptr,
-                  int64_t argmax_rows = 0, const float* qm_src = nullptr, int64_t qm_rows = 0,
-                  float* qm_out = nullptr) {
+                  int64_t out_stride, hipStream_t stream, int64_t* argmax_out,
+                  int64_t argmax_rows, const float* qm_src, int64_t qm_rows, float* qm_out) {
   const cascade::RowGeom geo = cascade::row_geom(V);
   const int64_t per_block = kThreads / cascade::kGroupThreads;
   const int64_t qm_blocks = qm_src ? (qm_rows * geo.groups + per_block - 1) / per_block : 0;
@@ -898,6 +900,88 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
 #undef RLT_PROBS_CASE
 }
 
+// ------------------------------------------------------------------ split form (host)
+
+// The split form (probs_split.h) serves calls that filter no row (max_top_k == 0 and
+// no top-p): E elements per thread, the largest of {16, 32, 64} that still gives
+// >= 1024 workgroups, else the smallest whose slice count fits kMaxSlices.
+struct SplitPlan {
+  int E, S;
+};
+
+bool split_plan(int64_t n_dist, int V, SplitPlan& p) {
+  const int options[3] = {16, 32, 64};
+  int pick = 0;
+  for (int i = 0; i < 3; ++i) {
+    const int64_t L = (int64_t)split::kThreads * options[i];
+    const int64_t S = (V + L - 1) / L;
+    if (S > split::kMaxSlices) continue;
+    if (!pick || n_dist * S >= 1024) pick = options[i];
+  }
+  if (!pick) return false;
+  p.E = pick;
+  const int64_t L = (int64_t)split::kThreads * pick;
+  p.S = (int)((V + L - 1) / L);
+  return true;
+}
+
+size_t split_bytes(int64_t n_dist, int64_t n_arg) {
+  return rlt_align_up((size_t)(n_dist + n_arg) * split::kMaxSlices * sizeof(split::SliceStat), 256);
+}
+
+// The split form's two launches.  targets: argmax outputs -- of the distribution rows
+// when fused, else of logits rows [0, n_arg).
+template <int DT, int E>
+void launch_split_e(const SplitPlan& pl, int64_t n_dist, const void* logits, const int64_t* rows,
+                    int64_t n_src, int64_t row_stride, int V, const float* temperature,
+                    float* out, int64_t out_stride, hipStream_t stream, int64_t* targets,
+                    int64_t n_arg, bool fused, const float* qm_src, int64_t qm_rows,
+                    float* qm_out, void* ws) {
+  split::View v;
+  v.stats = (split::SliceStat*)ws;
+  v.S = pl.S;
+  v.L = split::kThreads * E;
+  v.n_dist = n_dist;
+  v.n_arg = fused ? 0 : n_arg;
+  v.targets = targets;
+  v.fused = fused;
+  const int esz = DT == RLT_F32 ? 4 : 2;
+  const bool vec = V % 4 == 0 && row_stride % 4 == 0 && (uintptr_t)logits % (4 * esz) == 0;
+  const bool out_vec = out_stride % 4 == 0 && (uintptr_t)out % 16 == 0;
+  const cascade::RowGeom geo = cascade::row_geom(V);
+  const int64_t per_block = split::kThreads / cascade::kGroupThreads;
+  const int64_t qm_blocks = qm_src ? (qm_rows * geo.groups + per_block - 1) / per_block : 0;
+  const int64_t g1 = (n_dist + v.n_arg) * pl.S + qm_blocks;
+  const int64_t g2 = n_dist * pl.S + (v.n_arg + split::kThreads - 1) / split::kThreads;
+#define RLT_SPLIT_LAUNCH(VEC)                                                                  \
+  hipLaunchKernelGGL((split::rlt_probs_slice_kernel<DT, E, VEC>), dim3((unsigned)g1),          \
+                     dim3(split::kThreads), 0, stream, logits, rows, n_src, row_stride, V,       \
+                     temperature, v, qm_src, qm_rows, qm_out);                                   \
+  hipLaunchKernelGGL((split::rlt_probs_write_kernel<DT, E, VEC>), dim3((unsigned)g2),          \
+                     dim3(split::kThreads), 0, stream, logits, rows, n_src, row_stride, V,       \
+                     temperature, v, out, out_stride, (int)out_vec)
+  if (vec) {
+    RLT_SPLIT_LAUNCH(true);
+  } else {
+    RLT_SPLIT_LAUNCH(false);
+  }
+#undef RLT_SPLIT_LAUNCH
+}
+
+template <int DT>
+void launch_split(const SplitPlan& pl, int64_t n_dist, const void* logits, const int64_t* rows,
+                  int64_t n_src, int64_t row_stride, int V, const float* temperature, float* out,
+                  int64_t out_stride, hipStream_t stream, int64_t* targets, int64_t n_arg,
+                  bool fused, const float* qm_src, int64_t qm_rows, float* qm_out, void* ws) {
+#define RLT_SPLIT_E(EE)                                                                         \
+  launch_split_e<DT, EE>(pl, n_dist, logits, rows, n_src, row_stride, V, temperature, out,      \
+                         out_stride, stream, targets, n_arg, fused, qm_src, qm_rows, qm_out, ws)
+  if (pl.E == 16) RLT_SPLIT_E(16);
+  else if (pl.E == 32) RLT_SPLIT_E(32);
+  else RLT_SPLIT_E(64);
+#undef RLT_SPLIT_E
+}
+
 }  // namespace
 
 // spec_sampling.hip: the acceptance workspace's q-row partials, and the acceptance
@@ -916,11 +1000,19 @@ int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u,
 
 extern "C" {
 
+size_t rlt_probabilities_workspace_size(int64_t rows, int64_t argmax_rows, int64_t vocab) {
+  SplitPlan pl;
+  if (rows < 0 || argmax_rows < 0 || vocab < 1 || vocab > 0x7fffffff ||
+      !split_plan(rows, (int)vocab, pl))
+    return 0;
+  return split_bytes(rows, argmax_rows);
+}
+
 int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t row_stride,
                               int64_t n, int64_t vocab, const float* temperature,
                               const int64_t* top_k, const float* top_p, int64_t max_top_k,
                               int32_t apply_top_p, float* out, int64_t out_stride,
-                              hipStream_t stream) {
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (n < 0 || vocab < 1 || max_top_k < 0 || row_stride < vocab || out_stride < vocab)
     return RLT_ERR_ARGUMENT;
   if (n == 0) return RLT_OK;
@@ -928,22 +1020,26 @@ int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t 
   if (vocab > (int64_t)kMaxStreamChunks * kThreads || n > 0x7fffffff) return RLT_ERR_UNSUPPORTED;
   const int mtk = max_top_k > vocab ? (int)vocab : (int)max_top_k;
   const int V = (int)vocab;
+  // the row-split form for calls that filter no row, when a workspace is given
+  SplitPlan pl;
+  const bool sp = workspace && mtk == 0 && !apply_top_p && split_plan(n, V, pl);
+  if (sp && workspace_bytes < split_bytes(n, 0)) return RLT_ERR_WORKSPACE;
+#define RLT_PROBS(DT)                                                                          \
+  do {                                                                                         \
+    if (sp)                                                                                    \
+      launch_split<DT>(pl, n, logits, nullptr, n, row_stride, V, temperature, out, out_stride, \
+                       stream, nullptr, 0, false, nullptr, 0, nullptr, workspace);             \
+    else                                                                                       \
+      dispatch_probs<DT>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk, \
+                         apply_top_p != 0, out, out_stride, stream);                           \
+  } while (0)
   switch (logits_dtype) {
-    case RLT_F32:
-      dispatch_probs<RLT_F32>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk,
-                              apply_top_p != 0, out, out_stride, stream);
-      break;
-    case RLT_BF16:
-      dispatch_probs<RLT_BF16>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk,
-                               apply_top_p != 0, out, out_stride, stream);
-      break;
-    case RLT_F16:
-      dispatch_probs<RLT_F16>(n, logits, nullptr, n, row_stride, V, temperature, top_k, top_p, mtk,
-                              apply_top_p != 0, out, out_stride, stream);
-      break;
-    default:
-      return RLT_ERR_UNSUPPORTED;
+    case RLT_F32: RLT_PROBS(RLT_F32); break;
+    case RLT_BF16: RLT_PROBS(RLT_BF16); break;
+    case RLT_F16: RLT_PROBS(RLT_F16); break;
+    default: return RLT_ERR_UNSUPPORTED;
   }
+#undef RLT_PROBS
   return rlt_launch_status();
 }
 
@@ -981,6 +1077,12 @@ int rlt_greedy_accept(const int64_t* draft_tokens, const int64_t* drafts, const 
   return rlt_launch_status();
 }
 
+size_t rlt_propose_drafts_workspace_size(int64_t m, int64_t r, int64_t vocab) {
+  if (m < 0 || r < 0) return 0;
+  return rlt_align_up(r > 0 ? rlt_categorical_workspace_size(r, vocab) : 0, 256) +
+         (r > 0 ? rlt_probabilities_workspace_size(r, m, vocab) : 0);
+}
+
 int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_stride, int64_t m,
                        int64_t vocab, const int64_t* random_rows, int64_t r,
                        const float* temperature, const int64_t* top_k, const float* top_p,
@@ -1000,6 +1102,11 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
     return RLT_ERR_WORKSPACE;
   const int V = (int)vocab;
   const int mtk = max_top_k > vocab ? V : (int)max_top_k;
+  // the split form when the workspace holds its part too
+  const size_t cat_bytes = r > 0 ? rlt_align_up(rlt_categorical_workspace_size(r, vocab), 256) : 0;
+  SplitPlan pl;
+  const bool sp = r > 0 && mtk == 0 && !apply_top_p && split_plan(r, V, pl) &&
+                  workspace_bytes >= cat_bytes + split_bytes(r, m);
   // greedy proposals for every row (extra workgroups of the distribution launch when
   // there are random rows), then the random rows' draws
 #define RLT_PROPOSE(DT)                                                                       \
@@ -1007,6 +1114,10 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
     if (r == 0)                                                                               \
       hipLaunchKernelGGL(rlt_argmax_rows_kernel<DT>, dim3((unsigned)m), dim3(kThreads), 0,    \
                          stream, logits, row_stride, V, proposed);                            \
+    else if (sp)                                                                              \
+      launch_split<DT>(pl, r, logits, random_rows, m, row_stride, V, temperature, q_out,      \
+                       q_stride, stream, proposed, m, false, nullptr, 0, nullptr,             \
+                       (char*)workspace + cat_bytes);                                         \
     else                                                                                      \
       dispatch_probs<DT>(r, logits, random_rows, m, row_stride, V, temperature, top_k, top_p, \
                          mtk, apply_top_p != 0, q_out, q_stride, stream, proposed, m);        \
@@ -1029,7 +1140,8 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
                              int64_t m, int64_t vocab, const int64_t* random_rows, int64_t r,
                              const float* temperature, const int64_t* top_k, const float* top_p,
                              int64_t max_top_k, int32_t apply_top_p, float* p_out,
-                             int64_t p_stride, int64_t* targets, hipStream_t stream) {
+                             int64_t p_stride, int64_t* targets, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
   if (m < 0 || r < 0 || vocab < 1 || vocab > 0x7fffffff || row_stride < vocab ||
       max_top_k < 0 || (r > 0 && p_stride < vocab))
     return RLT_ERR_ARGUMENT;
@@ -1041,12 +1153,19 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
     return RLT_ERR_UNSUPPORTED;
   const int V = (int)vocab;
   const int mtk = max_top_k > vocab ? V : (int)max_top_k;
-  // targets of every row as extra workgroups of the distribution launch
+  SplitPlan pl;
+  const bool sp = r > 0 && workspace && mtk == 0 && !apply_top_p && split_plan(r, V, pl);
+  if (sp && workspace_bytes < split_bytes(r, m)) return RLT_ERR_WORKSPACE;
+  // targets of every row as extra workgroups of the distribution launch (split form:
+  // extra slices of launch 1, finished by launch 2 or 3)
 #define RLT_VERIFY(DT)                                                                        \
   do {                                                                                        \
     if (r == 0)                                                                               \
       hipLaunchKernelGGL(rlt_argmax_rows_kernel<DT>, dim3((unsigned)m), dim3(kThreads), 0,    \
                          stream, logits, row_stride, V, targets);                             \
+    else if (sp)                                                                              \
+      launch_split<DT>(pl, r, logits, random_rows, m, row_stride, V, temperature, p_out,      \
+                       p_stride, stream, targets, m, false, nullptr, 0, nullptr, workspace);  \
     else                                                                                      \
       dispatch_probs<DT>(r, logits, random_rows, m, row_stride, V, temperature, top_k, top_p, \
                          mtk, apply_top_p != 0, p_out, p_stride, stream, targets, m);         \
@@ -1059,6 +1178,12 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
   }
 #undef RLT_VERIFY
   return rlt_launch_status();
+}
+
+size_t rlt_verify_accept_workspace_size(int64_t n, int32_t w1, int64_t vocab) {
+  if (n < 0 || w1 < 0) return 0;
+  return rlt_align_up(rlt_speculative_accept_workspace_size(n, w1, vocab), 256) +
+         rlt_probabilities_workspace_size(n * (w1 + 1), 0, vocab);
 }
 
 int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t row_stride,
@@ -1085,12 +1210,26 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
   const int64_t q_rows = n * (int64_t)w1;
   const int V = (int)vocab;
   const int mtk = max_top_k > vocab ? V : (int)max_top_k;
-  // one launch: distributions of every verify row, their argmax targets, and the
-  // draft rows' row-sum partials; then the acceptance sums only p
+  // the split form when the workspace holds its part too
+  const size_t acc_bytes =
+      rlt_align_up(rlt_speculative_accept_workspace_size(n, w1, vocab), 256);
+  SplitPlan pl;
+  const bool sp = mtk == 0 && !apply_top_p && split_plan(rows, V, pl) &&
+                  workspace_bytes >= acc_bytes + split_bytes(rows, 0);
+  // distributions of every verify row, their argmax targets, and the draft rows'
+  // row-sum partials (one launch, or the split form's launches); then the acceptance
+  // sums only p
 #define RLT_VERIFY_ACCEPT(DT)                                                                 \
-  dispatch_probs<DT>(rows, target_logits, nullptr, rows, row_stride, V, temperature, top_k,    \
-                     top_p, mtk, apply_top_p != 0, p_out, vocab, stream, targets, rows,        \
-                     q_rows > 0 ? q : nullptr, q_rows, qm_out)
+  do {                                                                                        \
+    if (sp)                                                                                   \
+      launch_split<DT>(pl, rows, target_logits, nullptr, rows, row_stride, V, temperature,    \
+                       p_out, vocab, stream, targets, rows, true, q_rows > 0 ? q : nullptr,   \
+                       q_rows, qm_out, (char*)workspace + acc_bytes);                         \
+    else                                                                                      \
+      dispatch_probs<DT>(rows, target_logits, nullptr, rows, row_stride, V, temperature,      \
+                         top_k, top_p, mtk, apply_top_p != 0, p_out, vocab, stream, targets,  \
+                         rows, q_rows > 0 ? q : nullptr, q_rows, qm_out);                     \
+  } while (0)
   switch (logits_dtype) {
     case RLT_F32: RLT_VERIFY_ACCEPT(RLT_F32); break;
     case RLT_BF16: RLT_VERIFY_ACCEPT(RLT_BF16); break;

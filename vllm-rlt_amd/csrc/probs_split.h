@@ -1,0 +1,355 @@
+// Row-split form of the sampling-distribution kernel for calls without top-k or
+// top-p (gfx950).
+//
+// rlt_probs_kernel (probabilities.hip) gives each logits row one 1024-thread
+// workgroup, so a launch of n rows keeps at most n CUs busy, every row streams at the
+// rate one CU pulls, and rows beyond one per CU run in further rounds.  Without a
+// filter a row needs no selection, only its max and total, so the split form
+// spreads each row over S workgroups of kThreads threads, each owning one contiguous
+// slice (slice length L = kThreads * E, E elements per thread in registers), in two
+// launches:
+//
+//   1. rlt_probs_slice_kernel, one workgroup per (row, slice): the slice max m_s, NaN
+//      flag, argmax key and float64 mass z_s = sum exp2((l - m_s) c) relative to the
+//      slice max (c = log2(e) / T);
+//   2. rlt_probs_write_kernel, one workgroup per (row, slice): the row max lmax and
+//      total z = sum_s z_s 2^((m_s - lmax) c) (float64) from the row's slices, then
+//      out = exp2((l - lmax) c) / z for the slice, NaN rows as NaN.
+//
+// The outputs are those of the single-workgroup form up to the order of the float64
+// total's summation.  Argmax-only rows (greedy targets next to the distributions)
+// are extra slices of launch 1, finished in launch 2; the acceptance sampler's draft
+// row partial sums can ride as extra workgroups of launch 1.  Included inside
+// probabilities.hip's anonymous namespace, after the order-key helpers.
+
+#pragma once
+
+namespace split {
+
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / RLT_WAVE;
+constexpr int kMaxSlices = 16;
+
+struct SliceStat {
+  float m;                  // slice max logit (NaN ignored)
+  uint32_t nan;             // the slice holds a NaN
+  double z;                 // sum of exp2((l - m) c) (0 when m is not finite)
+  unsigned long long best;  // argmax key: (order key, NaN highest) << 32 | ~column
+};
+
+// Workspace view and the call's shape.
+struct View {
+  SliceStat* stats;  // [(n_dist + n_arg) * S]
+  int S, L;
+  int64_t n_dist;    // distribution rows
+  int64_t n_arg;     // argmax-only rows (their statistics follow)
+  int64_t* targets;  // argmax outputs, or nullptr
+  int fused;         // distribution row r's argmax goes to targets[r]
+};
+
+__device__ __forceinline__ int64_t argmax_column(unsigned long long best) {
+  return (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+}
+
+// targets[i] for argmax-only row i from its slices' keys (one thread per row).
+__device__ __forceinline__ void finish_argmax_row(const View& v, int64_t i) {
+  if (i >= v.n_arg || !v.targets) return;
+  const SliceStat* st = v.stats + (v.n_dist + i) * v.S;
+  unsigned long long best = 0;
+  for (int s = 0; s < v.S; ++s) best = st[s].best > best ? st[s].best : best;
+  v.targets[i] = argmax_column(best);
+}
+
+// ---------------------------------------------------------------- slice loads
+
+// Element j of thread t in slice s: column s L + 4 (kThreads (j / 4) + t) + j % 4, so
+// every group of four is one 16-byte (fp32) or 8-byte (16-bit) load.
+template <int E>
+__device__ __forceinline__ int64_t slice_col(int64_t c0, int j) {
+  return c0 + 4 * ((int64_t)kThreads * (j >> 2) + threadIdx.x) + (j & 3);
+}
+
+// kVec: V % 4 == 0 and the row base aligned to four elements.  Padding reads NaN.
+template <int DT, int E, bool kVec>
+__device__ __forceinline__ void load_slice(const void* __restrict__ src, int64_t c0, int V,
+                                           float (&x)[E]) {
+  static_assert(E % 4 == 0, "four elements per load");
+#pragma unroll
+  for (int q = 0; q < E / 4; ++q) {
+    const int64_t col = slice_col<E>(c0, 4 * q);
+    if (kVec) {
+      if (col < V) {
+        if (DT == RLT_F32) {
+          const float4 f = *(const float4*)((const float*)src + col);
+          x[4 * q] = f.x;
+          x[4 * q + 1] = f.y;
+          x[4 * q + 2] = f.z;
+          x[4 * q + 3] = f.w;
+        } else {
+          const uint2 u = *(const uint2*)((const uint16_t*)src + col);
+          const uint16_t h[4] = {(uint16_t)(u.x & 0xffff), (uint16_t)(u.x >> 16),
+                                 (uint16_t)(u.y & 0xffff), (uint16_t)(u.y >> 16)};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            x[4 * q + k] = DT == RLT_BF16 ? bf16_bits_to_f32(h[k]) : f16_bits_to_f32(h[k]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[4 * q + k] = NAN;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        x[4 * q + k] = col + k < V ? load_as_f32<DT>(src, col + k) : NAN;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- block reductions
+
+struct ReduceShared {
+  float f[kWaves];
+  uint32_t u[kWaves];
+  uint32_t flag[kWaves];
+  double d[kWaves];
+};
+
+// Block max of a float and OR of a flag (every thread gets both).
+__device__ __forceinline__ void block_max_or(ReduceShared& sh, float& fm, bool& flag) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int off = 32; off >= 1; off >>= 1) fm = fmaxf(fm, __shfl_xor(fm, off, RLT_WAVE));
+  const bool any = __ballot(flag) != 0;
+  if (lane == 0) {
+    sh.f[w] = fm;
+    sh.flag[w] = any;
+  }
+  __syncthreads();
+  fm = sh.f[0];
+  flag = sh.flag[0] != 0;
+  for (int i = 1; i < kWaves; ++i) {
+    fm = fmaxf(fm, sh.f[i]);
+    flag |= sh.flag[i] != 0;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t block_min_u32(ReduceShared& sh, uint32_t x) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int off = 32; off >= 1; off >>= 1) x = min(x, (uint32_t)__shfl_xor(x, off, RLT_WAVE));
+  if (lane == 0) sh.u[w] = x;
+  __syncthreads();
+  x = sh.u[0];
+  for (int i = 1; i < kWaves; ++i) x = min(x, sh.u[i]);
+  __syncthreads();
+  return x;
+}
+
+// float64 sum in a fixed order (lane tree, then waves in order).
+__device__ __forceinline__ double block_sum(ReduceShared& sh, double x) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, RLT_WAVE);
+  if (lane == 0) sh.d[w] = x;
+  __syncthreads();
+  double s = sh.d[0];
+  for (int i = 1; i < kWaves; ++i) s += sh.d[i];
+  __syncthreads();
+  return s;
+}
+
+// ---------------------------------------------------------------- launch 1
+
+struct SliceShared {
+  ReduceShared red;
+};
+
+// Column of element j of this thread: base = c0 + 4 t (32 bits: V < 2^31).
+template <int E>
+__device__ __forceinline__ uint32_t elem_col(uint32_t base, int j) {
+  return base + (uint32_t)(4 * kThreads * (j >> 2) + (j & 3));
+}
+
+// One slice's statistics.  kFull: every element of the slice is a column of the row
+// (no bounds tests).
+template <int DT, int E, bool kVec, bool kFull>
+__device__ __forceinline__ void slice_body(SliceShared& sh, const void* __restrict__ src, int64_t c0,
+                                           int V, bool dist, bool need_argmax, float temp,
+                                           SliceStat* __restrict__ out) {
+  const int t = threadIdx.x;
+  const uint32_t base = (uint32_t)(c0 + 4 * t);
+  auto ok = [&](int j) { return kFull || (int64_t)elem_col<E>(base, j) < V; };
+  float x[E];
+  load_slice<DT, E, kVec>(src, c0, V, x);
+  float m = -INFINITY;
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    if (!ok(j)) continue;
+    nan |= x[j] != x[j];
+    m = fmaxf(m, x[j]);  // NaN ignored
+  }
+  block_max_or(sh.red, m, nan);
+  // argmax key: the first column holding the max (the first NaN when there is one)
+  unsigned long long best = 0;
+  if (need_argmax) {
+    uint32_t col = 0xffffffffu;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const bool hit = ok(j) && (nan ? x[j] != x[j] : x[j] == m);
+      col = hit ? min(col, elem_col<E>(base, j)) : col;
+    }
+    col = block_min_u32(sh.red, col);
+    const uint32_t key = nan ? 0xffffffffu : order_key(m);
+    best = ((unsigned long long)key << 32) | (0xffffffffu - col);
+  }
+  double z = 0.0;
+  if (dist) {
+    const float c = 1.44269504088896341f / temp;
+    const bool finite = isfinite(m) && isfinite(c) && !nan;
+    double zs = 0.0;
+    if (finite) {
+#pragma unroll
+      for (int j = 0; j < E; ++j)
+        if (ok(j)) zs += (double)__builtin_amdgcn_exp2f((x[j] - m) * c);
+    }
+    z = block_sum(sh.red, zs);
+    if (!finite) z = 0.0;
+  }
+  if (t == 0) {
+    out->m = m;
+    out->nan = nan;
+    out->z = z;
+    out->best = best;
+  }
+}
+
+// Workgroups [0, (n_dist + n_arg) S): slice statistics of distribution row r < n_dist
+// (logits row rows[r], or r) or of argmax-only logits row r - n_dist; then the draft
+// rows' float32 row-sum partials of the acceptance sampler (two 8192-float groups per
+// workgroup) when qm_src is set.
+template <int DT, int E, bool kVec>
+__global__ __launch_bounds__(kThreads) void rlt_probs_slice_kernel(
+    const void* __restrict__ logits, const int64_t* __restrict__ rows, int64_t n_src,
+    int64_t row_stride, int V, const float* __restrict__ temperature, View v,
+    const float* __restrict__ qm_src, int64_t qm_rows, float* __restrict__ qm_out) {
+  __shared__ union {
+    SliceShared s;
+    cascade::ChunkSums cs[kThreads / cascade::kGroupThreads];
+  } lds;
+  const int t = threadIdx.x;
+  const int64_t n_slices = (v.n_dist + v.n_arg) * v.S;
+  if ((int64_t)blockIdx.x >= n_slices) {
+    const cascade::RowGeom geo = cascade::row_geom(V);
+    const int sub = t / cascade::kGroupThreads, st = t % cascade::kGroupThreads;
+    const int64_t task = ((int64_t)blockIdx.x - n_slices) * (kThreads / cascade::kGroupThreads) + sub;
+    const int64_t qrow = geo.groups > 0 ? task / geo.groups : qm_rows;
+    const int64_t g = geo.groups > 0 ? task % geo.groups : 0;
+    const bool live = qrow < qm_rows;
+    const float* x = qm_src + qrow * V;
+    if (live) {
+      if (V % 4 == 0 && (uintptr_t)qm_src % 16 == 0)
+        cascade::group_chunk_sums<true>(x, g, geo.full_chunks, st, lds.cs[sub]);
+      else
+        cascade::group_chunk_sums<false>(x, g, geo.full_chunks, st, lds.cs[sub]);
+    }
+    __syncthreads();
+    if (live)
+      cascade::group_stream_sums(g, geo.full_chunks, st, lds.cs[sub],
+                                 qm_out + (qrow * geo.groups + g) * cascade::kStreams);
+    return;
+  }
+  const int64_t r = (int64_t)blockIdx.x / v.S;
+  const int s = (int)((int64_t)blockIdx.x % v.S);
+  const bool dist = r < v.n_dist;
+  int64_t src_r = dist ? (rows ? rows[r] : r) : r - v.n_dist;
+  if (src_r < 0 || src_r >= n_src) src_r = 0;  // the row is written as NaN (launch 2)
+  const int64_t c0 = (int64_t)s * v.L;
+  const void* src = (const char*)logits + src_r * row_stride * (DT == RLT_F32 ? 4 : 2);
+  const bool need_argmax = !dist || (v.fused && v.targets);
+  const float temp = dist ? temperature[r] : 1.f;
+  SliceStat* out = v.stats + blockIdx.x;
+  if (c0 + v.L <= V)
+    slice_body<DT, E, kVec, true>(lds.s, src, c0, V, dist, need_argmax, temp, out);
+  else
+    slice_body<DT, E, kVec, false>(lds.s, src, c0, V, dist, need_argmax, temp, out);
+}
+
+// ---------------------------------------------------------------- launch 2
+
+template <int DT, int E, bool kVec, bool kFull>
+__device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t c0, int V,
+                                           bool nan_row, float lmax, float c, float inv,
+                                           float* __restrict__ dst, bool out_vec) {
+  const uint32_t base = (uint32_t)(c0 + 4 * threadIdx.x);
+  float y[E];
+  if (nan_row) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) y[j] = NAN;
+  } else {
+    float x[E];
+    load_slice<DT, E, kVec>(src, c0, V, x);
+#pragma unroll
+    for (int j = 0; j < E; ++j) y[j] = __builtin_amdgcn_exp2f((x[j] - lmax) * c) * inv;
+  }
+#pragma unroll
+  for (int q = 0; q < E / 4; ++q) {
+    const uint32_t col = elem_col<E>(base, 4 * q);
+    if (kVec && out_vec) {
+      if (kFull || (int64_t)col < V)
+        *(float4*)(dst + col) = make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (kFull || (int64_t)col + k < V) dst[col + k] = y[4 * q + k];
+    }
+  }
+}
+
+// Workgroups [0, n_dist S): slice s of distribution row r, normalized by the row's
+// total from its slices; workgroups past n_dist S finish the argmax-only rows (one
+// thread per row).  out_vec: out rows aligned to four floats (vector stores).
+template <int DT, int E, bool kVec>
+__global__ __launch_bounds__(kThreads) void rlt_probs_write_kernel(
+    const void* __restrict__ logits, const int64_t* __restrict__ rows, int64_t n_src,
+    int64_t row_stride, int V, const float* __restrict__ temperature, View v,
+    float* __restrict__ out, int64_t out_stride, int out_vec) {
+  const int t = threadIdx.x;
+  const int64_t n_slices = v.n_dist * v.S;
+  if ((int64_t)blockIdx.x >= n_slices) {
+    finish_argmax_row(v, ((int64_t)blockIdx.x - n_slices) * kThreads + t);
+    return;
+  }
+  const int64_t r = (int64_t)blockIdx.x / v.S;
+  const int s = (int)((int64_t)blockIdx.x % v.S);
+  const int64_t src_r = rows ? rows[r] : r;
+  const bool src_ok = src_r >= 0 && src_r < n_src;
+  const SliceStat* st = v.stats + r * v.S;
+  float lmax = -INFINITY;
+  bool bad = false;
+  unsigned long long best = 0;
+  for (int i = 0; i < v.S; ++i) {
+    lmax = fmaxf(lmax, st[i].m);
+    bad |= st[i].nan != 0;
+    best = st[i].best > best ? st[i].best : best;
+  }
+  if (v.fused && v.targets && s == 0 && t == 0) v.targets[r] = argmax_column(best);
+  const float temp = temperature[r];
+  const float c = 1.44269504088896341f / temp;
+  const bool nan_row = bad || !src_ok || !isfinite(lmax) || !(temp > 0.f) || !isfinite(c);
+  float inv = 0.f;
+  if (!nan_row) {
+    double z = 0.0;
+    for (int i = 0; i < v.S; ++i) z += st[i].z * exp2(((double)st[i].m - (double)lmax) * (double)c);
+    inv = (float)(1.0 / z);
+  }
+  const int64_t c0 = (int64_t)s * v.L;
+  const void* src =
+      (const char*)logits + (src_ok ? src_r : 0) * row_stride * (DT == RLT_F32 ? 4 : 2);
+  float* dst = out + r * out_stride;
+  if (c0 + v.L <= V)
+    write_body<DT, E, kVec, true>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0);
+  else
+    write_body<DT, E, kVec, false>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0);
+}
+
+}  // namespace split

@@ -236,10 +236,13 @@ Tensor spec_probs(const Tensor& logits, const Tensor& temperature, const Tensor&
   const Tensor x = logit_rows(logits);
   const Tensor t = as(temperature, at::kFloat), k = as(top_k, at::kLong), p = as(top_p, at::kFloat);
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  // row-split form (several workgroups per row) when it applies to this vocabulary
+  const size_t nbytes = rlt_probabilities_workspace_size(n, 0, vocab);
+  const Tensor ws = workspace(nbytes, x);
   const int status = rlt_batched_probabilities(
       ptr(x), dtype_code(x.scalar_type()), x.stride(0), n, vocab, (const float*)ptr(t),
       (const int64_t*)ptr(k), (const float*)ptr(p), max_top_k, apply_top_p ? 1 : 0,
-      (float*)ptr(out), out.stride(0), stream_of(x));
+      (float*)ptr(out), out.stride(0), nbytes ? ptr(ws) : nullptr, nbytes, stream_of(x));
   check_status(status, "rlt_batched_probabilities");
   return out;
 }
@@ -351,11 +354,13 @@ std::tuple<Tensor, Tensor> verify_distributions(const Tensor& logits, const Tens
     p = as(top_p, at::kFloat);
   }
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const size_t nbytes = r ? rlt_probabilities_workspace_size(r, m, vocab) : 0;
+  const Tensor ws = workspace(nbytes, x);
   const int status = rlt_verify_distributions(
       ptr(x), dtype_code(x.scalar_type()), x.stride(0), m, vocab, (const int64_t*)ptr(rows), r,
       (const float*)ptr(t), (const int64_t*)ptr(k), (const float*)ptr(p), max_top_k,
       apply_top_p ? 1 : 0, (float*)ptr(p_out), r ? p_out.stride(0) : vocab,
-      (int64_t*)ptr(target), stream_of(x));
+      (int64_t*)ptr(target), nbytes ? ptr(ws) : nullptr, nbytes, stream_of(x));
   check_status(status, "rlt_verify_distributions");
   return {target, p_out};
 }
@@ -392,7 +397,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> verify_accept(
   const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
   const Tensor qq = as(q, at::kFloat), ua = as(u_accept, at::kFloat), uf = as(u_final, at::kFloat);
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
-  const Tensor ws = workspace(rlt_speculative_accept_workspace_size(n, (int32_t)w1, vocab), x);
+  const Tensor ws = workspace(rlt_verify_accept_workspace_size(n, (int32_t)w1, vocab), x);
   const int status = rlt_verify_accept(
       ptr(x), dtype_code(x.scalar_type()), x.stride(0), (const float*)ptr(t),
       (const int64_t*)ptr(k), (const float*)ptr(pp), max_top_k, apply_top_p ? 1 : 0,

@@ -161,7 +161,7 @@ def propose_drafts(logits, random_rows, temperature, top_k, top_p, u, *, max_top
     x = _rows(x)
     rows = _i64(random_rows)
     lib = _lib.library()
-    ws = _lib.workspace(lib.rlt_categorical_workspace_size(r, vocab) if r else 0, device)
+    ws = _lib.workspace(lib.rlt_propose_drafts_workspace_size(m, r, vocab), device)
     args = (_f32(temperature), _i64(top_k), _f32(top_p), _f32(u)) if r else (None,) * 4
     status = lib.rlt_propose_drafts(
         _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), m, vocab, _lib.ptr(rows), r,
@@ -213,10 +213,14 @@ def verify_distributions(logits, random_rows, temperature, top_k, top_p, *, max_
     x = logits if logits.dtype in _LOGIT_DTYPES else logits.float()
     x = _rows(x)
     args = (_f32(temperature), _i64(top_k), _f32(top_p)) if r else (None,) * 3
-    status = _lib.library().rlt_verify_distributions(
+    lib = _lib.library()
+    nbytes = lib.rlt_probabilities_workspace_size(r, m, vocab) if r else 0
+    ws = _lib.workspace(nbytes, device) if nbytes else None
+    status = lib.rlt_verify_distributions(
         _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), m, vocab, _lib.ptr(_i64(random_rows)),
         r, *(_lib.ptr(a) for a in args), int(max_top_k), int(bool(apply_top_p)), _lib.ptr(p_out),
-        p_out.stride(0) if r else vocab, _lib.ptr(target), _lib.stream_of(device))
+        p_out.stride(0) if r else vocab, _lib.ptr(target), _lib.ptr(ws), nbytes,
+        _lib.stream_of(device))
     _lib.check(status, "rlt_verify_distributions")
     return target, p_out
 
