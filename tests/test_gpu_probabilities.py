@@ -413,21 +413,32 @@ def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vo
     assert bool((out[:, 0] == -1).all()) and bool((out[:, 2] == -1).all())
 
 
-@pytest.mark.parametrize("dtype,vocab,n,w1", [(torch.bfloat16, 32000, 6, 4),
-                                              (torch.float32, 1000, 3, 1),
-                                              (torch.float16, 151936, 2, 3),
-                                              (torch.bfloat16, 5000, 40, 8)])
-def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1):
+@pytest.mark.parametrize("dtype,vocab,n,w1,filtered", [
+    (torch.bfloat16, 32000, 6, 4, True),
+    (torch.float32, 1000, 3, 1, True),
+    (torch.float16, 151936, 2, 3, True),
+    (torch.bfloat16, 5000, 40, 8, True),
+    # no row filtered: the row-split distributions, whose write launch also sums p
+    (torch.float32, 65536, 24, 4, False),
+    (torch.float32, 49152, 32, 4, False),
+    (torch.bfloat16, 40000 + 3, 5, 2, False),
+    (torch.float16, 300, 4, 3, False),
+])
+def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, filtered):
     """verify_accept (distributions, argmax targets and the draft rows' partial sums in
     one launch, then the acceptance) is bitwise verify_distributions over every row
     followed by speculative_accept."""
-    _say("verify accept", dtype, vocab, n, w1)
+    _say("verify accept", dtype, vocab, n, w1, filtered)
     g = torch.Generator().manual_seed(vocab + n)
     rows = n * (w1 + 1)
     logits = (torch.randn(n, w1 + 1, vocab, generator=g) * 3).to(dtype)
+    if not filtered:
+        logits[1, 2, 7] = float("nan")  # a NaN row: NaN p, an error for its request
     t = torch.rand(rows, generator=g) + 0.5
     k = torch.where(torch.rand(rows, generator=g) < 0.3, 40, -1)
     p = torch.where(torch.rand(rows, generator=g) < 0.5, 0.9, 1.0)
+    if not filtered:
+        k, p = torch.full((rows,), -1), torch.ones(rows)
     plan = _host_args(k.tolist(), p.tolist(), vocab)
     q = (torch.randn(n, w1, vocab, generator=g) * 2).softmax(-1)
     u = torch.rand(n, 2 * w1 + 1, generator=g)
@@ -535,3 +546,22 @@ def test_split_form_output_stride_and_filtered_calls(pkg, dev):
     a = _probs_abi(dev, logits, t, k, p, plan, split=True)
     b = _probs_abi(dev, logits, t, k, p, plan, split=False)
     assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_split_form_is_batch_invariant(pkg, dev):
+    """The split form's slice width follows the batch (16, 32 or 64 columns per thread),
+    but a row's statistics come from fixed 4096-column blocks: a row gives the same bits
+    in a batch of 1024 rows as alone."""
+    _say("split batch invariance")
+    g = torch.Generator().manual_seed(9)
+    n, vocab = 1024, 65536
+    logits = (torch.randn(n, vocab, generator=g) * 3).to(dev)
+    t = torch.full((n,), 0.9, device=dev)
+    k = torch.full((n,), -1, dtype=torch.int64, device=dev)
+    p = torch.ones(n, device=dev)
+    plan = {"max_top_k": 0, "apply_top_p": False}
+    big = _probs_abi(dev, logits, t, k, p, plan, split=True)
+    for rows in ([5], [0, 700, 1023]):
+        idx = torch.tensor(rows, device=dev)
+        small = _probs_abi(dev, logits[idx].contiguous(), t[idx], k[idx], p[idx], plan, split=True)
+        assert torch.equal(small.view(torch.int32), big[idx].view(torch.int32)), rows

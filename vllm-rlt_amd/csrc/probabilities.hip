@@ -909,10 +909,11 @@ struct SplitPlan {
   int E, S;
 };
 
-bool split_plan(int64_t n_dist, int V, SplitPlan& p) {
+bool split_plan(int64_t n_dist, int V, SplitPlan& p, int min_e = 16) {
   const int options[3] = {16, 32, 64};
   int pick = 0;
   for (int i = 0; i < 3; ++i) {
+    if (options[i] < min_e) continue;
     const int64_t L = (int64_t)split::kThreads * options[i];
     const int64_t S = (V + L - 1) / L;
     if (S > split::kMaxSlices) continue;
@@ -925,26 +926,30 @@ bool split_plan(int64_t n_dist, int V, SplitPlan& p) {
   return true;
 }
 
-size_t split_bytes(int64_t n_dist, int64_t n_arg) {
-  return rlt_align_up((size_t)(n_dist + n_arg) * split::kMaxSlices * sizeof(split::SliceStat), 256);
+size_t split_bytes(int64_t n_dist, int64_t n_arg, int V) {
+  const int64_t nb = (V + split::kBlockCols - 1) / split::kBlockCols;
+  return rlt_align_up((size_t)(n_dist + n_arg) * nb * sizeof(split::BlockStat), 256);
 }
 
 // The split form's two launches.  targets: argmax outputs -- of the distribution rows
-// when fused, else of logits rows [0, n_arg).
+// when fused, else of logits rows [0, n_arg).  pm_out: the written rows' row-sum
+// partials (plans with E >= 32).
 template <int DT, int E>
 void launch_split_e(const SplitPlan& pl, int64_t n_dist, const void* logits, const int64_t* rows,
                     int64_t n_src, int64_t row_stride, int V, const float* temperature,
                     float* out, int64_t out_stride, hipStream_t stream, int64_t* targets,
                     int64_t n_arg, bool fused, const float* qm_src, int64_t qm_rows,
-                    float* qm_out, void* ws) {
+                    float* qm_out, void* ws, float* pm_out) {
   split::View v;
-  v.stats = (split::SliceStat*)ws;
+  v.stats = (split::BlockStat*)ws;
   v.S = pl.S;
   v.L = split::kThreads * E;
+  v.NB = (V + split::kBlockCols - 1) / split::kBlockCols;
   v.n_dist = n_dist;
   v.n_arg = fused ? 0 : n_arg;
   v.targets = targets;
   v.fused = fused;
+  v.pm_out = pm_out;
   const int esz = DT == RLT_F32 ? 4 : 2;
   const bool vec = V % 4 == 0 && row_stride % 4 == 0 && (uintptr_t)logits % (4 * esz) == 0;
   const bool out_vec = out_stride % 4 == 0 && (uintptr_t)out % 16 == 0;
@@ -972,10 +977,12 @@ template <int DT>
 void launch_split(const SplitPlan& pl, int64_t n_dist, const void* logits, const int64_t* rows,
                   int64_t n_src, int64_t row_stride, int V, const float* temperature, float* out,
                   int64_t out_stride, hipStream_t stream, int64_t* targets, int64_t n_arg,
-                  bool fused, const float* qm_src, int64_t qm_rows, float* qm_out, void* ws) {
+                  bool fused, const float* qm_src, int64_t qm_rows, float* qm_out, void* ws,
+                  float* pm_out = nullptr) {
 #define RLT_SPLIT_E(EE)                                                                         \
   launch_split_e<DT, EE>(pl, n_dist, logits, rows, n_src, row_stride, V, temperature, out,      \
-                         out_stride, stream, targets, n_arg, fused, qm_src, qm_rows, qm_out, ws)
+                         out_stride, stream, targets, n_arg, fused, qm_src, qm_rows, qm_out, ws, \
+                         pm_out)
   if (pl.E == 16) RLT_SPLIT_E(16);
   else if (pl.E == 32) RLT_SPLIT_E(32);
   else RLT_SPLIT_E(64);
@@ -984,9 +991,15 @@ void launch_split(const SplitPlan& pl, int64_t n_dist, const void* logits, const
 
 }  // namespace
 
-// spec_sampling.hip: the acceptance workspace's q-row partials, and the acceptance
-// launches that use them instead of summing q again.
+// spec_sampling.hip: the acceptance workspace's p-row and q-row partials, and the
+// acceptance launches that use them instead of summing q (and p) again.
+float* rlt_accept_p_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab);
 float* rlt_accept_q_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab);
+int rlt_accept_after_pq_partials(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
+                                 const float* p, const float* u_accept, const float* u_final,
+                                 int64_t n, int32_t w1, int64_t vocab, int64_t* tokens,
+                                 int64_t* accepted, int64_t* final_token, uint8_t* error,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 int rlt_accept_after_q_partials(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
                                 const float* p, const float* u_accept, const float* u_final,
                                 int64_t n, int32_t w1, int64_t vocab, int64_t* tokens,
@@ -1005,7 +1018,7 @@ size_t rlt_probabilities_workspace_size(int64_t rows, int64_t argmax_rows, int64
   if (rows < 0 || argmax_rows < 0 || vocab < 1 || vocab > 0x7fffffff ||
       !split_plan(rows, (int)vocab, pl))
     return 0;
-  return split_bytes(rows, argmax_rows);
+  return split_bytes(rows, argmax_rows, (int)vocab);
 }
 
 int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t row_stride,
@@ -1023,7 +1036,7 @@ int rlt_batched_probabilities(const void* logits, int32_t logits_dtype, int64_t 
   // the row-split form for calls that filter no row, when a workspace is given
   SplitPlan pl;
   const bool sp = workspace && mtk == 0 && !apply_top_p && split_plan(n, V, pl);
-  if (sp && workspace_bytes < split_bytes(n, 0)) return RLT_ERR_WORKSPACE;
+  if (sp && workspace_bytes < split_bytes(n, 0, V)) return RLT_ERR_WORKSPACE;
 #define RLT_PROBS(DT)                                                                          \
   do {                                                                                         \
     if (sp)                                                                                    \
@@ -1106,7 +1119,7 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
   const size_t cat_bytes = r > 0 ? rlt_align_up(rlt_categorical_workspace_size(r, vocab), 256) : 0;
   SplitPlan pl;
   const bool sp = r > 0 && mtk == 0 && !apply_top_p && split_plan(r, V, pl) &&
-                  workspace_bytes >= cat_bytes + split_bytes(r, m);
+                  workspace_bytes >= cat_bytes + split_bytes(r, m, V);
   // greedy proposals for every row (extra workgroups of the distribution launch when
   // there are random rows), then the random rows' draws
 #define RLT_PROPOSE(DT)                                                                       \
@@ -1155,7 +1168,7 @@ int rlt_verify_distributions(const void* logits, int32_t logits_dtype, int64_t r
   const int mtk = max_top_k > vocab ? V : (int)max_top_k;
   SplitPlan pl;
   const bool sp = r > 0 && workspace && mtk == 0 && !apply_top_p && split_plan(r, V, pl);
-  if (sp && workspace_bytes < split_bytes(r, m)) return RLT_ERR_WORKSPACE;
+  if (sp && workspace_bytes < split_bytes(r, m, V)) return RLT_ERR_WORKSPACE;
   // targets of every row as extra workgroups of the distribution launch (split form:
   // extra slices of launch 1, finished by launch 2 or 3)
 #define RLT_VERIFY(DT)                                                                        \
@@ -1214,8 +1227,9 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
   const size_t acc_bytes =
       rlt_align_up(rlt_speculative_accept_workspace_size(n, w1, vocab), 256);
   SplitPlan pl;
-  const bool sp = mtk == 0 && !apply_top_p && split_plan(rows, V, pl) &&
-                  workspace_bytes >= acc_bytes + split_bytes(rows, 0);
+  const bool sp = mtk == 0 && !apply_top_p && split_plan(rows, V, pl, 32) &&
+                  workspace_bytes >= acc_bytes + split_bytes(rows, 0, V);
+  float* pm_out = sp ? rlt_accept_p_partials(workspace, n, w1, vocab) : nullptr;
   // distributions of every verify row, their argmax targets, and the draft rows'
   // row-sum partials (one launch, or the split form's launches); then the acceptance
   // sums only p
@@ -1224,7 +1238,7 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
     if (sp)                                                                                   \
       launch_split<DT>(pl, rows, target_logits, nullptr, rows, row_stride, V, temperature,    \
                        p_out, vocab, stream, targets, rows, true, q_rows > 0 ? q : nullptr,   \
-                       q_rows, qm_out, (char*)workspace + acc_bytes);                         \
+                       q_rows, qm_out, (char*)workspace + acc_bytes, pm_out);                 \
     else                                                                                      \
       dispatch_probs<DT>(rows, target_logits, nullptr, rows, row_stride, V, temperature,      \
                          top_k, top_p, mtk, apply_top_p != 0, p_out, vocab, stream, targets,  \
@@ -1239,6 +1253,10 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
 #undef RLT_VERIFY_ACCEPT
   const int st = rlt_launch_status();
   if (st != RLT_OK) return st;
+  if (sp)  // the write launch summed p as well
+    return rlt_accept_after_pq_partials(draft_tokens, drafts, q, p_out, u_accept, u_final, n, w1,
+                                        vocab, tokens, accepted, final_token, error, workspace,
+                                        workspace_bytes, stream);
   return rlt_accept_after_q_partials(draft_tokens, drafts, q, p_out, u_accept, u_final, n, w1,
                                      vocab, tokens, accepted, final_token, error, workspace,
                                      workspace_bytes, stream);

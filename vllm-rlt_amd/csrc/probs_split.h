@@ -9,55 +9,62 @@
 // slice (slice length L = kThreads * E, E elements per thread in registers), in two
 // launches:
 //
-//   1. rlt_probs_slice_kernel, one workgroup per (row, slice): the slice max m_s, NaN
-//      flag, argmax key and float64 mass z_s = sum exp2((l - m_s) c) relative to the
-//      slice max (c = log2(e) / T);
-//   2. rlt_probs_write_kernel, one workgroup per (row, slice): the row max lmax and
-//      total z = sum_s z_s 2^((m_s - lmax) c) (float64) from the row's slices, then
-//      out = exp2((l - lmax) c) / z for the slice, NaN rows as NaN.
+//   1. rlt_probs_slice_kernel, one workgroup per (row, slice): for every 4096-column
+//      block b of the slice, its max m_b, NaN flag and float64 mass
+//      z_b = sum exp2((l - m_b) c) (c = log2(e) / T), plus the slice's argmax key;
+//   2. rlt_probs_write_kernel, one workgroup per (row, slice): the row max lmax and the
+//      total z = sum_b z_b 2^((m_b - lmax) c), summed over the row's blocks by a fixed
+//      lane tree, then out = exp2((l - lmax) c) / z for the slice, NaN rows as NaN.
 //
-// The outputs are those of the single-workgroup form up to the order of the float64
-// total's summation.  Argmax-only rows (greedy targets next to the distributions)
-// are extra slices of launch 1, finished in launch 2; the acceptance sampler's draft
-// row partial sums can ride as extra workgroups of launch 1.  Included inside
+// A block's statistics depend only on its own columns (thread t holds the same
+// columns of a block whatever the slice length), so the results do not depend on
+// the slicing; they equal the single-workgroup form's up to the order of the
+// float64 total's summation.  Argmax-only rows (greedy targets next to the
+// distributions) are extra slices of launch 1, finished in launch 2; the acceptance
+// sampler's draft-row partial sums can ride as extra workgroups of launch 1, and the
+// written rows' partial sums are formed in launch 2.  Included inside
 // probabilities.hip's anonymous namespace, after the order-key helpers.
 
 #pragma once
 
 namespace split {
 
-
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / RLT_WAVE;
 constexpr int kMaxSlices = 16;
+constexpr int kBlockCols = 4096;   // statistics block: 16 elements per thread
+constexpr int kMaxBlocks = 64;     // V <= 262144: one lane per block in the row total
 
-struct SliceStat {
-  float m;                  // slice max logit (NaN ignored)
-  uint32_t nan;             // the slice holds a NaN
+struct BlockStat {
+  float m;                  // block max logit (NaN ignored)
+  uint32_t nan;             // the block holds a NaN
   double z;                 // sum of exp2((l - m) c) (0 when m is not finite)
-  unsigned long long best;  // argmax key: (order key, NaN highest) << 32 | ~column
+  unsigned long long best;  // argmax key of the slice, (order key, NaN highest) << 32 |
+                            // ~column, in the slice's first block (0 in the others)
 };
 
 // Workspace view and the call's shape.
 struct View {
-  SliceStat* stats;  // [(n_dist + n_arg) * S]
-  int S, L;
+  BlockStat* stats;  // [(n_dist + n_arg) * NB]
+  int S, L, NB;      // slices per row, slice length, blocks per row
   int64_t n_dist;    // distribution rows
   int64_t n_arg;     // argmax-only rows (their statistics follow)
   int64_t* targets;  // argmax outputs, or nullptr
   int fused;         // distribution row r's argmax goes to targets[r]
+  float* pm_out;     // torch-order row-sum partials of the written rows, or nullptr
+                     // (row r, group g at pm_out + (r groups + g) 32; L % 8192 == 0)
 };
 
 __device__ __forceinline__ int64_t argmax_column(unsigned long long best) {
   return (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
 }
 
-// targets[i] for argmax-only row i from its slices' keys (one thread per row).
+// targets[i] for argmax-only row i from its blocks' keys (one thread per row).
 __device__ __forceinline__ void finish_argmax_row(const View& v, int64_t i) {
   if (i >= v.n_arg || !v.targets) return;
-  const SliceStat* st = v.stats + (v.n_dist + i) * v.S;
+  const BlockStat* st = v.stats + (v.n_dist + i) * v.NB;
   unsigned long long best = 0;
-  for (int s = 0; s < v.S; ++s) best = st[s].best > best ? st[s].best : best;
+  for (int b = 0; b < v.NB; ++b) best = st[b].best > best ? st[b].best : best;
   v.targets[i] = argmax_column(best);
 }
 
@@ -108,33 +115,41 @@ __device__ __forceinline__ void load_slice(const void* __restrict__ src, int64_t
 
 // ---------------------------------------------------------------- block reductions
 
+template <int N>
 struct ReduceShared {
-  float f[kWaves];
+  float f[kWaves][N];
+  double d[kWaves][N];
   uint32_t u[kWaves];
   uint32_t flag[kWaves];
-  double d[kWaves];
 };
 
-// Block max of a float and OR of a flag (every thread gets both).
-__device__ __forceinline__ void block_max_or(ReduceShared& sh, float& fm, bool& flag) {
+// Block max of N floats and OR of a flag (every thread gets the results).
+template <int N>
+__device__ __forceinline__ void block_max_or(ReduceShared<N>& sh, float (&fm)[N], bool& flag) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int off = 32; off >= 1; off >>= 1) fm = fmaxf(fm, __shfl_xor(fm, off, RLT_WAVE));
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    for (int off = 32; off >= 1; off >>= 1) fm[i] = fmaxf(fm[i], __shfl_xor(fm[i], off, RLT_WAVE));
   const bool any = __ballot(flag) != 0;
   if (lane == 0) {
-    sh.f[w] = fm;
+#pragma unroll
+    for (int i = 0; i < N; ++i) sh.f[w][i] = fm[i];
     sh.flag[w] = any;
   }
   __syncthreads();
-  fm = sh.f[0];
-  flag = sh.flag[0] != 0;
-  for (int i = 1; i < kWaves; ++i) {
-    fm = fmaxf(fm, sh.f[i]);
-    flag |= sh.flag[i] != 0;
+  flag = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) fm[i] = sh.f[0][i];
+  for (int k = 0; k < kWaves; ++k) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) fm[i] = fmaxf(fm[i], sh.f[k][i]);
+    flag |= sh.flag[k] != 0;
   }
   __syncthreads();
 }
 
-__device__ __forceinline__ uint32_t block_min_u32(ReduceShared& sh, uint32_t x) {
+template <int N>
+__device__ __forceinline__ uint32_t block_min_u32(ReduceShared<N>& sh, uint32_t x) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int off = 32; off >= 1; off >>= 1) x = min(x, (uint32_t)__shfl_xor(x, off, RLT_WAVE));
   if (lane == 0) sh.u[w] = x;
@@ -145,23 +160,27 @@ __device__ __forceinline__ uint32_t block_min_u32(ReduceShared& sh, uint32_t x) 
   return x;
 }
 
-// float64 sum in a fixed order (lane tree, then waves in order).
-__device__ __forceinline__ double block_sum(ReduceShared& sh, double x) {
+// float64 sums of N values in a fixed order (lane tree, then waves in order).
+template <int N>
+__device__ __forceinline__ void block_sum(ReduceShared<N>& sh, double (&x)[N]) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, RLT_WAVE);
-  if (lane == 0) sh.d[w] = x;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    for (int off = 32; off >= 1; off >>= 1) x[i] += __shfl_xor(x[i], off, RLT_WAVE);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) sh.d[w][i] = x[i];
+  }
   __syncthreads();
-  double s = sh.d[0];
-  for (int i = 1; i < kWaves; ++i) s += sh.d[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    x[i] = sh.d[0][i];
+    for (int k = 1; k < kWaves; ++k) x[i] += sh.d[k][i];
+  }
   __syncthreads();
-  return s;
 }
 
 // ---------------------------------------------------------------- launch 1
-
-struct SliceShared {
-  ReduceShared red;
-};
 
 // Column of element j of this thread: base = c0 + 4 t (32 bits: V < 2^31).
 template <int E>
@@ -169,57 +188,69 @@ __device__ __forceinline__ uint32_t elem_col(uint32_t base, int j) {
   return base + (uint32_t)(4 * kThreads * (j >> 2) + (j & 3));
 }
 
-// One slice's statistics.  kFull: every element of the slice is a column of the row
-// (no bounds tests).
+// One slice's block statistics.  Element j lies in block j / 16 of the slice.  kFull:
+// every element of the slice is a column of the row (no bounds tests).
 template <int DT, int E, bool kVec, bool kFull>
-__device__ __forceinline__ void slice_body(SliceShared& sh, const void* __restrict__ src, int64_t c0,
-                                           int V, bool dist, bool need_argmax, float temp,
-                                           SliceStat* __restrict__ out) {
+__device__ __forceinline__ void slice_body(ReduceShared<E / 16>& sh, const void* __restrict__ src,
+                                           int64_t c0, int V, bool dist, bool need_argmax,
+                                           float temp, BlockStat* __restrict__ out, int nb_here) {
+  constexpr int NB = E / 16;
   const int t = threadIdx.x;
   const uint32_t base = (uint32_t)(c0 + 4 * t);
   auto ok = [&](int j) { return kFull || (int64_t)elem_col<E>(base, j) < V; };
   float x[E];
   load_slice<DT, E, kVec>(src, c0, V, x);
-  float m = -INFINITY;
+  float m[NB];
   bool nan = false;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) m[b] = -INFINITY;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
     if (!ok(j)) continue;
     nan |= x[j] != x[j];
-    m = fmaxf(m, x[j]);  // NaN ignored
+    m[j / 16] = fmaxf(m[j / 16], x[j]);  // NaN ignored
   }
-  block_max_or(sh.red, m, nan);
-  // argmax key: the first column holding the max (the first NaN when there is one)
+  block_max_or<NB>(sh, m, nan);
+  // argmax key: the first column holding the slice max (the first NaN when there is one)
   unsigned long long best = 0;
   if (need_argmax) {
+    float ms = m[0];
+#pragma unroll
+    for (int b = 1; b < NB; ++b) ms = fmaxf(ms, m[b]);
     uint32_t col = 0xffffffffu;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const bool hit = ok(j) && (nan ? x[j] != x[j] : x[j] == m);
+      const bool hit = ok(j) && (nan ? x[j] != x[j] : x[j] == ms);
       col = hit ? min(col, elem_col<E>(base, j)) : col;
     }
-    col = block_min_u32(sh.red, col);
-    const uint32_t key = nan ? 0xffffffffu : order_key(m);
+    col = block_min_u32<NB>(sh, col);
+    const uint32_t key = nan ? 0xffffffffu : order_key(ms);
     best = ((unsigned long long)key << 32) | (0xffffffffu - col);
   }
-  double z = 0.0;
-  if (dist) {
-    const float c = 1.44269504088896341f / temp;
-    const bool finite = isfinite(m) && isfinite(c) && !nan;
-    double zs = 0.0;
-    if (finite) {
+  double z[NB];
 #pragma unroll
-      for (int j = 0; j < E; ++j)
-        if (ok(j)) zs += (double)__builtin_amdgcn_exp2f((x[j] - m) * c);
-    }
-    z = block_sum(sh.red, zs);
-    if (!finite) z = 0.0;
+  for (int b = 0; b < NB; ++b) z[b] = 0.0;
+  const float c = 1.44269504088896341f / temp;
+  if (dist && isfinite(c) && !nan) {
+#pragma unroll
+    for (int j = 0; j < E; ++j)
+      if (ok(j) && isfinite(m[j / 16]))
+        z[j / 16] += (double)__builtin_amdgcn_exp2f((x[j] - m[j / 16]) * c);
+    block_sum<NB>(sh, z);
   }
-  if (t == 0) {
-    out->m = m;
-    out->nan = nan;
-    out->z = z;
-    out->best = best;
+  if (t < nb_here) {
+    // thread b writes block b's record (the slice's blocks that hold columns)
+    float mb = m[0];
+    double zb = z[0];
+#pragma unroll
+    for (int b = 1; b < NB; ++b) {
+      mb = t == b ? m[b] : mb;
+      zb = t == b ? z[b] : zb;
+    }
+    out[t].m = mb;
+    out[t].nan = nan;
+    out[t].z = isfinite(mb) ? zb : 0.0;
+    out[t].best = t == 0 ? best : 0ull;
   }
 }
 
@@ -233,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_slice_kernel(
     int64_t row_stride, int V, const float* __restrict__ temperature, View v,
     const float* __restrict__ qm_src, int64_t qm_rows, float* __restrict__ qm_out) {
   __shared__ union {
-    SliceShared s;
+    ReduceShared<E / 16> red;
     cascade::ChunkSums cs[kThreads / cascade::kGroupThreads];
   } lds;
   const int t = threadIdx.x;
@@ -267,19 +298,53 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_slice_kernel(
   const void* src = (const char*)logits + src_r * row_stride * (DT == RLT_F32 ? 4 : 2);
   const bool need_argmax = !dist || (v.fused && v.targets);
   const float temp = dist ? temperature[r] : 1.f;
-  SliceStat* out = v.stats + blockIdx.x;
+  BlockStat* out = v.stats + r * v.NB + (int64_t)s * (E / 16);
+  const int nb_here = min(E / 16, v.NB - s * (E / 16));
   if (c0 + v.L <= V)
-    slice_body<DT, E, kVec, true>(lds.s, src, c0, V, dist, need_argmax, temp, out);
+    slice_body<DT, E, kVec, true>(lds.red, src, c0, V, dist, need_argmax, temp, out, nb_here);
   else
-    slice_body<DT, E, kVec, false>(lds.s, src, c0, V, dist, need_argmax, temp, out);
+    slice_body<DT, E, kVec, false>(lds.red, src, c0, V, dist, need_argmax, temp, out, nb_here);
 }
 
 // ---------------------------------------------------------------- launch 2
 
+// The float32 row-sum partials (torch's CPU order, cascade.h) of the values y of this
+// slice, one 8192-float group at a time staged through LDS; the same arithmetic as the
+// acceptance sampler's mass kernel over the written row.
+template <int E>
+__device__ __forceinline__ void slice_partials(float (&y)[E], int64_t c0, int V, float* stage,
+                                               cascade::ChunkSums* cs, float* __restrict__ pm) {
+  constexpr int kGroups = E * kThreads / cascade::kGroupFloats;  // groups per slice
+  constexpr int kQPerGroup = cascade::kGroupFloats / (4 * kThreads);
+  static_assert(kGroups >= 1 && cascade::kGroupFloats % (4 * kThreads) == 0, "whole groups");
+  const int t = threadIdx.x;
+  const cascade::RowGeom geo = cascade::row_geom(V);
+  const int64_t g0 = c0 / cascade::kGroupFloats;
+#pragma unroll
+  for (int gl = 0; gl < kGroups; ++gl) {
+    if (gl > 0) __syncthreads();  // the previous group's readers are done with stage
+#pragma unroll
+    for (int q = 0; q < kQPerGroup; ++q) {
+      const int qq = gl * kQPerGroup + q;
+      *(float4*)(stage + 4 * (kThreads * q + t)) =
+          make_float4(y[4 * qq], y[4 * qq + 1], y[4 * qq + 2], y[4 * qq + 3]);
+    }
+    __syncthreads();
+    const int64_t g = g0 + gl;
+    const int sub = t / cascade::kGroupThreads, st = t % cascade::kGroupThreads;
+    const int64_t fc = geo.full_chunks - g * cascade::kGroupChunks;  // chunks of group g on
+    if (sub == 0 && fc > 0) cascade::group_chunk_sums<true>(stage, 0, fc, st, *cs);
+    __syncthreads();
+    if (sub == 0 && fc > 0)
+      cascade::group_stream_sums(0, fc, st, *cs, pm + g * cascade::kStreams);
+  }
+}
+
 template <int DT, int E, bool kVec, bool kFull>
 __device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t c0, int V,
                                            bool nan_row, float lmax, float c, float inv,
-                                           float* __restrict__ dst, bool out_vec) {
+                                           float* __restrict__ dst, bool out_vec,
+                                           float* __restrict__ pm) {
   const uint32_t base = (uint32_t)(c0 + 4 * threadIdx.x);
   float y[E];
   if (nan_row) {
@@ -303,17 +368,24 @@ __device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t
         if (kFull || (int64_t)col + k < V) dst[col + k] = y[4 * q + k];
     }
   }
+  if constexpr (E * kThreads % cascade::kGroupFloats == 0) {
+    if (pm) {
+      __shared__ float stage[cascade::kGroupFloats];
+      __shared__ cascade::ChunkSums cs;
+      slice_partials<E>(y, c0, V, stage, &cs, pm);
+    }
+  }
 }
 
 // Workgroups [0, n_dist S): slice s of distribution row r, normalized by the row's
-// total from its slices; workgroups past n_dist S finish the argmax-only rows (one
+// total from its blocks; workgroups past n_dist S finish the argmax-only rows (one
 // thread per row).  out_vec: out rows aligned to four floats (vector stores).
 template <int DT, int E, bool kVec>
 __global__ __launch_bounds__(kThreads) void rlt_probs_write_kernel(
     const void* __restrict__ logits, const int64_t* __restrict__ rows, int64_t n_src,
     int64_t row_stride, int V, const float* __restrict__ temperature, View v,
     float* __restrict__ out, int64_t out_stride, int out_vec) {
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & 63;
   const int64_t n_slices = v.n_dist * v.S;
   if ((int64_t)blockIdx.x >= n_slices) {
     finish_argmax_row(v, ((int64_t)blockIdx.x - n_slices) * kThreads + t);
@@ -323,33 +395,38 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_write_kernel(
   const int s = (int)((int64_t)blockIdx.x % v.S);
   const int64_t src_r = rows ? rows[r] : r;
   const bool src_ok = src_r >= 0 && src_r < n_src;
-  const SliceStat* st = v.stats + r * v.S;
-  float lmax = -INFINITY;
-  bool bad = false;
-  unsigned long long best = 0;
-  for (int i = 0; i < v.S; ++i) {
-    lmax = fmaxf(lmax, st[i].m);
-    bad |= st[i].nan != 0;
-    best = st[i].best > best ? st[i].best : best;
-  }
-  if (v.fused && v.targets && s == 0 && t == 0) v.targets[r] = argmax_column(best);
   const float temp = temperature[r];
   const float c = 1.44269504088896341f / temp;
+  // the row's max, NaN state, argmax and total: lane b holds block b; every wave
+  // computes the same values (the lane tree's pairings do not depend on the wave)
+  BlockStat b{-INFINITY, 0u, 0.0, 0ull};
+  if (lane < v.NB) b = v.stats[r * v.NB + lane];
+  float lmax = b.m;
+  unsigned long long best = b.best;
+  for (int off = 32; off >= 1; off >>= 1) {
+    lmax = fmaxf(lmax, __shfl_xor(lmax, off, RLT_WAVE));
+    const unsigned long long o = __shfl_xor(best, off, RLT_WAVE);
+    best = o > best ? o : best;
+  }
+  const bool bad = __ballot(b.nan != 0) != 0;
+  if (v.fused && v.targets && s == 0 && t == 0) v.targets[r] = argmax_column(best);
   const bool nan_row = bad || !src_ok || !isfinite(lmax) || !(temp > 0.f) || !isfinite(c);
   float inv = 0.f;
   if (!nan_row) {
-    double z = 0.0;
-    for (int i = 0; i < v.S; ++i) z += st[i].z * exp2(((double)st[i].m - (double)lmax) * (double)c);
-    inv = (float)(1.0 / z);
+    double term = lane < v.NB && isfinite(b.m)
+                      ? b.z * exp2(((double)b.m - (double)lmax) * (double)c) : 0.0;
+    for (int off = 32; off >= 1; off >>= 1) term += __shfl_xor(term, off, RLT_WAVE);
+    inv = (float)(1.0 / term);
   }
   const int64_t c0 = (int64_t)s * v.L;
   const void* src =
       (const char*)logits + (src_ok ? src_r : 0) * row_stride * (DT == RLT_F32 ? 4 : 2);
   float* dst = out + r * out_stride;
+  float* pm = v.pm_out ? v.pm_out + r * cascade::row_geom(V).groups * cascade::kStreams : nullptr;
   if (c0 + v.L <= V)
-    write_body<DT, E, kVec, true>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0);
+    write_body<DT, E, kVec, true>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0, pm);
   else
-    write_body<DT, E, kVec, false>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0);
+    write_body<DT, E, kVec, false>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0, pm);
 }
 
 }  // namespace split

@@ -885,7 +885,7 @@ int accept_launch(const int64_t* draft_tokens, const int64_t* drafts, const floa
                   const float* p, const float* u_accept, const float* u_final, int64_t n,
                   int32_t w1, int64_t vocab, int64_t* tokens, int64_t* accepted,
                   int64_t* final_token, uint8_t* error, void* workspace, size_t workspace_bytes,
-                  bool q_partials_ready, hipStream_t stream) {
+                  int partials_ready, hipStream_t stream) {
   if (n < 0 || w1 < 0 || w1 > kMaxW1 || vocab < 1) return RLT_ERR_ARGUMENT;
   if (vocab >= ((int64_t)1 << 25)) return RLT_ERR_UNSUPPORTED;
   if (n == 0) return RLT_OK;
@@ -902,9 +902,10 @@ int accept_launch(const int64_t* draft_tokens, const int64_t* drafts, const floa
   const int64_t tiles = (vocab + kTile - 1) / kTile;
   if (tiles > 65535) return RLT_ERR_UNSUPPORTED;  // grid.y of the tile kernel
   const int64_t p_rows = n * (w1 + 1);
-  if (q_partials_ready)
+  // partials_ready: 0 none, 1 the q rows', 2 the p and q rows'
+  if (partials_ready == 1)
     launch_mass_groups(p, nullptr, p_rows, p_rows, vocab, partials, stream);
-  else
+  else if (partials_ready == 0)
     launch_mass_groups(p, w1 > 0 ? q : nullptr, p_rows, rows, vocab, partials, stream);
   rlt_accept_tiles_kernel<<<dim3((unsigned)n, (unsigned)tiles), kDrawThreads, 0, stream>>>(
       p, q, w1, vocab, n, geo.groups > 0 ? partials : nullptr, geo.groups, draft_tokens, drafts,
@@ -916,6 +917,13 @@ int accept_launch(const int64_t* draft_tokens, const int64_t* drafts, const floa
 }
 
 }  // namespace
+
+// The mass partials of the p rows inside an acceptance workspace (p row r at
+// partials + r * groups * 32), for a launch that computes them.
+float* rlt_accept_p_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab) {
+  const Layout l = layout_for(n * (2 * (int64_t)w1 + 1), n, vocab);
+  return (float*)((char*)workspace + l.partials);
+}
 
 // The mass partials of the q rows inside an acceptance workspace (q row r at
 // partials + r * groups * 32), for a launch that computes them.
@@ -932,7 +940,17 @@ int rlt_accept_after_q_partials(const int64_t* draft_tokens, const int64_t* draf
                                 int64_t* accepted, int64_t* final_token, uint8_t* error,
                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
-                       accepted, final_token, error, workspace, workspace_bytes, true, stream);
+                       accepted, final_token, error, workspace, workspace_bytes, 1, stream);
+}
+
+// speculative_accept after the p and q rows' partials were written into the workspace.
+int rlt_accept_after_pq_partials(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
+                                 const float* p, const float* u_accept, const float* u_final,
+                                 int64_t n, int32_t w1, int64_t vocab, int64_t* tokens,
+                                 int64_t* accepted, int64_t* final_token, uint8_t* error,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
+                       accepted, final_token, error, workspace, workspace_bytes, 2, stream);
 }
 
 // ------------------------------------------------------------ no-allocation form
@@ -982,7 +1000,7 @@ int rlt_speculative_accept(const int64_t* draft_tokens, const int64_t* drafts, c
                            int64_t* final_token, uint8_t* error, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
   return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
-                       accepted, final_token, error, workspace, workspace_bytes, false, stream);
+                       accepted, final_token, error, workspace, workspace_bytes, 0, stream);
 }
 
 size_t rlt_speculative_accept_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
@@ -1001,7 +1019,7 @@ int rlt_speculative_accept_noalloc(const int64_t* draft_tokens, const int64_t* d
   void* ws = scratch_for_current_device();
   if (!ws) return RLT_ERR_LAUNCH;
   return accept_launch(draft_tokens, drafts, q, p, u_accept, u_final, n, w1, vocab, tokens,
-                       accepted, final_token, error, ws, kNoAllocScratchBytes, false, stream);
+                       accepted, final_token, error, ws, kNoAllocScratchBytes, 0, stream);
 }
 
 int rlt_categorical(const float* weights, const float* u, int64_t m, int64_t vocab,
