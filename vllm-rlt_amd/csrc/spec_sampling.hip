@@ -658,11 +658,13 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
     const float* __restrict__ partials, int64_t groups, const int64_t* __restrict__ draft_tokens,
     const int64_t* __restrict__ drafts, const float* __restrict__ u_accept,
     double* __restrict__ tile_sum, uint32_t* __restrict__ tile_flags,
-    StopState* __restrict__ stop) {
+    StopState* __restrict__ stop, int64_t tiles, int tiles_per_group) {
   __shared__ AcceptShared sh;
+  __shared__ double wave_part[2][kDrawWaves];
+  __shared__ uint32_t wave_flags[2][kDrawWaves];
   const int64_t i = blockIdx.x;
-  const int64_t k = blockIdx.y;
-  const int64_t tiles = gridDim.y;
+  const int64_t k0 = (int64_t)blockIdx.y * tiles_per_group;
+  const int64_t k1 = min(k0 + tiles_per_group, tiles);
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -725,30 +727,37 @@ __global__ __launch_bounds__(kDrawThreads) void rlt_accept_tiles_kernel(
   const WeightRow w = stop_weights(p, q, i, W1, V, s, at_end, sh.pm[s], at_end ? 1.f : sh.qm[s]);
   const bool vec_ok =
       (V % 4 == 0) && ((((uintptr_t)w.a) | ((uintptr_t)(w.b ? w.b : w.a))) % 16 == 0);
-  // ---- this workgroup's tile of the final weights
-  {
-    float wv[kElems];
-    load_weights(w, V, k, t, vec_ok, wv);
+  // ---- this workgroup's tiles of the final weights (the stop state above is paid
+  // once for all of them); the next tile's loads are in flight while one is reduced,
+  // and the wave partials alternate between two buffers (one barrier per tile)
+  float cur[kElems];
+  load_weights(w, V, k0, t, vec_ok, cur);
+  for (int64_t k = k0; k < k1; ++k) {
+    float nxt[kElems];
+    if (k + 1 < k1) load_weights(w, V, k + 1, t, vec_ok, nxt);
     uint32_t fl = 0;
-    const double part = tile_partial(wv, fl);
+    const double part = tile_partial(cur, fl);
     fl = wave_or_flags(fl);
+    const int b = (int)((k - k0) & 1);
     if (lane == 0) {
-      sh.wave_part[wave] = part;
-      sh.wave_flags[wave] = fl;
+      wave_part[b][wave] = part;
+      wave_flags[b][wave] = fl;
     }
-  }
-  __syncthreads();
-  if (t == 0) {
-    double tk = 0.0;
-    uint32_t fl = 0;
-    for (int wv = 0; wv < kDrawWaves; ++wv) {
-      tk += sh.wave_part[wv];
-      fl |= sh.wave_flags[wv];
+    __syncthreads();
+    if (t == 0) {
+      double tk = 0.0;
+      uint32_t f = 0;
+      for (int wv = 0; wv < kDrawWaves; ++wv) {
+        tk += wave_part[b][wv];
+        f |= wave_flags[b][wv];
+      }
+      tile_sum[i * tiles + k] = tk;
+      tile_flags[i * tiles + k] = f;
     }
-    tile_sum[i * tiles + k] = tk;
-    tile_flags[i * tiles + k] = fl;
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) cur[e] = nxt[e];
   }
-  if (k == 0) {
+  if (k0 == 0) {
     StopState& st = stop[i];
     if (t < W1) st.tok[t] = sh.tok[t];
     if (t == 0) {
@@ -907,9 +916,13 @@ int accept_launch(const int64_t* draft_tokens, const int64_t* drafts, const floa
     launch_mass_groups(p, nullptr, p_rows, p_rows, vocab, partials, stream);
   else if (partials_ready == 0)
     launch_mass_groups(p, w1 > 0 ? q : nullptr, p_rows, rows, vocab, partials, stream);
-  rlt_accept_tiles_kernel<<<dim3((unsigned)n, (unsigned)tiles), kDrawThreads, 0, stream>>>(
+  // tiles per workgroup: enough workgroups to fill the GPU twice, the stop state (row
+  // masses, accept chain) paid once per workgroup
+  const int64_t tpg = std::max<int64_t>(1, std::min<int64_t>(tiles, n * tiles / 512));
+  const int64_t groups_y = (tiles + tpg - 1) / tpg;
+  rlt_accept_tiles_kernel<<<dim3((unsigned)n, (unsigned)groups_y), kDrawThreads, 0, stream>>>(
       p, q, w1, vocab, n, geo.groups > 0 ? partials : nullptr, geo.groups, draft_tokens, drafts,
-      u_accept, tile_sum, tile_flags, stop);
+      u_accept, tile_sum, tile_flags, stop, tiles, (int)tpg);
   rlt_accept_draw_kernel<<<(unsigned)n, kDrawThreads, 0, stream>>>(
       p, q, w1, vocab, tiles, u_final, tile_sum, tile_flags, stop, final_token, tokens, accepted,
       error, slow);
