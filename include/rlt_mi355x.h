@@ -97,6 +97,35 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
+/*
+ * The packed verify window with its own keys and values stored first: row r of
+ * new_k / new_v ([num_q_rows, kv_heads, head_dim], strides in elements, 16-byte
+ * aligned rows) is written into the pool at the position of packed q row r
+ * (context_lengths[s] - q_len_s + i for window row i of sequence s) through the block
+ * table, then attention runs as rlt_paged_attention (no scales, no sliding window).
+ * Replaces the writer that precedes attention in every layer
+ * (vllm_rlt/kernels/graph_kv.py:52-67, the KV scatter of the window rows) followed by
+ * the packed attention call (vllm_rlt/kernels/triton_attention.py:386-404), in one
+ * launch pair: the attention waves that read a window position store it before
+ * reading.  bf16 / fp16 q and pool of one dtype, windows shorter than the prefill
+ * tiling's threshold (rlt_paged_attention_uses_prefill == 0); other shapes return
+ * RLT_ERR_UNSUPPORTED (the caller then stores and attends separately).  Table entries
+ * outside [0, num_blocks) are not written.  Workspace: rlt_paged_attention_workspace_size.
+ */
+int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                              void* key_cache, void* value_cache, int64_t k_block_stride,
+                              int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                              int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                              const int32_t* block_tables, int64_t table_stride,
+                              int32_t table_width, const int32_t* context_lengths,
+                              const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                              int32_t num_q_rows, int32_t num_q_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t block_size, int32_t dtype,
+                              const void* new_k, const void* new_v, int64_t new_row_stride,
+                              int64_t new_head_stride, void* out, int64_t out_row_stride,
+                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream);
+
 /* 1 when (q dtype, kv dtype, head_dim) runs on the MFMA kernel, else 0 (vector kernel). */
 int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim);
 

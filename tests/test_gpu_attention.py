@@ -504,3 +504,124 @@ def test_row_lengths_on_the_grid_kernel(kernel, dev):
     sel = [0, 1, 8198, 16399]
     want = oatt.paged_attention(q[sel], k, v, row_tables[sel], row_len[sel])
     _close(got[sel].cpu(), want, dtype)
+
+
+# ------------------------------------------------------------ window store + attention
+
+def _window_store_case(g, dtype, d, hq, hkv, bs, lengths, q_lens, pool_blocks, layers=2,
+                       layer=1):
+    kpool, vpool, _, _ = make_pool(pool_blocks, layers, bs, hkv, d, dtype, g)
+    tables = random_tables(lengths, bs, pool_blocks, g)
+    rows = sum(q_lens)
+    q = torch.randn(rows, hq, d, generator=g).to(dtype)
+    k_new = torch.randn(rows, hkv, d, generator=g).to(dtype)
+    v_new = torch.randn(rows, hkv, d, generator=g).to(dtype)
+    cu = torch.tensor([0] + list(torch.tensor(q_lens).cumsum(0)), dtype=torch.int32)
+    return kpool, vpool, tables, q, k_new, v_new, cu
+
+
+@pytest.mark.parametrize("dtype,d,hq,hkv,bs", [
+    (torch.bfloat16, 128, 16, 4, 16),   # config 3's heads
+    (torch.float16, 64, 8, 8, 16),
+    (torch.bfloat16, 96, 4, 1, 16),
+    (torch.bfloat16, 128, 8, 2, 5),     # blocks that do not hold whole tiles
+])
+def test_prefill_store_equals_store_then_prefill(kernel, pkg, dev, dtype, d, hq, hkv, bs):
+    """The fused window store + attention writes the pool and returns the output of
+    store_kv at the window positions followed by prefill, bit for bit.  Windows sit on
+    both sides of the 256-position half-chunk and 512-position chunk boundaries, and a
+    9-row window over GQA 4 spans two row groups (two units write the same positions)."""
+    _say("prefill_store", dtype, d, hq, hkv, bs)
+    g = torch.Generator().manual_seed(d + hq + bs)
+    lengths = [5, 258, 514, 1030, 3000, 9, 40, 1]
+    q_lens = [5, 5, 5, 9, 1, 9, 33, 1]
+    pages = sum(-(-x // bs) for x in lengths) + 7
+    kpool, vpool, tables, q, k_new, v_new, cu = _window_store_case(
+        g, dtype, d, hq, hkv, bs, lengths, q_lens, pages)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    max_q = max(q_lens)
+    # separate: store_kv at the window positions, then prefill
+    ka, va = kpool.to(dev), vpool.to(dev)
+    seq = torch.repeat_interleave(torch.arange(len(q_lens)), torch.tensor(q_lens))
+    pos = ctx.long()[seq] - torch.tensor(q_lens)[seq] + torch.arange(len(seq)) - cu.long()[seq]
+    blocks = tables.long()[seq, pos // bs]
+    pkg.store_kv(ka[:, 1], va[:, 1], k_new.to(dev), v_new.to(dev), blocks.to(dev),
+                 (pos % bs).to(dev))
+    want = kernel.prefill(q.to(dev), ka[:, 1], va[:, 1], tables.to(dev), ctx.to(dev),
+                          cu.to(dev), max_q)
+    # fused
+    kb, vb = kpool.to(dev), vpool.to(dev)
+    got = kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kb[:, 1], vb[:, 1],
+                               tables.to(dev), ctx.to(dev), cu.to(dev), max_q)
+    assert torch.equal(kb.view(torch.int16), ka.view(torch.int16))
+    assert torch.equal(vb.view(torch.int16), va.view(torch.int16))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # the other layer of the pool is untouched
+    assert torch.equal(kb[:, 0].cpu().view(torch.int16), kpool[:, 0].view(torch.int16))
+
+
+def test_prefill_store_graph_replays_and_other_shapes(kernel, pkg, dev):
+    """Replayed from a HIP graph the fused form gives the eager result every time (the
+    pool is rewritten with the same rows); shapes it does not serve -- float32 q, a
+    prefill-length window -- store and attend separately with the same result; a table
+    entry outside the pool writes nothing."""
+    _say("prefill_store graph / fallbacks")
+    g = torch.Generator().manual_seed(77)
+    bs, hq, hkv, d = 16, 16, 4, 128
+    lengths, q_lens = [700, 1500, 64, 2049], [5, 5, 64, 5]
+    pages = sum(-(-x // bs) for x in lengths) + 3
+    kpool, vpool, tables, q, k_new, v_new, cu = _window_store_case(
+        g, torch.bfloat16, d, hq, hkv, bs, lengths, q_lens, pages, layers=1, layer=0)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    args = lambda kp, vp, qq: (qq, k_new.to(dev), v_new.to(dev), kp[:, 0], vp[:, 0],
+                               tables.to(dev), ctx.to(dev), cu.to(dev), max(q_lens))
+    # q_len 64 takes the prefill tiling: a separate store, then attention
+    seq = torch.repeat_interleave(torch.arange(4), torch.tensor(q_lens))
+    pos = ctx.long()[seq] - torch.tensor(q_lens)[seq] + torch.arange(len(seq)) - cu.long()[seq]
+    ks, vs = kpool.to(dev), vpool.to(dev)
+    pkg.store_kv(ks[:, 0], vs[:, 0], k_new.to(dev), v_new.to(dev),
+                 tables.long()[seq, pos // bs].to(dev), (pos % bs).to(dev))
+    ka, va = kpool.to(dev), vpool.to(dev)
+    got64 = kernel.prefill_store(*args(ka, va, q.to(dev)))
+    assert torch.equal(ka.view(torch.int16), ks.view(torch.int16))
+    assert torch.equal(va.view(torch.int16), vs.view(torch.int16))
+    want64 = kernel.prefill(q.to(dev), ks[:, 0], vs[:, 0], tables.to(dev), ctx.to(dev),
+                            cu.to(dev), 64)
+    assert torch.equal(got64.view(torch.int16), want64.view(torch.int16))
+    # three 5-row windows: the fused form, bitwise the separate store + verify kernels
+    sel = [0, 1, 3]
+    rows = torch.cat([torch.arange(cu[s], cu[s + 1]) for s in sel])
+    cu3 = torch.tensor([0, 5, 10, 15], dtype=torch.int32)
+    kb, vb = kpool.to(dev), vpool.to(dev)
+    qd, kn, vn = q[rows].to(dev), k_new[rows].to(dev), v_new[rows].to(dev)
+    t3, c3 = tables[sel].to(dev), ctx[sel].to(dev)
+    eager = kernel.prefill_store(qd, kn, vn, kb[:, 0], vb[:, 0], t3, c3, cu3.to(dev), 5)
+    want = kernel.prefill(qd, ks[:, 0], vs[:, 0], t3, c3, cu3.to(dev), 5)
+    assert torch.equal(eager.view(torch.int16), want.view(torch.int16))
+    stream = torch.cuda.Stream()
+    cu3d = cu3.to(dev)
+    with torch.cuda.stream(stream):
+        kernel.prefill_store(qd, kn, vn, kb[:, 0], vb[:, 0], t3, c3, cu3d, 5)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = kernel.prefill_store(qd, kn, vn, kb[:, 0], vb[:, 0], t3, c3, cu3d, 5)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        torch.cuda.synchronize()
+    # float32 q: the vector kernels, separate store
+    kc, vc = kpool.to(dev), vpool.to(dev)
+    got32 = kernel.prefill_store(qd.float(), kn, vn, kc[:, 0], vc[:, 0], t3, c3, cu3.to(dev), 5)
+    assert torch.equal(kc.view(torch.int16), kb.view(torch.int16))
+    ref32 = kernel.prefill(qd.float(), kb[:, 0], vb[:, 0], t3, c3, cu3.to(dev), 5)
+    assert torch.equal(got32, ref32)
+    # a table entry outside the pool: that window position is not written
+    bad = t3.clone()
+    last = (c3[0].item() - 1) // bs
+    bad[0, last] = pages + 5
+    kd, vd = kpool.to(dev), vpool.to(dev)
+    kernel.prefill_store(qd, kn, vn, kd[:, 0], vd[:, 0], bad, c3, cu3.to(dev), 5)
+    blk = t3[0, last].item()
+    assert torch.equal(kd[blk].cpu().view(torch.int16), kpool[blk].view(torch.int16))

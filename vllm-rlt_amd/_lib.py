@@ -60,6 +60,16 @@ _SIGNATURES = {
         _p, _i64, _i64,                 # out
         _p, _sz, _p,                    # workspace, bytes, stream
     ]),
+    "rlt_paged_attention_store": (ctypes.c_int, [
+        _p, _i64, _i64,                 # q
+        _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32,  # pools, strides, blocks
+        _p, _i64, _i32, _p,             # tables, stride, width, lengths
+        _p, _i32, _i32, _i32,           # cu, num_seqs, max_q_len, num_q_rows
+        _i32, _i32, _i32, _i32, _i32,   # hq, hkv, head_dim, block_size, dtype
+        _p, _p, _i64, _i64,             # new k, v, row / head strides
+        _p, _i64, _i64,                 # out
+        _p, _sz, _p,                    # workspace, bytes, stream
+    ]),
     "rlt_merge_random_round": (ctypes.c_int, [
         _p, _i64, _p, _p, _p, _p, _i64,  # target, rows, accepted, next, starts, inputs, n
         _p, _i32, _p, _p, _p, _p, _i64,  # tokens, width, accepted, final, error, requests, r

@@ -89,6 +89,12 @@ struct AttnParams {
   int64_t out_row_stride, out_head_stride;
   float* part_ml;  // [rows][hq][max_chunks][2]  (max in log2 units, sum)
   float* part_o;   // [rows][hq][max_chunks][head_dim]
+  // packed form with the window rows' own keys / values to store first (nullptr: none):
+  // row r of [rows, kv_heads, head_dim] (strides in elements) goes to its window
+  // position through the block table
+  const void* new_k;
+  const void* new_v;
+  int64_t new_row_stride, new_head_stride;
 };
 
 struct SeqView {
@@ -538,6 +544,36 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
   if (SM == 1) {
     qk_scale *= P.k_scale[0];
     st.v_mul = P.v_scale[0];
+  }
+
+  if constexpr (KVT == QT) {
+    if (P.new_k && t0 < t1) {
+      // The window rows' own keys and values, stored through the block table before
+      // any tile of this span is read.  Every wave that reads a window position writes
+      // it first (identical bytes when several do), so no wave depends on another's
+      // store; the wait makes this wave's stores visible to its own loads.
+      const int base_pos = sv.kv_len - sv.q_len;  // position of window row 0
+      const int i0 = max(0, w_begin + t0 * kTileTok - base_pos);
+      const int i1 = min(sv.q_len, w_begin + t1 * kTileTok - base_pos);
+      constexpr int kPieces = D * 2 / 16;  // 16-byte pieces of one (row, kv head)
+      const int piece = lane & 31;
+      for (int i = i0 + (lane >> 5); i < i1; i += 2) {
+        const int pos = base_pos + i;
+        const int idx = pos / P.block_size;
+        const int32_t e = idx < P.table_width ? P.tables[(int64_t)seq * P.table_stride + idx] : -1;
+        if (piece < kPieces && e >= 0 && e < P.num_blocks) {
+          const int64_t row = (int64_t)(sv.q_begin + i) * P.new_row_stride + (int64_t)kvh * P.new_head_stride;
+          const int64_t off = (int64_t)(pos % P.block_size);
+          const uint4 kx = ((const uint4*)((const uint16_t*)P.new_k + row))[piece];
+          const uint4 vx = ((const uint4*)((const uint16_t*)P.new_v + row))[piece];
+          ((uint4*)((uint16_t*)P.k + (int64_t)e * P.k_block_stride + off * P.k_token_stride +
+                    (int64_t)kvh * P.k_head_stride))[piece] = kx;
+          ((uint4*)((uint16_t*)P.v + (int64_t)e * P.v_block_stride + off * P.v_token_stride +
+                    (int64_t)kvh * P.v_head_stride))[piece] = vx;
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
   }
 
   if (t0 < t1) {
@@ -1764,7 +1800,17 @@ size_t rlt_paged_attention_workspace_size(int32_t num_q_rows, int32_t num_q_head
   return rlt_align_up(sizeof(float) * slots * 2, 256) + rlt_align_up(sizeof(float) * slots * head_dim, 256);
 }
 
-int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+}  // extern "C"
+
+namespace {
+
+struct WindowStore {
+  const void* k;
+  const void* v;
+  int64_t row_stride, head_stride;
+};
+
+int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                              const void* key_cache, const void* value_cache, int64_t k_block_stride,
                              int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
                              int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
@@ -1777,7 +1823,7 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
                              int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
                              int32_t window, void* out, int64_t out_row_stride,
                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
-                             hipStream_t stream) {
+                             hipStream_t stream, const WindowStore* store) {
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return RLT_ERR_ARGUMENT;
   if (head_dim <= 0 || head_dim > 256 || block_size <= 0 || window < 0) return RLT_ERR_ARGUMENT;
   if (num_seqs < 0 || num_q_rows < 0 || max_q_len < 0 || table_width < 0) return RLT_ERR_ARGUMENT;
@@ -1836,6 +1882,22 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
   P.part_ml = (float*)workspace;
   P.part_o = (float*)((char*)workspace + rlt_align_up(sizeof(float) * slots * 2, 256));
   if (P.max_chunks == 0) P.max_chunks = 1;  // zero-width tables: every row is empty
+  P.new_k = store ? store->k : nullptr;
+  P.new_v = store ? store->v : nullptr;
+  P.new_row_stride = store ? store->row_stride : 0;
+  P.new_head_stride = store ? store->head_stride : 0;
+  if (store) {
+    // the fused window store: packed bf16 / fp16 windows on the verify kernels only
+    if (!cu_seqlens_q || row_lengths || kv_dtype != q_dtype ||
+        (q_dtype != RLT_BF16 && q_dtype != RLT_F16) ||
+        !rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) ||
+        rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len))
+      return RLT_ERR_UNSUPPORTED;
+    if (!store->k || !store->v || ((uintptr_t)store->k | (uintptr_t)store->v) % 16 ||
+        (store->row_stride * 2) % 16 || (store->head_stride * 2) % 16 ||
+        (k_token_stride * 2) % 16 || (v_token_stride * 2) % 16)
+      return RLT_ERR_ARGUMENT;
+  }
 
   const int rows_per_seq = max_q_len * P.group;
   const bool mfma = rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim);
@@ -1914,6 +1976,57 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
     case RLT_BF16: launch_merge<RLT_BF16>(P, mgrid, stream); break;
   }
   return rlt_launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                             const void* key_cache, const void* value_cache, int64_t k_block_stride,
+                             int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                             int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                             const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                             const int32_t* context_lengths, const int32_t* row_lengths,
+                             const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                             int32_t num_q_rows, const float* key_scale, const float* value_scale,
+                             int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
+                             int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
+                             int32_t window, void* out, int64_t out_row_stride,
+                             int64_t out_head_stride, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+  return attention_impl(q, q_row_stride, q_head_stride, key_cache, value_cache, k_block_stride,
+                        k_token_stride, k_head_stride, v_block_stride, v_token_stride,
+                        v_head_stride, num_blocks, block_tables, table_stride, table_width,
+                        context_lengths, row_lengths, cu_seqlens_q, num_seqs, max_q_len,
+                        num_q_rows, key_scale, value_scale, scale_mode, s_block_stride,
+                        s_token_stride, s_head_stride, num_q_heads, num_kv_heads, head_dim,
+                        block_size, q_dtype, kv_dtype, window, out, out_row_stride,
+                        out_head_stride, workspace, workspace_bytes, stream, nullptr);
+}
+
+int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                              void* key_cache, void* value_cache, int64_t k_block_stride,
+                              int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                              int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+                              const int32_t* block_tables, int64_t table_stride,
+                              int32_t table_width, const int32_t* context_lengths,
+                              const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t max_q_len,
+                              int32_t num_q_rows, int32_t num_q_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t block_size, int32_t dtype,
+                              const void* new_k, const void* new_v, int64_t new_row_stride,
+                              int64_t new_head_stride, void* out, int64_t out_row_stride,
+                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream) {
+  const WindowStore st{new_k, new_v, new_row_stride, new_head_stride};
+  return attention_impl(q, q_row_stride, q_head_stride, key_cache, value_cache, k_block_stride,
+                        k_token_stride, k_head_stride, v_block_stride, v_token_stride,
+                        v_head_stride, num_blocks, block_tables, table_stride, table_width,
+                        context_lengths, nullptr, cu_seqlens_q, num_seqs, max_q_len, num_q_rows,
+                        nullptr, nullptr, 0, 0, 0, 0, num_q_heads, num_kv_heads, head_dim,
+                        block_size, dtype, dtype, 0, out, out_row_stride, out_head_stride,
+                        workspace, workspace_bytes, stream, &st);
 }
 
 int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
