@@ -441,7 +441,8 @@ def main():
                     help="skip the secondary config-2 decode attention measurement")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the config-4 and config-5 attention + verify_accept measurements")
-    ap.add_argument("--only", choices=("kv_write", "attention", "probs", "accept", "verify", "copy",
+    ap.add_argument("--only", choices=("kv_write", "attention", "attention_store", "probs", "accept",
+                                       "verify", "copy",
                                        "config5_attention"),
                     help="replay only this part K times and exit (for counter collection); "
                          "'copy' copies a 1 GiB buffer K times (counter calibration); "
@@ -498,6 +499,12 @@ def main():
     def attn(layer=1):
         return backend.prefill(w["q"], kcs[layer], vcs[layer], tables, lengths, cu, w["window"])
 
+    def attn_store(layer=1):
+        # the two calls above as one launch pair: the attention waves that read a window
+        # position store its K/V first
+        return backend.prefill_store(w["q"], w["k_new"], w["v_new"], kcs[layer], vcs[layer],
+                                     tables, lengths, cu, w["window"])
+
     all_rows = torch.arange(rows, device=dev)
 
     def probs():
@@ -520,8 +527,7 @@ def main():
                                  max_top_k=0, apply_top_p=True)
 
     def step(layer=1):
-        kv_write(layer)
-        attn(layer)
+        attn_store(layer)
         verify()
 
     for _ in range(max(args.warmup, 1)):
@@ -539,12 +545,16 @@ def main():
     spg = max(1, min(args.steps_per_graph, args.steps))
     g_kv, g_attn, g_probs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     g_acc, g_step, g_ver = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    g_fused = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_kv):
         for i in range(spg):
             kv_write(i % 2)
     with torch.cuda.graph(g_attn):
         for i in range(spg):
             out_attn = attn(i % 2)
+    with torch.cuda.graph(g_fused):
+        for i in range(spg):
+            out_fused = attn_store(i % 2)
     with torch.cuda.graph(g_probs):
         for _ in range(spg):
             out_probs = probs()
@@ -561,7 +571,8 @@ def main():
         g_step.replay()
     torch.cuda.synchronize()
     if args.only:
-        graph = {"kv_write": g_kv, "attention": g_attn, "probs": g_probs,
+        graph = {"kv_write": g_kv, "attention": g_attn, "attention_store": g_fused,
+                 "probs": g_probs,
                  "accept": g_acc, "verify": g_ver}[args.only]
         for _ in range(max(1, args.steps // spg)):
             graph.replay()
@@ -595,6 +606,7 @@ def main():
 
     t_kv = launch_time(g_kv)
     t_attn = launch_time(g_attn)
+    t_fused = launch_time(g_fused)
     t_probs = launch_time(g_probs)
     t_acc = launch_time(g_acc)
     t_ver = launch_time(g_ver)
@@ -606,6 +618,9 @@ def main():
     eager_ver = verify()
     torch.cuda.synchronize()
     assert torch.equal(eager_attn, out_attn)
+    # the fused store + attention: the same output (the pool already holds the window's
+    # K/V from the warmup, and stores of the same bytes change nothing)
+    assert torch.equal(eager_attn, out_fused)
     assert torch.equal(eager_probs, out_probs)
     for a, b in zip(eager_acc, out_acc):
         assert torch.equal(a, b)
@@ -645,7 +660,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded random KV, q and logits; no model or dataset)",
         "config": {
-            "workload": "config3 verify step: window KV write, packed q_len=5 causal window, 16q/4kv heads, D=128, "
+            "workload": "config3 verify step: window KV write fused into the attention launch, packed q_len=5 causal window, 16q/4kv heads, D=128, "
                         "bf16 SHARED KV, batch 32, ctx U[1024,8192]; target argmax and distributions from "
                         "fp32 logits (T=0.7, top-p 0.9) and acceptance, V=49152",
             "batch": w["n"], "window": w["window"], "q_heads": w["hq"], "kv_heads": w["hkv"],
@@ -655,6 +670,7 @@ def main():
         "hbm_frac_step": round((kv_bytes + a_bytes + p_bytes + c_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
         "kv_write_ms": round(t_kv * 1e3, 4),
         "attention_ms": round(t_attn * 1e3, 4),
+        "attention_with_kv_store_ms": round(t_fused * 1e3, 4),
         "probs_ms": round(t_probs * 1e3, 4),
         "accept_ms": round(t_acc * 1e3, 4),
         "verify_accept_ms": round(t_ver * 1e3, 4),
@@ -675,7 +691,7 @@ def main():
         },
     }
     if not args.no_config2:
-        del g_kv, g_attn, g_probs, g_acc, g_step, g_ver
+        del g_kv, g_attn, g_fused, g_probs, g_acc, g_step, g_ver
         result["config2_decode_attention"] = config2_decode(pkg, dev)
     if not args.no_secondary:
         result["batch64_ctx4096_verify"] = target_step(pkg, dev)

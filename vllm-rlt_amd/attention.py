@@ -62,6 +62,9 @@ class AttentionBackend:
     def prefill(self, *args, **kwargs):
         return self.kernel.prefill(*args, **kwargs)
 
+    def prefill_store(self, *args, **kwargs):
+        return self.kernel.prefill_store(*args, **kwargs)
+
     def windowed(self, *args, **kwargs):
         method = getattr(self.kernel, "windowed", None)
         if method is None:
