@@ -646,7 +646,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     const float* __restrict__ top_p, int max_top_k, int apply_top_p, float* __restrict__ out,
     int64_t out_stride, int64_t* __restrict__ argmax_out, int64_t argmax_rows,
     const float* __restrict__ qm_src, int64_t qm_rows, float* __restrict__ qm_out,
-    int64_t qm_blocks) {
+    int64_t qm_blocks, float* __restrict__ pm_out) {
   constexpr int NPT = NREG + NLDS;
   // the exact path (crowded rows) reuses the fast path's LDS
   constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
@@ -692,6 +692,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     return;
   }
   __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
+  do {
   const int64_t r = blockIdx.x;
   const int64_t src_r = rows ? rows[r] : r;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -778,7 +779,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   __syncthreads();
   if (bad || !src_ok || !isfinite(lmax) || !(temp > 0.f) || !isfinite(row.c)) {
     for (int64_t i = t; i < V; i += kThreads) dst[i] = NAN;
-    return;
+    break;
   }
   row.lmax = lmax;
 
@@ -811,7 +812,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
       const float e = row.e(j);
       if (e == e) dst[(int64_t)j * kThreads + t] = e * inv;
     });
-    return;
+    break;
   }
 
   const unsigned long long kk =
@@ -820,6 +821,34 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     __syncthreads();
     exact::exact_row<DT, kTC>(lds.ex, logits, src_r, row_stride, V, temperature, top_k, top_p,
                               max_top_k, apply_top_p, out, out_stride);
+  }
+  } while (0);
+  if (pm_out) {
+    // the written row's float32 row-sum partials for the acceptance sampler (p row r
+    // at pm_out + r * groups * 32): the row is read back from L2 after the barrier,
+    // which makes every wave's stores visible to the workgroup; eight 8192-float
+    // groups per pass, staged like the q rows' blocks above
+    __syncthreads();
+    cascade::ChunkSums* cs = reinterpret_cast<cascade::ChunkSums*>(&lds);
+    const cascade::RowGeom geo = cascade::row_geom(V);
+    const int t = threadIdx.x;
+    const int sub = t / cascade::kGroupThreads, st = t % cascade::kGroupThreads;
+    const float* x = out + (int64_t)blockIdx.x * out_stride;
+    constexpr int kPer = kThreads / cascade::kGroupThreads;
+    for (int64_t g0 = 0; g0 < geo.groups; g0 += kPer) {
+      const int64_t g = g0 + sub;
+      if (g < geo.groups) {
+        if (out_stride % 4 == 0 && (uintptr_t)out % 16 == 0)
+          cascade::group_chunk_sums<true>(x, g, geo.full_chunks, st, cs[sub]);
+        else
+          cascade::group_chunk_sums<false>(x, g, geo.full_chunks, st, cs[sub]);
+      }
+      __syncthreads();
+      if (g < geo.groups)
+        cascade::group_stream_sums(g, geo.full_chunks, st, cs[sub],
+                                   pm_out + ((int64_t)blockIdx.x * geo.groups + g) * cascade::kStreams);
+      __syncthreads();
+    }
   }
 }
 
@@ -857,7 +886,8 @@ void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_
                   int64_t row_stride, int V, const float* temperature, const int64_t* top_k,
                   const float* top_p, int max_top_k, int apply_top_p, float* out,
                   int64_t out_stride, hipStream_t stream, int64_t* argmax_out,
-                  int64_t argmax_rows, const float* qm_src, int64_t qm_rows, float* qm_out) {
+                  int64_t argmax_rows, const float* qm_src, int64_t qm_rows, float* qm_out,
+                  float* pm_out) {
   const cascade::RowGeom geo = cascade::row_geom(V);
   const int64_t per_block = kThreads / cascade::kGroupThreads;
   const int64_t qm_blocks = qm_src ? (qm_rows * geo.groups + per_block - 1) / per_block : 0;
@@ -865,7 +895,7 @@ void launch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t n_
                      dim3((unsigned)(n + argmax_rows + qm_blocks)), dim3(kThreads), 0, stream,
                      logits, rows, n_src, row_stride, V, temperature, top_k, top_p, max_top_k,
                      apply_top_p, out, out_stride, argmax_out, argmax_rows, qm_src, qm_rows,
-                     qm_out, qm_blocks);
+                     qm_out, qm_blocks, pm_out);
 }
 
 // Row placement by chunks per thread: registers first (at most 32, beyond which
@@ -878,12 +908,12 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
                     int max_top_k, int apply_top_p, float* out, int64_t out_stride,
                     hipStream_t stream, int64_t* argmax_out = nullptr, int64_t argmax_rows = 0,
                     const float* qm_src = nullptr, int64_t qm_rows = 0,
-                    float* qm_out = nullptr) {
+                    float* qm_out = nullptr, float* pm_out = nullptr) {
   const int chunks = (V + kThreads - 1) / kThreads;
 #define RLT_PROBS_CASE(R, L)                                                                  \
   launch_probs<DT, R, L>(n, logits, rows, n_src, row_stride, V, temperature, top_k, top_p,     \
                          max_top_k, apply_top_p, out, out_stride, stream, argmax_out,         \
-                         argmax_rows, qm_src, qm_rows, qm_out)
+                         argmax_rows, qm_src, qm_rows, qm_out, pm_out)
   if (chunks <= 4) RLT_PROBS_CASE(4, 0);
   else if (chunks <= 16) RLT_PROBS_CASE(8, 8);
   else if (chunks <= 32) RLT_PROBS_CASE(16, 16);
@@ -896,7 +926,7 @@ void dispatch_probs(int64_t n, const void* logits, const int64_t* rows, int64_t 
     launch_probs<DT, kTailReg, kTailLds, true>(n, logits, rows, n_src, row_stride, V,
                                                temperature, top_k, top_p, max_top_k,
                                                apply_top_p, out, out_stride, stream, argmax_out,
-                                               argmax_rows, qm_src, qm_rows, qm_out);
+                                               argmax_rows, qm_src, qm_rows, qm_out, pm_out);
 #undef RLT_PROBS_CASE
 }
 
@@ -1224,7 +1254,8 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
   SplitPlan pl;
   const bool sp = mtk == 0 && !apply_top_p && split_plan(rows, V, pl, 32) &&
                   workspace_bytes >= acc_bytes + split_bytes(rows, 0, V);
-  float* pm_out = sp ? rlt_accept_p_partials(workspace, n, w1, vocab) : nullptr;
+  // both forms write the p rows' row-sum partials alongside the distributions
+  float* pm_out = rlt_accept_p_partials(workspace, n, w1, vocab);
   // distributions of every verify row, their argmax targets, and the draft rows'
   // row-sum partials (one launch, or the split form's launches); then the acceptance
   // sums only p
@@ -1237,7 +1268,7 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
     else                                                                                      \
       dispatch_probs<DT>(rows, target_logits, nullptr, rows, row_stride, V, temperature,      \
                          top_k, top_p, mtk, apply_top_p != 0, p_out, vocab, stream, targets,  \
-                         rows, q_rows > 0 ? q : nullptr, q_rows, qm_out);                     \
+                         rows, q_rows > 0 ? q : nullptr, q_rows, qm_out, pm_out);             \
   } while (0)
   switch (logits_dtype) {
     case RLT_F32: RLT_VERIFY_ACCEPT(RLT_F32); break;
@@ -1248,13 +1279,9 @@ int rlt_verify_accept(const void* target_logits, int32_t logits_dtype, int64_t r
 #undef RLT_VERIFY_ACCEPT
   const int st = rlt_launch_status();
   if (st != RLT_OK) return st;
-  if (sp)  // the write launch summed p as well
-    return rlt_accept_after_pq_partials(draft_tokens, drafts, q, p_out, u_accept, u_final, n, w1,
-                                        vocab, tokens, accepted, final_token, error, workspace,
-                                        workspace_bytes, stream);
-  return rlt_accept_after_q_partials(draft_tokens, drafts, q, p_out, u_accept, u_final, n, w1,
-                                     vocab, tokens, accepted, final_token, error, workspace,
-                                     workspace_bytes, stream);
+  return rlt_accept_after_pq_partials(draft_tokens, drafts, q, p_out, u_accept, u_final, n, w1,
+                                      vocab, tokens, accepted, final_token, error, workspace,
+                                      workspace_bytes, stream);
 }
 
 }  // extern "C"
