@@ -384,6 +384,39 @@ def target_step(pkg, dev):
             "verified_tokens_per_s": round(rows / (t_attn + t_ver), 1),
             "graph_replays_equal_eager": s1 and s2 and s3}
 
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def prefill_steps(pkg, dev):
+    """The packed causal prefill tiling (a prompt's whole window attends to itself through the
+    pool, triton_attention.py:250-383): bf16, 16 q / 4 kv heads, D = 128, block size 16; batches
+    of 8 x 2048, 4 x 4096 and 1 x 8192-token prompts.  MFMA-bound: 4 * Hq * D * sum L(L+1)/2
+    flops per launch."""
+    g = torch.Generator().manual_seed(6)
+    gd = torch.Generator(device=dev).manual_seed(6)
+    hq, hkv, d, bs = 16, 4, 128, 16
+    kern = pkg.MI355XPagedAttention()
+    out = {}
+    for n, L in ((8, 2048), (4, 4096), (1, 8192)):
+        per = L // bs
+        kc = torch.randn(n * per, bs, hkv, d, generator=gd, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn(n * per, bs, hkv, d, generator=gd, device=dev, dtype=torch.bfloat16)
+        tables = torch.randperm(n * per, generator=g).int().view(n, per).to(dev)
+        lengths = torch.full((n,), L, dtype=torch.int32, device=dev)
+        cu = torch.arange(0, n * L + 1, L, dtype=torch.int32, device=dev)
+        q = torch.randn(n * L, hq, d, generator=gd, device=dev, dtype=torch.bfloat16)
+        t, same = _graph_time(lambda: kern.prefill(q, kc, vc, tables, lengths, cu, L), reps=11,
+                              per_graph=4)
+        flops = 4 * hq * d * n * L * (L + 1) // 2
+        tf = flops / t / 1e12
+        out[f"{n}x{L}"] = {"us": round(t * 1e6, 1), "tflops": round(tf, 1),
+                           "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                           "graph_replays_equal_eager": same}
+        del kc, vc, q
+    return {"workload": "packed causal prefill, bf16, 16 q / 4 kv heads, D=128, block 16",
+            "flops_per_launch": "4 * Hq * D * sum L(L+1)/2", "launches": out}
+
+
 def _secondary(workload, tokens, t_attn, a_bytes, t_acc, c_bytes, replay_equal):
     return {"workload": workload,
             "verified_tokens_per_s": round(tokens / (t_attn + t_acc), 1),
@@ -441,6 +474,8 @@ def main():
                     help="skip the secondary config-2 decode attention measurement")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the config-4 and config-5 attention + verify_accept measurements")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="print only the prefill measurements and exit")
     ap.add_argument("--only", choices=("kv_write", "attention", "attention_store", "probs", "accept",
                                        "verify", "copy",
                                        "config5_attention"),
@@ -465,6 +500,9 @@ def main():
             dst_buf.copy_(src_buf)
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_launch": 1 << 30, "steps": args.steps}), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps(prefill_steps(pkg, dev)), flush=True)
         return
     if args.only == "config5_attention":
         print(json.dumps(config5_step(pkg, dev, attention_only=True)), flush=True)
@@ -699,6 +737,8 @@ def main():
         result["config4_verify"] = config4_step(pkg, dev)
         torch.cuda.empty_cache()
         result["config5_verify"] = config5_step(pkg, dev)
+        torch.cuda.empty_cache()
+        result["prefill"] = prefill_steps(pkg, dev)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)

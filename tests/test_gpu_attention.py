@@ -383,6 +383,32 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
         torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("bs,window", [(8, 0), (8, 256), (48, 0), (32, 100)])
+def test_long_prompt_prefill_block_sizes(kernel, dev, bs, window):
+    """The prefill tiling's two address paths: blocks holding whole 16-position groups
+    (one table lookup per group, 32 and 48 here) and smaller blocks (a lookup per
+    position, 8 here), with and without a sliding window."""
+    _say("long prefill block size", bs, window)
+    g = torch.Generator().manual_seed(22)
+    hq, hkv, d, dtype = 16, 4, 128, torch.bfloat16
+    seqs = [(1024, 1024), (2000, 700), (129, 129)]
+    pages = sum(-(-n // bs) for n, _ in seqs) + 2
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables([n for n, _ in seqs], bs, pages, g)
+    total = sum(c for _, c in seqs)
+    q = torch.randn(total, hq, d, generator=g).to(dtype)
+    lengths = torch.tensor([n for n, _ in seqs], dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor([c for _, c in seqs]).cumsum(0)), dtype=torch.int32)
+    got = kernel.prefill(q.to(dev), k.to(dev), v.to(dev), tables.to(dev), lengths.to(dev),
+                         cu.to(dev), max(c for _, c in seqs), window=window).cpu()
+    for s, (n, c) in enumerate(seqs):
+        pages_s = tables[s, : -(-n // bs)].long()
+        k_seq = k[pages_s].reshape(-1, hkv, d)[:n]
+        v_seq = v[pages_s].reshape(-1, hkv, d)[:n]
+        want = _dense_packed(q[cu[s]:cu[s + 1]], k_seq, v_seq, c, n, window)
+        torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
+
+
 # ------------------------------------------ packed rows with explicit row lengths
 
 def _group_rows_by_plane(n, w, planes, d0, row_len, order="ascending"):

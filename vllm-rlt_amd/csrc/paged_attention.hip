@@ -1463,16 +1463,26 @@ constexpr int kPfRows = 4 * 16 * kPfNT;  // q rows per workgroup (4 waves)
 constexpr int kPfKeys = 64;     // key positions per LDS tile
 constexpr int kPfThreads = 256;
 constexpr int kPfMinQ = 64;     // q window length from which a call takes this path
+constexpr float kPfLazy = 8.f;  // log2 headroom before the running max moves
 
 template <int D>
 struct PrefillLds {
-  static constexpr int kKRow = D * 2 + 16;            // bytes per K position row
-  static constexpr int kVRowW = kPfKeys / 2 + 1;      // dwords per V^T dim row (odd: fewer conflicts)
+  static constexpr int kKRow = D * 2 + 16;        // bytes per K position row
+  static constexpr int kVRowW = kPfKeys / 2 + 2;  // dwords per V^T dim row (32 position pairs + 2)
   uint8_t k[2][kPfKeys * kKRow];
   uint32_t vt[2][D * kVRowW];
 };
 
-template <int QT, int D>
+// Dword column of position pair `col` in V^T dim row r.  With rows 34 dwords apart
+// (2 mod 32 banks) the compute reads -- 16 dim rows x one dword pair per lane, 16 lanes
+// at a time -- cover the 32 banks once; flipping bit 3 of the column in rows with bit 4
+// set spreads the staging stores (8 position pairs x 4 pieces per 32 lanes) over all
+// 32 banks too.  Dword pairs (2j, 2j + 1) stay adjacent for 8-byte reads.
+__device__ __forceinline__ int vt_col(int r, int col) { return col ^ (8 * ((r >> 4) & 1)); }
+
+// UB: block_size % 16 == 0, so each 16-position group of a tile lies in one block
+// and its address comes from one wave-uniform table lookup.
+template <int QT, int D, bool UB>
 __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_kernel(AttnParams P) {
   using M = Mfma<QT>;
   using L = PrefillLds<D>;
@@ -1482,8 +1492,9 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   constexpr int KCH = D / 8;        // 16-byte pieces per position row
   constexpr int KSTEP = kPfThreads / KCH;          // K rows one pass of the workgroup loads
   constexpr int KPT = kPfKeys / KSTEP;             // K pieces per thread per tile
-  constexpr int VPAIRS = kPfThreads / KCH;         // V position pairs per pass
-  constexpr int VPT = kPfKeys / (2 * VPAIRS);      // V passes per tile (two pieces each)
+  constexpr int VPASS = KCH / 8;    // V passes per tile: a wave loads 8 pieces of 16 positions
+  static_assert(16 % (64 / KCH) == 0, "a wave's K rows of one pass stay in one 16-position group");
+  static_assert(kPfKeys == 16 * (kPfThreads / 64), "a wave stages one 16-position group of V");
   __shared__ L sh;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
 
@@ -1504,6 +1515,9 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   // this lane's rows (one per 16-row tile): B operand of S^T = K Q^T
   uint4 qreg[NT][NQS];
   int row_lo[NT], row_hi[NT];
+  // the wave's common visible range: tiles inside [wlo, whi) need no position masks
+  // (rows past the group are not stored and do not narrow it)
+  int wlo = -(1 << 30), whi = 1 << 30;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int local = w * 16 * NT + nt * 16 + l16;
@@ -1512,6 +1526,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
       const int qi = rho / P.group;
       const int head = kvh * P.group + rho % P.group;
       row_range(P, sv, qi, row_lo[nt], row_hi[nt]);
+      wlo = max(wlo, row_lo[nt]);
+      whi = min(whi, row_hi[nt]);
       const uint16_t* qp = (const uint16_t*)P.q + (int64_t)(sv.q_begin + qi) * P.q_row_stride +
                            (int64_t)head * P.q_head_stride + grp * 8;
 #pragma unroll
@@ -1522,6 +1538,13 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
       for (int s = 0; s < NQS; ++s) qreg[nt][s] = make_uint4(0, 0, 0, 0);
     }
   }
+  for (int off = 32; off >= 1; off >>= 1) {
+    wlo = max(wlo, __shfl_xor(wlo, off, RLT_WAVE));
+    whi = min(whi, __shfl_xor(whi, off, RLT_WAVE));
+  }
+  wlo = __builtin_amdgcn_readfirstlane(wlo);
+  whi = __builtin_amdgcn_readfirstlane(whi);
+
   f32x4 oacc[NT][ND];
   float m_run[NT], l_run[NT];
 #pragma unroll
@@ -1532,60 +1555,89 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- global -> registers -> LDS staging of one 64-position tile
+  // ---- global -> registers -> LDS staging of one 64-position tile.
+  // K: thread (piece, krow) loads rows krow + KSTEP j.  V: wave w loads positions
+  // 16 w + [0, 16) as 8 pairs (lane & 7) x 8 pieces (lane >> 3, + 8 per pass).
   const int piece = t % KCH;
-  const int krow = t / KCH;  // K: rows krow + KSTEP j;  V: pairs (2 krow, 2 krow + 1) + 2 VPAIRS h
+  const int krow = t / KCH;
+  const int vpair = lane & 7;
+  const int vpiece = lane >> 3;
   const int64_t k_head = (int64_t)kvh * P.k_head_stride + piece * 8;
-  const int64_t v_head = (int64_t)kvh * P.v_head_stride + piece * 8;
+  const int64_t v_head = (int64_t)kvh * P.v_head_stride + vpiece * 8;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 kr[KPT], vr[2 * VPT];
-  auto token = [&](int pos, int64_t block_stride, int64_t token_stride) {
+  u32x4 kr[KPT], vr[2 * VPASS];
+  // (block id, offset) of position pos: block ids outside the pool read block 0
+  auto block_of = [&](int pos, int64_t& blk, int& off) {
     const int idx = min(pos / P.block_size, P.table_width - 1);
     const int32_t e = P.tables[(int64_t)seq * P.table_stride + idx];
-    const int64_t blk = (e >= 0 && e < P.num_blocks) ? e : 0;
-    return blk * block_stride + (int64_t)(pos % P.block_size) * token_stride;
+    blk = (e >= 0 && e < P.num_blocks) ? e : 0;
+    off = pos % P.block_size;
   };
   auto load = [&](int tile) {
     const int base = tile * kPfKeys;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const int pos = base + krow + KSTEP * j;
-      kr[j] = *(const u32x4*)((const uint16_t*)P.k + token(pos, P.k_block_stride, P.k_token_stride) +
-                               k_head);
+      const int r = krow + KSTEP * j;
+      int64_t blk;
+      int off;
+      if (UB) {
+        // the wave's rows of this pass share one 16-position group
+        block_of(__builtin_amdgcn_readfirstlane(base + (r & ~15)), blk, off);
+        off += r & 15;
+      } else {
+        block_of(base + r, blk, off);
+      }
+      kr[j] = *(const u32x4*)((const uint16_t*)P.k + blk * P.k_block_stride +
+                               (int64_t)off * P.k_token_stride + k_head);
     }
+    int64_t vblk = 0;
+    int voff0 = 0;
+    if (UB) block_of(__builtin_amdgcn_readfirstlane(base + 16 * w), vblk, voff0);
 #pragma unroll
-    for (int h = 0; h < VPT; ++h)
+    for (int e = 0; e < 2; ++e) {
+      const int pos = base + 16 * w + 2 * vpair + e;
+      int64_t blk = vblk;
+      int off = voff0 + 2 * vpair + e;
+      if (!UB) block_of(pos, blk, off);
+      const uint16_t* vp = (const uint16_t*)P.v + blk * P.v_block_stride +
+                           (int64_t)off * P.v_token_stride + v_head;
+      const bool ok = pos < hi_last;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int pos = base + 2 * krow + 2 * VPAIRS * h + e;
-        const u32x4 v = *(const u32x4*)((const uint16_t*)P.v +
-                                        token(pos, P.v_block_stride, P.v_token_stride) + v_head);
+      for (int h = 0; h < VPASS; ++h) {
+        const u32x4 v = *(const u32x4*)(vp + 64 * h);
         // positions past the sequence may hold any bits (NaN included): zero them,
         // since their weight 0 times NaN would not vanish
-        vr[2 * h + e] = pos < hi_last ? v : u32x4{0u, 0u, 0u, 0u};
+        vr[2 * h + e] = ok ? v : u32x4{0u, 0u, 0u, 0u};
       }
+    }
   };
   auto store = [&](int b) {
 #pragma unroll
     for (int j = 0; j < KPT; ++j)
       *(u32x4*)(sh.k[b] + (krow + KSTEP * j) * L::kKRow + piece * 16) = kr[j];
+    const int col = 8 * w + vpair;  // dword column: positions 2 col, 2 col + 1
 #pragma unroll
-    for (int h = 0; h < VPT; ++h) {
+    for (int h = 0; h < VPASS; ++h) {
       const u32x4 av = vr[2 * h], cv = vr[2 * h + 1];
-      const int col = krow + VPAIRS * h;  // dword column: positions 2 col, 2 col + 1
+      const int pc = vpiece + 8 * h;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        // dims piece*8 + 2q (low halves) and + 2q + 1 (high halves)
-        const uint32_t lo = (av[q] & 0xffffu) | (cv[q] << 16);
-        const uint32_t hi = (av[q] >> 16) | (cv[q] & 0xffff0000u);
-        sh.vt[b][(piece * 8 + 2 * q) * L::kVRowW + col] = lo;
-        sh.vt[b][(piece * 8 + 2 * q + 1) * L::kVRowW + col] = hi;
+        // dims pc*8 + 2q (low halves of both positions) and + 2q + 1 (high halves)
+        const int r0 = pc * 8 + 2 * q;
+        sh.vt[b][r0 * L::kVRowW + vt_col(r0, col)] = __builtin_amdgcn_perm(cv[q], av[q], 0x05040100u);
+        sh.vt[b][(r0 + 1) * L::kVRowW + vt_col(r0 + 1, col)] =
+            __builtin_amdgcn_perm(cv[q], av[q], 0x07060302u);
       }
     }
   };
 
+  // V^T reads: dim row r = 16 dt + l16 holds column vt_col(r, 16 c + 2 grp + 8 k) at
+  // 2 grp + ((16 c + 8 k) ^ 8 (dt & 1)): one lane offset plus compile-time constants
+  const int vlane = l16 * L::kVRowW + 2 * grp;
+
   const float qk_scale = P.qk_scale_log2;
-  auto compute = [&](int tile, int b) {
+  auto compute = [&](int tile, int b, auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
     const int base = tile * kPfKeys;
     const uint8_t* kb = sh.k[b];
     const uint32_t* vb = sh.vt[b];
@@ -1603,7 +1655,10 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) sc[kt][nt] = M::qk(a, qreg[nt][s], sc[kt][nt]);
       }
-    // ---- online softmax (log2 domain); lane holds positions base + 16 kt + 4 grp + i
+    // ---- online softmax (log2 domain); lane holds positions base + 16 kt + 4 grp + i.
+    // The running max m moves only when a tile's max exceeds it by more than kPfLazy
+    // (weights stay below 2^kPfLazy), so the accumulators are rarely rescaled; the
+    // scale enters as one fma per score (qk_scale > 0: the max of raw scores scales).
     uint4 pop[2][NT];
     bool rescale = false;
     float corr[NT];
@@ -1615,23 +1670,28 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int pos = base + kt * 16 + 4 * grp + i;
-          const float v = sc[kt][nt][i] * qk_scale;
-          x[kt][i] = (pos >= row_lo[nt] && pos < row_hi[nt]) ? v : -INFINITY;
+          const float v = sc[kt][nt][i];
+          if (FULL) {
+            x[kt][i] = v;
+          } else {
+            const int pos = base + kt * 16 + 4 * grp + i;
+            x[kt][i] = (pos >= row_lo[nt] && pos < row_hi[nt]) ? v : -INFINITY;
+          }
           mx = fmaxf(mx, x[kt][i]);
         }
-      mx = group_max(mx);
-      const float m_new = fmaxf(m_run[nt], mx);
+      const float mxs = group_max(mx) * qk_scale;
+      const bool grow = mxs > m_run[nt] + kPfLazy;
+      const float m_new = grow ? mxs : m_run[nt];
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      corr[nt] = m_new == m_run[nt] ? 1.f : __builtin_amdgcn_exp2f(m_run[nt] - m_use);
-      rescale |= corr[nt] != 1.f;
+      corr[nt] = grow ? __builtin_amdgcn_exp2f(m_run[nt] - m_use) : 1.f;
+      rescale |= grow;
       float rs = 0.f;
       float pr[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pr[kt][i] = __builtin_amdgcn_exp2f(x[kt][i] - m_use);
+          pr[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], qk_scale, -m_use));
           rs += pr[kt][i];
         }
       l_run[nt] = l_run[nt] * corr[nt] + group_sum(rs);
@@ -1655,8 +1715,10 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) {
-        const uint32_t* row = vb + (dt * 16 + l16) * L::kVRowW + 16 * c + 2 * grp;
-        const uint4 a = make_uint4(row[0], row[1], row[8], row[9]);
+        const uint32_t* rows = vb + dt * 16 * L::kVRowW + vlane;
+        const uint2 x0 = *(const uint2*)(rows + ((16 * c) ^ (8 * (dt & 1))));
+        const uint2 x1 = *(const uint2*)(rows + ((16 * c + 8) ^ (8 * (dt & 1))));
+        const uint4 a = make_uint4(x0.x, x0.y, x1.x, x1.y);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::qk(a, pop[c][nt], oacc[nt][dt]);
       }
@@ -1665,18 +1727,26 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   const int kt0 = lo_first / kPfKeys;
   const int kt1 = (hi_last + kPfKeys - 1) / kPfKeys;
   if (kt0 < kt1) {
-    load(kt0);
-    store(0);
-    __syncthreads();
-    for (int tile = kt0; tile < kt1; ++tile) {
+    auto step = [&](int tile, auto full_tag) {
       const int b = (tile - kt0) & 1;
       const bool more = tile + 1 < kt1;
       if (more) load(tile + 1);
-      compute(tile, b);
+      compute(tile, b, full_tag);
       // buffer b ^ 1 was last read in the previous iteration, before its barrier
       if (more) store(b ^ 1);
       __syncthreads();
-    }
+    };
+    // tiles [fa, fb) lie inside every row's visible range: three loops, so that no
+    // branch between the two compute forms sits inside one (its join would copy the
+    // accumulators)
+    const int fa = min(kt1, max(kt0, (max(wlo, 0) + kPfKeys - 1) / kPfKeys));
+    const int fb = max(fa, min(kt1, whi / kPfKeys));
+    load(kt0);
+    store(0);
+    __syncthreads();
+    for (int tile = kt0; tile < fa; ++tile) step(tile, Flag<false>{});
+    for (int tile = fa; tile < fb; ++tile) step(tile, Flag<true>{});
+    for (int tile = fb; tile < kt1; ++tile) step(tile, Flag<false>{});
   }
 
   // ---- normalized output: lane holds dims 16 dt + 4 grp + i of its rows
@@ -1748,6 +1818,18 @@ int launch_vec_q(const AttnParams& P, int kv_dtype, dim3 grid, hipStream_t strea
     default: return RLT_ERR_ARGUMENT;
   }
   return RLT_OK;
+}
+
+template <int QT, int D>
+void launch_prefill_d(const AttnParams& P, dim3 grid, hipStream_t stream) {
+  if (P.block_size % 16 == 0) rlt_prefill_kernel<QT, D, true><<<grid, kPfThreads, 0, stream>>>(P);
+  else rlt_prefill_kernel<QT, D, false><<<grid, kPfThreads, 0, stream>>>(P);
+}
+
+template <int QT>
+void launch_prefill(const AttnParams& P, int head_dim, dim3 grid, hipStream_t stream) {
+  if (head_dim == 64) launch_prefill_d<QT, 64>(P, grid, stream);
+  else launch_prefill_d<QT, 128>(P, grid, stream);
 }
 
 template <int OT>
@@ -1922,13 +2004,8 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
       const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads;
       if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
       const dim3 grid((unsigned)wgs);
-      if (q_dtype == RLT_BF16) {
-        if (head_dim == 64) rlt_prefill_kernel<RLT_BF16, 64><<<grid, kPfThreads, 0, stream>>>(P);
-        else rlt_prefill_kernel<RLT_BF16, 128><<<grid, kPfThreads, 0, stream>>>(P);
-      } else {
-        if (head_dim == 64) rlt_prefill_kernel<RLT_F16, 64><<<grid, kPfThreads, 0, stream>>>(P);
-        else rlt_prefill_kernel<RLT_F16, 128><<<grid, kPfThreads, 0, stream>>>(P);
-      }
+      if (q_dtype == RLT_BF16) launch_prefill<RLT_BF16>(P, head_dim, grid, stream);
+      else launch_prefill<RLT_F16>(P, head_dim, grid, stream);
       return rlt_launch_status();
     }
     const int nt = (rows_per_seq > 16 && head_dim <= 128) ? 2 : 1;
