@@ -24,6 +24,22 @@ def test_attention_and_sampling_ops_match_the_api(pkg, dev):
     assert torch.equal(got, want)
     torch.library.opcheck(torch.ops.rlt_mi355x.paged_attention, args, test_utils=CHECKS)
 
+    # the window's K/V stored by the attention launch: the pool afterwards and the output
+    # equal the separate store + attention (the pool is rewritten with the same rows)
+    kn = torch.randn(15, 4, 128, generator=g).bfloat16().to(dev)
+    vn = torch.randn(15, 4, 128, generator=g).bfloat16().to(dev)
+    kd, vd = k.to(dev), v.to(dev)
+    sa = (q.to(dev), kn, vn, kd, vd, tables.to(dev), lengths.to(dev), cu.to(dev), 5)
+    got = torch.ops.rlt_mi355x.paged_attention_store(*sa)
+    ks, vs = k.to(dev), v.to(dev)
+    seq = torch.arange(3).repeat_interleave(5)
+    pos = lengths.long()[seq] - 5 + torch.arange(15) % 5
+    pkg.store_kv(ks, vs, kn, vn, tables.long()[seq, pos // 16].to(dev), (pos % 16).to(dev))
+    want = pkg.MI355XPagedAttention().prefill(q.to(dev), ks, vs, tables.to(dev), lengths.to(dev),
+                                              cu.to(dev), 5)
+    assert torch.equal(got, want) and torch.equal(kd, ks) and torch.equal(vd, vs)
+    torch.library.opcheck(torch.ops.rlt_mi355x.paged_attention_store, sa, test_utils=CHECKS)
+
     logits = torch.randn(6, 3000, generator=g).to(dev)
     t, tk = torch.full((6,), 0.8, device=dev), torch.full((6,), -1, dtype=torch.int64, device=dev)
     tp = torch.full((6,), 0.9, device=dev)

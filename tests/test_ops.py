@@ -13,6 +13,7 @@ def test_operators_are_registered_with_reference_shaped_schemas(pkg):
     assert "!) key_cache" in names["store_kv"]
     assert "float? fixed_scale" in names["store_fp8"]
     assert "Tensor? row_lengths=None" in names["paged_attention"]
+    assert "!) key_cache" in names["paged_attention_store"]
     assert names["merge_random_round"].endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
 
 
@@ -24,7 +25,7 @@ def test_per_step_operators_are_cpp(pkg):
     from vllm_rlt_amd import _lib
 
     assert os.path.exists(_lib.OPS_PATH)
-    for op in ("paged_attention", "store_kv", "spec_probs", "categorical", "spec_accept",
+    for op in ("paged_attention", "paged_attention_store", "store_kv", "spec_probs", "categorical", "spec_accept",
                "greedy_accept", "verify_distributions", "verify_accept"):
         kernels = torch._C._dispatch_dump(f"rlt_mi355x::{op}")
         assert "CUDA: registered at" in kernels and "torch_bindings.cpp" in kernels, op

@@ -21,7 +21,6 @@ from dataclasses import dataclass, replace
 import torch
 
 from . import _lib
-from .kv_write import store_kv
 
 
 @dataclass(frozen=True)
@@ -150,56 +149,11 @@ class MI355XPagedAttention:
         """
         _lib.require_gpu(q, k_new, v_new, key_cache, value_cache, block_tables, context_lengths,
                          cu_seqlens_q)
-        rows, hq, d = q.shape
-        hkv = key_cache.shape[2]
-        if k_new.shape != (rows, hkv, d) or v_new.shape != k_new.shape:
-            raise ValueError("k_new, v_new must be [q rows, kv_heads, head_dim]")
-        if k_new.dtype != key_cache.dtype or v_new.dtype != key_cache.dtype:
-            raise ValueError("k_new, v_new must have the pool's dtype")
-        if key_cache.stride() != value_cache.stride() or key_cache.stride(3) != 1:
-            raise ValueError("key and value pools must share a layout with a unit dim stride")
-        lib = _lib.library()
-        fused = (q.dtype == key_cache.dtype and q.dtype in (torch.bfloat16, torch.float16)
-                 and rows > 0 and not lib.rlt_paged_attention_uses_prefill(
-                     _lib.dtype_code(q.dtype), _lib.dtype_code(key_cache.dtype), d,
-                     int(max_seqlen_q)))
-        if fused:
-            qq = q if q.stride(2) == 1 else q.contiguous()
-            kn = k_new if k_new.stride(2) == 1 else k_new.contiguous()
-            vn = v_new if v_new.stride() == kn.stride() else v_new.contiguous()
-            if vn.stride() != kn.stride():
-                kn, vn = kn.contiguous(), vn.contiguous()
-            tables = block_tables.to(torch.int32)
-            tables = tables if tables.stride(1) == 1 else tables.contiguous()
-            lengths = context_lengths.to(torch.int32)
-            cu = cu_seqlens_q.to(torch.int32)
-            out = torch.empty_like(q)
-            ws = _lib.workspace(lib.rlt_paged_attention_workspace_size(
-                rows, hq, d, tables.shape[1], key_cache.shape[1]), q.device)
-            status = lib.rlt_paged_attention_store(
-                _lib.ptr(qq), qq.stride(0), qq.stride(1), _lib.ptr(key_cache), _lib.ptr(value_cache),
-                key_cache.stride(0), key_cache.stride(1), key_cache.stride(2), value_cache.stride(0),
-                value_cache.stride(1), value_cache.stride(2), key_cache.shape[0], _lib.ptr(tables),
-                tables.stride(0), tables.shape[1], _lib.ptr(lengths), _lib.ptr(cu),
-                tables.shape[0], int(max_seqlen_q), rows, hq, hkv, d, key_cache.shape[1],
-                _lib.dtype_code(q.dtype), _lib.ptr(kn), _lib.ptr(vn), kn.stride(0), kn.stride(1),
-                _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(ws), ws.numel(),
-                _lib.stream_of(q.device))
-            if status != 2:  # 2: a shape the fused form does not serve
-                _lib.check(status, "rlt_paged_attention_store")
-                return out
-        # separate store and attention: positions -> (block, offset) through the tables
-        cu = cu_seqlens_q.to(torch.int64)
-        q_len = cu[1:] - cu[:-1]
-        seq = torch.repeat_interleave(torch.arange(len(q_len), device=q.device), q_len,
-                                      output_size=rows)
-        pos = (context_lengths.to(torch.int64)[seq] - q_len[seq]
-               + torch.arange(rows, device=q.device) - cu[seq])
-        bs = key_cache.shape[1]
-        blocks = block_tables.to(torch.int64)[seq, pos // bs]
-        store_kv(key_cache, value_cache, k_new, v_new, blocks, pos % bs)
-        return self.prefill(q, key_cache, value_cache, block_tables, context_lengths,
-                            cu_seqlens_q, max_seqlen_q)
+        # argument checks, the one-launch form or the separate store + attention:
+        # torch.ops.rlt_mi355x.paged_attention_store (csrc/torch_bindings.cpp)
+        return _lib.ops().paged_attention_store(q, k_new, v_new, key_cache, value_cache,
+                                                block_tables, context_lengths, cu_seqlens_q,
+                                                int(max_seqlen_q))
 
     def uses_mfma(self, q_dtype, kv_dtype, head_dim):
         lib = _lib.library()

@@ -409,6 +409,88 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> verify_accept(
   return {target, p, tokens, accepted, final_token, error};
 }
 
+// ---------------------------------------------------------------- window store + attention
+
+// reference: vllm_rlt/kernels/graph_kv.py:52-67 (the window rows' KV write) followed by
+// vllm_rlt/kernels/triton_attention.py:386-404 (packed window attention).  Row r of
+// k_new / v_new goes to packed q row r's position (context_lengths[s] - q_len + i).
+// bf16 / fp16 windows below the prefill tiling run as one launch pair
+// (rlt_paged_attention_store); other shapes store with the scatter kernel and attend
+// separately, with the same result.
+Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tensor& v_new_in,
+                             const Tensor& key_cache, const Tensor& value_cache,
+                             const Tensor& block_tables, const Tensor& context_lengths,
+                             const Tensor& cu_seqlens_q, int64_t max_seqlen_q) {
+  TORCH_CHECK_VALUE(q.dim() == 3, "q must be [rows, heads, dim]");
+  check_view(key_cache, "key_cache");
+  check_view(value_cache, "value_cache");
+  TORCH_CHECK_VALUE(key_cache.strides() == value_cache.strides() &&
+                        key_cache.sizes() == value_cache.sizes(),
+                    "key and value pools must share a layout with a unit dim stride");
+  const int64_t rows = q.size(0), head_dim = q.size(2), kv_heads = key_cache.size(2);
+  const Tensor k_new = rows3(k_new_in, "k_new"), v_new = rows3(v_new_in, "v_new");
+  TORCH_CHECK_VALUE(k_new.size(0) == rows && k_new.size(1) == kv_heads && k_new.size(2) == head_dim &&
+                        v_new.sizes() == k_new.sizes(),
+                    "k_new, v_new must be [q rows, kv_heads, head_dim]");
+  TORCH_CHECK_VALUE(k_new.scalar_type() == key_cache.scalar_type() &&
+                        v_new.scalar_type() == key_cache.scalar_type(),
+                    "k_new, v_new must have the pool's dtype");
+  const bool half = q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf;
+  if (rows > 0 && half && q.scalar_type() == key_cache.scalar_type() &&
+      !rlt_paged_attention_uses_prefill(dtype_code(q.scalar_type()),
+                                        dtype_code(key_cache.scalar_type()), (int32_t)head_dim,
+                                        (int32_t)max_seqlen_q)) {
+    const Tensor qq = q.stride(2) == 1 ? q : q.contiguous();
+    Tensor kn = k_new, vn = v_new;
+    if (vn.strides() != kn.strides()) {
+      kn = kn.contiguous();
+      vn = vn.contiguous();
+    }
+    Tensor tables = block_tables.scalar_type() == at::kInt ? block_tables : block_tables.to(at::kInt);
+    if (tables.stride(1) != 1) tables = tables.contiguous();
+    const Tensor lengths = as(context_lengths, at::kInt);
+    const Tensor cu = as(cu_seqlens_q, at::kInt);
+    const int64_t num_seqs = tables.size(0), width = tables.size(1), heads = q.size(1);
+    TORCH_CHECK_VALUE(cu.size(0) == num_seqs + 1 && lengths.size(0) == num_seqs,
+                      "cu_seqlens_q must be [sequences + 1] and lengths [sequences]");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    Tensor output = at::empty_like(q);
+    const Tensor ws = workspace(
+        rlt_paged_attention_workspace_size((int32_t)rows, (int32_t)heads, (int32_t)head_dim,
+                                           (int32_t)width, (int32_t)key_cache.size(1)),
+        q);
+    const int status = rlt_paged_attention_store(
+        ptr(qq), qq.stride(0), qq.stride(1), ptr(key_cache), ptr(value_cache), key_cache.stride(0),
+        key_cache.stride(1), key_cache.stride(2), value_cache.stride(0), value_cache.stride(1),
+        value_cache.stride(2), (int32_t)key_cache.size(0), (const int32_t*)ptr(tables),
+        tables.stride(0), (int32_t)width, (const int32_t*)ptr(lengths), (const int32_t*)ptr(cu),
+        (int32_t)num_seqs, (int32_t)max_seqlen_q, (int32_t)rows, (int32_t)heads, (int32_t)kv_heads,
+        (int32_t)head_dim, (int32_t)key_cache.size(1), dtype_code(q.scalar_type()), ptr(kn), ptr(vn),
+        kn.stride(0), kn.stride(1), ptr(output), output.stride(0), output.stride(1), ptr(ws),
+        ws.numel(), stream_of(q));
+    if (status != 2) {  // 2: a shape the one-launch form does not serve
+      check_status(status, "rlt_paged_attention_store");
+      return output;
+    }
+  }
+  // separate store and attention: positions -> (block, offset) through the tables
+  if (rows > 0) {
+    const Tensor cu = cu_seqlens_q.to(at::kLong);
+    const int64_t num_seqs = cu.size(0) - 1;
+    const Tensor q_len = cu.slice(0, 1) - cu.slice(0, 0, num_seqs);
+    const Tensor seq = at::repeat_interleave(
+        at::arange(num_seqs, cu.options()), q_len, /*dim=*/0, /*output_size=*/rows);
+    const Tensor pos = context_lengths.to(at::kLong).index({seq}) - q_len.index({seq}) +
+                       at::arange(rows, cu.options()) - cu.index({seq});
+    const int64_t bs = key_cache.size(1);
+    const Tensor blocks = block_tables.to(at::kLong).index({seq, at::floor_divide(pos, bs)});
+    store_kv(key_cache, value_cache, k_new, v_new, blocks, at::remainder(pos, bs), std::nullopt,
+             std::nullopt);
+  }
+  return paged_attention(q, key_cache, value_cache, block_tables, context_lengths, std::nullopt,
+                         std::nullopt, cu_seqlens_q, max_seqlen_q, 0, std::nullopt);
+}
+
 }  // namespace
 
 TORCH_LIBRARY(rlt_mi355x, m) {
@@ -429,6 +511,9 @@ TORCH_LIBRARY(rlt_mi355x, m) {
   m.def("verify_accept(Tensor target_logits, Tensor temperature, Tensor top_k, Tensor top_p, "
         "Tensor draft_tokens, Tensor drafts, Tensor q, Tensor u_accept, Tensor u_final, "
         "int max_top_k, bool apply_top_p) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("paged_attention_store(Tensor q, Tensor k_new, Tensor v_new, Tensor(a!) key_cache, "
+        "Tensor(b!) value_cache, Tensor block_tables, Tensor context_lengths, "
+        "Tensor cu_seqlens_q, int max_seqlen_q) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(rlt_mi355x, CUDA, m) {
@@ -440,4 +525,5 @@ TORCH_LIBRARY_IMPL(rlt_mi355x, CUDA, m) {
   m.impl("greedy_accept", &greedy_accept);
   m.impl("verify_distributions", &verify_distributions);
   m.impl("verify_accept", &verify_accept);
+  m.impl("paged_attention_store", &paged_attention_store);
 }

@@ -3,8 +3,8 @@
 The reference binds its native code as a ``TORCH_LIBRARY`` schema
 (csrc/torch_bindings.cpp:7-13) next to Python ``torch.library`` fragments
 (vllm_rlt/kernels/activation.py:34-39).  This package does the same for the gfx950
-kernels: the per-step entry points -- ``paged_attention``, ``store_kv``,
-``spec_probs``, ``categorical``, ``spec_accept``, ``greedy_accept``,
+kernels: the per-step entry points -- ``paged_attention``, ``paged_attention_store``,
+``store_kv``, ``spec_probs``, ``categorical``, ``spec_accept``, ``greedy_accept``,
 ``verify_distributions``, ``verify_accept`` -- are C++ operators
 (``csrc/torch_bindings.cpp`` -> ``_C.so``: schema, argument checks, workspace and
 launch, one dispatcher call per step); the rest are Python ``torch.library``
@@ -29,6 +29,12 @@ _lib.ops()  # registers the C++ operators (raises if _C.so is missing)
 @torch.library.register_fake("rlt_mi355x::paged_attention")
 def _(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value_scale,
       cu_seqlens_q, max_seqlen_q, window, row_lengths=None):
+    return torch.empty_like(q)
+
+
+@torch.library.register_fake("rlt_mi355x::paged_attention_store")
+def _(q, k_new, v_new, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+      max_seqlen_q):
     return torch.empty_like(q)
 
 
@@ -160,7 +166,7 @@ def finalize_rows(descriptor: torch.Tensor, tables: torch.Tensor, key_pool: torc
     _kv.finalize_rows(descriptor, tables, key_pool, value_pool, block_size)
 
 
-OPS = ("paged_attention", "spec_probs", "categorical", "spec_accept", "greedy_accept",
+OPS = ("paged_attention", "paged_attention_store", "spec_probs", "categorical", "spec_accept", "greedy_accept",
        "propose_drafts", "verify_distributions", "verify_accept", "merge_random_round",
        "rejection_rows", "store_kv",
        "store_fp8", "finalize_rows")
