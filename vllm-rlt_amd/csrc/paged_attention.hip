@@ -53,7 +53,12 @@ constexpr int kWaves = 4;
 constexpr int kWaveSpan = kChunk / kWaves;  // 128 positions per wave
 constexpr int kTileTok = 16;
 constexpr int kStages = 2;  // KV tiles in flight per wave (MFMA path)
-constexpr int kSplit = 2;   // waves per work unit on the MFMA path (equal position spans)
+// Waves per work unit on the MFMA path (equal position spans combined in a fixed
+// order): two for 16-bit KV; one for fp8 KV, whose 512-position unit is half the bytes
+// (one wave streams it alone faster than two that wait at the combine).  Fixed per
+// dtype pair, so a row's result never depends on the batch.
+template <int QT, int KVT>
+constexpr int unit_split() { return KVT == QT ? 2 : 1; }
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -447,9 +452,9 @@ struct UnitState {
   bool active;  // the unit has rows and visible positions in this chunk
 };
 
-// Part `part` (of kSplit equal spans) of one work unit -- (sequence, row-group,
-// kv head, chunk) -- on one wave: the wave streams the kv head over positions
-// [512c + part * 512 / kSplit, + 512 / kSplit) for every row of the row-group.
+// Part `part` (of KS = unit_split equal spans) of one work unit -- (sequence,
+// row-group, kv head, chunk) -- on one wave: the wave streams the kv head over
+// positions [512c + part * 512 / KS, + 512 / KS) for every row of the row-group.
 // tbl_lds: this wave's 512-entry LDS slice for the chunk's block ids.
 // SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).  UB: block_size is a
 // multiple of 16, so the 16 positions of a tile share one block.
@@ -463,7 +468,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
   constexpr int NQS = D / 32;  // 32-wide contraction slices
   constexpr int ND = D / 16;   // 16-wide output column tiles (= dims per lane)
   constexpr int KV_ELT = KVT == QT ? 2 : 1;
-  constexpr int kSpan = kChunk / kSplit;
+  constexpr int kSpan = kChunk / unit_split<QT, KVT>();
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
   const int grp = lane >> 4;
@@ -970,15 +975,16 @@ __device__ __forceinline__ void pair_chunks(const AttnParams& P, int p, int& c0,
 }
 
 constexpr int kPersistWaves = 8;     // waves of a persistent workgroup (one per CU)
-constexpr int kSlots = kPersistWaves / kSplit;  // units a persistent workgroup runs at once
 constexpr int kMaxPairs = 8192;      // (sequence, row-group) pairs the persistent kernel indexes
 
-template <int NT, int ND>
+// KS: waves per unit; the workgroup runs kPersistWaves / KS units at a time
+template <int NT, int ND, int KS>
 struct PersistShared {
+  static constexpr int kSlots = kPersistWaves / KS;
   int32_t first[kMaxPairs + 1];  // units before pair p (prefix sum)
   int32_t c0[kMaxPairs];         // first active chunk of pair p
   int32_t tbl[kPersistWaves][kChunk];
-  PartBuffer<NT, ND> part[kSplit > 1 ? kSlots : 1][kSplit > 1 ? kSplit / 2 : 1];
+  PartBuffer<NT, ND> part[KS > 1 ? kSlots : 1][KS > 1 ? KS / 2 : 1];
   int32_t wave_total[kPersistWaves];
 };
 
@@ -1008,17 +1014,19 @@ __device__ __forceinline__ void unit_of(const AttnParams& P, const int32_t* firs
 // gets the same number of units whatever the mix of sequence lengths (a grid of
 // one workgroup per unit leaves the placement of the busy workgroups to the
 // dispatcher, and CUs end up with 1 to 8 of them).  kSlots units run at a time,
-// each on kSplit waves that split its positions and combine through LDS in a
+// each on KS waves that split its positions and combine through LDS in a
 // fixed order, so a unit's arithmetic never depends on the assignment.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
 __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnParams P) {
   constexpr int ND = D / 16;
-  __shared__ PersistShared<NT, ND> sh;
+  constexpr int KS = unit_split<QT, KVT>();
+  constexpr int kSlots = kPersistWaves / KS;
+  __shared__ PersistShared<NT, ND, KS> sh;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int slot = wave / kSplit;
-  const int part = wave - slot * kSplit;
+  const int slot = wave / KS;
+  const int part = wave - slot * KS;
   const int pairs = P.num_seqs * P.rowgroups;
   // units per pair, summed per thread over a contiguous run of pairs
   const int per = (pairs + 64 * kPersistWaves - 1) / (64 * kPersistWaves);
@@ -1061,9 +1069,9 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
     } else {
       st.active = false;
     }
-    // tree combine of the unit's parts: part p absorbs part p + h, h = kSplit/2 .. 1
+    // tree combine of the unit's parts: part p absorbs part p + h, h = KS/2 .. 1
 #pragma unroll
-    for (int h = kSplit / 2; h >= 1; h /= 2) {
+    for (int h = KS / 2; h >= 1; h /= 2) {
       if (part >= h && part < 2 * h && st.active) publish_part(st, sh.part[slot][part - h]);
       __syncthreads();
       if (part < h && st.active) absorb_part(st, sh.part[slot][part]);
@@ -1073,19 +1081,20 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
   }
 }
 
-// Fallback for batches with more than kMaxPairs pairs: one kSplit-wave workgroup
+// Fallback for batches with more than kMaxPairs pairs: one KS-wave workgroup
 // per (sequence, row-group, kv head, chunk), the same per-unit arithmetic.
 template <int QT, int KVT, int D, int NT, int SM, bool UB>
-__global__ __launch_bounds__(64 * kSplit) void rlt_attn_mfma_grid_kernel(AttnParams P) {
+__global__ __launch_bounds__((64 * unit_split<QT, KVT>())) void rlt_attn_mfma_grid_kernel(AttnParams P) {
   constexpr int ND = D / 16;
-  __shared__ int32_t tbl[kSplit][kChunk];
-  __shared__ PartBuffer<NT, ND> buf[kSplit > 1 ? kSplit / 2 : 1];
+  constexpr int KS = unit_split<QT, KVT>();
+  __shared__ int32_t tbl[KS][kChunk];
+  __shared__ PartBuffer<NT, ND> buf[KS > 1 ? KS / 2 : 1];
   const int part = threadIdx.x >> 6;
   const WorkItem wi = work_item(P, blockIdx.x);
   UnitState<NT, ND> st;
   attend_span<QT, KVT, D, NT, SM, UB>(P, wi.seq, wi.rg, wi.hg, wi.chunk, part, tbl[part], st);
 #pragma unroll
-  for (int h = kSplit / 2; h >= 1; h /= 2) {
+  for (int h = KS / 2; h >= 1; h /= 2) {
     if (part >= h && part < 2 * h && st.active) publish_part(st, buf[part - h]);
     __syncthreads();
     if (part < h && st.active) absorb_part(st, buf[part]);
@@ -1771,7 +1780,7 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
 template <int QT, int KVT, int D, int SM, bool UB, int NT>
 void launch_mfma_nt(const AttnParams& P, dim3 grid, hipStream_t stream) {
   if (P.persistent) rlt_attn_mfma_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * kPersistWaves, 0, stream>>>(P);
-  else rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * kSplit, 0, stream>>>(P);
+  else rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * unit_split<QT, KVT>(), 0, stream>>>(P);
 }
 
 template <int QT, int KVT, int D, int SM, bool UB>
