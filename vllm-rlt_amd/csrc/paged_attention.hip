@@ -1476,18 +1476,21 @@ constexpr float kPfLazy = 8.f;  // log2 headroom before the running max moves
 
 template <int D>
 struct PrefillLds {
-  static constexpr int kKRow = D * 2 + 16;        // bytes per K position row
-  static constexpr int kVRowW = kPfKeys / 2 + 2;  // dwords per V^T dim row (32 position pairs + 2)
-  uint8_t k[2][kPfKeys * kKRow];
-  uint32_t vt[2][D * kVRowW];
+  static constexpr int kRowB = D * 2;  // bytes per position row (no padding: XOR-swizzled slots)
+  uint8_t k[2][kPfKeys * kRowB];
+  uint8_t v[2][kPfKeys * kRowB];
 };
 
-// Dword column of position pair `col` in V^T dim row r.  With rows 34 dwords apart
-// (2 mod 32 banks) the compute reads -- 16 dim rows x one dword pair per lane, 16 lanes
-// at a time -- cover the 32 banks once; flipping bit 3 of the column in rows with bit 4
-// set spreads the staging stores (8 position pairs x 4 pieces per 32 lanes) over all
-// 32 banks too.  Dword pairs (2j, 2j + 1) stay adjacent for 8-byte reads.
-__device__ __forceinline__ int vt_col(int r, int col) { return col ^ (8 * ((r >> 4) & 1)); }
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte slot of piece `piece` (8 dims) in row r of a staged tile.  K rows XOR the
+// slot with r & 7, so the S^T operand reads (8 lanes = 8 rows of one piece column)
+// meet 8 distinct bank groups; V rows XOR it with 2 (r & 3), which keeps each piece
+// pair adjacent for the transpose reads (16 lanes = 4 rows x one 32-byte pair) and puts
+// the four rows on distinct bank groups.
+__device__ __forceinline__ int k_slot(int r, int piece) { return piece ^ (r & 7); }
+__device__ __forceinline__ int v_slot(int r, int piece) { return piece ^ (2 * (r & 3)); }
 
 // UB: block_size % 16 == 0, so each 16-position group of a tile lies in one block
 // and its address comes from one wave-uniform table lookup.
@@ -1498,12 +1501,10 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   constexpr int NT = kPfNT;
   constexpr int NQS = D / 32;       // 32-wide contraction slices of S^T
   constexpr int ND = D / 16;        // 16-wide dim tiles of O^T
-  constexpr int KCH = D / 8;        // 16-byte pieces per position row
-  constexpr int KSTEP = kPfThreads / KCH;          // K rows one pass of the workgroup loads
-  constexpr int KPT = kPfKeys / KSTEP;             // K pieces per thread per tile
-  constexpr int VPASS = KCH / 8;    // V passes per tile: a wave loads 8 pieces of 16 positions
-  static_assert(16 % (64 / KCH) == 0, "a wave's K rows of one pass stay in one 16-position group");
-  static_assert(kPfKeys == 16 * (kPfThreads / 64), "a wave stages one 16-position group of V");
+  constexpr int SLOTS = D / 8;      // 16-byte pieces per position row
+  constexpr int ROWS_PER_LD = 64 / SLOTS;                // rows one wave-wide direct load fills
+  constexpr int LDS_PER_WAVE = kPfKeys / ROWS_PER_LD / 4;  // direct loads per wave per tile (K, V each)
+  static_assert(16 % ROWS_PER_LD == 0, "a direct load's rows stay in one 16-position group");
   __shared__ L sh;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
 
@@ -1564,17 +1565,13 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     for (int dt = 0; dt < ND; ++dt) oacc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- global -> registers -> LDS staging of one 64-position tile.
-  // K: thread (piece, krow) loads rows krow + KSTEP j.  V: wave w loads positions
-  // 16 w + [0, 16) as 8 pairs (lane & 7) x 8 pieces (lane >> 3, + 8 per pass).
-  const int piece = t % KCH;
-  const int krow = t / KCH;
-  const int vpair = lane & 7;
-  const int vpiece = lane >> 3;
-  const int64_t k_head = (int64_t)kvh * P.k_head_stride + piece * 8;
-  const int64_t v_head = (int64_t)kvh * P.v_head_stride + vpiece * 8;
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 kr[KPT], vr[2 * VPASS];
+  // ---- global -> LDS staging of one 64-position tile by direct loads: wave w's j-th
+  // load fills rows ROWS_PER_LD (LDS_PER_WAVE w + j) + [0, ROWS_PER_LD); lane L takes row
+  // + L / SLOTS and LDS slot L % SLOTS, into which it loads the row's swizzled piece
+  const int ld_row = lane / SLOTS;
+  const int ld_slot = lane % SLOTS;
+  const int64_t k_head = (int64_t)kvh * P.k_head_stride;
+  const int64_t v_head = (int64_t)kvh * P.v_head_stride;
   // (block id, offset) of position pos: block ids outside the pool read block 0
   auto block_of = [&](int pos, int64_t& blk, int& off) {
     const int idx = min(pos / P.block_size, P.table_width - 1);
@@ -1582,74 +1579,58 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     blk = (e >= 0 && e < P.num_blocks) ? e : 0;
     off = pos % P.block_size;
   };
-  auto load = [&](int tile) {
+  auto load = [&](int tile, int b) {
     const int base = tile * kPfKeys;
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int r = krow + KSTEP * j;
+    for (int j = 0; j < LDS_PER_WAVE; ++j) {
+      const int r0 = ROWS_PER_LD * (LDS_PER_WAVE * w + j);  // wave-uniform
+      const int r = r0 + ld_row;
       int64_t blk;
       int off;
       if (UB) {
-        // the wave's rows of this pass share one 16-position group
-        block_of(__builtin_amdgcn_readfirstlane(base + (r & ~15)), blk, off);
+        block_of(__builtin_amdgcn_readfirstlane(base + (r0 & ~15)), blk, off);
         off += r & 15;
       } else {
         block_of(base + r, blk, off);
       }
-      kr[j] = *(const u32x4*)((const uint16_t*)P.k + blk * P.k_block_stride +
-                               (int64_t)off * P.k_token_stride + k_head);
-    }
-    int64_t vblk = 0;
-    int voff0 = 0;
-    if (UB) block_of(__builtin_amdgcn_readfirstlane(base + 16 * w), vblk, voff0);
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int pos = base + 16 * w + 2 * vpair + e;
-      int64_t blk = vblk;
-      int off = voff0 + 2 * vpair + e;
-      if (!UB) block_of(pos, blk, off);
+      const uint16_t* kp = (const uint16_t*)P.k + blk * P.k_block_stride +
+                           (int64_t)off * P.k_token_stride + k_head + k_slot(r, ld_slot) * 8;
       const uint16_t* vp = (const uint16_t*)P.v + blk * P.v_block_stride +
-                           (int64_t)off * P.v_token_stride + v_head;
-      const bool ok = pos < hi_last;
-#pragma unroll
-      for (int h = 0; h < VPASS; ++h) {
-        const u32x4 v = *(const u32x4*)(vp + 64 * h);
-        // positions past the sequence may hold any bits (NaN included): zero them,
-        // since their weight 0 times NaN would not vanish
-        vr[2 * h + e] = ok ? v : u32x4{0u, 0u, 0u, 0u};
-      }
+                           (int64_t)off * P.v_token_stride + v_head + v_slot(r, ld_slot) * 8;
+      __builtin_amdgcn_global_load_lds((const void*)kp, (lds_void*)(sh.k[b] + r0 * L::kRowB), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)vp, (lds_void*)(sh.v[b] + r0 * L::kRowB), 16, 0, 0);
     }
   };
-  auto store = [&](int b) {
+  // After this wave's loads of tile `tile` into buffer b landed: its V rows past the
+  // sequence may hold any bits (NaN included) and are zeroed, since their weight 0
+  // times NaN would not vanish.  Only the tiles that reach past hi_last do work.
+  auto settle = [&](int tile, int b) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int base = tile * kPfKeys;
+    if (base + kPfKeys > hi_last) {
 #pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      *(u32x4*)(sh.k[b] + (krow + KSTEP * j) * L::kKRow + piece * 16) = kr[j];
-    const int col = 8 * w + vpair;  // dword column: positions 2 col, 2 col + 1
-#pragma unroll
-    for (int h = 0; h < VPASS; ++h) {
-      const u32x4 av = vr[2 * h], cv = vr[2 * h + 1];
-      const int pc = vpiece + 8 * h;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        // dims pc*8 + 2q (low halves of both positions) and + 2q + 1 (high halves)
-        const int r0 = pc * 8 + 2 * q;
-        sh.vt[b][r0 * L::kVRowW + vt_col(r0, col)] = __builtin_amdgcn_perm(cv[q], av[q], 0x05040100u);
-        sh.vt[b][(r0 + 1) * L::kVRowW + vt_col(r0 + 1, col)] =
-            __builtin_amdgcn_perm(cv[q], av[q], 0x07060302u);
+      for (int j = 0; j < LDS_PER_WAVE; ++j) {
+        const int r = ROWS_PER_LD * (LDS_PER_WAVE * w + j) + ld_row;
+        if (base + r >= hi_last)
+          *(uint4*)(sh.v[b] + r * L::kRowB + ld_slot * 16) = make_uint4(0, 0, 0, 0);
       }
     }
   };
 
-  // V^T reads: dim row r = 16 dt + l16 holds column vt_col(r, 16 c + 2 grp + 8 k) at
-  // 2 grp + ((16 c + 8 k) ^ 8 (dt & 1)): one lane offset plus compile-time constants
-  const int vlane = l16 * L::kVRowW + 2 * grp;
+  // S^T operand reads: row kt 16 + l16, piece 4 s + grp at slot (4 s + grp) ^ (l16 & 7)
+  const int k_lane = l16 * L::kRowB;
+  // V^T operand reads (transpose loads): lane (l16, grp) of the 16-lane group grp reads
+  // row 32 c + 4 grp + (l16 >> 2) (+16 for the second half) at dims 16 dt + 4 (l16 & 3),
+  // piece 2 dt + ((l16 >> 1) & 1) -> slot 2 (dt ^ m) + ((l16 >> 1) & 1), m = (l16 >> 2) & 3
+  const int vm = (l16 >> 2) & 3;
+  const int v_lane = (4 * grp + (l16 >> 2)) * L::kRowB + ((l16 >> 1) & 1) * 16 + (l16 & 1) * 8;
 
   const float qk_scale = P.qk_scale_log2;
   auto compute = [&](int tile, int b, auto full_tag) {
     constexpr bool FULL = decltype(full_tag)::value;
     const int base = tile * kPfKeys;
     const uint8_t* kb = sh.k[b];
-    const uint32_t* vb = sh.vt[b];
+    const uint8_t* vb = sh.v[b];
     // ---- S^T = K Q^T for the tile's four 16-position sub-tiles
     f32x4 sc[4][NT];
 #pragma unroll
@@ -1660,7 +1641,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     for (int s = 0; s < NQS; ++s)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const uint4 a = *(const uint4*)(kb + (kt * 16 + l16) * L::kKRow + (s * 32 + grp * 8) * 2);
+        const uint4 a = *(const uint4*)(kb + kt * 16 * L::kRowB + k_lane +
+                                        (((4 * s + grp) ^ (l16 & 7)) * 16));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) sc[kt][nt] = M::qk(a, qreg[nt][s], sc[kt][nt]);
       }
@@ -1724,10 +1706,14 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) {
-        const uint32_t* rows = vb + dt * 16 * L::kVRowW + vlane;
-        const uint2 x0 = *(const uint2*)(rows + ((16 * c) ^ (8 * (dt & 1))));
-        const uint2 x1 = *(const uint2*)(rows + ((16 * c + 8) ^ (8 * (dt & 1))));
-        const uint4 a = make_uint4(x0.x, x0.y, x1.x, x1.y);
+        const uint8_t* vr = vb + 32 * c * L::kRowB + v_lane + 32 * (dt ^ vm);
+        const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(lds_void*)vr);
+        const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(lds_void*)(vr + 16 * L::kRowB));
+        uint4 a;
+        __builtin_memcpy(&a, &x0, 8);
+        __builtin_memcpy((char*)&a + 8, &x1, 8);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) oacc[nt][dt] = M::qk(a, pop[c][nt], oacc[nt][dt]);
       }
@@ -1739,10 +1725,10 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     auto step = [&](int tile, auto full_tag) {
       const int b = (tile - kt0) & 1;
       const bool more = tile + 1 < kt1;
-      if (more) load(tile + 1);
-      compute(tile, b, full_tag);
       // buffer b ^ 1 was last read in the previous iteration, before its barrier
-      if (more) store(b ^ 1);
+      if (more) load(tile + 1, b ^ 1);
+      compute(tile, b, full_tag);
+      if (more) settle(tile + 1, b ^ 1);
       __syncthreads();
     };
     // tiles [fa, fb) lie inside every row's visible range: three loops, so that no
@@ -1750,8 +1736,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     // accumulators)
     const int fa = min(kt1, max(kt0, (max(wlo, 0) + kPfKeys - 1) / kPfKeys));
     const int fb = max(fa, min(kt1, whi / kPfKeys));
-    load(kt0);
-    store(0);
+    load(kt0, 0);
+    settle(kt0, 0);
     __syncthreads();
     for (int tile = kt0; tile < fa; ++tile) step(tile, Flag<false>{});
     for (int tile = fa; tile < fb; ++tile) step(tile, Flag<true>{});
