@@ -1485,12 +1485,17 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte slot of piece `piece` (8 dims) in row r of a staged tile.  K rows XOR the
-// slot with r & 7, so the S^T operand reads (8 lanes = 8 rows of one piece column)
-// meet 8 distinct bank groups; V rows XOR it with 2 (r & 3), which keeps each piece
+// slot with r mod SLOTS, so the S^T operand reads (16 lanes = 16 rows of one piece
+// column) meet distinct bank groups; V rows XOR it with 2 (r & 3), which keeps each piece
 // pair adjacent for the transpose reads (16 lanes = 4 rows x one 32-byte pair) and puts
-// the four rows on distinct bank groups.
-__device__ __forceinline__ int k_slot(int r, int piece) { return piece ^ (r & 7); }
-__device__ __forceinline__ int v_slot(int r, int piece) { return piece ^ (2 * (r & 3)); }
+// the four rows on distinct bank groups, and with 8 in rows with bit 2 set (D = 128), so
+// the next 16 lanes (rows 4 further on) use the other half of the banks.
+template <int SLOTS>
+__device__ __forceinline__ int k_slot(int r, int piece) { return piece ^ (r & (SLOTS - 1)); }
+template <int SLOTS>
+__device__ __forceinline__ int v_slot(int r, int piece) {
+  return piece ^ (2 * (r & 3)) ^ (SLOTS >= 16 ? 8 * ((r >> 2) & 1) : 0);
+}
 
 // UB: block_size % 16 == 0, so each 16-position group of a tile lies in one block
 // and its address comes from one wave-uniform table lookup.
@@ -1594,9 +1599,9 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
         block_of(base + r, blk, off);
       }
       const uint16_t* kp = (const uint16_t*)P.k + blk * P.k_block_stride +
-                           (int64_t)off * P.k_token_stride + k_head + k_slot(r, ld_slot) * 8;
+                           (int64_t)off * P.k_token_stride + k_head + k_slot<SLOTS>(r, ld_slot) * 8;
       const uint16_t* vp = (const uint16_t*)P.v + blk * P.v_block_stride +
-                           (int64_t)off * P.v_token_stride + v_head + v_slot(r, ld_slot) * 8;
+                           (int64_t)off * P.v_token_stride + v_head + v_slot<SLOTS>(r, ld_slot) * 8;
       __builtin_amdgcn_global_load_lds((const void*)kp, (lds_void*)(sh.k[b] + r0 * L::kRowB), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((const void*)vp, (lds_void*)(sh.v[b] + r0 * L::kRowB), 16, 0, 0);
     }
@@ -1617,12 +1622,13 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
     }
   };
 
-  // S^T operand reads: row kt 16 + l16, piece 4 s + grp at slot (4 s + grp) ^ (l16 & 7)
+  // S^T operand reads: row kt 16 + l16, piece 4 s + grp at slot (4 s + grp) ^ (l16 mod SLOTS)
   const int k_lane = l16 * L::kRowB;
   // V^T operand reads (transpose loads): lane (l16, grp) of the 16-lane group grp reads
   // row 32 c + 4 grp + (l16 >> 2) (+16 for the second half) at dims 16 dt + 4 (l16 & 3),
   // piece 2 dt + ((l16 >> 1) & 1) -> slot 2 (dt ^ m) + ((l16 >> 1) & 1), m = (l16 >> 2) & 3
-  const int vm = (l16 >> 2) & 3;
+  // (^ 4 for odd grp when D = 128: the slot's bit-3 flip)
+  const int vm = ((l16 >> 2) & 3) ^ (ND >= 8 ? 4 * (grp & 1) : 0);
   const int v_lane = (4 * grp + (l16 >> 2)) * L::kRowB + ((l16 >> 1) & 1) * 16 + (l16 & 1) * 8;
 
   const float qk_scale = P.qk_scale_log2;
@@ -1642,7 +1648,7 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         const uint4 a = *(const uint4*)(kb + kt * 16 * L::kRowB + k_lane +
-                                        (((4 * s + grp) ^ (l16 & 7)) * 16));
+                                        (((4 * s + grp) ^ (l16 & (SLOTS - 1))) * 16));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) sc[kt][nt] = M::qk(a, qreg[nt][s], sc[kt][nt]);
       }
