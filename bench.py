@@ -385,6 +385,37 @@ def target_step(pkg, dev):
             "graph_replays_equal_eager": s1 and s2 and s3}
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def draft_steps(pkg, dev):
+    """One draft offset of the _draft step (async_speculative.py:645-663): argmax of every
+    row, the random rows' distributions q_o and their categorical draws, in one
+    ``propose_drafts`` call.  Config 3's shape (32 requests, V = 49152, T = 0.7, top-p 0.9:
+    the filtered single-workgroup form) and config 5's (256 requests, V = 65536, T = 1, no
+    truncation: the row-split form).  Algorithmic bytes: the fp32 logits read once and q_o
+    written once."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    out = {}
+    for name, m, vocab, temp, top_p in (("config3", 32, 49152, 0.7, 0.9),
+                                        ("config5", 256, 65536, 1.0, 1.0)):
+        logits = torch.randn(m, vocab, generator=g, device=dev) * 4
+        rows = torch.arange(m, device=dev)
+        t = torch.full((m,), temp, device=dev)
+        tk = torch.full((m,), -1, dtype=torch.int64, device=dev)
+        tp = torch.full((m,), top_p, device=dev)
+        u = torch.rand(m, generator=g, device=dev)
+        filt = top_p < 1.0
+        t_us, same = _graph_time(lambda: pkg.propose_drafts(logits, rows, t, tk, tp, u, max_top_k=0,
+                                                            apply_top_p=filt))
+        nbytes = 2 * 4 * m * vocab
+        out[name] = {"rows": m, "vocab": vocab, "us": round(t_us * 1e6, 1),
+                     "algorithmic_bytes": nbytes,
+                     "frac_hbm": round(nbytes / t_us / 1e9 / PEAK_HBM_GBS, 4),
+                     "graph_replays_equal_eager": same}
+        del logits
+    return {"workload": "one draft offset: argmax + distributions + categorical draws "
+                        "(propose_drafts), all rows random", "launches": out}
 
 
 def prefill_steps(pkg, dev):
@@ -476,6 +507,8 @@ def main():
                     help="skip the config-4 and config-5 attention + verify_accept measurements")
     ap.add_argument("--prefill-only", action="store_true",
                     help="print only the prefill measurements and exit")
+    ap.add_argument("--draft-only", action="store_true",
+                    help="print only the draft-step measurements and exit")
     ap.add_argument("--only", choices=("kv_write", "attention", "attention_store", "probs", "accept",
                                        "verify", "copy",
                                        "config5_attention"),
@@ -503,6 +536,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps(prefill_steps(pkg, dev)), flush=True)
+        return
+    if args.draft_only:
+        print(json.dumps(draft_steps(pkg, dev)), flush=True)
         return
     if args.only == "config5_attention":
         print(json.dumps(config5_step(pkg, dev, attention_only=True)), flush=True)
@@ -739,6 +775,8 @@ def main():
         result["config5_verify"] = config5_step(pkg, dev)
         torch.cuda.empty_cache()
         result["prefill"] = prefill_steps(pkg, dev)
+        torch.cuda.empty_cache()
+        result["draft_step"] = draft_steps(pkg, dev)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
