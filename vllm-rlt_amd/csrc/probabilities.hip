@@ -349,6 +349,40 @@ struct Row {
     const float l = x(j);
     return l == l ? mass(l) : NAN;
   }
+  // f(j, e(j)) for every chunk with the values of four LDS chunks read before their
+  // four calls (the output pass: its global stores do not wait for the next LDS reads).
+  template <class F>
+  __device__ __forceinline__ void for_chunks_e4(F f) const {
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) f(j, e(j));
+    if (kNpt > 0) {
+      const int end = kTail ? kNpt : npt;
+      int j = NREG;
+#pragma unroll 1
+      for (; j + 4 <= end; j += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = e(j + u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f(j + u, v[u]);
+      }
+#pragma unroll 1
+      for (; j < end; ++j) f(j, e(j));
+    }
+    if (kNpt == 0 || kTail) {
+      int j = kNpt;
+#pragma unroll 1
+      for (; j + 4 <= npt; j += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = e(j + u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f(j + u, v[u]);
+      }
+#pragma unroll 1
+      for (; j < npt; ++j) f(j, e(j));
+    }
+  }
   // f(j) for every chunk: register chunks unrolled (static register indices),
   // LDS chunks in a rolled loop, re-read chunks four at a time (loads in flight).
   // Calls are wave-uniform (ballots allowed).
@@ -579,13 +613,15 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   const float inv = (float)(kFixScale / (double)cut.kept);
   uint32_t clo, chi;
   bin_bits(cut.bin, clo, chi);
-  row.for_chunks([&](int j) {
-    const float e = row.e(j);
+  // stores through a global-space pointer: they cannot alias the row's LDS chunks, so
+  // the next chunks' LDS reads need not wait for them
+  __attribute__((address_space(1))) float* gdst = (__attribute__((address_space(1))) float*)dst;
+  row.for_chunks_e4([&](int j, float e) {
     if (e != e) return;
     // bins before the cut bin hold larger masses (kept), later bins smaller ones
     const uint32_t bits = __float_as_uint(e);
-    if (bits > chi) dst[(int64_t)j * kThreads + t] = e * inv;
-    else if (bits < clo) dst[(int64_t)j * kThreads + t] = 0.f;
+    if (bits > chi) gdst[(int64_t)j * kThreads + t] = e * inv;
+    else if (bits < clo) gdst[(int64_t)j * kThreads + t] = 0.f;
   });
   const int nl = min((int)sh.list_n, Shared::kCap);
   for (int i = t; i < nl; i += kThreads) {
