@@ -383,14 +383,20 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
         torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
 
 
-@pytest.mark.parametrize("bs,window", [(8, 0), (8, 256), (48, 0), (32, 100)])
-def test_long_prompt_prefill_block_sizes(kernel, dev, bs, window):
+@pytest.mark.parametrize("bs,window,dtype,d", [(8, 0, torch.bfloat16, 128),
+                                               (8, 256, torch.bfloat16, 128),
+                                               (48, 0, torch.bfloat16, 128),
+                                               (32, 100, torch.bfloat16, 128),
+                                               (8, 0, torch.float16, 64),
+                                               (32, 300, torch.float16, 64)])
+def test_long_prompt_prefill_block_sizes(kernel, dev, bs, window, dtype, d):
     """The prefill tiling's two address paths: blocks holding whole 16-position groups
     (one table lookup per group, 32 and 48 here) and smaller blocks (a lookup per
-    position, 8 here), with and without a sliding window."""
-    _say("long prefill block size", bs, window)
+    position, 8 here), with and without a sliding window, at head_dim 128 and 64 (the
+    direct loads fill 4 and 8 rows per instruction)."""
+    _say("long prefill block size", bs, window, dtype, d)
     g = torch.Generator().manual_seed(22)
-    hq, hkv, d, dtype = 16, 4, 128, torch.bfloat16
+    hq, hkv = 16, 4
     seqs = [(1024, 1024), (2000, 700), (129, 129)]
     pages = sum(-(-n // bs) for n, _ in seqs) + 2
     _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
