@@ -242,3 +242,28 @@ def test_verify_accept_checks_arguments(pkg):
     # workspace too small
     assert lib.rlt_verify_accept(fake, 0, 100, fake, fake, fake, 0, 0, fake, fake, fake, fake,
                                  fake, 2, 4, 100, *io, fake, 1, null) == 3
+
+
+def test_attention_with_window_store_checks_arguments(pkg):
+    """rlt_paged_attention_store serves packed bf16 / fp16 verify windows only: other forms
+    return RLT_ERR_UNSUPPORTED (2) and a missing or misaligned window buffer
+    RLT_ERR_ARGUMENT (1), before anything is launched."""
+    from vllm_rlt_amd import _lib
+
+    lib = _lib.library()
+    null, fake = None, 0x1000
+    hq, hkv, d, bs = 16, 4, 128, 16
+
+    def call(cu=fake, max_q=5, dtype=2, new_k=fake, new_v=fake, row_stride=hkv * d, seqs=2):
+        # q, pools [block, token, kv_head, dim] with 64 blocks, 2 sequences x 5 rows
+        return lib.rlt_paged_attention_store(
+            fake, hq * d, d, fake, fake, bs * hkv * d, hkv * d, d, bs * hkv * d, hkv * d, d, 64,
+            fake, 8, 8, fake, cu, seqs, max_q, 10, hq, hkv, d, bs, dtype, new_k, new_v, row_stride,
+            d, fake, hq * d, d, fake, 1 << 24, null)
+
+    assert call(cu=null, seqs=10) == 2  # per-row form: no window to store
+    assert call(dtype=0) == 2          # float32 q and pool
+    assert call(max_q=64) == 2         # prefill-length window (the prefill tiling)
+    assert call(new_k=null) == 1       # no rows to store
+    assert call(new_v=fake + 2) == 1   # misaligned rows
+    assert call(row_stride=hkv * d + 1) == 1
