@@ -59,9 +59,14 @@ constexpr int kStages = 2;  // KV tiles in flight per wave (MFMA path)
 // dtype pair, so a row's result never depends on the batch.
 template <int QT, int KVT>
 constexpr int unit_split() { return KVT == QT ? 2 : 1; }
+// Key positions per chunk on the MFMA path: 512 for 16-bit KV, 1024 for fp8 KV (whose
+// chunk is the same bytes; one wave streams it).  Fixed per dtype pair, like the split.
+template <int QT, int KVT>
+constexpr int unit_chunk() { return KVT == QT ? kChunk : 2 * kChunk; }
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
+  int chunk_log2;  // log2 of the chunk (split unit) in key positions: 9 or 10
   const void* q;
   int64_t q_row_stride, q_head_stride;
   const void* k;
@@ -468,11 +473,12 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
   constexpr int NQS = D / 32;  // 32-wide contraction slices
   constexpr int ND = D / 16;   // 16-wide output column tiles (= dims per lane)
   constexpr int KV_ELT = KVT == QT ? 2 : 1;
-  constexpr int kSpan = kChunk / unit_split<QT, KVT>();
+  constexpr int CH = unit_chunk<QT, KVT>();
+  constexpr int kSpan = CH / unit_split<QT, KVT>();
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
   const int grp = lane >> 4;
-  const int c_begin = chunk * kChunk;
+  const int c_begin = chunk * CH;
   const int w_begin = c_begin + part * kSpan;
 
   auto& oacc = st.oacc;
@@ -508,7 +514,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
   const int rg_rows = min(P.rows_per_rg, rows_total - rg_begin);
   int lo_first, hi_first, lo_last, hi_last;
   group_range(P, sv, rg_begin, rg_rows, lo_first, hi_first, lo_last, hi_last);
-  if (c_begin >= hi_last || c_begin + kChunk <= lo_first) return;
+  if (c_begin >= hi_last || c_begin + CH <= lo_first) return;
   st.active = true;
   st.rg_begin = rg_begin;
   st.rg_rows = rg_rows;
@@ -874,7 +880,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
 
 // Chunk partial (max, sum, unnormalized output) of the unit's rows whose merge
 // range contains the chunk.
-template <int D, int NT>
+template <int D, int NT, int CH>
 __device__ __forceinline__ void write_partial(const AttnParams& P, int kvh, int chunk,
                                               const UnitState<NT, D / 16>& st) {
   constexpr int ND = D / 16;
@@ -887,8 +893,8 @@ __device__ __forceinline__ void write_partial(const AttnParams& P, int kvh, int 
   for (int nt = 0; nt < NT; ++nt) {
     const int r_local = nt * 16 + l16;
     if (r_local >= st.rg_rows) continue;
-    const int lo_c = st.row_lo[nt] / kChunk;
-    const int hi_c = (st.row_hi[nt] + kChunk - 1) / kChunk;
+    const int lo_c = st.row_lo[nt] / CH;
+    const int hi_c = (st.row_hi[nt] + CH - 1) / CH;
     if (chunk < lo_c || chunk >= hi_c) continue;
     const int rho = st.rg_begin + r_local;
     const int qrow = st.q_begin + rho / P.group;
@@ -958,6 +964,7 @@ __device__ __forceinline__ void absorb_part(UnitState<NT, ND>& st, const PartBuf
 
 // Active chunk range [c0, c1) of (sequence, row-group) pair p: the chunks that
 // hold a position some row of the row-group sees.
+template <int CH>
 __device__ __forceinline__ void pair_chunks(const AttnParams& P, int p, int& c0, int& c1) {
   const int seq = p / P.rowgroups;
   const int rg = p - seq * P.rowgroups;
@@ -970,20 +977,20 @@ __device__ __forceinline__ void pair_chunks(const AttnParams& P, int p, int& c0,
   int lo_first, hi_first, lo_last, hi_last;
   group_range(P, sv, rg_begin, rg_rows, lo_first, hi_first, lo_last, hi_last);
   if (hi_last <= lo_first) return;
-  c0 = lo_first / kChunk;
-  c1 = (hi_last + kChunk - 1) / kChunk;
+  c0 = lo_first / CH;
+  c1 = (hi_last + CH - 1) / CH;
 }
 
 constexpr int kPersistWaves = 8;     // waves of a persistent workgroup (one per CU)
 constexpr int kMaxPairs = 8192;      // (sequence, row-group) pairs the persistent kernel indexes
 
-// KS: waves per unit; the workgroup runs kPersistWaves / KS units at a time
-template <int NT, int ND, int KS>
+// KS: waves per unit; the workgroup runs kPersistWaves / KS units at a time; CH: chunk
+template <int NT, int ND, int KS, int CH>
 struct PersistShared {
   static constexpr int kSlots = kPersistWaves / KS;
   int32_t first[kMaxPairs + 1];  // units before pair p (prefix sum)
   int32_t c0[kMaxPairs];         // first active chunk of pair p
-  int32_t tbl[kPersistWaves][kChunk];
+  int32_t tbl[kPersistWaves][CH];
   PartBuffer<NT, ND> part[KS > 1 ? kSlots : 1][KS > 1 ? KS / 2 : 1];
   int32_t wave_total[kPersistWaves];
 };
@@ -1020,8 +1027,9 @@ template <int QT, int KVT, int D, int NT, int SM, bool UB>
 __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnParams P) {
   constexpr int ND = D / 16;
   constexpr int KS = unit_split<QT, KVT>();
+  constexpr int CH = unit_chunk<QT, KVT>();
   constexpr int kSlots = kPersistWaves / KS;
-  __shared__ PersistShared<NT, ND, KS> sh;
+  __shared__ PersistShared<NT, ND, KS, CH> sh;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -1035,7 +1043,7 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
   int run = 0;
   for (int p = p_lo; p < p_hi; ++p) {
     int c0, c1;
-    pair_chunks(P, p, c0, c1);
+    pair_chunks<CH>(P, p, c0, c1);
     sh.c0[p] = c0;
     sh.first[p] = run;  // local prefix for now
     run += (c1 - c0) * P.hkv;
@@ -1077,7 +1085,7 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
       if (part < h && st.active) absorb_part(st, sh.part[slot][part]);
       __syncthreads();  // the buffers are reused by the next level / round
     }
-    if (part == 0 && st.active) write_partial<D, NT>(P, kvh, chunk, st);
+    if (part == 0 && st.active) write_partial<D, NT, CH>(P, kvh, chunk, st);
   }
 }
 
@@ -1087,7 +1095,8 @@ template <int QT, int KVT, int D, int NT, int SM, bool UB>
 __global__ __launch_bounds__((64 * unit_split<QT, KVT>())) void rlt_attn_mfma_grid_kernel(AttnParams P) {
   constexpr int ND = D / 16;
   constexpr int KS = unit_split<QT, KVT>();
-  __shared__ int32_t tbl[KS][kChunk];
+  constexpr int CH = unit_chunk<QT, KVT>();
+  __shared__ int32_t tbl[KS][CH];
   __shared__ PartBuffer<NT, ND> buf[KS > 1 ? KS / 2 : 1];
   const int part = threadIdx.x >> 6;
   const WorkItem wi = work_item(P, blockIdx.x);
@@ -1100,7 +1109,7 @@ __global__ __launch_bounds__((64 * unit_split<QT, KVT>())) void rlt_attn_mfma_gr
     if (part < h && st.active) absorb_part(st, buf[part]);
     __syncthreads();
   }
-  if (part == 0 && st.active) write_partial<D, NT>(P, wi.hg, wi.chunk, st);
+  if (part == 0 && st.active) write_partial<D, NT, CH>(P, wi.hg, wi.chunk, st);
 }
 
 // ============================================================ vector path
@@ -1346,7 +1355,7 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
   const int row = sv.q_begin + qi;
   int lo, hi;
   row_range(P, sv, qi, lo, hi);
-  const int c0 = lo / kChunk, c1 = (hi + kChunk - 1) / kChunk;
+  const int c0 = lo >> P.chunk_log2, c1 = (hi + (1 << P.chunk_log2) - 1) >> P.chunk_log2;
   const int nc = c1 - c0;
   const int64_t base = ((int64_t)row * P.hq + head) * P.max_chunks + c0;
   const int64_t out_off = (int64_t)row * P.out_row_stride + (int64_t)head * P.out_head_stride;
@@ -1856,9 +1865,9 @@ int compute_units() {
   return n;
 }
 
-int max_chunks_for(int32_t table_width, int32_t block_size) {
+int max_chunks_for(int32_t table_width, int32_t block_size, int chunk = kChunk) {
   const int64_t tokens = (int64_t)table_width * block_size;
-  return (int)((tokens + kChunk - 1) / kChunk);
+  return (int)((tokens + chunk - 1) / chunk);
 }
 
 }  // namespace
@@ -1956,7 +1965,11 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   P.head_dim = head_dim;
   P.block_size = block_size;
   P.window = window;
-  P.max_chunks = max_chunks_for(table_width, block_size);
+  // chunk size: 1024 for fp8 KV on the MFMA path (unit_chunk), 512 otherwise; the
+  // workspace query sizes the partials for 512, an upper bound
+  const bool fp8_mfma = kv_dtype == RLT_FP8_E4M3 && rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim);
+  P.chunk_log2 = fp8_mfma ? 10 : 9;
+  P.max_chunks = max_chunks_for(table_width, block_size, 1 << P.chunk_log2);
   P.qk_scale_log2 = kLog2e / sqrtf((float)head_dim);
   P.out = out;
   P.out_row_stride = out_row_stride;
