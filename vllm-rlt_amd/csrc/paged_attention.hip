@@ -11,9 +11,10 @@
 //
 // Work decomposition (static grids, graph-capturable: no host-side length reads):
 //  The unit of work is (sequence x row-group, kv head, chunk), a chunk being
-//  kChunk = 512 absolute key positions [512c, 512c + 512) processed in 16-position
-//  tiles by ONE wave.  Every row of the sequence (q_len window rows x GQA group)
-//  that attends to the kv head is in that wave's row-group, so each KV byte is read
+//  512 absolute key positions [512c, 512c + 512) (1024 for fp8 KV on the MFMA path)
+//  processed in 16-position tiles by two waves (one for fp8 KV) whose states combine
+//  in a fixed order.  Every row of the sequence (q_len window rows x GQA group)
+//  that attends to the kv head is in the unit's row-group, so each KV byte is read
 //  once per (sequence, kv head) instead of once per q row.  On the MFMA path one
 //  persistent 8-wave workgroup per CU enumerates the active units from the
 //  sequence lengths and takes an equal share of them; the vector path runs one
