@@ -39,6 +39,14 @@ def test_attention_and_sampling_ops_match_the_api(pkg, dev):
                                               cu.to(dev), 5)
     assert torch.equal(got, want) and torch.equal(kd, ks) and torch.equal(vd, vs)
     torch.library.opcheck(torch.ops.rlt_mi355x.paged_attention_store, sa, test_utils=CHECKS)
+    # an FP8 pool is refused before anything is stored (it needs scales)
+    k8, v8 = kd.to(torch.float8_e4m3fn), vd.to(torch.float8_e4m3fn)
+    k8_before = k8.view(torch.uint8).clone()
+    with pytest.raises(ValueError, match="FP8"):
+        torch.ops.rlt_mi355x.paged_attention_store(q.to(dev), kn.to(torch.float8_e4m3fn),
+                                                   vn.to(torch.float8_e4m3fn), k8, v8,
+                                                   tables.to(dev), lengths.to(dev), cu.to(dev), 5)
+    assert torch.equal(k8.view(torch.uint8), k8_before)
 
     logits = torch.randn(6, 3000, generator=g).to(dev)
     t, tk = torch.full((6,), 0.8, device=dev), torch.full((6,), -1, dtype=torch.int64, device=dev)

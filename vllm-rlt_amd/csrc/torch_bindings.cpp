@@ -435,6 +435,9 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
   TORCH_CHECK_VALUE(k_new.scalar_type() == key_cache.scalar_type() &&
                         v_new.scalar_type() == key_cache.scalar_type(),
                     "k_new, v_new must have the pool's dtype");
+  // checked before anything is stored: an FP8 pool needs scales this call does not take
+  TORCH_CHECK_VALUE(key_cache.scalar_type() != at::kFloat8_e4m3fn,
+                    "an FP8 KV pool needs key_scale / value_scale: use store_fp8 and prefill");
   const bool half = q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf;
   if (rows > 0 && half && q.scalar_type() == key_cache.scalar_type() &&
       !rlt_paged_attention_uses_prefill(dtype_code(q.scalar_type()),
