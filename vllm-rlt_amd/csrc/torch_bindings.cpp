@@ -435,9 +435,17 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
   TORCH_CHECK_VALUE(k_new.scalar_type() == key_cache.scalar_type() &&
                         v_new.scalar_type() == key_cache.scalar_type(),
                     "k_new, v_new must have the pool's dtype");
-  // checked before anything is stored: an FP8 pool needs scales this call does not take
+  // checked before anything is stored: an FP8 pool needs scales this call does not take,
+  // and the attention's own shape checks must not fail after the store
   TORCH_CHECK_VALUE(key_cache.scalar_type() != at::kFloat8_e4m3fn,
                     "an FP8 KV pool needs key_scale / value_scale: use store_fp8 and prefill");
+  TORCH_CHECK_VALUE(head_dim <= 256 && key_cache.size(3) == head_dim && q.size(1) % kv_heads == 0,
+                    "q heads must be a positive multiple of KV heads with equal head_dim <= 256");
+  TORCH_CHECK_VALUE(block_tables.dim() == 2 && context_lengths.dim() == 1 &&
+                        cu_seqlens_q.dim() == 1 &&
+                        cu_seqlens_q.size(0) == block_tables.size(0) + 1 &&
+                        context_lengths.size(0) == block_tables.size(0),
+                    "cu_seqlens_q must be [sequences + 1] and lengths [sequences]");
   const bool half = q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf;
   if (rows > 0 && half && q.scalar_type() == key_cache.scalar_type() &&
       !rlt_paged_attention_uses_prefill(dtype_code(q.scalar_type()),
