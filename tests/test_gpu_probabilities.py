@@ -388,6 +388,49 @@ def test_propose_drafts_greedy_only_and_bad_rows(pkg, dev):
     assert torch.equal(proposed.cpu(), want)
 
 
+@pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 65536), (torch.float32, 50001),
+                                         (torch.float16, 151936), (torch.bfloat16, 262144)])
+def test_propose_drafts_unfiltered_draws_match_categorical(pkg, dev, dtype, vocab):
+    """async_speculative.py:645-663 without top-k/top-p: the row-split distributions
+    write the draws' tile totals themselves; the tokens are still torch's categorical
+    of the q rows written (ragged last tile, NaN row, row outside the batch)."""
+    _say("propose_drafts unfiltered", dtype, vocab)
+    g = torch.Generator().manual_seed(vocab + 7)
+    m = 9
+    logits = (torch.randn(m, vocab, generator=g) * 2).to(dtype)
+    logits[4, vocab - 1] = float("nan")
+    logits[6] = 0.0  # uniform row
+    random_rows = torch.tensor([0, 2, 4, 6, 8, 11, 1])
+    r = len(random_rows)
+    t = torch.tensor([0.8, 1.0, 1.0, 1.0, 0.6, 1.0, 1.4])
+    u = torch.rand(r, generator=g)
+    u[3] = 0.5  # exact halfway of the uniform row
+    u[6] = 0.0
+    ones = torch.ones(r)
+    q = torch.full((r, vocab), -1.0, device=dev)
+    proposed, q_o = pkg.propose_drafts(logits.to(dev), random_rows.to(dev), t.to(dev),
+                                       torch.full((r,), -1).to(dev), ones.to(dev), u.to(dev),
+                                       q_out=q, max_top_k=0, apply_top_p=False)
+    got_q = q.cpu()
+    assert torch.isnan(got_q[2]).all() and torch.isnan(got_q[5]).all()
+    ok = [0, 1, 3, 4, 6]
+    x = logits[random_rows[ok]].float() / t[ok, None]
+    want_q = osamp.batched_probabilities(logits[random_rows[ok]], t[ok], torch.full((5,), -1),
+                                         torch.ones(5), max_top_k=0, apply_top_p=False)
+    # the kernel's total is float64: within 5e-6 of the float64 softmax of x = l / T;
+    # torch's float32 softmax (the oracle) itself drifts ~6e-11 V relative (1.6e-5 at
+    # V = 262144, measured against float64), so the oracle bound widens with V
+    torch.testing.assert_close(got_q[ok].double(), torch.softmax(x.double(), -1),
+                               rtol=5e-6, atol=1e-12)
+    torch.testing.assert_close(got_q[ok], want_q, rtol=max(RTOL, 1e-10 * vocab), atol=ATOL)
+    want = logits.float().argmax(-1)
+    sampled, _ = osamp.categorical(got_q, u)
+    for i, row in enumerate(random_rows.tolist()):
+        if row < m:
+            want[row] = sampled[i]
+    assert torch.equal(proposed.cpu(), want)
+
+
 @pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 3001)])
 def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vocab):
     """async_speculative.py:678-692: argmax of every verify row, distributions of the

@@ -1000,7 +1000,8 @@ void launch_split_e(const SplitPlan& pl, int64_t n_dist, const void* logits, con
                     int64_t n_src, int64_t row_stride, int V, const float* temperature,
                     float* out, int64_t out_stride, hipStream_t stream, int64_t* targets,
                     int64_t n_arg, bool fused, const float* qm_src, int64_t qm_rows,
-                    float* qm_out, void* ws, float* pm_out) {
+                    float* qm_out, void* ws, float* pm_out, double* tile_sum,
+                    uint32_t* tile_flags) {
   split::View v;
   v.stats = (split::BlockStat*)ws;
   v.S = pl.S;
@@ -1011,6 +1012,9 @@ void launch_split_e(const SplitPlan& pl, int64_t n_dist, const void* logits, con
   v.targets = targets;
   v.fused = fused;
   v.pm_out = pm_out;
+  v.tile_sum = tile_sum;
+  v.tile_flags = tile_flags;
+  v.tiles = (V + split::kBlockCols - 1) / split::kBlockCols;
   const int esz = DT == RLT_F32 ? 4 : 2;
   const bool vec = V % 4 == 0 && row_stride % 4 == 0 && (uintptr_t)logits % (4 * esz) == 0;
   const bool out_vec = out_stride % 4 == 0 && (uintptr_t)out % 16 == 0;
@@ -1039,11 +1043,12 @@ void launch_split(const SplitPlan& pl, int64_t n_dist, const void* logits, const
                   int64_t n_src, int64_t row_stride, int V, const float* temperature, float* out,
                   int64_t out_stride, hipStream_t stream, int64_t* targets, int64_t n_arg,
                   bool fused, const float* qm_src, int64_t qm_rows, float* qm_out, void* ws,
-                  float* pm_out = nullptr) {
+                  float* pm_out = nullptr, double* tile_sum = nullptr,
+                  uint32_t* tile_flags = nullptr) {
 #define RLT_SPLIT_E(EE)                                                                         \
   launch_split_e<DT, EE>(pl, n_dist, logits, rows, n_src, row_stride, V, temperature, out,      \
                          out_stride, stream, targets, n_arg, fused, qm_src, qm_rows, qm_out, ws, \
-                         pm_out)
+                         pm_out, tile_sum, tile_flags)
   if (pl.E == 16) RLT_SPLIT_E(16);
   else if (pl.E == 32) RLT_SPLIT_E(32);
   else RLT_SPLIT_E(64);
@@ -1056,6 +1061,12 @@ void launch_split(const SplitPlan& pl, int64_t n_dist, const void* logits, const
 // acceptance launches that use them instead of summing q (and p) again.
 float* rlt_accept_p_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab);
 float* rlt_accept_q_partials(void* workspace, int64_t n, int32_t w1, int64_t vocab);
+double* rlt_categorical_tile_sums(void* workspace, int64_t m, int64_t vocab);
+uint32_t* rlt_categorical_tile_flags(void* workspace, int64_t m, int64_t vocab);
+int rlt_categorical_rows_after_tiles(const float* weights, int64_t w_stride, const float* u,
+                                     int64_t m, int64_t vocab, int64_t* out_index,
+                                     const int64_t* scatter, int64_t n_out, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream);
 int rlt_accept_after_pq_partials(const int64_t* draft_tokens, const int64_t* drafts, const float* q,
                                  const float* p, const float* u_accept, const float* u_final,
                                  int64_t n, int32_t w1, int64_t vocab, int64_t* tokens,
@@ -1181,6 +1192,9 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
   SplitPlan pl;
   const bool sp = r > 0 && mtk == 0 && !apply_top_p && split_plan(r, V, pl) &&
                   workspace_bytes >= cat_bytes + split_bytes(r, m, V);
+  // the split form also writes the draws' tile totals (rows of at most 2M columns)
+  double* tsum = sp ? rlt_categorical_tile_sums(workspace, r, vocab) : nullptr;
+  uint32_t* tflags = sp ? rlt_categorical_tile_flags(workspace, r, vocab) : nullptr;
   // greedy proposals for every row (extra workgroups of the distribution launch when
   // there are random rows), then the random rows' draws
 #define RLT_PROPOSE(DT)                                                                       \
@@ -1191,7 +1205,7 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
     else if (sp)                                                                              \
       launch_split<DT>(pl, r, logits, random_rows, m, row_stride, V, temperature, q_out,      \
                        q_stride, stream, proposed, m, false, nullptr, 0, nullptr,             \
-                       (char*)workspace + cat_bytes);                                         \
+                       (char*)workspace + cat_bytes, nullptr, tsum, tflags);                  \
     else                                                                                      \
       dispatch_probs<DT>(r, logits, random_rows, m, row_stride, V, temperature, top_k, top_p, \
                          mtk, apply_top_p != 0, q_out, q_stride, stream, proposed, m);        \
@@ -1206,6 +1220,9 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
   if (r == 0) return rlt_launch_status();
   const int st = rlt_launch_status();
   if (st != RLT_OK) return st;
+  if (tsum)
+    return rlt_categorical_rows_after_tiles(q_out, q_stride, u, r, vocab, proposed, random_rows,
+                                            m, workspace, workspace_bytes, stream);
   return rlt_categorical_rows(q_out, q_stride, u, r, vocab, proposed, random_rows, m, workspace,
                               workspace_bytes, stream);
 }

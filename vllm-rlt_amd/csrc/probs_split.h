@@ -53,6 +53,9 @@ struct View {
   int fused;         // distribution row r's argmax goes to targets[r]
   float* pm_out;     // torch-order row-sum partials of the written rows, or nullptr
                      // (row r, group g at pm_out + (r groups + g) 32; L % 8192 == 0)
+  double* tile_sum;    // float64 totals of the written rows' 4096-column tiles, or
+  uint32_t* tile_flags;  // nullptr (row r, tile k at [r tiles + k]; L % 4096 == 0)
+  int tiles;           // tiles per row
 };
 
 __device__ __forceinline__ int64_t argmax_column(unsigned long long best) {
@@ -340,11 +343,63 @@ __device__ __forceinline__ void slice_partials(float (&y)[E], int64_t c0, int V,
   }
 }
 
+// The categorical draw's tile totals (float64) and flag bits (1 NaN, 2 +inf,
+// 4 negative, 8 positive) of this slice's written values.  Quad q of a thread holds
+// columns c0 + 4 (kThreads q + t) .. +3, so tile kt of the slice is quads 4kt..4kt+3.
+// The draw certifies its crossing against a bound that holds for every float64
+// summation order (and otherwise replays torch's sequential cumsum), so these totals
+// need not repeat the tile kernel's order: the drawn index is the same.
+template <int E, bool kFull>
+__device__ __forceinline__ void slice_tiles(const float (&y)[E], int64_t c0, int V,
+                                            double* __restrict__ ts,
+                                            uint32_t* __restrict__ tf, int64_t tile0,
+                                            int tiles) {
+  constexpr int kT = E / 16;
+  __shared__ double wsum[kT][kWaves];
+  __shared__ uint32_t wflag[kT][kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+#pragma unroll
+  for (int kt = 0; kt < kT; ++kt) {
+    double d = 0.0;
+    uint32_t f = 0;
+#pragma unroll
+    for (int j = 16 * kt; j < 16 * kt + 16; ++j) {
+      const float x = y[j];
+      if (!kFull && (int64_t)elem_col<E>((uint32_t)(c0 + 4 * t), j) >= V) continue;
+      if (isnan(x)) f |= 1u;
+      else if (isinf(x) && x > 0.f) f |= 2u;
+      if (x < 0.f) f |= 4u;
+      if (x > 0.f) f |= 8u;
+      d += (double)x;
+    }
+    for (int off = 32; off >= 1; off >>= 1) d += __shfl_xor(d, off, RLT_WAVE);
+    const uint32_t wf = (__ballot(f & 1u) ? 1u : 0u) | (__ballot(f & 2u) ? 2u : 0u) |
+                        (__ballot(f & 4u) ? 4u : 0u) | (__ballot(f & 8u) ? 8u : 0u);
+    if (lane == 0) {
+      wsum[kt][wave] = d;
+      wflag[kt][wave] = wf;
+    }
+  }
+  __syncthreads();
+  if (t < kT && tile0 + t < tiles) {
+    double d = 0.0;
+    uint32_t f = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      d += wsum[t][w];
+      f |= wflag[t][w];
+    }
+    ts[tile0 + t] = d;
+    tf[tile0 + t] = f;
+  }
+}
+
 template <int DT, int E, bool kVec, bool kFull>
 __device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t c0, int V,
                                            bool nan_row, float lmax, float c, float inv,
                                            float* __restrict__ dst, bool out_vec,
-                                           float* __restrict__ pm) {
+                                           float* __restrict__ pm, double* __restrict__ ts,
+                                           uint32_t* __restrict__ tf, int tiles) {
   const uint32_t base = (uint32_t)(c0 + 4 * threadIdx.x);
   float y[E];
   if (nan_row) {
@@ -368,6 +423,7 @@ __device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t
         if (kFull || (int64_t)col + k < V) dst[col + k] = y[4 * q + k];
     }
   }
+  if (ts) slice_tiles<E, kFull>(y, c0, V, ts, tf, c0 / (16 * kThreads), tiles);
   if constexpr (E * kThreads % cascade::kGroupFloats == 0) {
     if (pm) {
       __shared__ float stage[cascade::kGroupFloats];
@@ -423,10 +479,14 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_write_kernel(
       (const char*)logits + (src_ok ? src_r : 0) * row_stride * (DT == RLT_F32 ? 4 : 2);
   float* dst = out + r * out_stride;
   float* pm = v.pm_out ? v.pm_out + r * cascade::row_geom(V).groups * cascade::kStreams : nullptr;
+  double* ts = v.tile_sum ? v.tile_sum + r * v.tiles : nullptr;
+  uint32_t* tf = v.tile_sum ? v.tile_flags + r * v.tiles : nullptr;
   if (c0 + v.L <= V)
-    write_body<DT, E, kVec, true>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0, pm);
+    write_body<DT, E, kVec, true>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0, pm, ts,
+                                  tf, v.tiles);
   else
-    write_body<DT, E, kVec, false>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0, pm);
+    write_body<DT, E, kVec, false>(src, c0, V, nan_row, lmax, c, inv, dst, out_vec != 0, pm, ts,
+                                   tf, v.tiles);
 }
 
 }  // namespace split

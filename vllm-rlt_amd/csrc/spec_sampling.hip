@@ -863,24 +863,28 @@ void launch_mass_groups(const float* p, const float* q, int64_t p_rows, int64_t 
 // Categorical draws of m weight rows (w_stride floats apart): tile totals over the
 // whole GPU, then one draw workgroup per row; rows of more than kMaxTiles tiles run
 // the single-workgroup kernel (its draw replays them exactly).
+// tiles_ready: the workspace already holds the tile totals and flags (written with
+// the weights; rows of at most kMaxTiles tiles only).
 int launch_categorical(const float* weights, int64_t w_stride, const float* u, int64_t m,
                        int64_t vocab, int64_t* index, uint8_t* valid, const int64_t* scatter,
                        int64_t n_out, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream) {
+                       hipStream_t stream, bool tiles_ready = false) {
   const Layout l = layout_for(0, m, vocab);
   if (!workspace || workspace_bytes < l.total) return RLT_ERR_WORKSPACE;
   char* ws = (char*)workspace;
   int32_t* slow = (int32_t*)(ws + l.slow);
   const int64_t tiles = (vocab + kTile - 1) / kTile;
   if (tiles > kMaxTiles) {
+    if (tiles_ready) return RLT_ERR_ARGUMENT;
     rlt_categorical_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(
         weights, vocab, w_stride, u, index, valid, scatter, n_out, slow);
     return rlt_launch_status();
   }
   double* tile_sum = (double*)(ws + l.tile_sum);
   uint32_t* tile_flags = (uint32_t*)(ws + l.tile_flags);
-  rlt_categorical_tiles_kernel<<<dim3((unsigned)m, (unsigned)tiles), kDrawThreads, 0, stream>>>(
-      weights, vocab, w_stride, tile_sum, tile_flags);
+  if (!tiles_ready)
+    rlt_categorical_tiles_kernel<<<dim3((unsigned)m, (unsigned)tiles), kDrawThreads, 0,
+                                   stream>>>(weights, vocab, w_stride, tile_sum, tile_flags);
   rlt_categorical_draw_kernel<<<(unsigned)m, kDrawThreads, 0, stream>>>(
       weights, vocab, w_stride, tiles, u, tile_sum, tile_flags, index, valid, scatter, n_out,
       slow);
@@ -1074,6 +1078,31 @@ int rlt_categorical_rows(const float* weights, int64_t w_stride, const float* u,
   if (m == 0) return RLT_OK;
   return launch_categorical(weights, w_stride, u, m, vocab, out_index, nullptr, scatter, n_out,
                             workspace, workspace_bytes, stream);
+}
+
+// The tile totals and flags inside a categorical workspace of m rows (row i, tile k
+// at [i tiles + k]; tiles = ceil(vocab / 4096)), for a launch that writes them with the
+// weights; nullptr when rows of this vocabulary do not take the two-launch form.
+double* rlt_categorical_tile_sums(void* workspace, int64_t m, int64_t vocab) {
+  if ((vocab + kTile - 1) / kTile > kMaxTiles) return nullptr;
+  return (double*)((char*)workspace + layout_for(0, m, vocab).tile_sum);
+}
+
+uint32_t* rlt_categorical_tile_flags(void* workspace, int64_t m, int64_t vocab) {
+  if ((vocab + kTile - 1) / kTile > kMaxTiles) return nullptr;
+  return (uint32_t*)((char*)workspace + layout_for(0, m, vocab).tile_flags);
+}
+
+// rlt_categorical_rows after a launch that wrote the tile totals and flags of the
+// weight rows into the workspace (rlt_categorical_tile_sums): the draws only.
+int rlt_categorical_rows_after_tiles(const float* weights, int64_t w_stride, const float* u,
+                                     int64_t m, int64_t vocab, int64_t* out_index,
+                                     const int64_t* scatter, int64_t n_out, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+  if (m < 0 || vocab < 1 || w_stride < vocab) return RLT_ERR_ARGUMENT;
+  if (m == 0) return RLT_OK;
+  return launch_categorical(weights, w_stride, u, m, vocab, out_index, nullptr, scatter, n_out,
+                            workspace, workspace_bytes, stream, true);
 }
 
 // ============================================================ random-round merge
