@@ -1523,12 +1523,13 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   __shared__ L sh;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
 
-  // heaviest row-groups (latest positions) first
+  // heaviest row-groups (latest positions) first across the whole batch: the
+  // row-group index is outermost, then the sequence, then the kv head
   const int64_t id = blockIdx.x;
   const int kvh = (int)(id % P.hkv);
   const int64_t sr = id / P.hkv;
-  const int rg = P.rowgroups - 1 - (int)(sr % P.rowgroups);
-  const int seq = (int)(sr / P.rowgroups);
+  const int seq = (int)(sr % P.num_seqs);
+  const int rg = P.rowgroups - 1 - (int)(sr / P.num_seqs);
   const SeqView sv = seq_view(P, seq);
   const int rows_total = sv.q_len * P.group;
   const int rg_begin = rg * kPfRows;
