@@ -407,11 +407,12 @@ def test_propose_drafts_unfiltered_draws_match_categorical(pkg, dev, dtype, voca
     u[3] = 0.5  # exact halfway of the uniform row
     u[6] = 0.0
     ones = torch.ones(r)
-    q = torch.full((r, vocab), -1.0, device=dev)
+    q = torch.full((r, 3, vocab), -1.0, device=dev)  # written through the q[:, 1] view
     proposed, q_o = pkg.propose_drafts(logits.to(dev), random_rows.to(dev), t.to(dev),
                                        torch.full((r,), -1).to(dev), ones.to(dev), u.to(dev),
-                                       q_out=q, max_top_k=0, apply_top_p=False)
-    got_q = q.cpu()
+                                       q_out=q[:, 1], max_top_k=0, apply_top_p=False)
+    assert bool((q[:, 0] == -1).all()) and bool((q[:, 2] == -1).all())
+    got_q = q[:, 1].cpu()
     assert torch.isnan(got_q[2]).all() and torch.isnan(got_q[5]).all()
     ok = [0, 1, 3, 4, 6]
     x = logits[random_rows[ok]].float() / t[ok, None]
