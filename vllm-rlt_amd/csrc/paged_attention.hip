@@ -1478,9 +1478,10 @@ __global__ __launch_bounds__(256) void rlt_merge_kernel(AttnParams P) {
 // call are equal to the per-row form within floating-point tolerance, not bit for
 // bit (the tile boundaries differ).
 constexpr int kPfNT = 2;        // 16-row MFMA tiles per wave
-constexpr int kPfRows = 4 * 16 * kPfNT;  // q rows per workgroup (4 waves)
+constexpr int kPfWaves = 4;     // waves per workgroup (sharing each staged tile)
+constexpr int kPfRows = kPfWaves * 16 * kPfNT;  // q rows per workgroup
 constexpr int kPfKeys = 64;     // key positions per LDS tile
-constexpr int kPfThreads = 256;
+constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfMinQ = 64;     // q window length from which a call takes this path
 constexpr float kPfLazy = 8.f;  // log2 headroom before the running max moves
 
@@ -1510,7 +1511,7 @@ __device__ __forceinline__ int v_slot(int r, int piece) {
 // UB: block_size % 16 == 0, so each 16-position group of a tile lies in one block
 // and its address comes from one wave-uniform table lookup.
 template <int QT, int D, bool UB>
-__global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_kernel(AttnParams P) {
+__global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void rlt_prefill_kernel(AttnParams P) {
   using M = Mfma<QT>;
   using L = PrefillLds<D>;
   constexpr int NT = kPfNT;
@@ -1518,7 +1519,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 ? 1 : 2) void rlt_prefill_ker
   constexpr int ND = D / 16;        // 16-wide dim tiles of O^T
   constexpr int SLOTS = D / 8;      // 16-byte pieces per position row
   constexpr int ROWS_PER_LD = 64 / SLOTS;                // rows one wave-wide direct load fills
-  constexpr int LDS_PER_WAVE = kPfKeys / ROWS_PER_LD / 4;  // direct loads per wave per tile (K, V each)
+  constexpr int LDS_PER_WAVE = kPfKeys / ROWS_PER_LD / kPfWaves;  // direct loads per wave per tile (K, V each)
+  static_assert(LDS_PER_WAVE * ROWS_PER_LD * kPfWaves == kPfKeys, "the waves' loads cover a tile");
   static_assert(16 % ROWS_PER_LD == 0, "a direct load's rows stay in one 16-position group");
   __shared__ L sh;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
