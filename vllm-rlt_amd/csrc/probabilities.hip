@@ -1001,7 +1001,7 @@ void launch_split_e(const SplitPlan& pl, int64_t n_dist, const void* logits, con
                     float* out, int64_t out_stride, hipStream_t stream, int64_t* targets,
                     int64_t n_arg, bool fused, const float* qm_src, int64_t qm_rows,
                     float* qm_out, void* ws, float* pm_out, double* tile_sum,
-                    uint32_t* tile_flags) {
+                    uint32_t* tile_flags, bool skip_drawn) {
   split::View v;
   v.stats = (split::BlockStat*)ws;
   v.S = pl.S;
@@ -1015,6 +1015,7 @@ void launch_split_e(const SplitPlan& pl, int64_t n_dist, const void* logits, con
   v.tile_sum = tile_sum;
   v.tile_flags = tile_flags;
   v.tiles = (V + split::kBlockCols - 1) / split::kBlockCols;
+  v.skip_drawn = skip_drawn && rows && !fused && n_dist <= split::kMaxDrawnScan;
   const int esz = DT == RLT_F32 ? 4 : 2;
   const bool vec = V % 4 == 0 && row_stride % 4 == 0 && (uintptr_t)logits % (4 * esz) == 0;
   const bool out_vec = out_stride % 4 == 0 && (uintptr_t)out % 16 == 0;
@@ -1044,11 +1045,11 @@ void launch_split(const SplitPlan& pl, int64_t n_dist, const void* logits, const
                   int64_t out_stride, hipStream_t stream, int64_t* targets, int64_t n_arg,
                   bool fused, const float* qm_src, int64_t qm_rows, float* qm_out, void* ws,
                   float* pm_out = nullptr, double* tile_sum = nullptr,
-                  uint32_t* tile_flags = nullptr) {
+                  uint32_t* tile_flags = nullptr, bool skip_drawn = false) {
 #define RLT_SPLIT_E(EE)                                                                         \
   launch_split_e<DT, EE>(pl, n_dist, logits, rows, n_src, row_stride, V, temperature, out,      \
                          out_stride, stream, targets, n_arg, fused, qm_src, qm_rows, qm_out, ws, \
-                         pm_out, tile_sum, tile_flags)
+                         pm_out, tile_sum, tile_flags, skip_drawn)
   if (pl.E == 16) RLT_SPLIT_E(16);
   else if (pl.E == 32) RLT_SPLIT_E(32);
   else RLT_SPLIT_E(64);
@@ -1196,7 +1197,8 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
   double* tsum = sp ? rlt_categorical_tile_sums(workspace, r, vocab) : nullptr;
   uint32_t* tflags = sp ? rlt_categorical_tile_flags(workspace, r, vocab) : nullptr;
   // greedy proposals for every row (extra workgroups of the distribution launch when
-  // there are random rows), then the random rows' draws
+  // there are random rows; the split form skips the rows the draws overwrite), then
+  // the random rows' draws
 #define RLT_PROPOSE(DT)                                                                       \
   do {                                                                                        \
     if (r == 0)                                                                               \
@@ -1205,7 +1207,7 @@ int rlt_propose_drafts(const void* logits, int32_t logits_dtype, int64_t row_str
     else if (sp)                                                                              \
       launch_split<DT>(pl, r, logits, random_rows, m, row_stride, V, temperature, q_out,      \
                        q_stride, stream, proposed, m, false, nullptr, 0, nullptr,             \
-                       (char*)workspace + cat_bytes, nullptr, tsum, tflags);                  \
+                       (char*)workspace + cat_bytes, nullptr, tsum, tflags, true);            \
     else                                                                                      \
       dispatch_probs<DT>(r, logits, random_rows, m, row_stride, V, temperature, top_k, top_p, \
                          mtk, apply_top_p != 0, q_out, q_stride, stream, proposed, m);        \

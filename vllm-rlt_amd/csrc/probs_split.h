@@ -56,18 +56,25 @@ struct View {
   double* tile_sum;    // float64 totals of the written rows' 4096-column tiles, or
   uint32_t* tile_flags;  // nullptr (row r, tile k at [r tiles + k]; L % 4096 == 0)
   int tiles;           // tiles per row
+  int skip_drawn;      // argmax-only rows listed in rows[] (n_dist <= kMaxDrawnScan) are
+                       // skipped: the categorical draws that follow write their outputs
 };
+
+constexpr int kMaxDrawnScan = 4 * kThreads;  // rows[] entries an argmax slice scans
 
 __device__ __forceinline__ int64_t argmax_column(unsigned long long best) {
   return (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
 }
 
 // targets[i] for argmax-only row i from its blocks' keys (one thread per row).
+// A skipped row (skip_drawn) has every key 0, which no scanned slice leaves (its first
+// block's key holds ~column, nonzero), and keeps the output its draw writes.
 __device__ __forceinline__ void finish_argmax_row(const View& v, int64_t i) {
   if (i >= v.n_arg || !v.targets) return;
   const BlockStat* st = v.stats + (v.n_dist + i) * v.NB;
   unsigned long long best = 0;
   for (int b = 0; b < v.NB; ++b) best = st[b].best > best ? st[b].best : best;
+  if (v.skip_drawn && best == 0) return;
   v.targets[i] = argmax_column(best);
 }
 
@@ -295,6 +302,16 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_slice_kernel(
   const int64_t r = (int64_t)blockIdx.x / v.S;
   const int s = (int)((int64_t)blockIdx.x % v.S);
   const bool dist = r < v.n_dist;
+  if (!dist && v.skip_drawn && rows) {
+    // an argmax-only row that is also drawn: empty keys, no logits read
+    int hit = 0;
+    for (int64_t i = t; i < v.n_dist; i += kThreads) hit |= rows[i] == r - v.n_dist;
+    if (__syncthreads_or(hit)) {
+      BlockStat* out = v.stats + r * v.NB + (int64_t)s * (E / 16);
+      if (t < min(E / 16, v.NB - s * (E / 16))) out[t] = BlockStat{-INFINITY, 0u, 0.0, 0ull};
+      return;
+    }
+  }
   int64_t src_r = dist ? (rows ? rows[r] : r) : r - v.n_dist;
   if (src_r < 0 || src_r >= n_src) src_r = 0;  // the row is written as NaN (launch 2)
   const int64_t c0 = (int64_t)s * v.L;
