@@ -432,6 +432,26 @@ def test_propose_drafts_unfiltered_draws_match_categorical(pkg, dev, dtype, voca
     assert torch.equal(proposed.cpu(), want)
 
 
+def test_propose_drafts_unfiltered_many_random_rows(pkg, dev):
+    """More random rows than an argmax slice scans (1024): every greedy row's argmax is
+    computed, the random rows' tokens are the categorical of their q rows."""
+    _say("propose_drafts unfiltered, 1100 random rows of 1200")
+    g = torch.Generator().manual_seed(1200)
+    m, vocab = 1200, 4096
+    logits = torch.randn(m, vocab, generator=g) * 2
+    random_rows = torch.randperm(m, generator=g)[:1100]
+    r = len(random_rows)
+    t = torch.rand(r, generator=g) + 0.5
+    u = torch.rand(r, generator=g)
+    ones = torch.ones(r)
+    proposed, q_o = pkg.propose_drafts(logits.to(dev), random_rows.to(dev), t.to(dev),
+                                       torch.full((r,), -1).to(dev), ones.to(dev), u.to(dev),
+                                       max_top_k=0, apply_top_p=False)
+    want = logits.argmax(-1)
+    want[random_rows] = osamp.categorical(q_o.cpu(), u)[0]
+    assert torch.equal(proposed.cpu(), want)
+
+
 @pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 3001)])
 def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vocab):
     """async_speculative.py:678-692: argmax of every verify row, distributions of the
