@@ -24,6 +24,17 @@
 extern "C" {
 #endif
 
+/*
+ * Version of this interface.  It changes whenever an entry point's arguments change
+ * (e.g. the (workspace, workspace_bytes) pair of rlt_batched_probabilities and
+ * rlt_verify_distributions, added before their `stream` argument in version 2), so a
+ * caller built against another header can refuse the library instead of passing its
+ * arguments in the wrong slots.  No counterpart in the reference (its kernels are
+ * Python / Triton); for callers binding this library directly.
+ */
+#define RLT_MI355X_ABI_VERSION 3
+int rlt_abi_version(void);
+
 /* ---------------------------------------------------------------- attention */
 
 /*

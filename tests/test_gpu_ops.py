@@ -103,3 +103,57 @@ def test_merge_random_round_op(pkg, dev):
     assert acc.tolist() == [2, 1, 0] and nxt.tolist() == [55, 21, 0] and pos.tolist() == [8, 10, 13]
     assert values.tolist() == [[55, 8], [21, 10], [3, 12]] and err.tolist() == [0, 0, 1]
     torch.library.opcheck(torch.ops.rlt_mi355x.merge_random_round, args, test_utils=CHECKS)
+
+
+def test_ops_raise_on_host_tensors_and_on_conversions_they_would_need(pkg, dev):
+    """The C++ operators raise ValueError -- before any launch -- for a host tensor next
+    to device tensors (its pointer would fault the GPU), and for a dtype or layout they
+    do not read (no hidden copy); the package functions make the conversions the
+    reference's own functions make and give the same result."""
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(4, 1000, generator=g).to(dev)
+    t, tk = torch.full((4,), 0.8, device=dev), torch.full((4,), -1, dtype=torch.int64, device=dev)
+    tp = torch.full((4,), 0.9, device=dev)
+    with pytest.raises(ValueError, match="device"):
+        torch.ops.rlt_mi355x.spec_probs(logits, t.cpu(), tk, tp, 0, True)
+    with pytest.raises(ValueError, match="top_k"):
+        torch.ops.rlt_mi355x.spec_probs(logits, t, tk.int(), tp, 0, True)
+    want = torch.ops.rlt_mi355x.spec_probs(logits, t, tk, tp, 0, True)
+    assert torch.equal(pkg.batched_probabilities(logits.double(), t.half(), tk.int(), tp,
+                                                 max_top_k=0, apply_top_p=True),
+                       torch.ops.rlt_mi355x.spec_probs(logits.double().float(),
+                                                       t.half().float(), tk, tp, 0, True))
+    u = torch.rand(4, generator=g).to(dev)
+    with pytest.raises(ValueError, match="device"):
+        torch.ops.rlt_mi355x.categorical(want, u.cpu())
+    with pytest.raises(ValueError, match="weights"):
+        torch.ops.rlt_mi355x.categorical(want.t().contiguous().t(), u)
+    idx, _ = pkg.categorical(want.t().contiguous().t(), u)
+    assert torch.equal(idx, torch.ops.rlt_mi355x.categorical(want, u)[0])
+
+    _, _, k, v = make_pool(40, 1, 16, 4, 128, torch.bfloat16, g)
+    lengths = torch.tensor([100, 37], dtype=torch.int32)
+    tables = random_tables(lengths.tolist(), 16, 40, g)
+    q = torch.randn(2, 8, 128, generator=g).bfloat16().to(dev)
+    kd, vd = k.to(dev), v.to(dev)
+    base = (q, kd, vd, tables.to(dev), lengths.to(dev), None, None, None, 1, 0)
+    with pytest.raises(ValueError, match="device"):
+        torch.ops.rlt_mi355x.paged_attention(*base[:3], tables, *base[4:])
+    with pytest.raises(ValueError, match="block_tables"):
+        torch.ops.rlt_mi355x.paged_attention(*base[:3], tables.long().to(dev), *base[4:])
+    with pytest.raises(ValueError, match="context_lengths"):
+        torch.ops.rlt_mi355x.paged_attention(*base[:4], lengths.long().to(dev), *base[5:])
+    with pytest.raises(ValueError, match="head dimension"):
+        qs = torch.randn(2, 128, 8, generator=g).bfloat16().to(dev).transpose(1, 2)
+        torch.ops.rlt_mi355x.paged_attention(qs, *base[1:])
+
+    kc = torch.zeros(8, 16, 2, 64, dtype=torch.bfloat16, device=dev)
+    rows = torch.randn(2, 2, 64, device=dev).bfloat16()
+    blocks, offsets = torch.tensor([1, 5], device=dev), torch.tensor([0, 3], device=dev)
+    with pytest.raises(ValueError, match="device"):
+        torch.ops.rlt_mi355x.store_kv(kc, kc.clone(), rows, rows, blocks.cpu(), offsets, None, None)
+    with pytest.raises(ValueError, match="blocks"):
+        torch.ops.rlt_mi355x.store_kv(kc, kc.clone(), rows, rows, blocks.int(), offsets, None, None)
+    assert not kc.any()  # nothing was written by the refused calls
+    pkg.store_kv(kc, kc.clone(), rows, rows, blocks.int(), offsets)
+    assert torch.equal(kc[blocks, offsets], rows)

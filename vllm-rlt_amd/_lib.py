@@ -31,7 +31,11 @@ _STATUS = {
 
 _i32, _i64, _sz, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
+# the interface version of include/rlt_mi355x.h these signatures were written for
+ABI_VERSION = 3
+
 _SIGNATURES = {
+    "rlt_abi_version": (ctypes.c_int, []),
     "rlt_paged_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "rlt_paged_attention_uses_mfma": (ctypes.c_int, [_i32, _i32, _i32]),
     "rlt_paged_attention_uses_prefill": (ctypes.c_int, [_i32, _i32, _i32, _i32]),
@@ -150,6 +154,10 @@ def library():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        found = lib.rlt_abi_version()
+        if found != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} implements C ABI version {found}, these bindings "
+                               f"version {ABI_VERSION}: rebuild the library")
         _lib = lib
     return _lib
 

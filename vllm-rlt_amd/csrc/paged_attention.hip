@@ -729,121 +729,9 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
         }
       });
     };
-    // Measurement variant (build with -DRLT_DOT_NT1): one-row units on VALU dot products
-    // instead of a 16-row MFMA tile with one real row.  Config-2 decode (batch 64, 16/16
-    // heads, D = 128): 216.4 us against 213.1 us for MFMA, both within tolerance of the
-    // oracle; the launch is bound by the KV stream either way.  It is off by default:
-    // choosing the math path by row count would make a one-row decode and the packed
-    // window differ in arithmetic, and packed == per-row bit for bit would no longer hold.
-#ifdef RLT_DOT_NT1
-    constexpr bool kDot = NT == 1 && KVT == QT && SM == 0;
-#else
-    constexpr bool kDot = false;
-#endif
-    // Dot-product form: lane (l16, grp) scores position tb + l16 over its 32
-    // contraction elements, the four groups' partials summed by lane swaps; the
-    // P V update keeps dims ND l16 .. + ND of the row per lane over the group's four
-    // positions, summed over the groups at the end of the span.
-    const bool dot = kDot && st.rg_rows == 1;
-    float qf[kDot ? NQS : 1][8];
-    float od[kDot ? ND : 1];
-    float dm = -INFINITY, dl = 0.f;
-    int lo0 = 0, hi0 = 0;
-    auto unpack8 = [](uint4 a, float* f) {
-      const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (QT == RLT_BF16) {
-          f[2 * i] = __uint_as_float(w4[i] << 16);
-          f[2 * i + 1] = __uint_as_float(w4[i] & 0xffff0000u);
-        } else {
-          f[2 * i] = f16_bits_to_f32((uint16_t)(w4[i] & 0xffffu));
-          f[2 * i + 1] = f16_bits_to_f32((uint16_t)(w4[i] >> 16));
-        }
-      }
-    };
-    if constexpr (kDot) {
-      if (dot) {
-        const int src = grp * 16;  // row 0's q slice for this lane's contraction slots
-#pragma unroll
-        for (int s = 0; s < NQS; ++s) {
-          uint4 qv;
-          qv.x = __shfl(qreg[0][s].x, src, RLT_WAVE);
-          qv.y = __shfl(qreg[0][s].y, src, RLT_WAVE);
-          qv.z = __shfl(qreg[0][s].z, src, RLT_WAVE);
-          qv.w = __shfl(qreg[0][s].w, src, RLT_WAVE);
-          unpack8(qv, qf[s]);
-        }
-#pragma unroll
-        for (int d = 0; d < ND; ++d) od[d] = 0.f;
-        lo0 = __shfl(row_lo[0], 0, RLT_WAVE);
-        hi0 = __shfl(row_hi[0], 0, RLT_WAVE);
-      }
-    }
-    auto compute_dot = [&](int t, int b, auto full_tag) {
-      constexpr bool FULL = decltype(full_tag)::value;
-      const int tb = w_begin + t * kTileTok;
-      float acc = 0.f;
-#pragma unroll
-      for (int s = 0; s < NQS; ++s) {
-        float kf[8];
-        unpack8(kb[b].op(s, FULL ? true : okk[b]), kf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc += kf[e] * qf[s][e];
-      }
-      float x = group_sum(acc) * qk_scale;
-      if (!FULL) {
-        const int pos = tb + l16;
-        x = (pos >= lo0 && pos < hi0) ? x : -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (!(okv[b] >> i & 1u)) vq[b].zero(i);
-      }
-      float mx = x;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, RLT_WAVE));
-      const float m_new = fmaxf(dm, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float corr = m_new == dm ? 1.f : __builtin_amdgcn_exp2f(dm - m_use);
-      const float p = __builtin_amdgcn_exp2f(x - m_use);
-      float rs = p;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, RLT_WAVE);
-      dl = dl * corr + rs;
-      dm = m_new;
-      float pi[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pi[i] = __shfl(p, grp * 16 + 4 * grp + i, RLT_WAVE);
-#pragma unroll
-      for (int d = 0; d < ND; ++d) od[d] *= corr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float vf[ND];
-#pragma unroll
-        for (int d2 = 0; d2 < ND / 2; ++d2) {
-          const uint32_t w = vq[b].w[i][d2];
-          if (QT == RLT_BF16) {
-            vf[2 * d2] = __uint_as_float(w << 16);
-            vf[2 * d2 + 1] = __uint_as_float(w & 0xffff0000u);
-          } else {
-            vf[2 * d2] = f16_bits_to_f32((uint16_t)(w & 0xffffu));
-            vf[2 * d2 + 1] = f16_bits_to_f32((uint16_t)(w >> 16));
-          }
-        }
-#pragma unroll
-        for (int d = 0; d < ND; ++d) od[d] += pi[i] * vf[d];
-      }
-    };
     auto step = [&](int t, int b) {
       const int tb = w_begin + t * kTileTok;
       const bool full = tb >= full_lo && tb + kTileTok <= full_hi;
-      if constexpr (kDot) {
-        if (dot) {
-          if (full) compute_dot(t, b, Flag<true>{});
-          else compute_dot(t, b, Flag<false>{});
-          return;
-        }
-      }
       if (full) compute(t, b, Flag<true>{});
       else compute(t, b, Flag<false>{});
     };
@@ -858,21 +746,6 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
       for (int b = 0; b < kStages; ++b) {
         if (b == 0 || t + b < t1) step(t + b, b);
         issue(min(t + b + kStages, tl), b);
-      }
-    }
-    if constexpr (kDot) {
-      if (dot) {
-        // dims ND l16 + d summed over the four groups, then into the MFMA state layout
-        // of row 0 (accumulator element r of column tile dt is dim ND (4 grp + r) + dt)
-#pragma unroll
-        for (int d = 0; d < ND; ++d) od[d] = group_sum(od[d]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int dt = 0; dt < ND; ++dt)
-            oacc[0][dt][r] = __shfl(od[dt], grp * 16 + 4 * grp + r, RLT_WAVE);
-        m_run[0] = dm;
-        l_run[0] = dl;
       }
     }
   }
@@ -1877,6 +1750,8 @@ int max_chunks_for(int32_t table_width, int32_t block_size, int chunk = kChunk) 
 }  // namespace
 
 extern "C" {
+
+int rlt_abi_version(void) { return RLT_MI355X_ABI_VERSION; }
 
 int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim) {
   const bool qok = q_dtype == RLT_BF16 || q_dtype == RLT_F16;

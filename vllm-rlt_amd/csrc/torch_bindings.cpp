@@ -53,9 +53,18 @@ Tensor workspace(size_t bytes, const Tensor& like) {
 void* ptr(const Tensor& t) { return t.data_ptr(); }
 void* ptr(const OptTensor& t) { return t.has_value() ? t->data_ptr() : nullptr; }
 
-Tensor as(const Tensor& t, at::ScalarType dt) {
-  Tensor r = t.scalar_type() == dt ? t : t.to(dt);
-  return r.is_contiguous() ? r : r.contiguous();
+// The operators copy nothing behind the caller's back: a tensor of another dtype or
+// layout than the kernel reads raises ValueError.  The Python wrappers convert where
+// the reference's own functions convert (``logits.float()``, ``drafts.long()``).
+const Tensor& need(const Tensor& t, at::ScalarType dt, const char* name) {
+  TORCH_CHECK_VALUE(t.scalar_type() == dt, name, " must be ", dt, ", got ", t.scalar_type());
+  TORCH_CHECK_VALUE(t.is_contiguous(), name, " must be contiguous");
+  return t;
+}
+
+OptTensor need(const OptTensor& t, at::ScalarType dt, const char* name) {
+  if (t.has_value()) need(*t, dt, name);
+  return t;
 }
 
 bool logit_dtype(at::ScalarType t) {
@@ -63,9 +72,33 @@ bool logit_dtype(at::ScalarType t) {
 }
 
 // Rows with unit column stride (row stride free) in a supported logits dtype.
-Tensor logit_rows(const Tensor& t) {
-  Tensor r = logit_dtype(t.scalar_type()) ? t : t.to(at::kFloat);
-  return r.stride(-1) == 1 ? r : r.contiguous();
+const Tensor& logit_rows(const Tensor& t, const char* name) {
+  TORCH_CHECK_VALUE(logit_dtype(t.scalar_type()), name, " must be float32, bfloat16 or float16");
+  TORCH_CHECK_VALUE(t.stride(-1) == 1, name, " must have a unit column stride");
+  return t;
+}
+
+// Every tensor argument must live on the device of the first one: a host tensor's
+// pointer handed to a kernel would fault the GPU instead of raising.
+void device_check(const c10::Device&) {}
+template <class... Rest>
+void device_check(const c10::Device& dev, const Tensor& t, const Rest&... rest);
+template <class... Rest>
+void device_check(const c10::Device& dev, const OptTensor& t, const Rest&... rest) {
+  if (t.has_value()) device_check(dev, *t);
+  device_check(dev, rest...);
+}
+template <class... Rest>
+void device_check(const c10::Device& dev, const Tensor& t, const Rest&... rest) {
+  TORCH_CHECK_VALUE(t.device() == dev,
+                    "the MI355X kernels require every tensor on one ROCm device: got ",
+                    t.device(), " next to ", dev);
+  device_check(dev, rest...);
+}
+template <class... Rest>
+void same_device(const Tensor& first, const Rest&... rest) {
+  TORCH_CHECK_VALUE(first.is_cuda(), "the MI355X kernels require ROCm device tensors");
+  device_check(first.device(), first, rest...);
 }
 
 // ---------------------------------------------------------------- attention
@@ -80,6 +113,8 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
   TORCH_CHECK_VALUE(window >= 0, "window must be a nonnegative integer");
   TORCH_CHECK_VALUE(q.dim() == 3 && key_cache.dim() == 4 && value_cache.dim() == 4,
                     "q must be [rows, heads, dim] and caches [block, token, kv_head, dim]");
+  same_device(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value_scale,
+              cu_seqlens_q, row_lengths);
   const int64_t head_dim = q.size(2);
   TORCH_CHECK_VALUE(head_dim <= 256, "the MI355X attention backend supports head_dim <= 256");
   TORCH_CHECK_VALUE(key_cache.sizes() == value_cache.sizes() &&
@@ -94,7 +129,8 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
   Tensor output = at::empty_like(q);
   const int64_t rows = q.size(0);
   if (rows == 0 || block_tables.size(0) == 0) return output;
-  const Tensor qq = q.stride(2) == 1 ? q : q.contiguous();
+  TORCH_CHECK_VALUE(q.stride(2) == 1, "paged attention requires a contiguous head dimension");
+  const Tensor& qq = q;
   int32_t mode = 0;
   int64_t s_strides[3] = {0, 0, 0};
   TORCH_CHECK_VALUE(key_scale.has_value() == value_scale.has_value(),
@@ -115,9 +151,11 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
   }
   TORCH_CHECK_VALUE(!(key_cache.scalar_type() == at::kFloat8_e4m3fn && mode == 0),
                     "an FP8 KV pool needs key_scale / value_scale");
-  Tensor tables = block_tables.scalar_type() == at::kInt ? block_tables : block_tables.to(at::kInt);
-  if (tables.stride(1) != 1) tables = tables.contiguous();
-  const Tensor lengths = as(context_lengths, at::kInt);
+  TORCH_CHECK_VALUE(block_tables.dim() == 2 && block_tables.scalar_type() == at::kInt &&
+                        block_tables.stride(1) == 1,
+                    "block_tables must be int32 [sequences, width] with unit column stride");
+  const Tensor& tables = block_tables;
+  const Tensor& lengths = need(context_lengths, at::kInt, "context_lengths");
   const int64_t num_seqs = tables.size(0);
   OptTensor cu;
   int64_t max_q = 1;
@@ -125,7 +163,7 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
     TORCH_CHECK_VALUE(num_seqs == rows && lengths.size(0) == rows,
                       "per-row attention needs one block table and length per q row");
   } else {
-    cu = as(*cu_seqlens_q, at::kInt);
+    cu = need(*cu_seqlens_q, at::kInt, "cu_seqlens_q");
     TORCH_CHECK_VALUE(cu->size(0) == num_seqs + 1 && lengths.size(0) == num_seqs,
                       "cu_seqlens_q must be [sequences + 1] and lengths [sequences]");
     max_q = max_seqlen_q;
@@ -135,7 +173,7 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
     TORCH_CHECK_VALUE(cu_seqlens_q.has_value(), "row_lengths needs the packed form (cu_seqlens_q)");
     TORCH_CHECK_VALUE(row_lengths->dim() == 1 && row_lengths->size(0) == rows,
                       "row_lengths must be [q rows]");
-    rl = as(*row_lengths, at::kInt);
+    rl = need(*row_lengths, at::kInt, "row_lengths");
   }
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   const int64_t heads = q.size(1), width = tables.size(1);
@@ -165,14 +203,15 @@ void check_view(const Tensor& cache, const char* name) {
                     " must be a [block, token, kv_head, dim] view with unit dim stride");
 }
 
-Tensor rows3(const Tensor& x, const char* name) {
-  TORCH_CHECK_VALUE(x.dim() == 3, name, " must be [rows, kv_heads, head_dim]");
-  return x.stride(-1) == 1 ? x : x.contiguous();
+const Tensor& rows3(const Tensor& x, const char* name) {
+  TORCH_CHECK_VALUE(x.dim() == 3 && x.stride(-1) == 1, name,
+                    " must be [rows, kv_heads, head_dim] with unit dim stride");
+  return x;
 }
 
-Tensor index_of(const Tensor& t, int64_t rows, const char* name) {
+const Tensor& index_of(const Tensor& t, int64_t rows, const char* name) {
   TORCH_CHECK_VALUE(t.dim() == 1 && t.size(0) == rows, name, " must have shape [", rows, "]");
-  return as(t, at::kLong);
+  return need(t, at::kLong, name);
 }
 
 // reference: vllm_rlt/kernels/routing.py:210-223, vllm_rlt/kernels/graph_kv.py:52-67.
@@ -181,10 +220,12 @@ void store_kv(const Tensor& key_cache, const Tensor& value_cache, const Tensor& 
               const OptTensor& active) {
   check_view(key_cache, "key_cache");
   check_view(value_cache, "value_cache");
+  same_device(key_cache, value_cache, k_in, v_in, blocks, offsets, mask, active);
   TORCH_CHECK_VALUE(key_cache.strides() == value_cache.strides() &&
                         key_cache.sizes() == value_cache.sizes(),
                     "key and value pools must share a layout");
-  const Tensor k = rows3(k_in, "k"), v = rows3(v_in, "v");
+  const Tensor& k = rows3(k_in, "k");
+  const Tensor& v = rows3(v_in, "v");
   const int64_t rows = k.size(0);
   TORCH_CHECK_VALUE(v.sizes() == k.sizes() && k.size(1) == key_cache.size(2) &&
                         k.size(2) == key_cache.size(3),
@@ -193,17 +234,21 @@ void store_kv(const Tensor& key_cache, const Tensor& value_cache, const Tensor& 
                         v.scalar_type() == key_cache.scalar_type(),
                     "rows must have the pool's dtype");
   if (rows == 0) return;
-  const Tensor b = index_of(blocks, rows, "blocks"), o = index_of(offsets, rows, "offsets");
+  const Tensor& b = index_of(blocks, rows, "blocks");
+  const Tensor& o = index_of(offsets, rows, "offsets");
   OptTensor m, a;
   if (mask.has_value()) {
     TORCH_CHECK_VALUE(mask->dim() == 1 && mask->size(0) == rows, "mask must have shape [", rows,
                       "]");
     const auto mt = mask->scalar_type();
-    m = (mt == at::kBool || mt == at::kByte) ? mask->contiguous() : mask->to(at::kBool).contiguous();
+    TORCH_CHECK_VALUE((mt == at::kBool || mt == at::kByte) && mask->is_contiguous(),
+                      "mask must be a contiguous bool or uint8 tensor");
+    m = mask;
   }
   if (active.has_value()) {
-    TORCH_CHECK_VALUE(active->numel() == 1, "active must be one int32 row count");
-    a = active->reshape({}).to(at::kInt).contiguous();
+    TORCH_CHECK_VALUE(active->numel() == 1 && active->scalar_type() == at::kInt,
+                      "active must be one int32 row count");
+    a = active;
   }
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
   const int status = rlt_kv_store(
@@ -233,8 +278,11 @@ Tensor spec_probs(const Tensor& logits, const Tensor& temperature, const Tensor&
   TORCH_CHECK_VALUE(max_top_k >= 0, "max_top_k must be nonnegative");
   Tensor out = at::empty({n, vocab}, logits.options().dtype(at::kFloat));
   if (n == 0 || vocab == 0) return out;
-  const Tensor x = logit_rows(logits);
-  const Tensor t = as(temperature, at::kFloat), k = as(top_k, at::kLong), p = as(top_p, at::kFloat);
+  same_device(logits, temperature, top_k, top_p);
+  const Tensor& x = logit_rows(logits, "logits");
+  const Tensor& t = need(temperature, at::kFloat, "temperature");
+  const Tensor& k = need(top_k, at::kLong, "top_k");
+  const Tensor& p = need(top_p, at::kFloat, "top_p");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
   // row-split form (several workgroups per row) when it applies to this vocabulary
   const size_t nbytes = rlt_probabilities_workspace_size(n, 0, vocab);
@@ -256,7 +304,9 @@ std::tuple<Tensor, Tensor> categorical(const Tensor& weights, const Tensor& u) {
   Tensor index = at::empty({m}, weights.options().dtype(at::kLong));
   Tensor valid = at::empty({m}, weights.options().dtype(at::kBool));
   if (m == 0) return {index, valid};
-  const Tensor w = as(weights, at::kFloat), uu = as(u, at::kFloat);
+  same_device(weights, u);
+  const Tensor& w = need(weights, at::kFloat, "weights");
+  const Tensor& uu = need(u, at::kFloat, "u");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(w.device());
   const Tensor ws = workspace(rlt_categorical_workspace_size(m, vocab), w);
   const int status = rlt_categorical((const float*)ptr(w), (const float*)ptr(uu), m, vocab,
@@ -286,9 +336,13 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> spec_accept(const Tensor& draft_token
   Tensor error = at::empty({n}, p.options().dtype(at::kBool));
   if (n == 0) return {tokens, accepted, final_token, error};
   TORCH_CHECK_VALUE(w1 <= 32, "at most 32 draft tokens per request are supported");
-  const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
-  const Tensor qq = as(q, at::kFloat), pp = as(p, at::kFloat);
-  const Tensor ua = as(u_accept, at::kFloat), uf = as(u_final, at::kFloat);
+  same_device(p, draft_tokens, drafts, q, u_accept, u_final);
+  const Tensor& dt = need(draft_tokens, at::kLong, "draft_tokens");
+  const Tensor& dr = need(drafts, at::kLong, "drafts");
+  const Tensor& qq = need(q, at::kFloat, "q");
+  const Tensor& pp = need(p, at::kFloat, "p");
+  const Tensor& ua = need(u_accept, at::kFloat, "u_accept");
+  const Tensor& uf = need(u_final, at::kFloat, "u_final");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(p.device());
   const Tensor ws = workspace(rlt_speculative_accept_workspace_size(n, (int32_t)w1, vocab), p);
   const int status = rlt_speculative_accept(
@@ -315,9 +369,12 @@ std::tuple<Tensor, Tensor, Tensor> greedy_accept(const Tensor& draft_tokens, con
   Tensor next_token = at::empty({n}, target_logits.options().dtype(at::kLong));
   if (n == 0) return {targets, accepted, next_token};
   TORCH_CHECK_VALUE(vocab >= 1, "target_logits must have V >= 1");
-  Tensor x = logit_dtype(target_logits.scalar_type()) ? target_logits : target_logits.to(at::kFloat);
-  if (!(x.stride(2) == 1 && x.stride(0) == (w1 + 1) * x.stride(1))) x = x.contiguous();
-  const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
+  same_device(target_logits, draft_tokens, drafts);
+  const Tensor& x = logit_rows(target_logits, "target_logits");
+  TORCH_CHECK_VALUE(x.stride(0) == (w1 + 1) * x.stride(1),
+                    "target_logits rows of a request must be evenly strided ([n * (W1 + 1), V] view)");
+  const Tensor& dt = need(draft_tokens, at::kLong, "draft_tokens");
+  const Tensor& dr = need(drafts, at::kLong, "drafts");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
   const int status = rlt_greedy_accept(
       (const int64_t*)ptr(dt), (const int64_t*)ptr(dr), ptr(x), dtype_code(x.scalar_type()),
@@ -345,13 +402,14 @@ std::tuple<Tensor, Tensor> verify_distributions(const Tensor& logits, const Tens
   Tensor p_out = at::empty({r, vocab}, logits.options().dtype(at::kFloat));
   if (m == 0 && r == 0) return {target, p_out};
   TORCH_CHECK_VALUE(vocab >= 1, "logits must have V >= 1");
-  const Tensor x = logit_rows(logits);
-  const Tensor rows = as(random_rows, at::kLong);
+  same_device(logits, random_rows, temperature, top_k, top_p);
+  const Tensor& x = logit_rows(logits, "logits");
+  const Tensor& rows = need(random_rows, at::kLong, "random_rows");
   OptTensor t, k, p;
   if (r) {
-    t = as(temperature, at::kFloat);
-    k = as(top_k, at::kLong);
-    p = as(top_p, at::kFloat);
+    t = need(temperature, at::kFloat, "temperature");
+    k = need(top_k, at::kLong, "top_k");
+    p = need(top_p, at::kFloat, "top_p");
   }
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
   const size_t nbytes = r ? rlt_probabilities_workspace_size(r, m, vocab) : 0;
@@ -392,10 +450,20 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> verify_accept(
   Tensor accepted = at::empty({n}, i64), final_token = at::empty({n}, i64);
   Tensor error = at::empty({n}, target_logits.options().dtype(at::kBool));
   if (n == 0) return {target, p, tokens, accepted, final_token, error};
-  const Tensor x = logit_rows(target_logits.reshape({rows, vocab}));
-  const Tensor t = as(temperature, at::kFloat), k = as(top_k, at::kLong), pp = as(top_p, at::kFloat);
-  const Tensor dt = as(draft_tokens, at::kLong), dr = as(drafts, at::kLong);
-  const Tensor qq = as(q, at::kFloat), ua = as(u_accept, at::kFloat), uf = as(u_final, at::kFloat);
+  same_device(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
+              u_final);
+  logit_rows(target_logits, "target_logits");
+  TORCH_CHECK_VALUE(target_logits.stride(0) == (w1 + 1) * target_logits.stride(1),
+                    "target_logits rows of a request must be evenly strided ([n * (W1 + 1), V] view)");
+  const Tensor x = target_logits.view({rows, vocab});
+  const Tensor& t = need(temperature, at::kFloat, "temperature");
+  const Tensor& k = need(top_k, at::kLong, "top_k");
+  const Tensor& pp = need(top_p, at::kFloat, "top_p");
+  const Tensor& dt = need(draft_tokens, at::kLong, "draft_tokens");
+  const Tensor& dr = need(drafts, at::kLong, "drafts");
+  const Tensor& qq = need(q, at::kFloat, "q");
+  const Tensor& ua = need(u_accept, at::kFloat, "u_accept");
+  const Tensor& uf = need(u_final, at::kFloat, "u_final");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
   const Tensor ws = workspace(rlt_verify_accept_workspace_size(n, (int32_t)w1, vocab), x);
   const int status = rlt_verify_accept(
@@ -427,8 +495,11 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
   TORCH_CHECK_VALUE(key_cache.strides() == value_cache.strides() &&
                         key_cache.sizes() == value_cache.sizes(),
                     "key and value pools must share a layout with a unit dim stride");
+  same_device(q, k_new_in, v_new_in, key_cache, value_cache, block_tables, context_lengths,
+              cu_seqlens_q);
   const int64_t rows = q.size(0), head_dim = q.size(2), kv_heads = key_cache.size(2);
-  const Tensor k_new = rows3(k_new_in, "k_new"), v_new = rows3(v_new_in, "v_new");
+  const Tensor& k_new = rows3(k_new_in, "k_new");
+  const Tensor& v_new = rows3(v_new_in, "v_new");
   TORCH_CHECK_VALUE(k_new.size(0) == rows && k_new.size(1) == kv_heads && k_new.size(2) == head_dim &&
                         v_new.sizes() == k_new.sizes(),
                     "k_new, v_new must be [q rows, kv_heads, head_dim]");
@@ -446,24 +517,22 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
                         cu_seqlens_q.size(0) == block_tables.size(0) + 1 &&
                         context_lengths.size(0) == block_tables.size(0),
                     "cu_seqlens_q must be [sequences + 1] and lengths [sequences]");
+  TORCH_CHECK_VALUE(q.stride(2) == 1, "paged attention requires a contiguous head dimension");
+  TORCH_CHECK_VALUE(block_tables.scalar_type() == at::kInt && block_tables.stride(1) == 1,
+                    "block_tables must be int32 [sequences, width] with unit column stride");
+  need(context_lengths, at::kInt, "context_lengths");
+  need(cu_seqlens_q, at::kInt, "cu_seqlens_q");
+  TORCH_CHECK_VALUE(k_new.strides() == v_new.strides(), "k_new and v_new must share strides");
   const bool half = q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf;
   if (rows > 0 && half && q.scalar_type() == key_cache.scalar_type() &&
       !rlt_paged_attention_uses_prefill(dtype_code(q.scalar_type()),
                                         dtype_code(key_cache.scalar_type()), (int32_t)head_dim,
                                         (int32_t)max_seqlen_q)) {
-    const Tensor qq = q.stride(2) == 1 ? q : q.contiguous();
-    Tensor kn = k_new, vn = v_new;
-    if (vn.strides() != kn.strides()) {
-      kn = kn.contiguous();
-      vn = vn.contiguous();
-    }
-    Tensor tables = block_tables.scalar_type() == at::kInt ? block_tables : block_tables.to(at::kInt);
-    if (tables.stride(1) != 1) tables = tables.contiguous();
-    const Tensor lengths = as(context_lengths, at::kInt);
-    const Tensor cu = as(cu_seqlens_q, at::kInt);
+    const Tensor& qq = q;
+    const Tensor &kn = k_new, &vn = v_new;
+    const Tensor& tables = block_tables;
+    const Tensor &lengths = context_lengths, &cu = cu_seqlens_q;
     const int64_t num_seqs = tables.size(0), width = tables.size(1), heads = q.size(1);
-    TORCH_CHECK_VALUE(cu.size(0) == num_seqs + 1 && lengths.size(0) == num_seqs,
-                      "cu_seqlens_q must be [sequences + 1] and lengths [sequences]");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     Tensor output = at::empty_like(q);
     const Tensor ws = workspace(
@@ -484,17 +553,24 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
       return output;
     }
   }
-  // separate store and attention: positions -> (block, offset) through the tables
+  // separate store and attention: positions -> (block, offset) through the tables; a
+  // position whose block index falls outside the table gets block -1, which the
+  // scatter skips (the one-launch form does not write such positions either)
   if (rows > 0) {
     const Tensor cu = cu_seqlens_q.to(at::kLong);
-    const int64_t num_seqs = cu.size(0) - 1;
+    const int64_t num_seqs = cu.size(0) - 1, width = block_tables.size(1);
     const Tensor q_len = cu.slice(0, 1) - cu.slice(0, 0, num_seqs);
     const Tensor seq = at::repeat_interleave(
         at::arange(num_seqs, cu.options()), q_len, /*dim=*/0, /*output_size=*/rows);
     const Tensor pos = context_lengths.to(at::kLong).index({seq}) - q_len.index({seq}) +
                        at::arange(rows, cu.options()) - cu.index({seq});
     const int64_t bs = key_cache.size(1);
-    const Tensor blocks = block_tables.to(at::kLong).index({seq, at::floor_divide(pos, bs)});
+    const Tensor idx = at::floor_divide(pos, bs);
+    const Tensor inside = (idx >= 0) & (idx < width);
+    const Tensor blocks =
+        width == 0 ? at::full({rows}, -1, cu.options())
+                   : at::where(inside, block_tables.to(at::kLong).index({seq, idx.clamp(0, width - 1)}),
+                               at::full({rows}, -1, cu.options()));
     store_kv(key_cache, value_cache, k_new, v_new, blocks, at::remainder(pos, bs), std::nullopt,
              std::nullopt);
   }

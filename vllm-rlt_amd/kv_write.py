@@ -74,8 +74,10 @@ def store_kv(key_cache, value_cache, k, v, blocks, offsets, *, mask=None, active
     _lib.require_gpu(key_cache, value_cache, k, v, blocks, offsets, mask, active)
     if rows == 0:
         return
-    # index / mask conversions and the launch: torch.ops.rlt_mi355x.store_kv
-    _lib.ops().store_kv(key_cache, value_cache, k, v, blocks, offsets, mask, active)
+    # the operator reads int64 indices, a bool / uint8 mask and an int32 count as given
+    # (it raises on anything else): torch.ops.rlt_mi355x.store_kv
+    _lib.ops().store_kv(key_cache, value_cache, k, v, _index(blocks, rows, "blocks"),
+                        _index(offsets, rows, "offsets"), _mask(mask, rows), _active(active))
 
 
 def masked_kv_store(keys, values, k, v, metadata):
