@@ -263,18 +263,22 @@ def test_config4_wide_heads_d96_32_planes(kernel, dev):
     _close(got, oatt.packed_window_attention(q, k, v, seq_tables, lengths, cu), torch.bfloat16)
 
 
-def test_config5_fp8_rows_at_different_planes(kernel, dev):
-    _say("config5")
-    g = torch.Generator().manual_seed(5)
+@pytest.mark.parametrize("ctx_lo", [16384, 32760])
+def test_config5_fp8_rows_at_different_planes(kernel, dev, ctx_lo):
+    """Config 5's rows (fp8 KV, per-tensor scales, window row j at plane (d0 + j) mod 4)
+    at both ends of its context range U[16384, 32768]: every 1024-position fp8 chunk up
+    to the 32nd is compared with the oracle."""
+    _say("config5", ctx_lo)
+    g = torch.Generator().manual_seed(5 + ctx_lo)
     n, w, planes, bs, hq, hkv, d = 2, 5, 4, 16, 16, 8, 128
-    max_len = 16384 + 8
+    max_len = ctx_lo + 8
     per = -(-max_len // bs)
     pool = n * planes * per
     x = (torch.randn(pool, 1, bs, hkv, d, generator=g) * 8)
     kc = x.clamp(-448, 448).to(torch.float8_e4m3fn)[:, 0]
     vc = (torch.randn(pool, 1, bs, hkv, d, generator=g) * 8).clamp(-448, 448).to(torch.float8_e4m3fn)[:, 0]
     tables = _plane_tables(n, planes, max_len, bs, g, pool)
-    start = torch.randint(16384, 16384 + 4, (n,), generator=g)
+    start = torch.randint(ctx_lo, ctx_lo + 4, (n,), generator=g)
     d0 = torch.randint(0, planes, (n,), generator=g)
     rows_t, rows_len = [], []
     for i in range(n):
@@ -657,3 +661,46 @@ def test_prefill_store_graph_replays_and_other_shapes(kernel, pkg, dev):
     kernel.prefill_store(qd, kn, vn, kd[:, 0], vd[:, 0], bad, c3, cu3.to(dev), 5)
     blk = t3[0, last].item()
     assert torch.equal(kd[blk].cpu().view(torch.int16), kpool[blk].view(torch.int16))
+
+
+@pytest.mark.parametrize("form", ["fused", "prefill_tiling", "float32_q"])
+def test_prefill_store_skips_positions_outside_the_table_or_pool(kernel, pkg, dev, form):
+    """Every form of prefill_store (the one-launch form, and the separate store of a
+    prefill-length window or float32 q) leaves unwritten a window position whose block
+    index lies beyond the table width or whose table entry lies outside the pool, and
+    writes every other window position."""
+    _say("prefill_store outside", form)
+    g = torch.Generator().manual_seed(91)
+    bs, hq, hkv, d = 16, 8, 2, 128
+    q_len = 64 if form == "prefill_tiling" else 5
+    lengths = [700, 2049, 300]
+    pages = sum(-(-x // bs) for x in lengths) + 3
+    kpool, vpool, tables, q, k_new, v_new, cu = _window_store_case(
+        g, torch.bfloat16, d, hq, hkv, bs, lengths, [q_len] * 3, pages, layers=1, layer=0)
+    width = -(-2049 // bs) - 1  # position 2048 of sequence 1 lies beyond the table
+    tables = tables[:, :width]
+    tables[0, (700 - 1) // bs] = pages + 5  # sequence 0's last block: outside the pool
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    if form == "float32_q":
+        q = q.float()
+    kd, vd = kpool.to(dev), vpool.to(dev)
+    kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kd[:, 0], vd[:, 0],
+                         tables.to(dev), ctx.to(dev), cu.to(dev), q_len)
+    torch.cuda.synchronize()
+    ke, ve = kpool.clone(), vpool.clone()
+    written = 0
+    for s_ in range(3):
+        for i in range(q_len):
+            pos = lengths[s_] - q_len + i
+            idx = pos // bs
+            if idx >= width:
+                continue
+            e = int(tables[s_, idx])
+            if not 0 <= e < pages:
+                continue
+            r = s_ * q_len + i
+            ke[e, 0, pos % bs], ve[e, 0, pos % bs] = k_new[r], v_new[r]
+            written += 1
+    assert 0 < written < 3 * q_len
+    assert torch.equal(kd.cpu().view(torch.int16), ke.view(torch.int16))
+    assert torch.equal(vd.cpu().view(torch.int16), ve.view(torch.int16))

@@ -93,6 +93,18 @@ def _rows(t):
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _request_rows(t):
+    """``[n, W1 + 1, V]`` logits whose rows are one evenly strided ``[n * (W1 + 1), V]``
+    view, in a supported dtype (the layout the greedy and verify kernels read)."""
+    t = _rows(t)
+    return t if t.stride(0) == t.shape[1] * t.stride(1) else t.contiguous()
+
+
+# The C++ operators raise on a dtype or layout they do not read; these wrappers make
+# the conversions the reference's own functions make (``logits.float()``,
+# ``drafts.long()``, speculative_sampling.py:39,131-146), and only when needed.
+
+
 def batched_probabilities(logits, temperature, top_k, top_p, *, max_top_k, apply_top_p):
     """Temperature / strict top-k / top-p distribution of every row as ``[n, V]`` float32.
 
@@ -103,8 +115,8 @@ def batched_probabilities(logits, temperature, top_k, top_p, *, max_top_k, apply
     ``torch.ops.rlt_mi355x.spec_probs``.
     """
     _lib.require_gpu(logits, temperature, top_k, top_p)
-    return _lib.ops().spec_probs(logits, temperature, top_k, top_p, int(max_top_k),
-                                 bool(apply_top_p))
+    return _lib.ops().spec_probs(_rows(logits), _f32(temperature), _i64(top_k), _f32(top_p),
+                                 int(max_top_k), bool(apply_top_p))
 
 
 def greedy_accept_batched(draft_tokens, drafts, target_logits):
@@ -117,7 +129,9 @@ def greedy_accept_batched(draft_tokens, drafts, target_logits):
     Runs ``torch.ops.rlt_mi355x.greedy_accept``.
     """
     _lib.require_gpu(draft_tokens, drafts, target_logits)
-    return _lib.ops().greedy_accept(draft_tokens, drafts, target_logits)
+    if target_logits.ndim != 3:
+        raise ValueError("target_logits must be [n, W1 + 1, V]")
+    return _lib.ops().greedy_accept(_i64(draft_tokens), _i64(drafts), _request_rows(target_logits))
 
 
 def propose_drafts(logits, random_rows, temperature, top_k, top_p, u, *, max_top_k, apply_top_p,
@@ -198,8 +212,9 @@ def verify_distributions(logits, random_rows, temperature, top_k, top_p, *, max_
     _lib.require_gpu(logits, random_rows, *((temperature, top_k, top_p) if r else ()), p_out)
     if p_out is None and r:
         # new output rows: the C++ operator torch.ops.rlt_mi355x.verify_distributions
-        return tuple(_lib.ops().verify_distributions(logits, random_rows, temperature, top_k,
-                                                     top_p, int(max_top_k), bool(apply_top_p)))
+        return tuple(_lib.ops().verify_distributions(
+            _rows(logits), _i64(random_rows), _f32(temperature), _i64(top_k), _f32(top_p),
+            int(max_top_k), bool(apply_top_p)))
     device = logits.device
     target = torch.empty(m, dtype=torch.int64, device=device)
     if p_out is None:
@@ -232,14 +247,15 @@ def categorical(weights, u):
     Runs ``torch.ops.rlt_mi355x.categorical``.
     """
     _lib.require_gpu(weights, u)
-    return _lib.ops().categorical(weights, u)
+    return _lib.ops().categorical(_f32(weights), _f32(u))
 
 
 def speculative_accept(draft_tokens, drafts, q, p, u_accept, u_final):
     """Batched speculative rejection sampling; reference: speculative_sampling.py:104-181.
     Runs ``torch.ops.rlt_mi355x.spec_accept``."""
     _lib.require_gpu(draft_tokens, drafts, q, p, u_accept, u_final)
-    return AcceptResult(*_lib.ops().spec_accept(draft_tokens, drafts, q, p, u_accept, u_final))
+    return AcceptResult(*_lib.ops().spec_accept(_i64(draft_tokens), _i64(drafts), _f32(q), _f32(p),
+                                                _f32(u_accept), _f32(u_final)))
 
 
 def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
@@ -256,8 +272,12 @@ def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts
     """
     _lib.require_gpu(target_logits, temperature, top_k, top_p, draft_tokens, drafts, q, u_accept,
                      u_final)
-    out = _lib.ops().verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts,
-                                   q, u_accept, u_final, int(max_top_k), bool(apply_top_p))
+    if target_logits.ndim != 3:
+        raise ValueError("target_logits must be [n, W1 + 1, V]")
+    out = _lib.ops().verify_accept(_request_rows(target_logits), _f32(temperature), _i64(top_k),
+                                   _f32(top_p), _i64(draft_tokens), _i64(drafts), _f32(q),
+                                   _f32(u_accept), _f32(u_final), int(max_top_k),
+                                   bool(apply_top_p))
     return out[0], out[1], AcceptResult(*out[2:])
 
 
@@ -266,7 +286,7 @@ def verify_accept(target_logits, temperature, top_k, top_p, draft_tokens, drafts
 REJECT_ALL_ACCEPTED, REJECT_REJECTED, REJECT_ZERO_MASS, REJECT_BAD_RESIDUAL, REJECT_BAD_TOKEN = range(5)
 
 
-def rejection_rows(candidates, counts, target, proposal, uniforms, *, sum_threads=None):
+def rejection_rows(candidates, counts, target, proposal, uniforms, *, sum_threads=1):
     """Device part of sync-mode rejection sampling for a batch: ``(status int32 [n],
     accepted int64 [n], residual float32 [n, V])``.
 
@@ -276,8 +296,12 @@ def rejection_rows(candidates, counts, target, proposal, uniforms, *, sum_thread
     ``[n, K + 1, V]``, ``proposal`` ``[n, K, V]``, ``uniforms`` ``[n, K]``.  Status:
     0 all drafts accepted, 1 rejected at ``accepted`` (``residual`` row = the normalized
     residual), 2 zero proposal mass, 3 invalid residual mass, 4 candidate out of range.
-    The residual total follows torch's CPU order for ``residual.sum()`` with
-    ``sum_threads`` threads (default ``torch.get_num_threads()``).
+    The residual total follows one fixed summation order, whatever the calling process's
+    thread count: torch's CPU order for ``residual.sum()`` on ``sum_threads`` threads
+    (default 1, the single-thread order; pass the thread count of a CPU run to reproduce
+    that run bit for bit).  Against the reference run on device tensors, whose total is
+    torch-ROCm's reduction, the total may differ by a few float32 ulps; only a
+    multinomial draw that lands that close to a CDF boundary can then differ.
     """
     if candidates.ndim != 2:
         raise ValueError("candidates must be [n, K]")
@@ -295,7 +319,9 @@ def _launch_rejection(candidates, counts, target, proposal, uniforms, k, sum_thr
     j > count of a request are never read, so one verified draft may pass a [1, 1, V]
     target)."""
     n, vocab = candidates.shape[0], target.shape[-1]
-    threads = int(torch.get_num_threads() if sum_threads is None else sum_threads)
+    threads = int(sum_threads)
+    if threads < 1:
+        raise ValueError("sum_threads must be a positive thread count")
     _lib.require_gpu(candidates, counts, target, proposal, uniforms)
     device = target.device
     status = torch.empty(n, dtype=torch.int32, device=device)
@@ -343,7 +369,7 @@ def rejection_sample(candidate, target, proposal, generator):
     counts = torch.ones(1, dtype=torch.int64, device=device)
     # one draft: row 0 of the target is all the kernel reads
     status, _, residual = _launch_rejection(cand, counts, target.view(1, 1, vocab),
-                                            proposal.view(1, 1, vocab), u.view(1, 1), 1, None)
+                                            proposal.view(1, 1, vocab), u.view(1, 1), 1, 1)
     code = int(status[0])
     if code in (REJECT_ZERO_MASS, REJECT_BAD_TOKEN):
         generator.set_state(before)  # the reference raises before drawing u
@@ -353,7 +379,7 @@ def rejection_sample(candidate, target, proposal, generator):
     return int(torch.multinomial(residual[0], 1, generator=generator).squeeze(0).item()), False
 
 
-def rejection_round(candidates, target, proposal, generators, *, sum_threads=None):
+def rejection_round(candidates, target, proposal, generators, *, sum_threads=1):
     """The stochastic branch of the synchronous runner's round for a batch of requests:
     a list of ``(tokens, accepted)`` per request.
 
