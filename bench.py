@@ -330,6 +330,32 @@ def config5_step(pkg, dev, attention_only=False):
         reps=5, per_graph=4)
     packed_equal = torch.equal(kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sv, row_lengths=rlp),
                                kern(q, kc, vc, rt, rl, sk, sv)[perm_d])
+    # the window's own K / V quantized into the pool by the attention launch (each row at
+    # position row_lengths - 1 of its plane), against store_fp8 then the same attention;
+    # replays rewrite the same codes.  One fixed scale for K and V here (store_fp8 takes one)
+    kn = (torch.randn(n * w, hkv, d, generator=gd, device=dev) * 2).bfloat16()[perm_d].contiguous()
+    vn = (torch.randn(n * w, hkv, d, generator=gd, device=dev) * 2).bfloat16()[perm_d].contiguous()
+    seq_of_row = torch.repeat_interleave(torch.arange(len(cu) - 1), torch.tensor(cu[1:]) - torch.tensor(cu[:-1]))
+    pos = row_len[torch.tensor(perm)].long() - 1
+    w_blocks = torch.stack(seq_tables).long()[seq_of_row, pos // bs].to(dev)
+    w_offs = (pos % bs).to(dev)
+    sp = torch.zeros(n * w, device=dev)  # scratch scale rows for store_fp8 (fixed scale)
+    sp_pool = sp.new_zeros(())  # not read with a fixed scale
+    scratch_scales = torch.zeros(pool, bs, hkv, device=dev)
+
+    def separate():
+        pkg.store_fp8(kn, vn, kc, vc, scratch_scales, scratch_scales, w_blocks, w_offs, 448.0,
+                      fixed_scale=0.03)
+        return kern.prefill(qp, kc, vc, st, sl, cu_d, max_q, sk, sk, row_lengths=rlp)
+
+    fused = lambda: kern.prefill_store(qp, kn, vn, kc, vc, st, sl, cu_d, max_q, sk, sk,  # noqa: E731
+                                       row_lengths=rlp)
+    store_equal = torch.equal(separate(), fused())
+    t_store_only, _ = _graph_time(
+        lambda: (pkg.store_fp8(kn, vn, kc, vc, scratch_scales, scratch_scales, w_blocks, w_offs,
+                               448.0, fixed_scale=0.03), kc)[1], reps=5, per_graph=4)
+    t_fused, same_fused = _graph_time(fused, reps=5, per_graph=4)
+    del sp, sp_pool, scratch_scales
     a_bytes = _kv_bytes_distinct(row_tables, row_len, req, hkv, d, 1, bs) + 2 * n * w * hq * d * 2
     row_bytes = int(row_len.sum()) * 2 * hkv * d
     del kc, vc
@@ -339,6 +365,9 @@ def config5_step(pkg, dev, attention_only=False):
                      "row_lengths; verify_accept V=65536, T=1, no truncation", n * w, t_attn, a_bytes,
                      t_acc, c_bytes, same_attn and same_acc and same_row)
     out["packed_rows_equal_per_row_bitwise"] = packed_equal
+    out["attention_with_kv_store_us"] = round(t_fused * 1e6, 1)
+    out["kv_store_fp8_us"] = round(t_store_only * 1e6, 1)
+    out["kv_store_fused_equals_store_fp8_then_attention"] = store_equal and same_fused
     out["per_row_attention_us"] = round(t_row * 1e6, 1)
     out["per_row_attention_frac"] = round(a_bytes / t_row / 1e9 / PEAK_HBM_GBS, 4)
     out["per_row_read_GBps"] = round(row_bytes / t_row / 1e9, 1)
@@ -444,7 +473,35 @@ def prefill_steps(pkg, dev):
                            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
                            "graph_replays_equal_eager": same}
         del kc, vc, q
-    return {"workload": "packed causal prefill, bf16, 16 q / 4 kv heads, D=128, block 16",
+    # shapes the prefill tiling does not take (fp8 pools, head_dim 96): the verify kernel's
+    # packed form at prompt length
+    n, L = 8, 2048
+    per = L // bs
+    tables = torch.randperm(n * per, generator=g).int().view(n, per).to(dev)
+    lengths = torch.full((n,), L, dtype=torch.int32, device=dev)
+    cu = torch.arange(0, n * L + 1, L, dtype=torch.int32, device=dev)
+    for name, dd, kv_dtype in (("fp8_d128_8x2048", 128, torch.float8_e4m3fn),
+                               ("bf16_d96_8x2048", 96, torch.bfloat16)):
+        if kv_dtype == torch.float8_e4m3fn:
+            kc = _fp8_pool((n * per, bs, hkv, dd), dev, gd)
+            vc = _fp8_pool((n * per, bs, hkv, dd), dev, gd)
+            scales = (torch.tensor(0.03, device=dev), torch.tensor(0.05, device=dev))
+        else:
+            kc = torch.randn(n * per, bs, hkv, dd, generator=gd, device=dev, dtype=kv_dtype)
+            vc = torch.randn(n * per, bs, hkv, dd, generator=gd, device=dev, dtype=kv_dtype)
+            scales = (None, None)
+        q = torch.randn(n * L, hq, dd, generator=gd, device=dev, dtype=torch.bfloat16)
+        t, same = _graph_time(lambda: kern.prefill(q, kc, vc, tables, lengths, cu, L, *scales),
+                              reps=5, per_graph=2)
+        flops = 4 * hq * dd * n * L * (L + 1) // 2
+        tf = flops / t / 1e12
+        out[name] = {"us": round(t * 1e6, 1), "tflops": round(tf, 1),
+                     "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "path": "verify kernel, packed form", "graph_replays_equal_eager": same}
+        del kc, vc, q
+    return {"workload": "packed causal prefill, bf16, 16 q / 4 kv heads, D=128, block 16 (the "
+                        "prefill tiling); fp8-e4m3 (per-tensor scales) and D=96 prompts run the "
+                        "verify kernel's packed form",
             "flops_per_launch": "4 * Hq * D * sum L(L+1)/2", "launches": out}
 
 

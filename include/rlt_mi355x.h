@@ -137,6 +137,39 @@ int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_hea
                               int64_t out_head_stride, void* workspace, size_t workspace_bytes,
                               hipStream_t stream);
 
+/*
+ * rlt_paged_attention_store with scales, explicit row lengths and either pool type:
+ *   - 16-bit pools as rlt_paged_attention_store (scale_mode 0);
+ *   - fp8-e4m3 pools (kv_dtype 3; q and the rows bf16 / fp16): the rows are quantized
+ *     as they are stored -- codes and scales bitwise rlt_kv_store_fp8's, i.e. the
+ *     reference's quantize_fp8 (vllm_rlt/core/kv_cache_manager.py:50-61) -- with the
+ *     per-tensor scales (scale_mode 1: key_scale / value_scale point at one float
+ *     each, read only) or with per-vector scales computed from each (row, kv head)
+ *     vector and written into the [block, token, kv_head] scale pools (scale_mode 2),
+ *     then read back by the attention with the same scales.  Replaces the fused
+ *     quantize-store vllm_rlt/kernels/triton_attention.py:506-623 (store_fp8)
+ *     followed by the packed attention call (:386-404), in one launch pair.
+ *   - row_lengths (int32 [num_q_rows], optional): packed row r sits at position
+ *     row_lengths[r] - 1 of its sequence (and sees that many keys, as in
+ *     rlt_paged_attention_rows) instead of context_lengths[s] - q_len_s + i.
+ * Pool strides must be multiples of 16 bytes (16-bit pools) or 8 bytes (fp8).
+ * Positions whose block index lies beyond the table, or whose table entry lies
+ * outside the pool, are not written.  Windows that reach the prefill tiling, and
+ * float32 q, return RLT_ERR_UNSUPPORTED.  Workspace: rlt_paged_attention_workspace_size.
+ */
+int rlt_paged_attention_store_scaled(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, void* key_cache,
+    void* value_cache, int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride,
+    int64_t v_block_stride, int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+    const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+    const int32_t* context_lengths, const int32_t* row_lengths, const int32_t* cu_seqlens_q,
+    int32_t num_seqs, int32_t max_q_len, int32_t num_q_rows, float* key_scale, float* value_scale,
+    int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride, int64_t s_head_stride,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int32_t q_dtype, int32_t kv_dtype, const void* new_k, const void* new_v,
+    int64_t new_row_stride, int64_t new_head_stride, void* out, int64_t out_row_stride,
+    int64_t out_head_stride, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* 1 when (q dtype, kv dtype, head_dim) runs on the MFMA kernel, else 0 (vector kernel). */
 int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim);
 

@@ -387,6 +387,48 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
         torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("per_vector", [False, True])
+@pytest.mark.parametrize("q_dtype,d,hq,hkv", [(torch.bfloat16, 128, 16, 8),
+                                              (torch.float16, 96, 8, 2)])
+def test_long_prompt_prefill_fp8_matches_dense_causal(kernel, dev, per_vector, q_dtype, d, hq,
+                                                      hkv):
+    """Prompt prefill over an FP8 pool (reference: triton_attention.py:335-362,460-487,
+    the packed kernel's HAS_SCALE loads): long prompts, a chunk after a prefix and ragged
+    windows against dense causal SDPA over the dequantized keys and values, with
+    per-tensor or per-vector scales.  FP8 pools run the verify kernel's packed form at
+    any q_len (the prefill tiling reads 16-bit pools only)."""
+    _say("long prefill fp8", per_vector, q_dtype, d)
+    g = torch.Generator().manual_seed(23 + d)
+    bs = 16
+    seqs = [(1024, 1024), (2048, 512), (3000, 37), (300, 97), (129, 129)]
+    pages = sum(-(-n // bs) for n, _ in seqs) + 2
+    x_k = torch.randn(pages, bs, hkv, d, generator=g) * 3
+    x_v = torch.randn(pages, bs, hkv, d, generator=g) * 3
+    if per_vector:
+        kc, ks = ofp8.quantize_fp8(x_k)
+        vc, vs = ofp8.quantize_fp8(x_v)
+        k_deq, v_deq = ofp8.dequantize_fp8(kc, ks, torch.float32), ofp8.dequantize_fp8(vc, vs, torch.float32)
+        sk, sv = ks.to(dev), vs.to(dev)
+    else:
+        kc, ks = ofp8.quantize_fp8(x_k, 0.02)
+        vc, vs = ofp8.quantize_fp8(x_v, 0.03)
+        k_deq, v_deq = kc.float() * 0.02, vc.float() * 0.03
+        sk, sv = torch.tensor(0.02, device=dev), torch.tensor(0.03, device=dev)
+    tables = random_tables([n for n, _ in seqs], bs, pages, g)
+    total = sum(c for _, c in seqs)
+    q = torch.randn(total, hq, d, generator=g).to(q_dtype)
+    lengths = torch.tensor([n for n, _ in seqs], dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor([c for _, c in seqs]).cumsum(0)), dtype=torch.int32)
+    got = kernel.prefill(q.to(dev), kc.to(dev), vc.to(dev), tables.to(dev), lengths.to(dev),
+                         cu.to(dev), max(c for _, c in seqs), sk, sv).cpu()
+    for s, (n, c) in enumerate(seqs):
+        pages_s = tables[s, : -(-n // bs)].long()
+        k_seq = k_deq[pages_s].reshape(-1, hkv, d)[:n]
+        v_seq = v_deq[pages_s].reshape(-1, hkv, d)[:n]
+        want = _dense_packed(q[cu[s]:cu[s + 1]], k_seq, v_seq, c, n, 0)
+        torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
+
+
 @pytest.mark.parametrize("bs,window,dtype,d", [(8, 0, torch.bfloat16, 128),
                                                (8, 256, torch.bfloat16, 128),
                                                (48, 0, torch.bfloat16, 128),
@@ -704,3 +746,176 @@ def test_prefill_store_skips_positions_outside_the_table_or_pool(kernel, pkg, de
     assert 0 < written < 3 * q_len
     assert torch.equal(kd.cpu().view(torch.int16), ke.view(torch.int16))
     assert torch.equal(vd.cpu().view(torch.int16), ve.view(torch.int16))
+
+
+# ------------------------------------------------------------ FP8 window store + attention
+
+def _fp8_store_case(g, n, w, hq, hkv, d, bs, lengths, pool_blocks, per_vector, q_dtype):
+    """FP8 pools (codes, per-vector scales), tables and a window of w rows per sequence."""
+    x = torch.randn(pool_blocks, bs, hkv, d, generator=g) * 3
+    kc, ks = ofp8.quantize_fp8(x)
+    vc, vs = ofp8.quantize_fp8(torch.randn(pool_blocks, bs, hkv, d, generator=g) * 3)
+    tables = random_tables(lengths, bs, pool_blocks, g)
+    q = torch.randn(n * w, hq, d, generator=g).to(q_dtype)
+    k_new = (torch.randn(n * w, hkv, d, generator=g) * 4).to(q_dtype)
+    v_new = (torch.randn(n * w, hkv, d, generator=g) * 4).to(q_dtype)
+    k_new[0, 0, 3] = 0.0  # a zero vector component and a fully zero vector (tiny scale)
+    v_new[1, 0].zero_()
+    return kc, vc, ks, vs, tables, q, k_new, v_new
+
+
+@pytest.mark.parametrize("per_vector", [False, True])
+@pytest.mark.parametrize("q_dtype,d,hq,hkv", [(torch.bfloat16, 128, 16, 8),
+                                              (torch.float16, 96, 4, 2)])
+def test_fp8_prefill_store_equals_store_fp8_then_prefill(kernel, pkg, dev, per_vector, q_dtype, d,
+                                                         hq, hkv):
+    """The FP8 window store fused with the attention launch writes the codes (and, with
+    per-vector scales, the scales) that store_fp8 writes -- bitwise the reference's
+    quantize_fp8 -- and returns the attention of prefill over that pool, bit for bit.
+    Per-tensor scales are read, never written."""
+    _say("fp8 prefill_store", per_vector, q_dtype, d)
+    g = torch.Generator().manual_seed(d + hq + per_vector)
+    bs, w = 16, 5
+    lengths = [5, 300, 1030, 1500, 2049]
+    n = len(lengths)
+    pages = sum(-(-x // bs) for x in lengths) + 5
+    kc, vc, ks, vs, tables, q, k_new, v_new = _fp8_store_case(
+        g, n, w, hq, hkv, d, bs, lengths, pages, per_vector, q_dtype)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    cu = torch.arange(0, n * w + 1, w, dtype=torch.int32)
+    seq = torch.arange(n).repeat_interleave(w)
+    pos = ctx.long()[seq] - w + torch.arange(n * w) % w
+    blocks, offs = tables.long()[seq, pos // bs], pos % bs
+    fixed = 0.0375
+    # separate: store_fp8, then prefill
+    ka, va, ksa, vsa = kc.to(dev), vc.to(dev), ks.to(dev), vs.to(dev)
+    pkg.store_fp8(k_new.to(dev), v_new.to(dev), ka, va, ksa, vsa, blocks.to(dev), offs.to(dev),
+                  448.0, fixed_scale=None if per_vector else fixed)
+    if per_vector:
+        want = kernel.prefill(q.to(dev), ka, va, tables.to(dev), ctx.to(dev), cu.to(dev), w, ksa, vsa)
+    else:
+        s0 = torch.tensor(fixed, device=dev)
+        want = kernel.prefill(q.to(dev), ka, va, tables.to(dev), ctx.to(dev), cu.to(dev), w, s0, s0)
+    # fused
+    kb, vb, ksb, vsb = kc.to(dev), vc.to(dev), ks.to(dev), vs.to(dev)
+    if per_vector:
+        got = kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kb, vb, tables.to(dev),
+                                   ctx.to(dev), cu.to(dev), w, ksb, vsb)
+        assert torch.equal(ksb, ksa) and torch.equal(vsb, vsa)
+    else:
+        s0 = torch.tensor(fixed, device=dev)
+        got = kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kb, vb, tables.to(dev),
+                                   ctx.to(dev), cu.to(dev), w, s0, s0)
+        assert float(s0) == float(torch.tensor(fixed))  # read, not written
+    assert torch.equal(kb.view(torch.uint8), ka.view(torch.uint8))
+    assert torch.equal(vb.view(torch.uint8), va.view(torch.uint8))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # the stored codes are the oracle's quantization of the rows at their positions
+    ke = kc.clone()
+    codes, _ = ofp8.quantize_fp8(k_new.float(), None if per_vector else fixed)
+    ke[blocks, offs] = codes
+    assert torch.equal(kb.cpu().view(torch.uint8), ke.view(torch.uint8))
+
+
+def test_fp8_prefill_store_with_row_lengths_config5_layout(kernel, pkg, dev):
+    """Config 5's packed pipeline rows (window row j at plane (d0 + j) mod 4, sequences
+    per (request, plane) with explicit row lengths): every row's K / V is quantized into
+    its own plane at position row_lengths - 1 and the attention equals store_fp8
+    followed by the row-lengths prefill, bit for bit; per-tensor scales; also from a
+    replayed HIP graph."""
+    _say("fp8 prefill_store row lengths")
+    g = torch.Generator().manual_seed(55)
+    n, w, planes, bs, hq, hkv, d = 3, 5, 4, 16, 16, 8, 128
+    max_len = 3000
+    per = -(-max_len // bs)
+    pool = n * planes * per
+    kc, _ = ofp8.quantize_fp8(torch.randn(pool, bs, hkv, d, generator=g) * 3)
+    vc, _ = ofp8.quantize_fp8(torch.randn(pool, bs, hkv, d, generator=g) * 3)
+    tables = torch.randperm(pool, generator=g)[: n * planes * per].view(n, planes, per).int()
+    start = torch.randint(1000, max_len - w, (n,), generator=g)
+    d0 = torch.randint(0, planes, (n,), generator=g)
+    seq_tables, seq_len, cu, row_len, src_row = [], [], [0], [], []
+    q_rows = torch.randn(n * w, hq, d, generator=g).bfloat16()
+    new_k = (torch.randn(n * w, hkv, d, generator=g) * 4).bfloat16()
+    new_v = (torch.randn(n * w, hkv, d, generator=g) * 4).bfloat16()
+    for i in range(n):
+        for pl in range(planes):
+            js = [j for j in range(w) if (int(d0[i]) + j) % planes == pl]
+            if not js:
+                continue
+            seq_tables.append(tables[i, pl])
+            seq_len.append(int(start[i]) + max(js) + 1)
+            for j in js:
+                row_len.append(int(start[i]) + j + 1)
+                src_row.append(i * w + j)
+            cu.append(cu[-1] + len(js))
+    seq_tables = torch.stack(seq_tables)
+    seq_len, cu = torch.tensor(seq_len, dtype=torch.int32), torch.tensor(cu, dtype=torch.int32)
+    row_len, src_row = torch.tensor(row_len, dtype=torch.int32), torch.tensor(src_row)
+    q, kn, vn = q_rows[src_row], new_k[src_row], new_v[src_row]
+    sk, sv = torch.tensor(0.04, device=dev), torch.tensor(0.05, device=dev)
+    seq_of_row = torch.repeat_interleave(torch.arange(len(seq_len)), cu[1:] - cu[:-1])
+    pos = row_len.long() - 1
+    blocks, offs = seq_tables.long()[seq_of_row, pos // bs], pos % bs
+    max_q = int((cu[1:] - cu[:-1]).max())
+    args = lambda kp, vp: (q.to(dev), kn.to(dev), vn.to(dev), kp, vp, seq_tables.to(dev),
+                           seq_len.to(dev), cu.to(dev), max_q)
+    # separate: K with the key scale, V with the value scale (store_fp8 takes one fixed
+    # scale for both, so each pool is written by its own call), then prefill
+    ka, va = kc.to(dev), vc.to(dev)
+    scratch_k, scratch_v = ka.clone(), va.clone()
+    sp = torch.zeros(pool, bs, hkv, device=dev)
+    pkg.store_fp8(kn.to(dev), kn.to(dev), ka, scratch_v, sp, sp.clone(), blocks.to(dev),
+                  offs.to(dev), 448.0, fixed_scale=0.04)
+    pkg.store_fp8(vn.to(dev), vn.to(dev), scratch_k, va, sp.clone(), sp.clone(), blocks.to(dev),
+                  offs.to(dev), 448.0, fixed_scale=0.05)
+    want = kernel.prefill(q.to(dev), ka, va, seq_tables.to(dev), seq_len.to(dev), cu.to(dev),
+                          max_q, sk, sv, row_lengths=row_len.to(dev))
+    kb, vb = kc.to(dev), vc.to(dev)
+    got = kernel.prefill_store(*args(kb, vb), sk, sv, row_lengths=row_len.to(dev))
+    assert torch.equal(kb.view(torch.uint8), ka.view(torch.uint8))
+    assert torch.equal(vb.view(torch.uint8), va.view(torch.uint8))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # replayed from a graph: every replay gives the eager result
+    kg, vg = kc.to(dev), vc.to(dev)
+    a = args(kg, vg)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        kernel.prefill_store(*a, sk, sv, row_lengths=row_len.to(dev))
+        rl = row_len.to(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = kernel.prefill_store(*a, sk, sv, row_lengths=rl)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+        assert torch.equal(kg.view(torch.uint8), ka.view(torch.uint8))
+
+
+def test_prefill_store_row_lengths_16bit_equals_store_then_prefill(kernel, pkg, dev):
+    """Explicit row lengths on a 16-bit pool: rows stored at row_lengths - 1, in any
+    order, then the row-lengths prefill, bit for bit (the one-launch form)."""
+    _say("prefill_store row lengths bf16")
+    g = torch.Generator().manual_seed(56)
+    bs, hq, hkv, d = 16, 8, 2, 128
+    lengths = [900, 1600]
+    pages = sum(-(-x // bs) for x in lengths) + 3
+    kpool, vpool, tables, q, k_new, v_new, cu = _window_store_case(
+        g, torch.bfloat16, d, hq, hkv, bs, lengths, [3, 4], pages, layers=1, layer=0)
+    row_len = torch.tensor([900, 896, 898, 1600, 1597, 1599, 1590], dtype=torch.int32)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    seq = torch.tensor([0, 0, 0, 1, 1, 1, 1])
+    pos = row_len.long() - 1
+    ka, va = kpool.to(dev), vpool.to(dev)
+    pkg.store_kv(ka[:, 0], va[:, 0], k_new.to(dev), v_new.to(dev),
+                 tables.long()[seq, pos // bs].to(dev), (pos % bs).to(dev))
+    want = kernel.prefill(q.to(dev), ka[:, 0], va[:, 0], tables.to(dev), ctx.to(dev), cu.to(dev),
+                          4, row_lengths=row_len.to(dev))
+    kb, vb = kpool.to(dev), vpool.to(dev)
+    got = kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kb[:, 0], vb[:, 0],
+                               tables.to(dev), ctx.to(dev), cu.to(dev), 4,
+                               row_lengths=row_len.to(dev))
+    assert torch.equal(kb.view(torch.int16), ka.view(torch.int16))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))

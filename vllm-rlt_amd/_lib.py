@@ -64,6 +64,19 @@ _SIGNATURES = {
         _p, _i64, _i64,                 # out
         _p, _sz, _p,                    # workspace, bytes, stream
     ]),
+    "rlt_paged_attention_store_scaled": (ctypes.c_int, [
+        _p, _i64, _i64,                 # q
+        _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32,  # pools, strides, blocks
+        _p, _i64, _i32,                 # tables, stride, width
+        _p, _p, _p,                     # lengths, row lengths, cu
+        _i32, _i32, _i32,               # num_seqs, max_q_len, num_q_rows
+        _p, _p, _i32, _i64, _i64, _i64,  # scales
+        _i32, _i32, _i32, _i32,         # hq, hkv, head_dim, block_size
+        _i32, _i32,                     # q dtype, kv dtype
+        _p, _p, _i64, _i64,             # new k, v, row / head strides
+        _p, _i64, _i64,                 # out
+        _p, _sz, _p,                    # workspace, bytes, stream
+    ]),
     "rlt_paged_attention_store": (ctypes.c_int, [
         _p, _i64, _i64,                 # q
         _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32,  # pools, strides, blocks

@@ -135,25 +135,31 @@ class MI355XPagedAttention:
                          max_seqlen_q, key_scale, value_scale, window, row_lengths)
 
     def prefill_store(self, q, k_new, v_new, key_cache, value_cache, block_tables,
-                      context_lengths, cu_seqlens_q, max_seqlen_q):
-        """Store the window rows' own keys / values, then ``prefill`` (no scales, no sliding
-        window).
+                      context_lengths, cu_seqlens_q, max_seqlen_q, key_scale=None,
+                      value_scale=None, *, row_lengths=None):
+        """Store the window rows' own keys / values, then ``prefill`` (no sliding window).
 
         ``k_new`` / ``v_new`` ``[q rows, kv_heads, head_dim]``: row r is written into the
         pool at packed q row r's position (``context_lengths[s] - q_len + i`` for window row
-        i of sequence s) through ``block_tables`` -- the KV write that precedes attention in
-        every layer (reference: vllm_rlt/kernels/graph_kv.py:52-67) -- and the attention
-        then reads it.  bf16 / fp16 windows below the prefill tiling run as one launch pair
-        (the attention waves that read a window position store it first); other shapes
-        store with ``store_kv`` and attend separately.  Returns the attention output.
+        i of sequence s, or ``row_lengths[r] - 1`` with explicit row lengths) through
+        ``block_tables`` -- the KV write that precedes attention in every layer (reference:
+        vllm_rlt/kernels/graph_kv.py:52-67; for FP8 pools the quantize-store
+        vllm_rlt/kernels/triton_attention.py:506-623) -- and the attention then reads it.
+        FP8 pools take bf16 / fp16 rows and quantize them as ``store_fp8`` does: with the
+        0-d per-tensor ``key_scale`` / ``value_scale`` (only read), or with per-vector
+        scales written into the ``[block, token, kv_head]`` scale views.  Verify windows on
+        the MFMA kernels run as one launch pair (the attention waves that read a window
+        position store it first); other 16-bit shapes store with ``store_kv`` and attend
+        separately.  Returns the attention output.
         """
         _lib.require_gpu(q, k_new, v_new, key_cache, value_cache, block_tables, context_lengths,
-                         cu_seqlens_q)
+                         cu_seqlens_q, key_scale, value_scale, row_lengths)
         # argument checks, the one-launch form or the separate store + attention:
         # torch.ops.rlt_mi355x.paged_attention_store (csrc/torch_bindings.cpp)
         return _lib.ops().paged_attention_store(q, k_new, v_new, key_cache, value_cache,
                                                 block_tables, context_lengths, cu_seqlens_q,
-                                                int(max_seqlen_q))
+                                                int(max_seqlen_q), key_scale, value_scale,
+                                                row_lengths)
 
     def uses_mfma(self, q_dtype, kv_dtype, head_dim):
         lib = _lib.library()

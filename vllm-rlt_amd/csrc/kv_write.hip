@@ -25,37 +25,14 @@
 // bounds).
 
 #include "common.h"
+#include "fp8_codec.h"
 #include "rlt_mi355x.h"
 
 #include <math.h>
 
 namespace {
 
-constexpr float kFp8Max = 448.f;
-
-__device__ __forceinline__ float nan_max(float a, float b) {
-  return (a != a || b != b) ? __int_as_float(0x7fc00000) : (a > b ? a : b);
-}
-
-// float -> OCP e4m3fn code, round to nearest even; |x| <= 448 or NaN (the
-// callers clamp first).  Normals: the 23-bit mantissa rounded to 3 bits on the
-// float's bit pattern (a carry moves into the exponent); below the smallest normal
-// 2^-6 the value is a multiple of 2^-9, rounded to an integer count of it.
-__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
-  const uint32_t bits = __float_as_uint(x);
-  const uint32_t sign = (bits >> 24) & 0x80u;
-  const float a = fabsf(x);
-  if (a != a) return sign | 0x7fu;
-  uint32_t code;
-  if (a < 0.015625f) {                   // 2^-6
-    code = (uint32_t)rintf(a * 512.f);   // 0..8 (8 is the smallest normal, 0x08)
-  } else {
-    const uint32_t b = __float_as_uint(a);
-    const uint32_t r = b + 0x7ffffu + ((b >> 20) & 1u);  // round the low 20 bits
-    code = (r >> 20) - ((127u - 7u) << 3);
-  }
-  return sign | code;
-}
+using rlt_fp8::nan_max;
 
 // One workgroup of 256 threads per (row, 16-byte-vector span); each thread moves
 // one 16-byte vector of K and one of V when kVec, else one element.
@@ -113,7 +90,6 @@ __global__ __launch_bounds__(256) void rlt_kv_store_fp8_kernel(
   if (blk < 0 || blk >= num_blocks || off < 0 || off >= block_size) return;  // outside the pool
   const int64_t c_at = blk * c_block + off * c_token + h * c_head;
   const int64_t s_at = blk * s_block + off * s_token + h * s_head;
-  const float inv_max = 1.f / kFp8Max;  // the float32 constant 1/448 (as torch and Triton)
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
     const void* src = which ? v : k;
@@ -129,22 +105,11 @@ __global__ __launch_bounds__(256) void rlt_kv_store_fp8_kernel(
       amax = nan_max(amax, fabsf(x[e]));
     }
     for (int o = 32; o >= 1; o >>= 1) amax = nan_max(amax, __shfl_xor(amax, o, RLT_WAVE));
-    float scale;
-    if (fixed) {
-      scale = fixed_scale;
-    } else {
-      scale = amax * inv_max;
-      scale = scale < 1.17549435e-38f ? 1.17549435e-38f : scale;  // clamp_min(finfo.tiny); NaN stays
-    }
+    const float scale = fixed ? fixed_scale : rlt_fp8::dynamic_scale(amax);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int d = lane + 64 * e;
-      if (d < dim) {
-        const float y = x[e] / scale;
-        // clamp(-448, 448) with NaN kept, as torch's clamp
-        const float q = y != y ? y : (y < -kFp8Max ? -kFp8Max : (y > kFp8Max ? kFp8Max : y));
-        codes[c_at + d] = (uint8_t)f32_to_e4m3(q);
-      }
+      if (d < dim) codes[c_at + d] = (uint8_t)rlt_fp8::encode(x[e], scale);
     }
     if (lane == 0) scales[s_at] = scale;
   }

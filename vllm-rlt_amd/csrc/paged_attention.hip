@@ -41,6 +41,7 @@
 //  * vector (fp32 q, or any other head_dim <= 256): fp32 FMA dot products.
 
 #include "common.h"
+#include "fp8_codec.h"
 #include "rlt_mi355x.h"
 
 #include <math.h>
@@ -458,6 +459,108 @@ struct UnitState {
   bool active;  // the unit has rows and visible positions in this chunk
 };
 
+// The verify window's own keys and values of kv head kvh whose positions lie in
+// [p0, p1), written into the pool through the sequence's block table.  Row i of the
+// sequence sits at position row_len[i] - 1 with explicit row lengths, else at
+// kv_len - q_len + i.  Every wave that reads a window position stores it first
+// (identical bytes when several do, the quantization being deterministic), so no wave
+// depends on another's store.  Positions whose block index lies beyond the table, or
+// whose table entry lies outside the pool, are not written.  16-bit pools receive the
+// rows as they are, half a wave per row; an fp8-e4m3 pool receives the codes of
+// rlt_fp8::encode with the per-tensor scale (SM 1) or with a per-vector scale stored
+// into the scale pool (SM 2), bitwise the scatter kernel's quantize-store, one row per
+// wave (lanes 0-31 key, 32-63 value).  Returns whether this wave stored anything.
+template <int QT, int KVT, int D, int SM>
+__device__ __forceinline__ bool store_window(const AttnParams& P, int seq, int kvh,
+                                             const SeqView& sv, int p0, int p1) {
+  const int lane = threadIdx.x & 63;
+  const int piece = lane & 31;
+  const int base_pos = sv.kv_len - sv.q_len;  // position of window row 0 (causal form)
+  // rows to visit: every row with explicit row lengths (any order), else the range
+  // whose positions meet [p0, p1)
+  const int i_lo = P.row_len ? 0 : max(0, p0 - base_pos);
+  const int i_hi = P.row_len ? sv.q_len : min(sv.q_len, p1 - base_pos);
+  auto position = [&](int i) { return P.row_len ? P.row_len[sv.q_begin + i] - 1 : base_pos + i; };
+  auto block = [&](int pos) {
+    const int idx = pos / P.block_size;
+    return idx < P.table_width ? P.tables[(int64_t)seq * P.table_stride + idx] : -1;
+  };
+  bool stored = false;
+  if constexpr (KVT == QT) {
+    constexpr int kPieces = D * 2 / 16;  // 16-byte pieces of one (row, kv head)
+    for (int i = i_lo + (lane >> 5); i < i_hi; i += 2) {
+      const int pos = position(i);
+      if (pos < p0 || pos >= p1 || pos < 0) continue;
+      const int32_t e = block(pos);
+      if (piece < kPieces && e >= 0 && e < P.num_blocks) {
+        const int64_t row = (int64_t)(sv.q_begin + i) * P.new_row_stride + (int64_t)kvh * P.new_head_stride;
+        const int64_t off = (int64_t)(pos % P.block_size);
+        const uint4 kx = ((const uint4*)((const uint16_t*)P.new_k + row))[piece];
+        const uint4 vx = ((const uint4*)((const uint16_t*)P.new_v + row))[piece];
+        ((uint4*)((uint16_t*)P.k + (int64_t)e * P.k_block_stride + off * P.k_token_stride +
+                  (int64_t)kvh * P.k_head_stride))[piece] = kx;
+        ((uint4*)((uint16_t*)P.v + (int64_t)e * P.v_block_stride + off * P.v_token_stride +
+                  (int64_t)kvh * P.v_head_stride))[piece] = vx;
+        stored = true;
+      }
+    }
+  } else {
+    constexpr int kPieces = D / 8;  // 8-element pieces: 16 bytes of the row, 8 of codes
+    const bool is_v = lane >= 32;
+    const uint16_t* src = (const uint16_t*)(is_v ? P.new_v : P.new_k);
+    uint8_t* pool = (uint8_t*)(is_v ? P.v : P.k);
+    const int64_t b_stride = is_v ? P.v_block_stride : P.k_block_stride;
+    const int64_t t_stride = is_v ? P.v_token_stride : P.k_token_stride;
+    const int64_t h_stride = is_v ? P.v_head_stride : P.k_head_stride;
+    float* scales = const_cast<float*>(is_v ? P.v_scale : P.k_scale);
+    const float fixed = SM == 1 ? scales[0] : 0.f;
+    for (int i = i_lo; i < i_hi; ++i) {  // wave-uniform: the lanes reduce together
+      const int pos = position(i);
+      if (pos < p0 || pos >= p1 || pos < 0) continue;
+      const int32_t e = block(pos);
+      if (e < 0 || e >= P.num_blocks) continue;
+      float x[8];
+      float amax = 0.f;
+      if (piece < kPieces) {
+        const int64_t row = (int64_t)(sv.q_begin + i) * P.new_row_stride + (int64_t)kvh * P.new_head_stride;
+        const uint4 raw = ((const uint4*)(src + row))[piece];
+        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (QT == RLT_BF16) {
+            x[2 * u] = __uint_as_float(w4[u] << 16);
+            x[2 * u + 1] = __uint_as_float(w4[u] & 0xffff0000u);
+          } else {
+            x[2 * u] = f16_bits_to_f32((uint16_t)(w4[u] & 0xffffu));
+            x[2 * u + 1] = f16_bits_to_f32((uint16_t)(w4[u] >> 16));
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) amax = rlt_fp8::nan_max(amax, fabsf(x[u]));
+      }
+      // the row's maximum over the 32 lanes of its half of the wave
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) amax = rlt_fp8::nan_max(amax, __shfl_xor(amax, o, RLT_WAVE));
+      const float scale = SM == 2 ? rlt_fp8::dynamic_scale(amax) : fixed;
+      const int64_t off = (int64_t)(pos % P.block_size);
+      if (piece < kPieces) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          lo |= rlt_fp8::encode(x[u], scale) << (8 * u);
+          hi |= rlt_fp8::encode(x[4 + u], scale) << (8 * u);
+        }
+        *(uint2*)(pool + (int64_t)e * b_stride + off * t_stride + (int64_t)kvh * h_stride + 8 * piece) =
+            make_uint2(lo, hi);
+      }
+      if (SM == 2 && piece == 0)
+        scales[(int64_t)e * P.s_block_stride + off * P.s_token_stride + (int64_t)kvh * P.s_head_stride] = scale;
+      stored = true;
+    }
+  }
+  return __builtin_amdgcn_ballot_w64(stored) != 0;
+}
+
 // Part `part` (of KS = unit_split equal spans) of one work unit -- (sequence,
 // row-group, kv head, chunk) -- on one wave: the wave streams the kv head over
 // positions [512c + part * 512 / KS, + 512 / KS) for every row of the row-group.
@@ -558,34 +661,13 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
     st.v_mul = P.v_scale[0];
   }
 
-  if constexpr (KVT == QT) {
-    if (P.new_k && t0 < t1) {
-      // The window rows' own keys and values, stored through the block table before
-      // any tile of this span is read.  Every wave that reads a window position writes
-      // it first (identical bytes when several do), so no wave depends on another's
-      // store; the wait makes this wave's stores visible to its own loads.
-      const int base_pos = sv.kv_len - sv.q_len;  // position of window row 0
-      const int i0 = max(0, w_begin + t0 * kTileTok - base_pos);
-      const int i1 = min(sv.q_len, w_begin + t1 * kTileTok - base_pos);
-      constexpr int kPieces = D * 2 / 16;  // 16-byte pieces of one (row, kv head)
-      const int piece = lane & 31;
-      for (int i = i0 + (lane >> 5); i < i1; i += 2) {
-        const int pos = base_pos + i;
-        const int idx = pos / P.block_size;
-        const int32_t e = idx < P.table_width ? P.tables[(int64_t)seq * P.table_stride + idx] : -1;
-        if (piece < kPieces && e >= 0 && e < P.num_blocks) {
-          const int64_t row = (int64_t)(sv.q_begin + i) * P.new_row_stride + (int64_t)kvh * P.new_head_stride;
-          const int64_t off = (int64_t)(pos % P.block_size);
-          const uint4 kx = ((const uint4*)((const uint16_t*)P.new_k + row))[piece];
-          const uint4 vx = ((const uint4*)((const uint16_t*)P.new_v + row))[piece];
-          ((uint4*)((uint16_t*)P.k + (int64_t)e * P.k_block_stride + off * P.k_token_stride +
-                    (int64_t)kvh * P.k_head_stride))[piece] = kx;
-          ((uint4*)((uint16_t*)P.v + (int64_t)e * P.v_block_stride + off * P.v_token_stride +
-                    (int64_t)kvh * P.v_head_stride))[piece] = vx;
-        }
-      }
+  if (P.new_k && t0 < t1) {
+    // The window rows' own keys and values, stored through the block table before any
+    // tile of this span is read; the wait makes this wave's stores visible to its own
+    // loads.
+    if (store_window<QT, KVT, D, SM>(P, seq, kvh, sv, w_begin + t0 * kTileTok,
+                                     w_begin + t1 * kTileTok))
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
   }
 
   if (t0 < t1) {
@@ -1677,9 +1759,13 @@ int launch_mfma_sm(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
 
 template <int QT, int KVT, int D>
 int launch_mfma_d(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
-  if (KVT == QT) return launch_mfma_sm<QT, KVT, D, 0>(P, grid, nt, stream);
-  if (P.scale_mode == 1) return launch_mfma_sm<QT, KVT, D, 1>(P, grid, nt, stream);
-  return launch_mfma_sm<QT, KVT, D, 2>(P, grid, nt, stream);
+  // 16-bit pools are read unscaled (scale_mode applies to fp8 pools only)
+  if constexpr (KVT == QT) {
+    return launch_mfma_sm<QT, KVT, D, 0>(P, grid, nt, stream);
+  } else {
+    if (P.scale_mode == 1) return launch_mfma_sm<QT, KVT, D, 1>(P, grid, nt, stream);
+    return launch_mfma_sm<QT, KVT, D, 2>(P, grid, nt, stream);
+  }
 }
 
 template <int QT, int KVT>
@@ -1862,15 +1948,22 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   P.new_row_stride = store ? store->row_stride : 0;
   P.new_head_stride = store ? store->head_stride : 0;
   if (store) {
-    // the fused window store: packed bf16 / fp16 windows on the verify kernels only
-    if (!cu_seqlens_q || row_lengths || kv_dtype != q_dtype ||
-        (q_dtype != RLT_BF16 && q_dtype != RLT_F16) ||
+    // the fused window store, on the verify kernels only: 16-bit pools (no scales), or
+    // fp8 pools with per-tensor or per-vector scales; the rows are bf16 / fp16 like q
+    const bool fp8 = kv_dtype == RLT_FP8_E4M3;
+    if (!cu_seqlens_q || (q_dtype != RLT_BF16 && q_dtype != RLT_F16) ||
+        !(kv_dtype == q_dtype || fp8) ||
         !rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) ||
         rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len))
       return RLT_ERR_UNSUPPORTED;
+    if (fp8 != (scale_mode != 0)) return RLT_ERR_ARGUMENT;
+    const int64_t piece = fp8 ? 8 : 16;  // bytes each lane stores into the pool
+    const int64_t elt = fp8 ? 1 : 2;
     if (!store->k || !store->v || ((uintptr_t)store->k | (uintptr_t)store->v) % 16 ||
         (store->row_stride * 2) % 16 || (store->head_stride * 2) % 16 ||
-        (k_token_stride * 2) % 16 || (v_token_stride * 2) % 16)
+        (k_token_stride * elt) % piece || (v_token_stride * elt) % piece ||
+        (k_head_stride * elt) % piece || (v_head_stride * elt) % piece ||
+        (k_block_stride * elt) % piece || (v_block_stride * elt) % piece)
       return RLT_ERR_ARGUMENT;
   }
 
@@ -1996,6 +2089,29 @@ int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_hea
                         context_lengths, nullptr, cu_seqlens_q, num_seqs, max_q_len, num_q_rows,
                         nullptr, nullptr, 0, 0, 0, 0, num_q_heads, num_kv_heads, head_dim,
                         block_size, dtype, dtype, 0, out, out_row_stride, out_head_stride,
+                        workspace, workspace_bytes, stream, &st);
+}
+
+int rlt_paged_attention_store_scaled(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, void* key_cache,
+    void* value_cache, int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride,
+    int64_t v_block_stride, int64_t v_token_stride, int64_t v_head_stride, int32_t num_blocks,
+    const int32_t* block_tables, int64_t table_stride, int32_t table_width,
+    const int32_t* context_lengths, const int32_t* row_lengths, const int32_t* cu_seqlens_q,
+    int32_t num_seqs, int32_t max_q_len, int32_t num_q_rows, float* key_scale, float* value_scale,
+    int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride, int64_t s_head_stride,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int32_t q_dtype, int32_t kv_dtype, const void* new_k, const void* new_v,
+    int64_t new_row_stride, int64_t new_head_stride, void* out, int64_t out_row_stride,
+    int64_t out_head_stride, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const WindowStore st{new_k, new_v, new_row_stride, new_head_stride};
+  return attention_impl(q, q_row_stride, q_head_stride, key_cache, value_cache, k_block_stride,
+                        k_token_stride, k_head_stride, v_block_stride, v_token_stride,
+                        v_head_stride, num_blocks, block_tables, table_stride, table_width,
+                        context_lengths, row_lengths, cu_seqlens_q, num_seqs, max_q_len,
+                        num_q_rows, key_scale, value_scale, scale_mode, s_block_stride,
+                        s_token_stride, s_head_stride, num_q_heads, num_kv_heads, head_dim,
+                        block_size, q_dtype, kv_dtype, 0, out, out_row_stride, out_head_stride,
                         workspace, workspace_bytes, stream, &st);
 }
 

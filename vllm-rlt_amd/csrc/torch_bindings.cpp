@@ -488,7 +488,9 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> verify_accept(
 Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tensor& v_new_in,
                              const Tensor& key_cache, const Tensor& value_cache,
                              const Tensor& block_tables, const Tensor& context_lengths,
-                             const Tensor& cu_seqlens_q, int64_t max_seqlen_q) {
+                             const Tensor& cu_seqlens_q, int64_t max_seqlen_q,
+                             const OptTensor& key_scale, const OptTensor& value_scale,
+                             const OptTensor& row_lengths) {
   TORCH_CHECK_VALUE(q.dim() == 3, "q must be [rows, heads, dim]");
   check_view(key_cache, "key_cache");
   check_view(value_cache, "value_cache");
@@ -496,20 +498,47 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
                         key_cache.sizes() == value_cache.sizes(),
                     "key and value pools must share a layout with a unit dim stride");
   same_device(q, k_new_in, v_new_in, key_cache, value_cache, block_tables, context_lengths,
-              cu_seqlens_q);
+              cu_seqlens_q, key_scale, value_scale, row_lengths);
   const int64_t rows = q.size(0), head_dim = q.size(2), kv_heads = key_cache.size(2);
   const Tensor& k_new = rows3(k_new_in, "k_new");
   const Tensor& v_new = rows3(v_new_in, "v_new");
   TORCH_CHECK_VALUE(k_new.size(0) == rows && k_new.size(1) == kv_heads && k_new.size(2) == head_dim &&
                         v_new.sizes() == k_new.sizes(),
                     "k_new, v_new must be [q rows, kv_heads, head_dim]");
-  TORCH_CHECK_VALUE(k_new.scalar_type() == key_cache.scalar_type() &&
-                        v_new.scalar_type() == key_cache.scalar_type(),
-                    "k_new, v_new must have the pool's dtype");
-  // checked before anything is stored: an FP8 pool needs scales this call does not take,
-  // and the attention's own shape checks must not fail after the store
-  TORCH_CHECK_VALUE(key_cache.scalar_type() != at::kFloat8_e4m3fn,
-                    "an FP8 KV pool needs key_scale / value_scale: use store_fp8 and prefill");
+  const bool fp8 = key_cache.scalar_type() == at::kFloat8_e4m3fn;
+  const bool half = q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf;
+  // everything is checked before anything is stored: the attention's own checks must
+  // not fail after the store
+  int32_t mode = 0;
+  int64_t s_strides[3] = {0, 0, 0};
+  TORCH_CHECK_VALUE(key_scale.has_value() == value_scale.has_value(),
+                    "key_scale and value_scale must be given together");
+  if (fp8) {
+    TORCH_CHECK_VALUE(half && k_new.scalar_type() == q.scalar_type() &&
+                          v_new.scalar_type() == q.scalar_type(),
+                      "an FP8 window store takes bfloat16 / float16 q, k_new and v_new");
+    TORCH_CHECK_VALUE(key_scale.has_value(), "an FP8 KV pool needs key_scale / value_scale");
+    TORCH_CHECK_VALUE(key_scale->scalar_type() == at::kFloat &&
+                          value_scale->scalar_type() == at::kFloat,
+                      "FP8 scales must be float32");
+    if (key_scale->dim() == 0 && value_scale->dim() == 0) {
+      mode = 1;
+    } else {
+      TORCH_CHECK_VALUE(key_scale->dim() == 3 && key_scale->strides() == value_scale->strides() &&
+                            key_scale->size(0) == key_cache.size(0) &&
+                            key_scale->size(1) == key_cache.size(1) &&
+                            key_scale->size(2) == kv_heads,
+                        "per-vector FP8 scales must be [block, token, kv_head] views of the pool "
+                        "sharing strides");
+      mode = 2;
+      for (int i = 0; i < 3; ++i) s_strides[i] = key_scale->stride(i);
+    }
+  } else {
+    TORCH_CHECK_VALUE(k_new.scalar_type() == key_cache.scalar_type() &&
+                          v_new.scalar_type() == key_cache.scalar_type(),
+                      "k_new, v_new must have the pool's dtype");
+    TORCH_CHECK_VALUE(!key_scale.has_value(), "a 16-bit KV pool takes no scales");
+  }
   TORCH_CHECK_VALUE(head_dim <= 256 && key_cache.size(3) == head_dim && q.size(1) % kv_heads == 0,
                     "q heads must be a positive multiple of KV heads with equal head_dim <= 256");
   TORCH_CHECK_VALUE(block_tables.dim() == 2 && context_lengths.dim() == 1 &&
@@ -522,51 +551,61 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
                     "block_tables must be int32 [sequences, width] with unit column stride");
   need(context_lengths, at::kInt, "context_lengths");
   need(cu_seqlens_q, at::kInt, "cu_seqlens_q");
+  if (row_lengths.has_value()) {
+    TORCH_CHECK_VALUE(row_lengths->dim() == 1 && row_lengths->size(0) == rows,
+                      "row_lengths must be [q rows]");
+    need(*row_lengths, at::kInt, "row_lengths");
+  }
   TORCH_CHECK_VALUE(k_new.strides() == v_new.strides(), "k_new and v_new must share strides");
-  const bool half = q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf;
-  if (rows > 0 && half && q.scalar_type() == key_cache.scalar_type() &&
-      !rlt_paged_attention_uses_prefill(dtype_code(q.scalar_type()),
-                                        dtype_code(key_cache.scalar_type()), (int32_t)head_dim,
-                                        (int32_t)max_seqlen_q)) {
-    const Tensor& qq = q;
-    const Tensor &kn = k_new, &vn = v_new;
-    const Tensor& tables = block_tables;
-    const Tensor &lengths = context_lengths, &cu = cu_seqlens_q;
-    const int64_t num_seqs = tables.size(0), width = tables.size(1), heads = q.size(1);
+  const int32_t qd = dtype_code(q.scalar_type()), kvd = dtype_code(key_cache.scalar_type());
+  const bool one_launch = half && (fp8 || q.scalar_type() == key_cache.scalar_type()) &&
+                          rlt_paged_attention_uses_mfma(qd, kvd, (int32_t)head_dim) &&
+                          !rlt_paged_attention_uses_prefill(qd, kvd, (int32_t)head_dim,
+                                                            (int32_t)max_seqlen_q);
+  TORCH_CHECK_VALUE(one_launch || !fp8,
+                    "an FP8 window store needs a head_dim the MFMA kernels serve (64, 96, 128, "
+                    "256): use store_fp8 and prefill");
+  if (rows > 0 && one_launch) {
+    const int64_t num_seqs = block_tables.size(0), width = block_tables.size(1), heads = q.size(1);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     Tensor output = at::empty_like(q);
     const Tensor ws = workspace(
         rlt_paged_attention_workspace_size((int32_t)rows, (int32_t)heads, (int32_t)head_dim,
                                            (int32_t)width, (int32_t)key_cache.size(1)),
         q);
-    const int status = rlt_paged_attention_store(
-        ptr(qq), qq.stride(0), qq.stride(1), ptr(key_cache), ptr(value_cache), key_cache.stride(0),
+    const int status = rlt_paged_attention_store_scaled(
+        ptr(q), q.stride(0), q.stride(1), ptr(key_cache), ptr(value_cache), key_cache.stride(0),
         key_cache.stride(1), key_cache.stride(2), value_cache.stride(0), value_cache.stride(1),
-        value_cache.stride(2), (int32_t)key_cache.size(0), (const int32_t*)ptr(tables),
-        tables.stride(0), (int32_t)width, (const int32_t*)ptr(lengths), (const int32_t*)ptr(cu),
-        (int32_t)num_seqs, (int32_t)max_seqlen_q, (int32_t)rows, (int32_t)heads, (int32_t)kv_heads,
-        (int32_t)head_dim, (int32_t)key_cache.size(1), dtype_code(q.scalar_type()), ptr(kn), ptr(vn),
-        kn.stride(0), kn.stride(1), ptr(output), output.stride(0), output.stride(1), ptr(ws),
+        value_cache.stride(2), (int32_t)key_cache.size(0), (const int32_t*)ptr(block_tables),
+        block_tables.stride(0), (int32_t)width, (const int32_t*)ptr(context_lengths),
+        (const int32_t*)ptr(row_lengths), (const int32_t*)ptr(cu_seqlens_q), (int32_t)num_seqs,
+        (int32_t)max_seqlen_q, (int32_t)rows, (float*)ptr(key_scale), (float*)ptr(value_scale),
+        mode, s_strides[0], s_strides[1], s_strides[2], (int32_t)heads, (int32_t)kv_heads,
+        (int32_t)head_dim, (int32_t)key_cache.size(1), qd, kvd, ptr(k_new), ptr(v_new),
+        k_new.stride(0), k_new.stride(1), ptr(output), output.stride(0), output.stride(1), ptr(ws),
         ws.numel(), stream_of(q));
-    if (status != 2) {  // 2: a shape the one-launch form does not serve
+    if (status != 2 || fp8) {  // 2: a 16-bit shape the one-launch form does not serve
       check_status(status, "rlt_paged_attention_store");
       return output;
     }
   }
-  // separate store and attention: positions -> (block, offset) through the tables; a
-  // position whose block index falls outside the table gets block -1, which the
-  // scatter skips (the one-launch form does not write such positions either)
+  // separate store and attention (16-bit pools): positions -> (block, offset) through
+  // the tables; a position whose block index falls outside the table gets block -1,
+  // which the scatter skips (the one-launch form does not write such positions either)
   if (rows > 0) {
     const Tensor cu = cu_seqlens_q.to(at::kLong);
     const int64_t num_seqs = cu.size(0) - 1, width = block_tables.size(1);
     const Tensor q_len = cu.slice(0, 1) - cu.slice(0, 0, num_seqs);
     const Tensor seq = at::repeat_interleave(
         at::arange(num_seqs, cu.options()), q_len, /*dim=*/0, /*output_size=*/rows);
-    const Tensor pos = context_lengths.to(at::kLong).index({seq}) - q_len.index({seq}) +
-                       at::arange(rows, cu.options()) - cu.index({seq});
+    const Tensor pos =
+        row_lengths.has_value()
+            ? row_lengths->to(at::kLong) - 1
+            : context_lengths.to(at::kLong).index({seq}) - q_len.index({seq}) +
+                  at::arange(rows, cu.options()) - cu.index({seq});
     const int64_t bs = key_cache.size(1);
     const Tensor idx = at::floor_divide(pos, bs);
-    const Tensor inside = (idx >= 0) & (idx < width);
+    const Tensor inside = (pos >= 0) & (idx < width);
     const Tensor blocks =
         width == 0 ? at::full({rows}, -1, cu.options())
                    : at::where(inside, block_tables.to(at::kLong).index({seq, idx.clamp(0, width - 1)}),
@@ -575,7 +614,7 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
              std::nullopt);
   }
   return paged_attention(q, key_cache, value_cache, block_tables, context_lengths, std::nullopt,
-                         std::nullopt, cu_seqlens_q, max_seqlen_q, 0, std::nullopt);
+                         std::nullopt, cu_seqlens_q, max_seqlen_q, 0, row_lengths);
 }
 
 }  // namespace
@@ -600,7 +639,8 @@ TORCH_LIBRARY(rlt_mi355x, m) {
         "int max_top_k, bool apply_top_p) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("paged_attention_store(Tensor q, Tensor k_new, Tensor v_new, Tensor(a!) key_cache, "
         "Tensor(b!) value_cache, Tensor block_tables, Tensor context_lengths, "
-        "Tensor cu_seqlens_q, int max_seqlen_q) -> Tensor");
+        "Tensor cu_seqlens_q, int max_seqlen_q, Tensor(c!)? key_scale=None, "
+        "Tensor(d!)? value_scale=None, Tensor? row_lengths=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(rlt_mi355x, CUDA, m) {

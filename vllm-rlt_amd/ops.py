@@ -34,7 +34,7 @@ def _(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value
 
 @torch.library.register_fake("rlt_mi355x::paged_attention_store")
 def _(q, k_new, v_new, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-      max_seqlen_q):
+      max_seqlen_q, key_scale=None, value_scale=None, row_lengths=None):
     return torch.empty_like(q)
 
 
