@@ -821,6 +821,20 @@ def main():
             "algorithmic_bytes": a_bytes,
         },
     }
+    if not args.no_secondary:
+        # the compensated P V option (the reference's compensate=True packed kernel) on the
+        # same launches, next to the plain kernel in the same harness (alternating layers)
+        comp = pkg.MI355XPagedAttention(compensate=True)
+        flip = {"i": 0}
+
+        def alternating(kernel):
+            flip["i"] ^= 1
+            return kernel.prefill(w["q"], kcs[flip["i"]], vcs[flip["i"]], tables, lengths, cu,
+                                  w["window"])
+        t_plain2, _ = _graph_time(lambda: alternating(backend.kernel), reps=21, per_graph=10)
+        t_comp, _ = _graph_time(lambda: alternating(comp), reps=21, per_graph=10)
+        result["compensated_attention"] = {"us": round(t_comp * 1e6, 1),
+                                           "plain_us_same_harness": round(t_plain2 * 1e6, 1)}
     if not args.no_config2:
         del g_kv, g_attn, g_fused, g_probs, g_acc, g_step, g_ver
         result["config2_decode_attention"] = config2_decode(pkg, dev)

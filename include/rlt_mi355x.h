@@ -32,8 +32,19 @@ extern "C" {
  * arguments in the wrong slots.  No counterpart in the reference (its kernels are
  * Python / Triton); for callers binding this library directly.
  */
-#define RLT_MI355X_ABI_VERSION 3
+#define RLT_MI355X_ABI_VERSION 4
 int rlt_abi_version(void);
+
+/*
+ * `flags` bits of the attention entry points that take them:
+ *   RLT_ATTN_COMPENSATE: the 16-bit P operand of O = P V is followed by a second MFMA
+ *   with what its cast dropped (P - float(bf16(P))), as the reference's compensated
+ *   packed kernel does (vllm_rlt/kernels/triton_attention.py:368-371, selected by
+ *   vllm_rlt/attention/backend.py:150-161).  MFMA calls only, blocks holding whole
+ *   16-position tiles (else RLT_ERR_UNSUPPORTED); packed calls then stay on the verify
+ *   kernels at every q_len, so packed rows still equal per-row rows bit for bit.
+ */
+#define RLT_ATTN_COMPENSATE 1
 
 /* ---------------------------------------------------------------- attention */
 
@@ -90,8 +101,9 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
  * plane (d0 + j) mod planes and rows d0 and d0 + planes fall on the same plane.  The
  * reference runs such rows through the per-row call (kernels/paged_attention.py:13-47,
  * one gathered table per row); every row here equals that per-row result bit for bit.
- * Never takes the long-prompt prefill tiling.  row_lengths == NULL is
- * rlt_paged_attention; row_lengths without cu_seqlens_q is RLT_ERR_ARGUMENT.
+ * Never takes the long-prompt prefill tiling.  row_lengths == NULL with flags == 0 is
+ * rlt_paged_attention; row_lengths without cu_seqlens_q is RLT_ERR_ARGUMENT.  flags:
+ * RLT_ATTN_COMPENSATE or 0.
  */
 int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                              const void* key_cache, const void* value_cache, int64_t k_block_stride,
@@ -104,7 +116,7 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
                              int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
                              int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
                              int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
-                             int32_t window, void* out, int64_t out_row_stride,
+                             int32_t window, int32_t flags, void* out, int64_t out_row_stride,
                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
@@ -155,7 +167,8 @@ int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_hea
  * Pool strides must be multiples of 16 bytes (16-bit pools) or 8 bytes (fp8).
  * Positions whose block index lies beyond the table, or whose table entry lies
  * outside the pool, are not written.  Windows that reach the prefill tiling, and
- * float32 q, return RLT_ERR_UNSUPPORTED.  Workspace: rlt_paged_attention_workspace_size.
+ * float32 q, return RLT_ERR_UNSUPPORTED.  flags: RLT_ATTN_COMPENSATE or 0.
+ * Workspace: rlt_paged_attention_workspace_size.
  */
 int rlt_paged_attention_store_scaled(
     const void* q, int64_t q_row_stride, int64_t q_head_stride, void* key_cache,
@@ -166,7 +179,7 @@ int rlt_paged_attention_store_scaled(
     int32_t num_seqs, int32_t max_q_len, int32_t num_q_rows, float* key_scale, float* value_scale,
     int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride, int64_t s_head_stride,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-    int32_t q_dtype, int32_t kv_dtype, const void* new_k, const void* new_v,
+    int32_t q_dtype, int32_t kv_dtype, int32_t flags, const void* new_k, const void* new_v,
     int64_t new_row_stride, int64_t new_head_stride, void* out, int64_t out_row_stride,
     int64_t out_head_stride, void* workspace, size_t workspace_bytes, hipStream_t stream);
 

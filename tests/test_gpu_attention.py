@@ -919,3 +919,94 @@ def test_prefill_store_row_lengths_16bit_equals_store_then_prefill(kernel, pkg, 
                                row_lengths=row_len.to(dev))
     assert torch.equal(kb.view(torch.int16), ka.view(torch.int16))
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+# ------------------------------------------------------------ compensated P V
+
+@pytest.mark.parametrize("d", [256, 128])
+def test_compensated_p_keeps_small_value_residual(pkg, dev, d):
+    """Reference known answer (tests/test_dory_gpu.py:501-517): two keys whose weighted
+    values nearly cancel; rounding the weights to bf16 before P V moves the result, the
+    compensated product keeps it (atol 5e-6 against the float64 closed form)."""
+    _say("compensated KAT", d)
+    q = torch.zeros((1, 1, d), dtype=torch.bfloat16)
+    kv = torch.zeros((1, 16, 1, d), dtype=torch.bfloat16)
+    k, v = kv.clone(), kv.clone()
+    # the score of key 1 is -0.5 (D = 256) or as close as a bf16 q allows (D = 128)
+    q0 = 16.0 if d == 256 else 11.3125
+    q[0, 0, 0], k[0, 1, 0, 0] = q0, -0.5
+    v[0, 0, 0, 0], v[0, 1, 0, 0] = -0.60546875, 1
+    s1 = q0 * -0.5 / math.sqrt(d)
+    w0, w1 = 1 / (1 + math.exp(s1)), math.exp(s1) / (1 + math.exp(s1))
+    expected = w0 * -0.60546875 + w1 * 1.0
+    assert expected > 0.0006
+    table = torch.tensor([[0]], dtype=torch.int32)
+    length = torch.tensor([2], dtype=torch.int32)
+    cu = torch.tensor([0, 1], dtype=torch.int32)
+    comp = pkg.MI355XPagedAttention(compensate=True)
+    args = (q.to(dev), k.to(dev), v.to(dev), table.to(dev), length.to(dev))
+    got = comp.prefill(*args, cu.to(dev), 1)
+    assert abs(float(got[0, 0, 0]) - expected) <= 5e-6
+    assert torch.equal(comp(*args), got)  # per-row == packed
+    plain = pkg.MI355XPagedAttention()(*args)
+    assert abs(float(plain[0, 0, 0]) - expected) > 5e-6  # the uncompensated cast loses it
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_compensated_packed_matches_per_row_and_is_closer(pkg, dev, dtype):
+    """Compensated verify windows: packed == per-row bit for bit and batch invariant;
+    against the float64 closed form the error is no larger than the uncompensated one's
+    and within the output rounding (bf16 2^-8, fp16 2^-11 of the value, plus 1e-4)."""
+    _say("compensated window", dtype)
+    g = torch.Generator().manual_seed(31)
+    bs, hq, hkv, d = 16, 16, 4, 128
+    seqs = [(700, 5), (1500, 5), (33, 5), (4097, 9)]
+    pages = sum(-(-n // bs) for n, _ in seqs) + 2
+    _, _, k, v = make_pool(pages, 1, bs, hkv, d, dtype, g)
+    tables = random_tables([n for n, _ in seqs], bs, pages, g)
+    total = sum(c for _, c in seqs)
+    q = torch.randn(total, hq, d, generator=g).to(dtype)
+    lengths = torch.tensor([n for n, _ in seqs], dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor([c for _, c in seqs]).cumsum(0)), dtype=torch.int32)
+    comp = pkg.MI355XPagedAttention(compensate=True)
+    plain = pkg.MI355XPagedAttention()
+    a = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), lengths.to(dev), cu.to(dev), 9)
+    got = comp.prefill(*a).cpu()
+    got_plain = plain.prefill(*a).cpu()
+    # per-row form: each row its own table and length
+    seq = torch.repeat_interleave(torch.arange(len(seqs)), torch.tensor([c for _, c in seqs]))
+    i = torch.arange(total) - cu.long()[seq]
+    row_len = lengths.long()[seq] - torch.tensor([c for _, c in seqs])[seq] + i + 1
+    rows = comp(q.to(dev), k.to(dev), v.to(dev), tables[seq].to(dev), row_len.int().to(dev)).cpu()
+    assert torch.equal(rows.view(torch.int16), got.view(torch.int16))
+    one = comp.prefill(q[:5].to(dev), k.to(dev), v.to(dev), tables[:1].to(dev), lengths[:1].to(dev),
+                       cu[:2].to(dev), 5).cpu()
+    assert torch.equal(one.view(torch.int16), got[:5].view(torch.int16))
+    err_c = err_p = 0.0
+    rel = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    for s, (n, c) in enumerate(seqs):
+        pages_s = tables[s, : -(-n // bs)].long()
+        ks = k[pages_s].reshape(-1, hkv, d)[:n].double()
+        vs = v[pages_s].reshape(-1, hkv, d)[:n].double()
+        kk = ks.repeat_interleave(hq // hkv, 1).transpose(0, 1)
+        vv = vs.repeat_interleave(hq // hkv, 1).transpose(0, 1)
+        qq = q[cu[s]:cu[s + 1]].double().transpose(0, 1)
+        sc = qq @ kk.transpose(1, 2) / math.sqrt(d)
+        pos = torch.arange(n - c, n).view(-1, 1)
+        sc = sc.masked_fill(torch.arange(n).view(1, -1) > pos, float("-inf"))
+        want = (torch.softmax(sc, -1) @ vv).transpose(0, 1)
+        gc, gp = got[cu[s]:cu[s + 1]].double(), got_plain[cu[s]:cu[s + 1]].double()
+        assert ((gc - want).abs() <= rel * want.abs() + 1e-4).all()
+        err_c = max(err_c, float((gc - want).abs().max()))
+        err_p = max(err_p, float((gp - want).abs().max()))
+    assert err_c <= err_p
+
+
+def test_packed_window_shape_selects_compensation(pkg, dev):
+    # reference: vllm_rlt/attention/backend.py:146-161 (a packed window shape opts in)
+    shape = type("PackedWindowShape", (), {})()
+    b = pkg.create_backend("auto", dev, torch.bfloat16, 128, 16, packed_window_shape=shape)
+    assert b.info["compensated_p"] and b.kernel.compensate
+    assert not pkg.create_backend("auto", dev, torch.bfloat16, 128, 16).kernel.compensate
+    assert not pkg.create_backend("auto", dev, torch.float16, 128, 16,
+                                  packed_window_shape=shape).kernel.compensate

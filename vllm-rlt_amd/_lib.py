@@ -32,7 +32,8 @@ _STATUS = {
 _i32, _i64, _sz, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
 # the interface version of include/rlt_mi355x.h these signatures were written for
-ABI_VERSION = 3
+RLT_ATTN_COMPENSATE = 1
+ABI_VERSION = 4
 
 _SIGNATURES = {
     "rlt_abi_version": (ctypes.c_int, []),
@@ -60,7 +61,7 @@ _SIGNATURES = {
         _p, _i32, _i32, _i32,           # cu, num_seqs, max_q_len, num_q_rows
         _p, _p, _i32, _i64, _i64, _i64,  # scales
         _i32, _i32, _i32, _i32,         # hq, hkv, head_dim, block_size
-        _i32, _i32, _i32,               # q dtype, kv dtype, window
+        _i32, _i32, _i32, _i32,         # q dtype, kv dtype, window, flags
         _p, _i64, _i64,                 # out
         _p, _sz, _p,                    # workspace, bytes, stream
     ]),
@@ -72,7 +73,7 @@ _SIGNATURES = {
         _i32, _i32, _i32,               # num_seqs, max_q_len, num_q_rows
         _p, _p, _i32, _i64, _i64, _i64,  # scales
         _i32, _i32, _i32, _i32,         # hq, hkv, head_dim, block_size
-        _i32, _i32,                     # q dtype, kv dtype
+        _i32, _i32, _i32,               # q dtype, kv dtype, flags
         _p, _p, _i64, _i64,             # new k, v, row / head strides
         _p, _i64, _i64,                 # out
         _p, _sz, _p,                    # workspace, bytes, stream

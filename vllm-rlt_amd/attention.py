@@ -90,9 +90,20 @@ MI355X_CAPABILITIES = BackendCapabilities(
 
 
 class MI355XPagedAttention:
-    """Split-KV paged GQA attention on gfx950 (per-row, windowed and packed forms)."""
+    """Split-KV paged GQA attention on gfx950 (per-row, windowed and packed forms).
+
+    ``compensate``: as the reference's ``TritonPagedAttention(compensate=True)``
+    (vllm_rlt/kernels/triton_attention.py:368-371), the 16-bit cast of the softmax
+    weights for the P V product is followed by a second MFMA with the bits it dropped,
+    so P V keeps ~16 bits of each weight instead of 8 (bf16).  Applies to bf16 / fp16
+    q on pools whose block size is a multiple of 16; packed calls then stay on the
+    verify kernels at every window length (rows equal per-row rows bit for bit).
+    """
 
     generation = None
+
+    def __init__(self, compensate=False):
+        self.compensate = bool(compensate)
 
     def _run(self, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
              max_seqlen_q, key_scale, value_scale, window, row_lengths=None):
@@ -105,7 +116,7 @@ class MI355XPagedAttention:
         return _lib.ops().paged_attention(q, key_cache, value_cache, block_tables,
                                           context_lengths, key_scale, value_scale, cu_seqlens_q,
                                           int(max_seqlen_q) if cu_seqlens_q is not None else 1,
-                                          window, row_lengths)
+                                          window, row_lengths, self.compensate)
 
     def __call__(self, q, key_cache, value_cache, block_tables, context_lengths,
                  key_scale=None, value_scale=None):
@@ -159,7 +170,7 @@ class MI355XPagedAttention:
         return _lib.ops().paged_attention_store(q, k_new, v_new, key_cache, value_cache,
                                                 block_tables, context_lengths, cu_seqlens_q,
                                                 int(max_seqlen_q), key_scale, value_scale,
-                                                row_lengths)
+                                                row_lengths, self.compensate)
 
     def uses_mfma(self, q_dtype, kv_dtype, head_dim):
         lib = _lib.library()
@@ -203,13 +214,19 @@ def create_backend(backend, device, dtype, head_dim, block_size, *,
                if getattr(required_capabilities, n) and not getattr(capabilities, n)]
     if missing:
         raise ValueError(f"mi355x lacks required capabilities: {', '.join(missing)}")
-    kernel = MI355XPagedAttention()
+    # a packed window shape opts into the compensated P V product for bf16, as the
+    # reference's packed-window tile selection does (vllm_rlt/attention/backend.py:146-161,
+    # kernels/triton_attention.py:626-628); the blocks must hold whole 16-position tiles
+    compensate = (packed_window_shape is not None and dtype == torch.bfloat16 and
+                  block_size % 16 == 0)
+    kernel = MI355XPagedAttention(compensate=compensate)
     info = {
         "backend": "mi355x",
         "requested_backend": backend,
         "selected_backend": "mi355x",
         "selection_reason": "single gfx950 implementation",
         "math": "mfma" if kernel.uses_mfma(dtype, dtype, head_dim) else "vector",
+        "compensated_p": compensate,
     }
     logging.getLogger(__name__).info("Attention selection: %s", info)
     return AttentionBackend(kernel, replace(capabilities), info)

@@ -86,6 +86,7 @@ struct AttnParams {
   const float* v_scale;
   int64_t s_block_stride, s_token_stride, s_head_stride;
   int32_t scale_mode;  // 0 none, 1 per-tensor (0-d), 2 per-vector [blk, tok, kvh]
+  int32_t compensate;  // MFMA path: P V also with the bits P loses in its 16-bit cast
   int32_t num_seqs;
   int32_t num_rows;  // total q rows
   int32_t hq, hkv, group, head_dim, block_size;
@@ -239,6 +240,9 @@ struct Mfma<RLT_BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, c, 0, 0, 0);
   }
   __device__ static uint16_t from_f32(float x) { return f32_to_bf16_bits(x); }
+  // the two values of a packed pair, exactly
+  __device__ static float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   // two floats -> packed pair (v_cvt_pk_bf16_f32, round to nearest even)
   __device__ static uint32_t pack2(float a, float b) {
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -262,6 +266,8 @@ struct Mfma<RLT_F16> {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, c, 0, 0, 0);
   }
   __device__ static uint16_t from_f32(float x) { return f32_to_f16_bits(x); }
+  __device__ static float lo_f32(uint32_t w) { return f16_bits_to_f32((uint16_t)(w & 0xffffu)); }
+  __device__ static float hi_f32(uint32_t w) { return f16_bits_to_f32((uint16_t)(w >> 16)); }
   __device__ static uint32_t pack2(float a, float b) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     const f16x2 v = {(_Float16)a, (_Float16)b};
@@ -567,7 +573,7 @@ __device__ __forceinline__ bool store_window(const AttnParams& P, int seq, int k
 // tbl_lds: this wave's 512-entry LDS slice for the chunk's block ids.
 // SM: FP8 scale mode (0 none, 1 per-tensor, 2 per-vector).  UB: block_size is a
 // multiple of 16, so the 16 positions of a tile share one block.
-template <int QT, int KVT, int D, int NT, int SM, bool UB>
+template <int QT, int KVT, int D, int NT, int SM, bool UB, bool CP>
 __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg, int kvh, int chunk,
                                             int part, int32_t* tbl_lds,
                                             UnitState<NT, D / 16>& st) {
@@ -754,6 +760,7 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
       }
       // ---- online softmax (log2 domain) and the P^T operand
       uint2 pop[NT];
+      uint2 plo[CP ? NT : 1];
       bool rescale = false;
       float corr[NT];
 #pragma unroll
@@ -790,6 +797,12 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
         }
         pop[nt].x = M::pack2(pr[0], pr[1]);
         pop[nt].y = M::pack2(pr[2], pr[3]);
+        if (CP) {
+          // what the cast dropped, as a second 16-bit operand (the reference's
+          // compensated dot, vllm_rlt/kernels/triton_attention.py:368-371)
+          plo[nt].x = M::pack2(pr[0] - M::lo_f32(pop[nt].x), pr[1] - M::hi_f32(pop[nt].x));
+          plo[nt].y = M::pack2(pr[2] - M::lo_f32(pop[nt].y), pr[3] - M::hi_f32(pop[nt].y));
+        }
       }
       // multiplying by exactly 1 changes no bit: skip the rescale when no row's
       // running max moved in this tile (wave-uniform vote)
@@ -808,6 +821,10 @@ __device__ __forceinline__ void attend_span(const AttnParams& P, int seq, int rg
         for (int nt = 0; nt < NT; ++nt) {
           oacc[nt][2 * K] = M::pv(a0, pop[nt], oacc[nt][2 * K]);
           oacc[nt][2 * K + 1] = M::pv(a1, pop[nt], oacc[nt][2 * K + 1]);
+          if (CP) {
+            oacc[nt][2 * K] = M::pv(a0, plo[nt], oacc[nt][2 * K]);
+            oacc[nt][2 * K + 1] = M::pv(a1, plo[nt], oacc[nt][2 * K + 1]);
+          }
         }
       });
     };
@@ -979,7 +996,7 @@ __device__ __forceinline__ void unit_of(const AttnParams& P, const int32_t* firs
 // dispatcher, and CUs end up with 1 to 8 of them).  kSlots units run at a time,
 // each on KS waves that split its positions and combine through LDS in a
 // fixed order, so a unit's arithmetic never depends on the assignment.
-template <int QT, int KVT, int D, int NT, int SM, bool UB>
+template <int QT, int KVT, int D, int NT, int SM, bool UB, bool CP>
 __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnParams P) {
   constexpr int ND = D / 16;
   constexpr int KS = unit_split<QT, KVT>();
@@ -1029,7 +1046,7 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
     int seq = 0, rg = 0, kvh = 0, chunk = 0;
     if (k < mine) {
       unit_of(P, sh.first, sh.c0, pairs, u, seq, rg, kvh, chunk);
-      attend_span<QT, KVT, D, NT, SM, UB>(P, seq, rg, kvh, chunk, part, sh.tbl[wave], st);
+      attend_span<QT, KVT, D, NT, SM, UB, CP>(P, seq, rg, kvh, chunk, part, sh.tbl[wave], st);
     } else {
       st.active = false;
     }
@@ -1047,7 +1064,7 @@ __global__ __launch_bounds__(64 * kPersistWaves) void rlt_attn_mfma_kernel(AttnP
 
 // Fallback for batches with more than kMaxPairs pairs: one KS-wave workgroup
 // per (sequence, row-group, kv head, chunk), the same per-unit arithmetic.
-template <int QT, int KVT, int D, int NT, int SM, bool UB>
+template <int QT, int KVT, int D, int NT, int SM, bool UB, bool CP>
 __global__ __launch_bounds__((64 * unit_split<QT, KVT>())) void rlt_attn_mfma_grid_kernel(AttnParams P) {
   constexpr int ND = D / 16;
   constexpr int KS = unit_split<QT, KVT>();
@@ -1057,7 +1074,7 @@ __global__ __launch_bounds__((64 * unit_split<QT, KVT>())) void rlt_attn_mfma_gr
   const int part = threadIdx.x >> 6;
   const WorkItem wi = work_item(P, blockIdx.x);
   UnitState<NT, ND> st;
-  attend_span<QT, KVT, D, NT, SM, UB>(P, wi.seq, wi.rg, wi.hg, wi.chunk, part, tbl[part], st);
+  attend_span<QT, KVT, D, NT, SM, UB, CP>(P, wi.seq, wi.rg, wi.hg, wi.chunk, part, tbl[part], st);
 #pragma unroll
   for (int h = KS / 2; h >= 1; h /= 2) {
     if (part >= h && part < 2 * h && st.active) publish_part(st, buf[part - h]);
@@ -1737,24 +1754,33 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
 
 // ============================================================ dispatch
 
-template <int QT, int KVT, int D, int SM, bool UB, int NT>
+template <int QT, int KVT, int D, int SM, bool UB, bool CP, int NT>
 void launch_mfma_nt(const AttnParams& P, dim3 grid, hipStream_t stream) {
-  if (P.persistent) rlt_attn_mfma_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * kPersistWaves, 0, stream>>>(P);
-  else rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB><<<grid, 64 * unit_split<QT, KVT>(), 0, stream>>>(P);
+  if (P.persistent)
+    rlt_attn_mfma_kernel<QT, KVT, D, NT, SM, UB, CP><<<grid, 64 * kPersistWaves, 0, stream>>>(P);
+  else
+    rlt_attn_mfma_grid_kernel<QT, KVT, D, NT, SM, UB, CP><<<grid, 64 * unit_split<QT, KVT>(), 0, stream>>>(P);
 }
 
-template <int QT, int KVT, int D, int SM, bool UB>
+template <int QT, int KVT, int D, int SM, bool UB, bool CP>
 int launch_mfma_ub(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
-  if (nt == 1) launch_mfma_nt<QT, KVT, D, SM, UB, 1>(P, grid, stream);
-  else if (D <= 128) launch_mfma_nt<QT, KVT, D, SM, UB, (D <= 128 ? 2 : 1)>(P, grid, stream);
+  if (nt == 1) launch_mfma_nt<QT, KVT, D, SM, UB, CP, 1>(P, grid, stream);
+  else if (D <= 128) launch_mfma_nt<QT, KVT, D, SM, UB, CP, (D <= 128 ? 2 : 1)>(P, grid, stream);
   else return RLT_ERR_UNSUPPORTED;
   return RLT_OK;
 }
 
+// Compensated P V is built for blocks holding whole 16-position tiles (the reference
+// pools' block size 16 and its multiples).
 template <int QT, int KVT, int D, int SM>
 int launch_mfma_sm(const AttnParams& P, dim3 grid, int nt, hipStream_t stream) {
-  if (P.block_size % kTileTok == 0) return launch_mfma_ub<QT, KVT, D, SM, true>(P, grid, nt, stream);
-  return launch_mfma_ub<QT, KVT, D, SM, false>(P, grid, nt, stream);
+  const bool ub = P.block_size % kTileTok == 0;
+  if (P.compensate) {
+    if (!ub) return RLT_ERR_UNSUPPORTED;
+    return launch_mfma_ub<QT, KVT, D, SM, true, true>(P, grid, nt, stream);
+  }
+  if (ub) return launch_mfma_ub<QT, KVT, D, SM, true, false>(P, grid, nt, stream);
+  return launch_mfma_ub<QT, KVT, D, SM, false, false>(P, grid, nt, stream);
 }
 
 template <int QT, int KVT, int D>
@@ -1878,7 +1904,7 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                              int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
                              int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
                              int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
-                             int32_t window, void* out, int64_t out_row_stride,
+                             int32_t window, int32_t flags, void* out, int64_t out_row_stride,
                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
                              hipStream_t stream, const WindowStore* store) {
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return RLT_ERR_ARGUMENT;
@@ -1888,6 +1914,7 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
     return RLT_ERR_ARGUMENT;
   if (kv_dtype == RLT_FP8_E4M3 && scale_mode == 0) return RLT_ERR_ARGUMENT;
   if (q_dtype == RLT_FP8_E4M3) return RLT_ERR_ARGUMENT;
+  if (flags & ~RLT_ATTN_COMPENSATE) return RLT_ERR_ARGUMENT;
   if (num_blocks <= 0) return RLT_ERR_ARGUMENT;
   if (num_q_rows == 0 || num_seqs == 0) return RLT_OK;
   if (!cu_seqlens_q && num_seqs != num_q_rows) return RLT_ERR_ARGUMENT;
@@ -1922,6 +1949,7 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   P.s_token_stride = s_token_stride;
   P.s_head_stride = s_head_stride;
   P.scale_mode = scale_mode;
+  P.compensate = (flags & RLT_ATTN_COMPENSATE) ? 1 : 0;
   P.num_seqs = num_seqs;
   P.num_rows = num_q_rows;
   P.hq = num_q_heads;
@@ -1982,7 +2010,8 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
         (k_head_stride * kv_elt) % kv_align == 0 && (v_block_stride * kv_elt) % kv_align == 0 &&
         (v_token_stride * kv_elt) % kv_align == 0 && (v_head_stride * kv_elt) % kv_align == 0;
     if (!aligned) return RLT_ERR_ARGUMENT;
-    if (cu_seqlens_q && !row_lengths &&
+    // (compensated calls stay on the verify kernels at every q_len)
+    if (cu_seqlens_q && !row_lengths && !P.compensate &&
         rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len)) {
       // long q windows: the prefill tiling, normalized in one launch
       P.rows_per_rg = kPfRows;
@@ -2056,7 +2085,7 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
                              int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride,
                              int64_t s_head_stride, int32_t num_q_heads, int32_t num_kv_heads,
                              int32_t head_dim, int32_t block_size, int32_t q_dtype, int32_t kv_dtype,
-                             int32_t window, void* out, int64_t out_row_stride,
+                             int32_t window, int32_t flags, void* out, int64_t out_row_stride,
                              int64_t out_head_stride, void* workspace, size_t workspace_bytes,
                              hipStream_t stream) {
   return attention_impl(q, q_row_stride, q_head_stride, key_cache, value_cache, k_block_stride,
@@ -2065,7 +2094,7 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
                         context_lengths, row_lengths, cu_seqlens_q, num_seqs, max_q_len,
                         num_q_rows, key_scale, value_scale, scale_mode, s_block_stride,
                         s_token_stride, s_head_stride, num_q_heads, num_kv_heads, head_dim,
-                        block_size, q_dtype, kv_dtype, window, out, out_row_stride,
+                        block_size, q_dtype, kv_dtype, window, flags, out, out_row_stride,
                         out_head_stride, workspace, workspace_bytes, stream, nullptr);
 }
 
@@ -2088,7 +2117,7 @@ int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_hea
                         v_head_stride, num_blocks, block_tables, table_stride, table_width,
                         context_lengths, nullptr, cu_seqlens_q, num_seqs, max_q_len, num_q_rows,
                         nullptr, nullptr, 0, 0, 0, 0, num_q_heads, num_kv_heads, head_dim,
-                        block_size, dtype, dtype, 0, out, out_row_stride, out_head_stride,
+                        block_size, dtype, dtype, 0, 0, out, out_row_stride, out_head_stride,
                         workspace, workspace_bytes, stream, &st);
 }
 
@@ -2101,7 +2130,7 @@ int rlt_paged_attention_store_scaled(
     int32_t num_seqs, int32_t max_q_len, int32_t num_q_rows, float* key_scale, float* value_scale,
     int32_t scale_mode, int64_t s_block_stride, int64_t s_token_stride, int64_t s_head_stride,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-    int32_t q_dtype, int32_t kv_dtype, const void* new_k, const void* new_v,
+    int32_t q_dtype, int32_t kv_dtype, int32_t flags, const void* new_k, const void* new_v,
     int64_t new_row_stride, int64_t new_head_stride, void* out, int64_t out_row_stride,
     int64_t out_head_stride, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const WindowStore st{new_k, new_v, new_row_stride, new_head_stride};
@@ -2111,8 +2140,8 @@ int rlt_paged_attention_store_scaled(
                         context_lengths, row_lengths, cu_seqlens_q, num_seqs, max_q_len,
                         num_q_rows, key_scale, value_scale, scale_mode, s_block_stride,
                         s_token_stride, s_head_stride, num_q_heads, num_kv_heads, head_dim,
-                        block_size, q_dtype, kv_dtype, 0, out, out_row_stride, out_head_stride,
-                        workspace, workspace_bytes, stream, &st);
+                        block_size, q_dtype, kv_dtype, 0, flags, out, out_row_stride,
+                        out_head_stride, workspace, workspace_bytes, stream, &st);
 }
 
 int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -2133,7 +2162,7 @@ int rlt_paged_attention(const void* q, int64_t q_row_stride, int64_t q_head_stri
       k_head_stride, v_block_stride, v_token_stride, v_head_stride, num_blocks, block_tables,
       table_stride, table_width, context_lengths, nullptr, cu_seqlens_q, num_seqs, max_q_len,
       num_q_rows, key_scale, value_scale, scale_mode, s_block_stride, s_token_stride,
-      s_head_stride, num_q_heads, num_kv_heads, head_dim, block_size, q_dtype, kv_dtype, window,
+      s_head_stride, num_q_heads, num_kv_heads, head_dim, block_size, q_dtype, kv_dtype, window, 0,
       out, out_row_stride, out_head_stride, workspace, workspace_bytes, stream);
 }
 

@@ -109,7 +109,7 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
                        const Tensor& block_tables, const Tensor& context_lengths,
                        const OptTensor& key_scale, const OptTensor& value_scale,
                        const OptTensor& cu_seqlens_q, int64_t max_seqlen_q, int64_t window,
-                       const OptTensor& row_lengths) {
+                       const OptTensor& row_lengths, bool compensate) {
   TORCH_CHECK_VALUE(window >= 0, "window must be a nonnegative integer");
   TORCH_CHECK_VALUE(q.dim() == 3 && key_cache.dim() == 4 && value_cache.dim() == 4,
                     "q must be [rows, heads, dim] and caches [block, token, kv_head, dim]");
@@ -122,6 +122,8 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
                     "key and value caches must share shape and dtype");
   const int64_t num_blocks = key_cache.size(0), block_size = key_cache.size(1);
   const int64_t kv_heads = key_cache.size(2);
+  TORCH_CHECK_VALUE(!compensate || block_size % 16 == 0,
+                    "compensated attention needs a block size that is a multiple of 16");
   TORCH_CHECK_VALUE(key_cache.size(3) == head_dim && q.size(1) % kv_heads == 0,
                     "q heads must be a positive multiple of KV heads with equal head_dim");
   TORCH_CHECK_VALUE(key_cache.stride(3) == 1 && value_cache.stride(3) == 1,
@@ -190,8 +192,8 @@ Tensor paged_attention(const Tensor& q, const Tensor& key_cache, const Tensor& v
       (const float*)ptr(key_scale), (const float*)ptr(value_scale), mode, s_strides[0],
       s_strides[1], s_strides[2], (int32_t)heads, (int32_t)kv_heads, (int32_t)head_dim,
       (int32_t)block_size, dtype_code(q.scalar_type()), dtype_code(key_cache.scalar_type()),
-      (int32_t)window, ptr(output), output.stride(0), output.stride(1), ptr(ws), ws.numel(),
-      stream_of(q));
+      (int32_t)window, compensate ? RLT_ATTN_COMPENSATE : 0, ptr(output), output.stride(0),
+      output.stride(1), ptr(ws), ws.numel(), stream_of(q));
   check_status(status, "rlt_paged_attention");
   return output;
 }
@@ -490,7 +492,7 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
                              const Tensor& block_tables, const Tensor& context_lengths,
                              const Tensor& cu_seqlens_q, int64_t max_seqlen_q,
                              const OptTensor& key_scale, const OptTensor& value_scale,
-                             const OptTensor& row_lengths) {
+                             const OptTensor& row_lengths, bool compensate) {
   TORCH_CHECK_VALUE(q.dim() == 3, "q must be [rows, heads, dim]");
   check_view(key_cache, "key_cache");
   check_view(value_cache, "value_cache");
@@ -581,7 +583,8 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
         (const int32_t*)ptr(row_lengths), (const int32_t*)ptr(cu_seqlens_q), (int32_t)num_seqs,
         (int32_t)max_seqlen_q, (int32_t)rows, (float*)ptr(key_scale), (float*)ptr(value_scale),
         mode, s_strides[0], s_strides[1], s_strides[2], (int32_t)heads, (int32_t)kv_heads,
-        (int32_t)head_dim, (int32_t)key_cache.size(1), qd, kvd, ptr(k_new), ptr(v_new),
+        (int32_t)head_dim, (int32_t)key_cache.size(1), qd, kvd,
+        compensate ? RLT_ATTN_COMPENSATE : 0, ptr(k_new), ptr(v_new),
         k_new.stride(0), k_new.stride(1), ptr(output), output.stride(0), output.stride(1), ptr(ws),
         ws.numel(), stream_of(q));
     if (status != 2 || fp8) {  // 2: a 16-bit shape the one-launch form does not serve
@@ -614,7 +617,7 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
              std::nullopt);
   }
   return paged_attention(q, key_cache, value_cache, block_tables, context_lengths, std::nullopt,
-                         std::nullopt, cu_seqlens_q, max_seqlen_q, 0, row_lengths);
+                         std::nullopt, cu_seqlens_q, max_seqlen_q, 0, row_lengths, compensate);
 }
 
 }  // namespace
@@ -622,7 +625,7 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
 TORCH_LIBRARY(rlt_mi355x, m) {
   m.def("paged_attention(Tensor q, Tensor key_cache, Tensor value_cache, Tensor block_tables, "
         "Tensor context_lengths, Tensor? key_scale, Tensor? value_scale, Tensor? cu_seqlens_q, "
-        "int max_seqlen_q, int window, Tensor? row_lengths=None) -> Tensor");
+        "int max_seqlen_q, int window, Tensor? row_lengths=None, bool compensate=False) -> Tensor");
   m.def("store_kv(Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor k, Tensor v, "
         "Tensor blocks, Tensor offsets, Tensor? mask, Tensor? active) -> ()");
   m.def("spec_probs(Tensor logits, Tensor temperature, Tensor top_k, Tensor top_p, "
@@ -640,7 +643,7 @@ TORCH_LIBRARY(rlt_mi355x, m) {
   m.def("paged_attention_store(Tensor q, Tensor k_new, Tensor v_new, Tensor(a!) key_cache, "
         "Tensor(b!) value_cache, Tensor block_tables, Tensor context_lengths, "
         "Tensor cu_seqlens_q, int max_seqlen_q, Tensor(c!)? key_scale=None, "
-        "Tensor(d!)? value_scale=None, Tensor? row_lengths=None) -> Tensor");
+        "Tensor(d!)? value_scale=None, Tensor? row_lengths=None, bool compensate=False) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(rlt_mi355x, CUDA, m) {

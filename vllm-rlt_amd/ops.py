@@ -28,13 +28,13 @@ _lib.ops()  # registers the C++ operators (raises if _C.so is missing)
 
 @torch.library.register_fake("rlt_mi355x::paged_attention")
 def _(q, key_cache, value_cache, block_tables, context_lengths, key_scale, value_scale,
-      cu_seqlens_q, max_seqlen_q, window, row_lengths=None):
+      cu_seqlens_q, max_seqlen_q, window, row_lengths=None, compensate=False):
     return torch.empty_like(q)
 
 
 @torch.library.register_fake("rlt_mi355x::paged_attention_store")
 def _(q, k_new, v_new, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-      max_seqlen_q, key_scale=None, value_scale=None, row_lengths=None):
+      max_seqlen_q, key_scale=None, value_scale=None, row_lengths=None, compensate=False):
     return torch.empty_like(q)
 
 
