@@ -27,6 +27,7 @@ stream) and ``cpu_baseline`` (the torch-CPU oracle on this host).
 """
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -122,15 +123,31 @@ def accept_bytes(w):
     return 4 * n * (k + 1) * v + 4 * n * k * v + 4 * n * (2 * k + 1) + 8 * n * (k + 1) + 8 * n * 3 + 8 * n * k
 
 
+def kernel_source_digest():
+    """First 16 hex digits of a sha256 over the library's HIP sources and headers (names
+    and contents, sorted by name): identifies the build a counter measurement is of."""
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "vllm-rlt_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
     """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (calibrated against a 1 GiB copy), or None."""
+    WRITE_SIZE passes (calibrated against a 1 GiB copy), and whether they were measured
+    on the kernel sources of this tree: (bytes or None, record)."""
     path = os.path.join(ROOT, "profiles", "verify_step_config3_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)["attention_launch_bytes"]
-    except (OSError, KeyError, ValueError):
-        return None
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None, {}
+    same = rec.get("kernel_source_digest") == kernel_source_digest()
+    return (rec.get("attention_launch_bytes") if same else None), rec
 
 
 def config2_decode(pkg, dev):
@@ -777,6 +794,7 @@ def main():
     kv_bytes = kv_write_bytes(w)
     achieved = a_bytes / t_attn / 1e9
     tokens = w["n"] * w["window"]
+    traffic, traffic_rec = measured_traffic()
     result = {
         "metric": METRIC,
         "value": round(tokens / step_s, 1),
@@ -816,8 +834,12 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(),
-            "traffic_source": "profiles/verify_step_config3_hbm_traffic.md (bytes per launch)",
+            "traffic": traffic,
+            "traffic_source": ("profiles/verify_step_config3_hbm_traffic.md (bytes per launch, "
+                               f"measured at commit {traffic_rec.get('measured_at_commit')}, kernel "
+                               f"sources {traffic_rec.get('kernel_source_digest')}: "
+                               + ("this build's)" if traffic is not None else
+                                  "not this build's, so not reported)")),
             "algorithmic_bytes": a_bytes,
         },
     }
