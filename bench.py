@@ -490,8 +490,8 @@ def prefill_steps(pkg, dev):
                            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
                            "graph_replays_equal_eager": same}
         del kc, vc, q
-    # shapes the prefill tiling does not take (fp8 pools, head_dim 96): the verify kernel's
-    # packed form at prompt length
+    # fp8 pools (the verify kernel's packed form at prompt length) and head_dim 96 (the
+    # prefill tiling on 128-dim LDS rows)
     n, L = 8, 2048
     per = L // bs
     tables = torch.randperm(n * per, generator=g).int().view(n, per).to(dev)
@@ -514,11 +514,13 @@ def prefill_steps(pkg, dev):
         tf = flops / t / 1e12
         out[name] = {"us": round(t * 1e6, 1), "tflops": round(tf, 1),
                      "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "path": "verify kernel, packed form", "graph_replays_equal_eager": same}
+                     "path": ("prefill tiling" if kern.uses_prefill_tiling(
+                         torch.bfloat16, kv_dtype, dd, L) else "verify kernel, packed form"),
+                     "graph_replays_equal_eager": same}
         del kc, vc, q
     return {"workload": "packed causal prefill, bf16, 16 q / 4 kv heads, D=128, block 16 (the "
-                        "prefill tiling); fp8-e4m3 (per-tensor scales) and D=96 prompts run the "
-                        "verify kernel's packed form",
+                        "prefill tiling); fp8-e4m3 (per-tensor scales) and D=96 prompts as "
+                        "labelled by each entry's path",
             "flops_per_launch": "4 * Hq * D * sum L(L+1)/2", "launches": out}
 
 

@@ -52,7 +52,8 @@ def test_workspace_queries_are_host_only(pkg):
     assert lib.rlt_paged_attention_uses_prefill(2, 2, 128, 64) == 1
     assert lib.rlt_paged_attention_uses_prefill(2, 2, 128, 33) == 0  # verify windows
     assert lib.rlt_paged_attention_uses_prefill(2, 3, 128, 512) == 0  # fp8 pools
-    assert lib.rlt_paged_attention_uses_prefill(2, 2, 96, 512) == 0
+    assert lib.rlt_paged_attention_uses_prefill(2, 2, 96, 512) == 1  # padded LDS rows
+    assert lib.rlt_paged_attention_uses_prefill(2, 2, 256, 512) == 0
 
 
 def test_argument_errors_return_status_without_launching(pkg):

@@ -434,12 +434,15 @@ def test_long_prompt_prefill_fp8_matches_dense_causal(kernel, dev, per_vector, q
                                                (48, 0, torch.bfloat16, 128),
                                                (32, 100, torch.bfloat16, 128),
                                                (8, 0, torch.float16, 64),
-                                               (32, 300, torch.float16, 64)])
+                                               (32, 300, torch.float16, 64),
+                                               (8, 0, torch.bfloat16, 96),
+                                               (32, 100, torch.float16, 96)])
 def test_long_prompt_prefill_block_sizes(kernel, dev, bs, window, dtype, d):
     """The prefill tiling's two address paths: blocks holding whole 16-position groups
     (one table lookup per group, 32 and 48 here) and smaller blocks (a lookup per
     position, 8 here), with and without a sliding window, at head_dim 128 and 64 (the
-    direct loads fill 4 and 8 rows per instruction)."""
+    direct loads fill 4 and 8 rows per instruction) and 96 (128-dim LDS rows whose pad
+    slots no lane loads)."""
     _say("long prefill block size", bs, window, dtype, d)
     g = torch.Generator().manual_seed(22)
     hq, hkv = 16, 4

@@ -1457,9 +1457,14 @@ constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfMinQ = 64;     // q window length from which a call takes this path
 constexpr float kPfLazy = 8.f;  // log2 headroom before the running max moves
 
+// LDS row width in dims: D = 96 rows take a 128-dim row whose last four 16-byte slots
+// (their place moves with the swizzle) are never loaded nor read
+template <int D>
+constexpr int pf_row_dims() { return D == 96 ? 128 : D; }
+
 template <int D>
 struct PrefillLds {
-  static constexpr int kRowB = D * 2;  // bytes per position row (no padding: XOR-swizzled slots)
+  static constexpr int kRowB = pf_row_dims<D>() * 2;  // bytes per position row (XOR-swizzled slots)
   uint8_t k[2][kPfKeys * kRowB];
   uint8_t v[2][kPfKeys * kRowB];
 };
@@ -1471,7 +1476,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // slot with r mod SLOTS, so the S^T operand reads (16 lanes = 16 rows of one piece
 // column) meet distinct bank groups; V rows XOR it with 2 (r & 3), which keeps each piece
 // pair adjacent for the transpose reads (16 lanes = 4 rows x one 32-byte pair) and puts
-// the four rows on distinct bank groups, and with 8 in rows with bit 2 set (D = 128), so
+// the four rows on distinct bank groups, and with 8 in rows with bit 2 set (16 slots), so
 // the next 16 lanes (rows 4 further on) use the other half of the banks.
 template <int SLOTS>
 __device__ __forceinline__ int k_slot(int r, int piece) { return piece ^ (r & (SLOTS - 1)); }
@@ -1489,7 +1494,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
   constexpr int NT = kPfNT;
   constexpr int NQS = D / 32;       // 32-wide contraction slices of S^T
   constexpr int ND = D / 16;        // 16-wide dim tiles of O^T
-  constexpr int SLOTS = D / 8;      // 16-byte pieces per position row
+  constexpr int PIECES = D / 8;     // 16-byte pieces of a position row in the pool
+  constexpr int SLOTS = pf_row_dims<D>() / 8;  // 16-byte slots per LDS row (>= PIECES)
   constexpr int ROWS_PER_LD = 64 / SLOTS;                // rows one wave-wide direct load fills
   constexpr int LDS_PER_WAVE = kPfKeys / ROWS_PER_LD / kPfWaves;  // direct loads per wave per tile (K, V each)
   static_assert(LDS_PER_WAVE * ROWS_PER_LD * kPfWaves == kPfKeys, "the waves' loads cover a tile");
@@ -1583,12 +1589,18 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
       } else {
         block_of(base + r, blk, off);
       }
+      // (the slot of lane ld_slot holds piece k_slot / v_slot of row r: an involution)
+      const int kpc = k_slot<SLOTS>(r, ld_slot);
+      const int vpc = v_slot<SLOTS>(r, ld_slot);
       const uint16_t* kp = (const uint16_t*)P.k + blk * P.k_block_stride +
-                           (int64_t)off * P.k_token_stride + k_head + k_slot<SLOTS>(r, ld_slot) * 8;
+                           (int64_t)off * P.k_token_stride + k_head + kpc * 8;
       const uint16_t* vp = (const uint16_t*)P.v + blk * P.v_block_stride +
-                           (int64_t)off * P.v_token_stride + v_head + v_slot<SLOTS>(r, ld_slot) * 8;
-      __builtin_amdgcn_global_load_lds((const void*)kp, (lds_void*)(sh.k[b] + r0 * L::kRowB), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)vp, (lds_void*)(sh.v[b] + r0 * L::kRowB), 16, 0, 0);
+                           (int64_t)off * P.v_token_stride + v_head + vpc * 8;
+      // padded rows: lanes whose slot holds a piece past the row load nothing
+      if (PIECES == SLOTS || kpc < PIECES)
+        __builtin_amdgcn_global_load_lds((const void*)kp, (lds_void*)(sh.k[b] + r0 * L::kRowB), 16, 0, 0);
+      if (PIECES == SLOTS || vpc < PIECES)
+        __builtin_amdgcn_global_load_lds((const void*)vp, (lds_void*)(sh.v[b] + r0 * L::kRowB), 16, 0, 0);
     }
   };
   // After this wave's loads of tile `tile` into buffer b landed: its V rows past the
@@ -1612,8 +1624,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
   // V^T operand reads (transpose loads): lane (l16, grp) of the 16-lane group grp reads
   // row 32 c + 4 grp + (l16 >> 2) (+16 for the second half) at dims 16 dt + 4 (l16 & 3),
   // piece 2 dt + ((l16 >> 1) & 1) -> slot 2 (dt ^ m) + ((l16 >> 1) & 1), m = (l16 >> 2) & 3
-  // (^ 4 for odd grp when D = 128: the slot's bit-3 flip)
-  const int vm = ((l16 >> 2) & 3) ^ (ND >= 8 ? 4 * (grp & 1) : 0);
+  // (^ 4 for odd grp when rows have 16 slots: the slot's bit-3 flip)
+  const int vm = ((l16 >> 2) & 3) ^ (SLOTS >= 16 ? 4 * (grp & 1) : 0);
   const int v_lane = (4 * grp + (l16 >> 2)) * L::kRowB + ((l16 >> 1) & 1) * 16 + (l16 & 1) * 8;
 
   const float qk_scale = P.qk_scale_log2;
@@ -1828,6 +1840,7 @@ void launch_prefill_d(const AttnParams& P, dim3 grid, hipStream_t stream) {
 template <int QT>
 void launch_prefill(const AttnParams& P, int head_dim, dim3 grid, hipStream_t stream) {
   if (head_dim == 64) launch_prefill_d<QT, 64>(P, grid, stream);
+  else if (head_dim == 96) launch_prefill_d<QT, 96>(P, grid, stream);
   else launch_prefill_d<QT, 128>(P, grid, stream);
 }
 
@@ -1874,7 +1887,7 @@ int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t hea
 int rlt_paged_attention_uses_prefill(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim,
                                      int32_t max_q_len) {
   return rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) && kv_dtype == q_dtype &&
-         (head_dim == 64 || head_dim == 128) && max_q_len >= kPfMinQ;
+         (head_dim == 64 || head_dim == 96 || head_dim == 128) && max_q_len >= kPfMinQ;
 }
 
 size_t rlt_paged_attention_workspace_size(int32_t num_q_rows, int32_t num_q_heads, int32_t head_dim,
