@@ -130,8 +130,9 @@ int rlt_paged_attention_rows(const void* q, int64_t q_row_stride, int64_t q_head
  * (vllm_rlt/kernels/graph_kv.py:52-67, the KV scatter of the window rows) followed by
  * the packed attention call (vllm_rlt/kernels/triton_attention.py:386-404), in one
  * launch pair: the attention waves that read a window position store it before
- * reading.  bf16 / fp16 q and pool of one dtype, windows shorter than the prefill
- * tiling's threshold (rlt_paged_attention_uses_prefill == 0); other shapes return
+ * reading.  Windows that take the prefill tiling (rlt_paged_attention_uses_prefill)
+ * run a window-store kernel, then the tiling, on the stream.  bf16 / fp16 q and pool
+ * of one dtype with a head_dim the MFMA kernels serve; other shapes return
  * RLT_ERR_UNSUPPORTED (the caller then stores and attends separately).  Table entries
  * outside [0, num_blocks) are not written.  Workspace: rlt_paged_attention_workspace_size.
  */
@@ -166,8 +167,9 @@ int rlt_paged_attention_store(const void* q, int64_t q_row_stride, int64_t q_hea
  *     rlt_paged_attention_rows) instead of context_lengths[s] - q_len_s + i.
  * Pool strides must be multiples of 16 bytes (16-bit pools) or 8 bytes (fp8).
  * Positions whose block index lies beyond the table, or whose table entry lies
- * outside the pool, are not written.  Windows that reach the prefill tiling, and
- * float32 q, return RLT_ERR_UNSUPPORTED.  flags: RLT_ATTN_COMPENSATE or 0.
+ * outside the pool, are not written.  Windows that take the prefill tiling store first,
+ * then attend (two launches); float32 q returns RLT_ERR_UNSUPPORTED.  flags:
+ * RLT_ATTN_COMPENSATE or 0.
  * Workspace: rlt_paged_attention_workspace_size.
  */
 int rlt_paged_attention_store_scaled(
@@ -187,7 +189,8 @@ int rlt_paged_attention_store_scaled(
 int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim);
 
 /* 1 when a packed call with this longest q window takes the long-prompt prefill
- * tiling (bf16 / fp16 q with KV of the same type, head_dim 64 or 128, max_q_len >= 64):
+ * tiling (bf16 / fp16 q with KV of the same type or fp8-e4m3, head_dim 64, 96 or 128,
+ * max_q_len >= 64; calls with row_lengths or RLT_ATTN_COMPENSATE never take it):
  * 128-row groups, K / V tiles shared through LDS, normalized in one launch.  Rows of
  * such a call match the per-row form within floating-point tolerance; every other
  * call (all verify windows) equals the per-row form bit for bit.  The reference's

@@ -51,7 +51,7 @@ def test_workspace_queries_are_host_only(pkg):
     assert lib.rlt_paged_attention_uses_mfma(2, 2, 7) == 0
     assert lib.rlt_paged_attention_uses_prefill(2, 2, 128, 64) == 1
     assert lib.rlt_paged_attention_uses_prefill(2, 2, 128, 33) == 0  # verify windows
-    assert lib.rlt_paged_attention_uses_prefill(2, 3, 128, 512) == 0  # fp8 pools
+    assert lib.rlt_paged_attention_uses_prefill(2, 3, 128, 512) == 1  # fp8 pools
     assert lib.rlt_paged_attention_uses_prefill(2, 2, 96, 512) == 1  # padded LDS rows
     assert lib.rlt_paged_attention_uses_prefill(2, 2, 256, 512) == 0
 
@@ -246,7 +246,7 @@ def test_verify_accept_checks_arguments(pkg):
 
 
 def test_attention_with_window_store_checks_arguments(pkg):
-    """rlt_paged_attention_store serves packed bf16 / fp16 verify windows only: other forms
+    """rlt_paged_attention_store serves packed bf16 / fp16 windows only: other forms
     return RLT_ERR_UNSUPPORTED (2) and a missing or misaligned window buffer
     RLT_ERR_ARGUMENT (1), before anything is launched."""
     from vllm_rlt_amd import _lib
@@ -264,7 +264,7 @@ def test_attention_with_window_store_checks_arguments(pkg):
 
     assert call(cu=null, seqs=10) == 2  # per-row form: no window to store
     assert call(dtype=0) == 2          # float32 q and pool
-    assert call(max_q=64) == 2         # prefill-length window (the prefill tiling)
     assert call(new_k=null) == 1       # no rows to store
+    assert call(max_q=64, new_k=null) == 1  # prefill-length windows (store kernel + tiling) too
     assert call(new_v=fake + 2) == 1   # misaligned rows
     assert call(row_stride=hkv * d + 1) == 1

@@ -388,18 +388,19 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
 
 
 @pytest.mark.parametrize("per_vector", [False, True])
-@pytest.mark.parametrize("q_dtype,d,hq,hkv", [(torch.bfloat16, 128, 16, 8),
-                                              (torch.float16, 96, 8, 2)])
+@pytest.mark.parametrize("q_dtype,d,hq,hkv,bs", [(torch.bfloat16, 128, 16, 8, 16),
+                                                 (torch.float16, 96, 8, 2, 16),
+                                                 (torch.bfloat16, 64, 8, 8, 8)])
 def test_long_prompt_prefill_fp8_matches_dense_causal(kernel, dev, per_vector, q_dtype, d, hq,
-                                                      hkv):
+                                                      hkv, bs):
     """Prompt prefill over an FP8 pool (reference: triton_attention.py:335-362,460-487,
     the packed kernel's HAS_SCALE loads): long prompts, a chunk after a prefix and ragged
     windows against dense causal SDPA over the dequantized keys and values, with
-    per-tensor or per-vector scales.  FP8 pools run the verify kernel's packed form at
-    any q_len (the prefill tiling reads 16-bit pools only)."""
-    _say("long prefill fp8", per_vector, q_dtype, d)
+    per-tensor or per-vector scales.  These windows take the prefill tiling (fp8 tiles
+    widened to q's type in LDS, head_dim 96 on 128-dim LDS rows)."""
+    _say("long prefill fp8", per_vector, q_dtype, d, bs)
     g = torch.Generator().manual_seed(23 + d)
-    bs = 16
+    assert kernel.uses_prefill_tiling(q_dtype, torch.float8_e4m3fn, d, 1024)
     seqs = [(1024, 1024), (2048, 512), (3000, 37), (300, 97), (129, 129)]
     pages = sum(-(-n // bs) for n, _ in seqs) + 2
     x_k = torch.randn(pages, bs, hkv, d, generator=g) * 3
@@ -767,19 +768,22 @@ def _fp8_store_case(g, n, w, hq, hkv, d, bs, lengths, pool_blocks, per_vector, q
     return kc, vc, ks, vs, tables, q, k_new, v_new
 
 
+@pytest.mark.parametrize("w", [5, 70])
 @pytest.mark.parametrize("per_vector", [False, True])
 @pytest.mark.parametrize("q_dtype,d,hq,hkv", [(torch.bfloat16, 128, 16, 8),
                                               (torch.float16, 96, 4, 2)])
 def test_fp8_prefill_store_equals_store_fp8_then_prefill(kernel, pkg, dev, per_vector, q_dtype, d,
-                                                         hq, hkv):
-    """The FP8 window store fused with the attention launch writes the codes (and, with
-    per-vector scales, the scales) that store_fp8 writes -- bitwise the reference's
-    quantize_fp8 -- and returns the attention of prefill over that pool, bit for bit.
-    Per-tensor scales are read, never written."""
-    _say("fp8 prefill_store", per_vector, q_dtype, d)
-    g = torch.Generator().manual_seed(d + hq + per_vector)
-    bs, w = 16, 5
-    lengths = [5, 300, 1030, 1500, 2049]
+                                                         hq, hkv, w):
+    """The FP8 window store fused with the attention launch (a 5-row window; a 70-row one
+    stores with the window-store kernel ahead of the prefill tiling) writes the codes
+    (and, with per-vector scales, the scales) that store_fp8 writes -- bitwise the
+    reference's quantize_fp8 -- and returns the attention of prefill over that pool, bit
+    for bit.  Per-tensor scales are read, never written."""
+    _say("fp8 prefill_store", per_vector, q_dtype, d, w)
+    g = torch.Generator().manual_seed(d + hq + per_vector + w)
+    bs = 16
+    assert kernel.uses_prefill_tiling(q_dtype, torch.float8_e4m3fn, d, w) == (w >= 64)
+    lengths = [w, 300, 1030, 1500, 2049]
     n = len(lengths)
     pages = sum(-(-x // bs) for x in lengths) + 5
     kc, vc, ks, vs, tables, q, k_new, v_new = _fp8_store_case(

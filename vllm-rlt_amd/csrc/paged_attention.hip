@@ -44,6 +44,7 @@
 #include "fp8_codec.h"
 #include "rlt_mi355x.h"
 
+#include <climits>
 #include <math.h>
 
 #include <type_traits>
@@ -476,16 +477,14 @@ struct UnitState {
 // rlt_fp8::encode with the per-tensor scale (SM 1) or with a per-vector scale stored
 // into the scale pool (SM 2), bitwise the scatter kernel's quantize-store, one row per
 // wave (lanes 0-31 key, 32-63 value).  Returns whether this wave stored anything.
+// The stores of window rows [i_lo, i_hi) whose positions lie in [p0, p1), on one wave;
+// whether this lane stored anything.
 template <int QT, int KVT, int D, int SM>
-__device__ __forceinline__ bool store_window(const AttnParams& P, int seq, int kvh,
-                                             const SeqView& sv, int p0, int p1) {
+__device__ __forceinline__ bool store_rows(const AttnParams& P, int seq, int kvh,
+                                           const SeqView& sv, int i_lo, int i_hi, int p0, int p1) {
   const int lane = threadIdx.x & 63;
   const int piece = lane & 31;
   const int base_pos = sv.kv_len - sv.q_len;  // position of window row 0 (causal form)
-  // rows to visit: every row with explicit row lengths (any order), else the range
-  // whose positions meet [p0, p1)
-  const int i_lo = P.row_len ? 0 : max(0, p0 - base_pos);
-  const int i_hi = P.row_len ? sv.q_len : min(sv.q_len, p1 - base_pos);
   auto position = [&](int i) { return P.row_len ? P.row_len[sv.q_begin + i] - 1 : base_pos + i; };
   auto block = [&](int pos) {
     const int idx = pos / P.block_size;
@@ -564,7 +563,18 @@ __device__ __forceinline__ bool store_window(const AttnParams& P, int seq, int k
       stored = true;
     }
   }
-  return __builtin_amdgcn_ballot_w64(stored) != 0;
+  return stored;
+}
+
+template <int QT, int KVT, int D, int SM>
+__device__ __forceinline__ bool store_window(const AttnParams& P, int seq, int kvh,
+                                             const SeqView& sv, int p0, int p1) {
+  const int base_pos = sv.kv_len - sv.q_len;
+  // rows to visit: every row with explicit row lengths (any order), else the range
+  // whose positions meet [p0, p1)
+  const int i_lo = P.row_len ? 0 : max(0, p0 - base_pos);
+  const int i_hi = P.row_len ? sv.q_len : min(sv.q_len, p1 - base_pos);
+  return __builtin_amdgcn_ballot_w64(store_rows<QT, KVT, D, SM>(P, seq, kvh, sv, i_lo, i_hi, p0, p1)) != 0;
 }
 
 // Part `part` (of KS = unit_split equal spans) of one work unit -- (sequence,
@@ -1467,6 +1477,8 @@ struct PrefillLds {
   static constexpr int kRowB = pf_row_dims<D>() * 2;  // bytes per position row (XOR-swizzled slots)
   uint8_t k[2][kPfKeys * kRowB];
   uint8_t v[2][kPfKeys * kRowB];
+  float ks[2][kPfKeys];  // per-vector fp8 scales of the tile's positions (SM 2)
+  float vs[2][kPfKeys];
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -1486,8 +1498,14 @@ __device__ __forceinline__ int v_slot(int r, int piece) {
 }
 
 // UB: block_size % 16 == 0, so each 16-position group of a tile lies in one block
-// and its address comes from one wave-uniform table lookup.
-template <int QT, int D, bool UB>
+// and its address comes from one wave-uniform table lookup (16-bit pools).
+// KVT: the pool type, QT's own or fp8-e4m3 with scale mode SM (1 per-tensor, 2
+// per-vector).  FP8 tiles are staged through registers: each thread loads 8-code pieces
+// (item e = 256 j + t: row e / PIECES, piece e % PIECES) while the previous tile is in
+// use, then widens them to QT (exact for e4m3) into the same swizzled LDS layout; the
+// per-tensor key scale folds into the score scale and the value scale into the output,
+// per-vector scales multiply each position's score and (for P V only) its weight.
+template <int QT, int KVT, int D, int SM, bool UB>
 __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void rlt_prefill_kernel(AttnParams P) {
   using M = Mfma<QT>;
   using L = PrefillLds<D>;
@@ -1500,6 +1518,11 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
   constexpr int LDS_PER_WAVE = kPfKeys / ROWS_PER_LD / kPfWaves;  // direct loads per wave per tile (K, V each)
   static_assert(LDS_PER_WAVE * ROWS_PER_LD * kPfWaves == kPfKeys, "the waves' loads cover a tile");
   static_assert(16 % ROWS_PER_LD == 0, "a direct load's rows stay in one 16-position group");
+  constexpr bool FP8 = KVT != QT;
+  static_assert(!FP8 || KVT == RLT_FP8_E4M3, "16-bit pools match q");
+  static_assert(FP8 == (SM != 0), "scale modes are for fp8 pools");
+  constexpr int FJ = kPfKeys * PIECES / kPfThreads;  // fp8 pieces per thread per tile (K, V each)
+  static_assert(FJ * kPfThreads == kPfKeys * PIECES, "the threads' fp8 pieces cover a tile");
   __shared__ L sh;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
 
@@ -1575,8 +1598,35 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
     blk = (e >= 0 && e < P.num_blocks) ? e : 0;
     off = pos % P.block_size;
   };
+  uint2 kraw[FP8 ? FJ : 1], vraw[FP8 ? FJ : 1];
+  float sraw = 0.f;
   auto load = [&](int tile, int b) {
     const int base = tile * kPfKeys;
+    if constexpr (FP8) {
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        const int e = j * kPfThreads + t;
+        const int r = e / PIECES, pc = e % PIECES;
+        int64_t blk;
+        int off;
+        block_of(base + r, blk, off);
+        kraw[j] = *(const uint2*)((const uint8_t*)P.k + blk * P.k_block_stride +
+                                  (int64_t)off * P.k_token_stride + k_head + pc * 8);
+        vraw[j] = *(const uint2*)((const uint8_t*)P.v + blk * P.v_block_stride +
+                                  (int64_t)off * P.v_token_stride + v_head + pc * 8);
+      }
+      if (SM == 2 && t < 2 * kPfKeys) {  // threads 0-63 key scales, 64-127 value scales
+        const int pos = base + (t & (kPfKeys - 1));
+        int64_t blk;
+        int off;
+        block_of(pos, blk, off);
+        const float x = (t < kPfKeys ? P.k_scale : P.v_scale)[blk * P.s_block_stride +
+                                                              (int64_t)off * P.s_token_stride +
+                                                              (int64_t)kvh * P.s_head_stride];
+        sraw = pos < hi_last ? x : 0.f;
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < LDS_PER_WAVE; ++j) {
       const int r0 = ROWS_PER_LD * (LDS_PER_WAVE * w + j);  // wave-uniform
@@ -1607,8 +1657,25 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
   // sequence may hold any bits (NaN included) and are zeroed, since their weight 0
   // times NaN would not vanish.  Only the tiles that reach past hi_last do work.
   auto settle = [&](int tile, int b) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const int base = tile * kPfKeys;
+    if constexpr (FP8) {
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        const int e = j * kPfThreads + t;
+        const int r = e / PIECES, pc = e % PIECES;
+        const uint2 k0 = fp8x4_to_16<QT>(kraw[j].x), k1 = fp8x4_to_16<QT>(kraw[j].y);
+        *(uint4*)(sh.k[b] + r * L::kRowB + k_slot<SLOTS>(r, pc) * 16) = make_uint4(k0.x, k0.y, k1.x, k1.y);
+        uint4 vx = make_uint4(0, 0, 0, 0);
+        if (base + r < hi_last) {
+          const uint2 v0 = fp8x4_to_16<QT>(vraw[j].x), v1 = fp8x4_to_16<QT>(vraw[j].y);
+          vx = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        }
+        *(uint4*)(sh.v[b] + r * L::kRowB + v_slot<SLOTS>(r, pc) * 16) = vx;
+      }
+      if (SM == 2 && t < 2 * kPfKeys) (t < kPfKeys ? sh.ks[b] : sh.vs[b])[t & (kPfKeys - 1)] = sraw;
+      return;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (base + kPfKeys > hi_last) {
 #pragma unroll
       for (int j = 0; j < LDS_PER_WAVE; ++j) {
@@ -1628,12 +1695,26 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
   const int vm = ((l16 >> 2) & 3) ^ (SLOTS >= 16 ? 4 * (grp & 1) : 0);
   const int v_lane = (4 * grp + (l16 >> 2)) * L::kRowB + ((l16 >> 1) & 1) * 16 + (l16 & 1) * 8;
 
-  const float qk_scale = P.qk_scale_log2;
+  float qk_scale = P.qk_scale_log2;
+  float v_mul = 1.f;
+  if (SM == 1) {
+    qk_scale *= P.k_scale[0];
+    v_mul = P.v_scale[0];
+  }
   auto compute = [&](int tile, int b, auto full_tag) {
     constexpr bool FULL = decltype(full_tag)::value;
     const int base = tile * kPfKeys;
     const uint8_t* kb = sh.k[b];
     const uint8_t* vb = sh.v[b];
+    // per-vector scales of the lane's positions 16 kt + 4 grp + i
+    f32x4 ksv[SM == 2 ? 4 : 1], vsv[SM == 2 ? 4 : 1];
+    if constexpr (SM == 2) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        ksv[kt] = *(const f32x4*)(sh.ks[b] + 16 * kt + 4 * grp);
+        vsv[kt] = *(const f32x4*)(sh.vs[b] + 16 * kt + 4 * grp);
+      }
+    }
     // ---- S^T = K Q^T for the tile's four 16-position sub-tiles
     f32x4 sc[4][NT];
 #pragma unroll
@@ -1664,7 +1745,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float v = sc[kt][nt][i];
+          float v = sc[kt][nt][i];
+          if constexpr (SM == 2) v *= ksv[kt][i];
           if (FULL) {
             x[kt][i] = v;
           } else {
@@ -1690,6 +1772,12 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
         }
       l_run[nt] = l_run[nt] * corr[nt] + group_sum(rs);
       m_run[nt] = m_new;
+      if constexpr (SM == 2) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pr[kt][i] *= vsv[kt][i];
+      }
 #pragma unroll
       for (int c = 0; c < 2; ++c)
         pop[c][nt] = make_uint4(M::pack2(pr[2 * c][0], pr[2 * c][1]),
@@ -1756,12 +1844,27 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
     const int qi = rho / P.group;
     const int head = kvh * P.group + rho % P.group;
     const int64_t off = (int64_t)(sv.q_begin + qi) * P.out_row_stride + (int64_t)head * P.out_head_stride;
-    const float inv = 1.f / fmaxf(l_run[nt], 1.0e-30f);
+    const float inv = v_mul / fmaxf(l_run[nt], 1.0e-30f);
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) store_from_f32<QT>(P.out, off + dt * 16 + 4 * grp + i, oacc[nt][dt][i] * inv);
   }
+}
+
+// Window store ahead of the prefill tiling (a store-and-attend call whose window takes
+// it): one 256-thread workgroup per (64 window rows, sequence, kv head), 16 rows per
+// wave, the verify kernels' fused per-row stores (store_rows).
+template <int QT, int KVT, int D, int SM>
+__global__ __launch_bounds__(256) void rlt_window_store_kernel(AttnParams P) {
+  const int64_t id = blockIdx.x;
+  const int kvh = (int)(id % P.hkv);
+  const int64_t sr = id / P.hkv;
+  const int seq = (int)(sr % P.num_seqs);
+  const int i0 = (int)(sr / P.num_seqs) * 64 + (int)(threadIdx.x >> 6) * 16;
+  const SeqView sv = seq_view(P, seq);
+  if (i0 >= sv.q_len) return;  // wave-uniform; no barriers follow
+  store_rows<QT, KVT, D, SM>(P, seq, kvh, sv, i0, min(sv.q_len, i0 + 16), 0, INT_MAX);
 }
 
 // ============================================================ dispatch
@@ -1831,17 +1934,32 @@ int launch_vec_q(const AttnParams& P, int kv_dtype, dim3 grid, hipStream_t strea
   return RLT_OK;
 }
 
-template <int QT, int D>
-void launch_prefill_d(const AttnParams& P, dim3 grid, hipStream_t stream) {
-  if (P.block_size % 16 == 0) rlt_prefill_kernel<QT, D, true><<<grid, kPfThreads, 0, stream>>>(P);
-  else rlt_prefill_kernel<QT, D, false><<<grid, kPfThreads, 0, stream>>>(P);
+template <int QT, int KVT, int D, int SM>
+void launch_prefill_sm(const AttnParams& P, dim3 grid, dim3 sgrid, hipStream_t stream) {
+  if (P.new_k) rlt_window_store_kernel<QT, KVT, D, SM><<<sgrid, 256, 0, stream>>>(P);
+  // (fp8 pools are staged per position: the whole-tile block form is for direct loads)
+  if constexpr (KVT == QT) {
+    if (P.block_size % 16 == 0) {
+      rlt_prefill_kernel<QT, KVT, D, SM, true><<<grid, kPfThreads, 0, stream>>>(P);
+      return;
+    }
+  }
+  rlt_prefill_kernel<QT, KVT, D, SM, false><<<grid, kPfThreads, 0, stream>>>(P);
 }
 
-template <int QT>
-void launch_prefill(const AttnParams& P, int head_dim, dim3 grid, hipStream_t stream) {
-  if (head_dim == 64) launch_prefill_d<QT, 64>(P, grid, stream);
-  else if (head_dim == 96) launch_prefill_d<QT, 96>(P, grid, stream);
-  else launch_prefill_d<QT, 128>(P, grid, stream);
+template <int QT, int KVT, int D>
+void launch_prefill_d(const AttnParams& P, dim3 grid, dim3 sgrid, hipStream_t stream) {
+  if constexpr (KVT == QT) launch_prefill_sm<QT, KVT, D, 0>(P, grid, sgrid, stream);
+  else if (P.scale_mode == 1) launch_prefill_sm<QT, KVT, D, 1>(P, grid, sgrid, stream);
+  else launch_prefill_sm<QT, KVT, D, 2>(P, grid, sgrid, stream);
+}
+
+// sgrid: the window store's grid (launched first when the call stores its rows)
+template <int QT, int KVT>
+void launch_prefill(const AttnParams& P, int head_dim, dim3 grid, dim3 sgrid, hipStream_t stream) {
+  if (head_dim == 64) launch_prefill_d<QT, KVT, 64>(P, grid, sgrid, stream);
+  else if (head_dim == 96) launch_prefill_d<QT, KVT, 96>(P, grid, sgrid, stream);
+  else launch_prefill_d<QT, KVT, 128>(P, grid, sgrid, stream);
 }
 
 template <int OT>
@@ -1886,7 +2004,7 @@ int rlt_paged_attention_uses_mfma(int32_t q_dtype, int32_t kv_dtype, int32_t hea
 
 int rlt_paged_attention_uses_prefill(int32_t q_dtype, int32_t kv_dtype, int32_t head_dim,
                                      int32_t max_q_len) {
-  return rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) && kv_dtype == q_dtype &&
+  return rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) &&
          (head_dim == 64 || head_dim == 96 || head_dim == 128) && max_q_len >= kPfMinQ;
 }
 
@@ -1994,8 +2112,7 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
     const bool fp8 = kv_dtype == RLT_FP8_E4M3;
     if (!cu_seqlens_q || (q_dtype != RLT_BF16 && q_dtype != RLT_F16) ||
         !(kv_dtype == q_dtype || fp8) ||
-        !rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim) ||
-        rlt_paged_attention_uses_prefill(q_dtype, kv_dtype, head_dim, max_q_len))
+        !rlt_paged_attention_uses_mfma(q_dtype, kv_dtype, head_dim))
       return RLT_ERR_UNSUPPORTED;
     if (fp8 != (scale_mode != 0)) return RLT_ERR_ARGUMENT;
     const int64_t piece = fp8 ? 8 : 16;  // bytes each lane stores into the pool
@@ -2032,8 +2149,17 @@ int attention_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
       const int64_t wgs = (int64_t)num_seqs * P.rowgroups * num_kv_heads;
       if (wgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
       const dim3 grid((unsigned)wgs);
-      if (q_dtype == RLT_BF16) launch_prefill<RLT_BF16>(P, head_dim, grid, stream);
-      else launch_prefill<RLT_F16>(P, head_dim, grid, stream);
+      const int64_t swgs = (int64_t)num_seqs * num_kv_heads * ((max_q_len + 63) / 64);
+      if (swgs >= ((int64_t)1 << 31)) return RLT_ERR_UNSUPPORTED;
+      const dim3 sgrid((unsigned)swgs);
+      const bool fp8 = kv_dtype == RLT_FP8_E4M3;
+      if (q_dtype == RLT_BF16) {
+        if (fp8) launch_prefill<RLT_BF16, RLT_FP8_E4M3>(P, head_dim, grid, sgrid, stream);
+        else launch_prefill<RLT_BF16, RLT_BF16>(P, head_dim, grid, sgrid, stream);
+      } else {
+        if (fp8) launch_prefill<RLT_F16, RLT_FP8_E4M3>(P, head_dim, grid, sgrid, stream);
+        else launch_prefill<RLT_F16, RLT_F16>(P, head_dim, grid, sgrid, stream);
+      }
       return rlt_launch_status();
     }
     const int nt = (rows_per_seq > 16 && head_dim <= 128) ? 2 : 1;

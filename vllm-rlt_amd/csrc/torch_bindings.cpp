@@ -560,14 +560,14 @@ Tensor paged_attention_store(const Tensor& q, const Tensor& k_new_in, const Tens
   }
   TORCH_CHECK_VALUE(k_new.strides() == v_new.strides(), "k_new and v_new must share strides");
   const int32_t qd = dtype_code(q.scalar_type()), kvd = dtype_code(key_cache.scalar_type());
-  const bool one_launch = half && (fp8 || q.scalar_type() == key_cache.scalar_type()) &&
-                          rlt_paged_attention_uses_mfma(qd, kvd, (int32_t)head_dim) &&
-                          !rlt_paged_attention_uses_prefill(qd, kvd, (int32_t)head_dim,
-                                                            (int32_t)max_seqlen_q);
-  TORCH_CHECK_VALUE(one_launch || !fp8,
+  // the C ABI's store-and-attend form: one launch on the verify kernels, or the window
+  // store then the prefill tiling for windows that take it
+  const bool abi_store = half && (fp8 || q.scalar_type() == key_cache.scalar_type()) &&
+                          rlt_paged_attention_uses_mfma(qd, kvd, (int32_t)head_dim);
+  TORCH_CHECK_VALUE(abi_store || !fp8,
                     "an FP8 window store needs a head_dim the MFMA kernels serve (64, 96, 128, "
                     "256): use store_fp8 and prefill");
-  if (rows > 0 && one_launch) {
+  if (rows > 0 && abi_store) {
     const int64_t num_seqs = block_tables.size(0), width = block_tables.size(1), heads = q.size(1);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     Tensor output = at::empty_like(q);
