@@ -491,13 +491,25 @@ def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vo
 def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, filtered):
     """verify_accept (distributions, argmax targets and the draft rows' partial sums in
     one launch, then the acceptance) is bitwise verify_distributions over every row
-    followed by speculative_accept."""
+    followed by speculative_accept; its targets equal torch's argmax (NaN rows, ties at
+    the maximum, signed zeros, all -inf rows)."""
     _say("verify accept", dtype, vocab, n, w1, filtered)
     g = torch.Generator().manual_seed(vocab + n)
     rows = n * (w1 + 1)
     logits = (torch.randn(n, w1 + 1, vocab, generator=g) * 3).to(dtype)
     if not filtered:
         logits[1, 2, 7] = float("nan")  # a NaN row: NaN p, an error for its request
+    else:
+        # argmax targets: a NaN (the maximum), a tie at the maximum (the first column),
+        # an all-zero row with -0.0 first, an all -inf row
+        logits[0, 1, vocab // 2] = float("nan")
+        logits[0, 1, vocab - 1] = float("nan")
+        top = logits[1, 0].float().max() + 1
+        logits[1, 0, vocab - 2] = top
+        logits[1, 0, 3 if vocab > 3 else 0] = top
+        logits[-1, -1] = 0.0
+        logits[-1, -1, 0] = -0.0
+        logits[-1, 0] = float("-inf")
     t = torch.rand(rows, generator=g) + 0.5
     k = torch.where(torch.rand(rows, generator=g) < 0.3, 40, -1)
     p = torch.where(torch.rand(rows, generator=g) < 0.5, 0.9, 1.0)
@@ -517,6 +529,7 @@ def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, 
     want = pkg.speculative_accept(args[4], args[5], args[6], want_p.view(n, w1 + 1, vocab),
                                   args[7], args[8])
     assert torch.equal(target.cpu(), want_t.cpu())
+    assert torch.equal(target.cpu(), logits.view(rows, vocab).float().argmax(-1))
     assert torch.equal(p_o.cpu().view(torch.int32), want_p.view(n, w1 + 1, vocab).cpu().view(torch.int32))
     for a, b, name in zip(res, want, want._fields):
         assert torch.equal(a.cpu(), b.cpu()), name

@@ -152,6 +152,9 @@ struct SharedT {
   uint32_t sel_bin_cnt;
   unsigned long long sel_bin_mass;
   uint32_t list_n;
+  uint32_t gather_n;  // tokens gathered by the current selection
+  uint32_t sel_kept_in_bin;
+  unsigned long long sel_kept_mass;
 };
 
 // Block-wide sum of a u32 and a u64 (every thread gets the totals).
@@ -239,7 +242,10 @@ __device__ __forceinline__ void scan_select(Shared& sh, int nb, uint32_t cnt_bef
       m += my;
     }
   }
-  if (t == 0) sh.sel_bin = -1;
+  if (t == 0) {
+    sh.sel_bin = -1;
+    sh.gather_n = 0;  // for the gather that follows a selection (no reader before)
+  }
   if (lane == 63) {
     sh.wave_u32[w] = c;
     sh.wave_u64[w] = m;
@@ -383,6 +389,40 @@ struct Row {
       for (; j < npt; ++j) f(j, e(j));
     }
   }
+  // f(j, x(j)) for every chunk (l before the mass pass), LDS chunks read four at a time
+  // before their four calls (one LDS round trip per four chunks, not per chunk).
+  template <class F>
+  __device__ __forceinline__ void for_chunks_x4(F f) const {
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) f(j, x(j));
+    if (kNpt > 0) {
+      const int end = kTail ? kNpt : npt;
+      int j = NREG;
+#pragma unroll 1
+      for (; j + 4 <= end; j += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = x(j + u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f(j + u, v[u]);
+      }
+#pragma unroll 1
+      for (; j < end; ++j) f(j, x(j));
+    }
+    if (kNpt == 0 || kTail) {
+      int j = kNpt;
+#pragma unroll 1
+      for (; j + 4 <= npt; j += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = x(j + u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f(j + u, v[u]);
+      }
+#pragma unroll 1
+      for (; j < npt; ++j) f(j, x(j));
+    }
+  }
   // f(j) for every chunk: register chunks unrolled (static register indices),
   // LDS chunks in a rolled loop, re-read chunks four at a time (loads in flight).
   // Calls are wave-uniform (ballots allowed).
@@ -464,12 +504,13 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
   const uint32_t cnt_before = sh.sel_cnt_before;
   const unsigned long long mass_before = sh.sel_mass_before;
   const uint32_t n = sh.sel_bin_cnt;
-  __syncthreads();
+  // (sel_* are rewritten only by a later selection, after further barriers)
 
   Cut out;
   out.bin = bin;
   int nl;
-  if (bin >= 0 && bin == mbin) {
+  const bool member = bin >= 0 && bin == mbin;
+  if (member) {
     nl = (int)mlist;  // the members are the sorted prefix already in the list
   } else {
     if (bin < 0 || n > (uint32_t)Shared::kCap) {
@@ -477,26 +518,76 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       out.bin = -1;
       return out;
     }
-    // gather the bin's columns (all members: bin < mbin), then their logits, one
-    // entry per thread, so no load waits inside the row loop
-    if (t == 0) sh.list_n = 0;
-    __syncthreads();
+    // gather the bin's columns (all members: bin < mbin) into the list (gather_n was
+    // zeroed by the scan)
     uint32_t blo, bhi;
     bin_bits(bin, blo, bhi);
-    row.for_chunks([&](int j) {
+    row.for_chunks_e4([&](int j, float e) {
       // the bin's bit range (NaN padding lies above every bin's range)
-      const uint32_t bits = __float_as_uint(row.e(j));
+      const uint32_t bits = __float_as_uint(e);
       const bool take = bits >= blo && bits <= bhi;
       const uint64_t m = __ballot(take);
       if (m == 0) return;
       uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&sh.list_n, (uint32_t)__popcll(m));
+      if (lane == 0) base = atomicAdd(&sh.gather_n, (uint32_t)__popcll(m));
       base = __shfl(base, 0, RLT_WAVE);
       const uint32_t pos = base + __popcll(m & lanemask_lt());
       if (take && pos < (uint32_t)Shared::kCap) sh.list[pos] = (uint32_t)(j * kThreads + t);
     });
     __syncthreads();
-    nl = min((int)sh.list_n, Shared::kCap);  // == n
+    nl = min((int)sh.gather_n, Shared::kCap);  // == n
+  }
+  if (nl <= RLT_WAVE) {
+    // one wave: the gathered columns' logits, a bitonic sort in registers, and the scan
+    // of the sorted members; one barrier publishes the result
+    if (t < RLT_WAVE) {
+      unsigned long long v = kCutNone;
+      if (lane < nl) {
+        v = sh.list[lane];
+        if (!member) {
+          const uint32_t col = (uint32_t)v;
+          v = composite(order_key(load_as_f32<R::kDtype>(row.src, col)), col);
+        }
+      }
+      if (!member) {
+#pragma unroll
+        for (int k = 2; k <= RLT_WAVE; k <<= 1) {
+#pragma unroll
+          for (int j = k >> 1; j > 0; j >>= 1) {
+            const unsigned long long o = __shfl_xor(v, j, RLT_WAVE);
+            const bool keep_min = ((lane & k) == 0) == ((lane & j) == 0);
+            v = keep_min ? (o < v ? o : v) : (o < v ? v : o);
+          }
+        }
+        if (lane < nl) sh.list[lane] = v;
+        if (lane == 0) sh.list_n = (uint32_t)nl;
+      }
+      // masses recomputed from the keys (the mass pass's arithmetic); members kept
+      // while the cut criterion is not reached
+      const unsigned long long fm =
+          lane < nl ? fixed_mass(row.mass(key_value(~(uint32_t)(v >> 32)))) : 0ull;
+      unsigned long long incl = fm;
+      for (int off = 1; off < 64; off <<= 1) {
+        const unsigned long long y = __shfl_up(incl, off, RLT_WAVE);
+        if (lane >= off) incl += y;
+      }
+      const unsigned long long before = mass_before + incl - fm;
+      const bool keep =
+          lane < nl && (kMass ? before <= limit : (uint32_t)lane < limit - cnt_before);
+      const unsigned long long km = wave_sum(keep ? fm : 0ull);
+      const uint32_t kn = (uint32_t)__popcll(__ballot(keep));  // (the whole wave votes)
+      if (lane == 0) {
+        sh.sel_kept_in_bin = kn;
+        sh.sel_kept_mass = km;
+      }
+    }
+    __syncthreads();
+    out.kept_in_bin = sh.sel_kept_in_bin;
+    out.kept = mass_before + sh.sel_kept_mass;
+    return out;
+  }
+  if (!member) {
+    if (t == 0) sh.list_n = (uint32_t)nl;  // (read after the barriers below)
     int p = 1;
     while (p < nl) p <<= 1;
     for (int i = t; i < p; i += kThreads) {
@@ -508,26 +599,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       sh.list[i] = v;
     }
     __syncthreads();
-    if (p <= RLT_WAVE) {
-      // one wave sorts in registers (bitonic network over lane shuffles)
-      if (t < RLT_WAVE) {
-        unsigned long long v = sh.list[lane & (p - 1)];
-        if (lane >= p) v = kCutNone;
-#pragma unroll
-        for (int k = 2; k <= RLT_WAVE; k <<= 1) {
-#pragma unroll
-          for (int j = k >> 1; j > 0; j >>= 1) {
-            const unsigned long long o = __shfl_xor(v, j, RLT_WAVE);
-            const bool keep_min = ((lane & k) == 0) == ((lane & j) == 0);
-            v = keep_min ? (o < v ? o : v) : (o < v ? v : o);
-          }
-        }
-        if (lane < p) sh.list[lane] = v;
-      }
-      __syncthreads();
-    } else {
-      sort_list(sh, p);
-    }
+    sort_list(sh, p);
   }
   // scan the sorted members: masses recomputed from the keys (same arithmetic as
   // the mass pass), kept while the cut criterion is not reached
@@ -617,11 +689,11 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   // the next chunks' LDS reads need not wait for them
   __attribute__((address_space(1))) float* gdst = (__attribute__((address_space(1))) float*)dst;
   row.for_chunks_e4([&](int j, float e) {
-    if (e != e) return;
-    // bins before the cut bin hold larger masses (kept), later bins smaller ones
+    // bins before the cut bin hold larger masses (kept), later bins smaller ones; the
+    // cut bin's tokens are written from the list below (NaN: padding); one store
     const uint32_t bits = __float_as_uint(e);
-    if (bits > chi) gdst[(int64_t)j * kThreads + t] = e * inv;
-    else if (bits < clo) gdst[(int64_t)j * kThreads + t] = 0.f;
+    const float v = bits > chi ? e * inv : 0.f;
+    if (e == e && (bits > chi || bits < clo)) gdst[(int64_t)j * kThreads + t] = v;
   });
   const int nl = min((int)sh.list_n, Shared::kCap);
   for (int i = t; i < nl; i += kThreads) {
@@ -829,8 +901,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   // (the tokens with e > 2^-16: a few percent of a row; where top-p cuts the
   // distributions of a verify step)
   double zs = 0.0;
-  row.for_chunks([&](int j) {
-    const float l = row.x(j);
+  row.for_chunks_x4([&](int j, float l) {
     const float e = l == l ? row.mass(l) : 0.f;
     if (NPT > 0) row.set(j, l == l ? e : NAN);
     zs += (double)e;
@@ -844,8 +915,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   const double z = block_sum_f64(sh, zs);
   if (!do_k && !do_p) {
     const float inv = (float)(1.0 / z);
-    row.for_chunks([&](int j) {
-      const float e = row.e(j);
+    row.for_chunks_e4([&](int j, float e) {
       if (e == e) dst[(int64_t)j * kThreads + t] = e * inv;
     });
     break;
