@@ -343,6 +343,12 @@ struct Row {
     asm volatile("" : "+v"(v));
     return v;
   }
+  // the on-chip value of chunk j without the opaque copy (batched reads: the copies
+  // follow all the reads of a batch, so one wait covers them)
+  __device__ __forceinline__ float x_raw(int j) const {
+    return j < NREG ? xr[j] : xl[(j - NREG) * kThreads + threadIdx.x];
+  }
+  __device__ __forceinline__ static void opaque(float& v) { asm volatile("" : "+v"(v)); }
   __device__ __forceinline__ float logit(int j) const {
     return valid(j) ? load_as_f32<DT>(src, (int64_t)j * kThreads + threadIdx.x) : NAN;
   }
@@ -368,7 +374,9 @@ struct Row {
       for (; j + 4 <= end; j += 4) {
         float v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = e(j + u);
+        for (int u = 0; u < 4; ++u) v[u] = x_raw(j + u);  // on chip: e is the slot
+#pragma unroll
+        for (int u = 0; u < 4; ++u) opaque(v[u]);
 #pragma unroll
         for (int u = 0; u < 4; ++u) f(j + u, v[u]);
       }
@@ -402,7 +410,9 @@ struct Row {
       for (; j + 4 <= end; j += 4) {
         float v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = x(j + u);
+        for (int u = 0; u < 4; ++u) v[u] = x_raw(j + u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) opaque(v[u]);
 #pragma unroll
         for (int u = 0; u < 4; ++u) f(j + u, v[u]);
       }
@@ -535,7 +545,12 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       if (take && pos < (uint32_t)Shared::kCap) sh.list[pos] = (uint32_t)(j * kThreads + t);
     });
     __syncthreads();
-    nl = min((int)sh.gather_n, Shared::kCap);  // == n
+    // (a top-p selection without a top-k cut has no bin counts: n = 0 above)
+    if (sh.gather_n > (uint32_t)Shared::kCap) {
+      out.bin = -1;  // crowded: the exact path (block-uniform)
+      return out;
+    }
+    nl = (int)sh.gather_n;
   }
   if (nl <= RLT_WAVE) {
     // one wave: the gathered columns' logits, a bitonic sort in registers, and the scan
@@ -902,14 +917,19 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   // distributions of a verify step)
   double zs = 0.0;
   row.for_chunks_x4([&](int j, float l) {
-    const float e = l == l ? row.mass(l) : 0.f;
-    if (NPT > 0) row.set(j, l == l ? e : NAN);
-    zs += (double)e;
-    const uint32_t bits = __float_as_uint(e);
+    // padding (NaN; rows holding a real NaN have left) keeps e = NaN in its slot and
+    // counts as 0: fmaxf returns the number of a (NaN, number) pair
+    const float e = row.mass(l);
+    if (NPT > 0) row.set(j, e);
+    const float e0 = fmaxf(e, 0.f);
+    zs += (double)e0;
+    const uint32_t bits = __float_as_uint(e0);
     if (bits > kFloor16) {
       const int b = bin_of(bits);
-      atomicAdd(&sh.cnt[b], 1u);
-      atomicAdd(&sh.mass[b], fixed_mass(e));
+      // counts only for a top-k cut: a top-p selection scans masses, and its gather
+      // counts the crossing bin's tokens itself
+      if (do_k) atomicAdd(&sh.cnt[b], 1u);
+      atomicAdd(&sh.mass[b], fixed_mass(e0));
     }
   });
   const double z = block_sum_f64(sh, zs);
