@@ -122,6 +122,20 @@ __device__ __forceinline__ unsigned long long fixed_mass(float e) {
   return s >= 0 ? (m24 << s) : (s > -24 ? (m24 >> -s) : 0ull);
 }
 
+// Mass of histogram bin b in 2^-40 fixed point.  With Shared::kF64Top the top bins (e in
+// (2^-16, 1]) hold the float64 sum of their tokens' e, added by the mass pass with LDS
+// float64 atomics: a top bin's tokens are within a factor of two of each other, each a
+// multiple of 2^-40 with 24 significant bits, at most 2^18 of them, so their sum needs at
+// most 43 significant bits: exact in any order, and equal to the fixed-point sum.  Other
+// bins hold fixed-point sums.
+template <class Shared>
+__device__ __forceinline__ unsigned long long bin_mass(const Shared& sh, int b) {
+  const unsigned long long raw = sh.mass[b];
+  if (Shared::kF64Top && b < kTopBins)
+    return (unsigned long long)(__longlong_as_double((long long)raw) * kFixScale);
+  return raw;
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int lane = threadIdx.x & 63;
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -135,9 +149,12 @@ __device__ __forceinline__ T wave_sum(T v) {
 
 #include "probs_split.h"
 
-template <int CAP>
+template <int CAP, bool F64TOP = false>
 struct SharedT {
   static constexpr int kCap = CAP;
+  // the top bins' masses as float64 sums (bin_mass); kernels whose registers are all
+  // taken keep fixed-point sums (the float64 conversion costs them spills)
+  static constexpr bool kF64Top = F64TOP;
   unsigned long long mass[kBins];
   uint32_t cnt[kBins];
   unsigned long long list[CAP];  // tokens of the crossing bin (columns, then composites)
@@ -228,7 +245,7 @@ __device__ __forceinline__ void scan_select(Shared& sh, int nb, uint32_t cnt_bef
   for (int i = 0; i < kBinsPerThread; ++i) {
     const int bin = t * kBinsPerThread + i;
     c_own[i] = bin < nb ? sh.cnt[bin] : 0u;
-    m_own[i] = bin < nb ? sh.mass[bin] : 0ull;
+    m_own[i] = bin < nb ? bin_mass(sh, bin) : 0ull;
     c += c_own[i];
     m += m_own[i];
   }
@@ -680,9 +697,12 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
       const Cut ck = cut;
       if (t == 0) {
         unsigned long long before = 0;
-        for (int i = 0; i < ck.bin; ++i) before += sh.mass[i];
+        for (int i = 0; i < ck.bin; ++i) before += bin_mass(sh, i);
         sh.cnt[ck.bin] = ck.kept_in_bin;
-        sh.mass[ck.bin] = ck.kept - before;
+        const unsigned long long kb = ck.kept - before;  // exact in float64 (as above)
+        sh.mass[ck.bin] = Shared::kF64Top && ck.bin < kTopBins
+                              ? (unsigned long long)__double_as_longlong((double)kb / kFixScale)
+                              : kb;
       }
       clear_hist(sh, ck.bin + 1, kBins);
       __syncthreads();
@@ -775,11 +795,11 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
   constexpr int kTC = NPT > 0 && !kTail ? NPT : kMaxStreamChunks;
   union Lds {
-    SharedT<kCapV> fast;
+    SharedT<kCapV, (NREG <= 16)> fast;
     exact::SharedT<kTC> ex;
   };
   __shared__ Lds lds;
-  SharedT<kCapV>& sh = lds.fast;
+  auto& sh = lds.fast;
   // blocks past the distribution rows take the argmax of logits rows 0..argmax_rows-1
   // (greedy proposals and targets, run alongside the distributions), then the float32
   // row-sum partials of the qm_rows draft rows for the acceptance sampler, eight
@@ -929,7 +949,10 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
       // counts only for a top-k cut: a top-p selection scans masses, and its gather
       // counts the crossing bin's tokens itself
       if (do_k) atomicAdd(&sh.cnt[b], 1u);
-      atomicAdd(&sh.mass[b], fixed_mass(e0));
+      if constexpr (decltype(lds.fast)::kF64Top)
+        atomicAdd(reinterpret_cast<double*>(&sh.mass[b]), (double)e0);  // a top bin
+      else
+        atomicAdd(&sh.mass[b], fixed_mass(e0));
     }
   });
   const double z = block_sum_f64(sh, zs);
