@@ -711,10 +711,10 @@ def test_prefill_store_graph_replays_and_other_shapes(kernel, pkg, dev):
 
 @pytest.mark.parametrize("form", ["fused", "prefill_tiling", "float32_q"])
 def test_prefill_store_skips_positions_outside_the_table_or_pool(kernel, pkg, dev, form):
-    """Every form of prefill_store (the one-launch form, and the separate store of a
-    prefill-length window or float32 q) leaves unwritten a window position whose block
-    index lies beyond the table width or whose table entry lies outside the pool, and
-    writes every other window position."""
+    """Every form of prefill_store (the one-launch form, the window-store kernel ahead of
+    the prefill tiling, and the separate store of float32 q) leaves unwritten a window
+    position whose block index lies beyond the table width or whose table entry lies
+    outside the pool, and writes every other window position."""
     _say("prefill_store outside", form)
     g = torch.Generator().manual_seed(91)
     bs, hq, hkv, d = 16, 8, 2, 128
@@ -750,6 +750,59 @@ def test_prefill_store_skips_positions_outside_the_table_or_pool(kernel, pkg, de
     assert 0 < written < 3 * q_len
     assert torch.equal(kd.cpu().view(torch.int16), ke.view(torch.int16))
     assert torch.equal(vd.cpu().view(torch.int16), ve.view(torch.int16))
+
+
+@pytest.mark.parametrize("per_vector", [False, True])
+def test_fp8_prefill_store_long_window_skips_positions_outside(kernel, pkg, dev, per_vector):
+    """The window-store kernel ahead of the prefill tiling on an FP8 pool: positions beyond
+    the table or in blocks outside the pool keep their codes (and scales); every other
+    window position holds the quantize_fp8 codes (and, per vector, scales) of its row."""
+    _say("fp8 long-window store outside", per_vector)
+    g = torch.Generator().manual_seed(92 + per_vector)
+    bs, hq, hkv, d, w = 16, 8, 2, 128, 64
+    lengths = [700, 2049, 300]
+    n = len(lengths)
+    pages = sum(-(-x // bs) for x in lengths) + 3
+    kc, vc, ks, vs, tables, q, k_new, v_new = _fp8_store_case(
+        g, n, w, hq, hkv, d, bs, lengths, pages, per_vector, torch.bfloat16)
+    assert kernel.uses_prefill_tiling(torch.bfloat16, torch.float8_e4m3fn, d, w)
+    width = -(-2049 // bs) - 1
+    tables = tables[:, :width].contiguous()
+    tables[0, (700 - 1) // bs] = pages + 5
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    cu = torch.arange(0, n * w + 1, w, dtype=torch.int32)
+    kd, vd, ksd, vsd = kc.to(dev), vc.to(dev), ks.to(dev), vs.to(dev)
+    fixed = 0.05
+    if per_vector:
+        kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kd, vd, tables.to(dev),
+                             ctx.to(dev), cu.to(dev), w, ksd, vsd)
+    else:
+        s0 = torch.tensor(fixed, device=dev)
+        kernel.prefill_store(q.to(dev), k_new.to(dev), v_new.to(dev), kd, vd, tables.to(dev),
+                             ctx.to(dev), cu.to(dev), w, s0, s0)
+    torch.cuda.synchronize()
+    ke, ve, kse, vse = kc.clone(), vc.clone(), ks.clone(), vs.clone()
+    kq, kqs = ofp8.quantize_fp8(k_new.float(), None if per_vector else fixed)
+    vq, vqs = ofp8.quantize_fp8(v_new.float(), None if per_vector else fixed)
+    written = 0
+    for s_ in range(n):
+        for i in range(w):
+            pos = lengths[s_] - w + i
+            idx = pos // bs
+            if idx >= width:
+                continue
+            e = int(tables[s_, idx])
+            if not 0 <= e < pages:
+                continue
+            r = s_ * w + i
+            ke[e, pos % bs], ve[e, pos % bs] = kq[r], vq[r]
+            if per_vector:
+                kse[e, pos % bs], vse[e, pos % bs] = kqs[r], vqs[r]
+            written += 1
+    assert 0 < written < n * w
+    assert torch.equal(kd.cpu().view(torch.uint8), ke.view(torch.uint8))
+    assert torch.equal(vd.cpu().view(torch.uint8), ve.view(torch.uint8))
+    assert torch.equal(ksd.cpu(), kse) and torch.equal(vsd.cpu(), vse)
 
 
 # ------------------------------------------------------------ FP8 window store + attention
