@@ -387,18 +387,19 @@ def test_long_prompt_prefill_matches_dense_causal(kernel, dev, window, dtype, d,
         torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("window", [0, 256])
 @pytest.mark.parametrize("per_vector", [False, True])
 @pytest.mark.parametrize("q_dtype,d,hq,hkv,bs", [(torch.bfloat16, 128, 16, 8, 16),
                                                  (torch.float16, 96, 8, 2, 16),
                                                  (torch.bfloat16, 64, 8, 8, 8)])
 def test_long_prompt_prefill_fp8_matches_dense_causal(kernel, dev, per_vector, q_dtype, d, hq,
-                                                      hkv, bs):
+                                                      hkv, bs, window):
     """Prompt prefill over an FP8 pool (reference: triton_attention.py:335-362,460-487,
     the packed kernel's HAS_SCALE loads): long prompts, a chunk after a prefix and ragged
     windows against dense causal SDPA over the dequantized keys and values, with
     per-tensor or per-vector scales.  These windows take the prefill tiling (fp8 tiles
     widened to q's type in LDS, head_dim 96 on 128-dim LDS rows)."""
-    _say("long prefill fp8", per_vector, q_dtype, d, bs)
+    _say("long prefill fp8", per_vector, q_dtype, d, bs, window)
     g = torch.Generator().manual_seed(23 + d)
     assert kernel.uses_prefill_tiling(q_dtype, torch.float8_e4m3fn, d, 1024)
     seqs = [(1024, 1024), (2048, 512), (3000, 37), (300, 97), (129, 129)]
@@ -421,12 +422,12 @@ def test_long_prompt_prefill_fp8_matches_dense_causal(kernel, dev, per_vector, q
     lengths = torch.tensor([n for n, _ in seqs], dtype=torch.int32)
     cu = torch.tensor([0] + list(torch.tensor([c for _, c in seqs]).cumsum(0)), dtype=torch.int32)
     got = kernel.prefill(q.to(dev), kc.to(dev), vc.to(dev), tables.to(dev), lengths.to(dev),
-                         cu.to(dev), max(c for _, c in seqs), sk, sv).cpu()
+                         cu.to(dev), max(c for _, c in seqs), sk, sv, window=window).cpu()
     for s, (n, c) in enumerate(seqs):
         pages_s = tables[s, : -(-n // bs)].long()
         k_seq = k_deq[pages_s].reshape(-1, hkv, d)[:n]
         v_seq = v_deq[pages_s].reshape(-1, hkv, d)[:n]
-        want = _dense_packed(q[cu[s]:cu[s + 1]], k_seq, v_seq, c, n, 0)
+        want = _dense_packed(q[cu[s]:cu[s + 1]], k_seq, v_seq, c, n, window)
         torch.testing.assert_close(got[cu[s]:cu[s + 1]].float(), want, atol=2e-2, rtol=2e-2)
 
 
