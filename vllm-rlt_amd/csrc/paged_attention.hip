@@ -1501,8 +1501,9 @@ __device__ __forceinline__ int v_slot(int r, int piece) {
 // and its address comes from one wave-uniform table lookup (16-bit pools).
 // KVT: the pool type, QT's own or fp8-e4m3 with scale mode SM (1 per-tensor, 2
 // per-vector).  FP8 tiles are staged through registers: each thread loads 8-code pieces
-// (item e = 256 j + t: row e / PIECES, piece e % PIECES) while the previous tile is in
-// use, then widens them to QT (exact for e4m3) into the same swizzled LDS layout; the
+// (item e = 256 j + t: LDS slot e % SLOTS of row e / SLOTS, holding the piece the
+// swizzle puts there) while the previous tile is in use, then widens them to QT (exact
+// for e4m3) into the same swizzled LDS layout, each wave writing contiguous slots; the
 // per-tensor key scale folds into the score scale and the value scale into the output,
 // per-vector scales multiply each position's score and (for P V only) its weight.
 template <int QT, int KVT, int D, int SM, bool UB>
@@ -1521,8 +1522,8 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
   constexpr bool FP8 = KVT != QT;
   static_assert(!FP8 || KVT == RLT_FP8_E4M3, "16-bit pools match q");
   static_assert(FP8 == (SM != 0), "scale modes are for fp8 pools");
-  constexpr int FJ = kPfKeys * PIECES / kPfThreads;  // fp8 pieces per thread per tile (K, V each)
-  static_assert(FJ * kPfThreads == kPfKeys * PIECES, "the threads' fp8 pieces cover a tile");
+  constexpr int FJ = kPfKeys * SLOTS / kPfThreads;  // fp8 LDS slots per thread per tile (K, V each)
+  static_assert(FJ * kPfThreads == kPfKeys * SLOTS, "the threads' fp8 slots cover a tile");
   __shared__ L sh;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, l16 = lane & 15, grp = lane >> 4;
 
@@ -1605,15 +1606,21 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
     if constexpr (FP8) {
 #pragma unroll
       for (int j = 0; j < FJ; ++j) {
+        // item e: LDS slot e % SLOTS of row e / SLOTS, so each wave's LDS writes are
+        // contiguous (scattered 16-byte writes of permuted slots conflicted); the slot
+        // holds the row's piece k_slot / v_slot (an involution), loaded here
         const int e = j * kPfThreads + t;
-        const int r = e / PIECES, pc = e % PIECES;
+        const int r = e / SLOTS, sl = e % SLOTS;
+        const int kpc = k_slot<SLOTS>(r, sl), vpc = v_slot<SLOTS>(r, sl);
         int64_t blk;
         int off;
         block_of(base + r, blk, off);
-        kraw[j] = *(const uint2*)((const uint8_t*)P.k + blk * P.k_block_stride +
-                                  (int64_t)off * P.k_token_stride + k_head + pc * 8);
-        vraw[j] = *(const uint2*)((const uint8_t*)P.v + blk * P.v_block_stride +
-                                  (int64_t)off * P.v_token_stride + v_head + pc * 8);
+        if (PIECES == SLOTS || kpc < PIECES)
+          kraw[j] = *(const uint2*)((const uint8_t*)P.k + blk * P.k_block_stride +
+                                    (int64_t)off * P.k_token_stride + k_head + kpc * 8);
+        if (PIECES == SLOTS || vpc < PIECES)
+          vraw[j] = *(const uint2*)((const uint8_t*)P.v + blk * P.v_block_stride +
+                                    (int64_t)off * P.v_token_stride + v_head + vpc * 8);
       }
       if (SM == 2 && t < 2 * kPfKeys) {  // threads 0-63 key scales, 64-127 value scales
         const int pos = base + (t & (kPfKeys - 1));
@@ -1662,15 +1669,26 @@ __global__ __launch_bounds__(kPfThreads, kPfNT > 2 || kPfWaves > 4 ? 1 : 2) void
 #pragma unroll
       for (int j = 0; j < FJ; ++j) {
         const int e = j * kPfThreads + t;
-        const int r = e / PIECES, pc = e % PIECES;
-        const uint2 k0 = fp8x4_to_16<QT>(kraw[j].x), k1 = fp8x4_to_16<QT>(kraw[j].y);
-        *(uint4*)(sh.k[b] + r * L::kRowB + k_slot<SLOTS>(r, pc) * 16) = make_uint4(k0.x, k0.y, k1.x, k1.y);
-        uint4 vx = make_uint4(0, 0, 0, 0);
-        if (base + r < hi_last) {
-          const uint2 v0 = fp8x4_to_16<QT>(vraw[j].x), v1 = fp8x4_to_16<QT>(vraw[j].y);
-          vx = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        const int r = e / SLOTS, sl = e % SLOTS;
+        // (pad slots of 96-dim rows are never read: left unwritten)
+        if (PIECES == SLOTS || k_slot<SLOTS>(r, sl) < PIECES) {
+          const uint2 k0 = fp8x4_to_16<QT>(kraw[j].x), k1 = fp8x4_to_16<QT>(kraw[j].y);
+          // two 8-byte halves: 16-byte LDS writes of a whole wave conflicted (the counters
+          // read 4x the cycles of an ideal write)
+          uint2* kd = (uint2*)(sh.k[b] + r * L::kRowB + sl * 16);
+          kd[0] = make_uint2(k0.x, k0.y);
+          kd[1] = make_uint2(k1.x, k1.y);
         }
-        *(uint4*)(sh.v[b] + r * L::kRowB + v_slot<SLOTS>(r, pc) * 16) = vx;
+        if (PIECES == SLOTS || v_slot<SLOTS>(r, sl) < PIECES) {
+          uint4 vx = make_uint4(0, 0, 0, 0);
+          if (base + r < hi_last) {
+            const uint2 v0 = fp8x4_to_16<QT>(vraw[j].x), v1 = fp8x4_to_16<QT>(vraw[j].y);
+            vx = make_uint4(v0.x, v0.y, v1.x, v1.y);
+          }
+          uint2* vd = (uint2*)(sh.v[b] + r * L::kRowB + sl * 16);
+          vd[0] = make_uint2(vx.x, vx.y);
+          vd[1] = make_uint2(vx.z, vx.w);
+        }
       }
       if (SM == 2 && t < 2 * kPfKeys) (t < kPfKeys ? sh.ks[b] : sh.vs[b])[t & (kPfKeys - 1)] = sraw;
       return;
