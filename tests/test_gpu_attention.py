@@ -603,21 +603,29 @@ def _window_store_case(g, dtype, d, hq, hkv, bs, lengths, q_lens, pool_blocks, l
     return kpool, vpool, tables, q, k_new, v_new, cu
 
 
+@pytest.mark.parametrize("long_window", [False, True])
 @pytest.mark.parametrize("dtype,d,hq,hkv,bs", [
     (torch.bfloat16, 128, 16, 4, 16),   # config 3's heads
     (torch.float16, 64, 8, 8, 16),
     (torch.bfloat16, 96, 4, 1, 16),
     (torch.bfloat16, 128, 8, 2, 5),     # blocks that do not hold whole tiles
 ])
-def test_prefill_store_equals_store_then_prefill(kernel, pkg, dev, dtype, d, hq, hkv, bs):
+def test_prefill_store_equals_store_then_prefill(kernel, pkg, dev, dtype, d, hq, hkv, bs,
+                                                 long_window):
     """The fused window store + attention writes the pool and returns the output of
     store_kv at the window positions followed by prefill, bit for bit.  Windows sit on
     both sides of the 256-position half-chunk and 512-position chunk boundaries, and a
-    9-row window over GQA 4 spans two row groups (two units write the same positions)."""
-    _say("prefill_store", dtype, d, hq, hkv, bs)
-    g = torch.Generator().manual_seed(d + hq + bs)
+    9-row window over GQA 4 spans two row groups (two units write the same positions).
+    With long windows (the longest 130 rows) the call takes the prefill tiling and stores
+    with the window-store kernel first."""
+    _say("prefill_store", dtype, d, hq, hkv, bs, long_window)
+    g = torch.Generator().manual_seed(d + hq + bs + long_window)
     lengths = [5, 258, 514, 1030, 3000, 9, 40, 1]
     q_lens = [5, 5, 5, 9, 1, 9, 33, 1]
+    if long_window:
+        lengths = [70, 300, 1030, 2000, 129, 64, 5]
+        q_lens = [70, 65, 130, 64, 129, 64, 5]
+    assert kernel.uses_prefill_tiling(dtype, dtype, d, max(q_lens)) == long_window
     pages = sum(-(-x // bs) for x in lengths) + 7
     kpool, vpool, tables, q, k_new, v_new, cu = _window_store_case(
         g, dtype, d, hq, hkv, bs, lengths, q_lens, pages)
