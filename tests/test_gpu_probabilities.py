@@ -482,6 +482,7 @@ def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vo
     (torch.float32, 1000, 3, 1, True),
     (torch.float16, 151936, 2, 3, True),
     (torch.bfloat16, 5000, 40, 8, True),
+    (torch.float32, 49152, 32, 4, True),
     # no row filtered: the row-split distributions, whose write launch also sums p
     (torch.float32, 65536, 24, 4, False),
     (torch.float32, 49152, 32, 4, False),
@@ -492,7 +493,9 @@ def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, 
     """verify_accept (distributions, argmax targets and the draft rows' partial sums in
     one launch, then the acceptance) is bitwise verify_distributions over every row
     followed by speculative_accept; its targets equal torch's argmax (NaN rows, ties at
-    the maximum, signed zeros, all -inf rows)."""
+    the maximum, signed zeros, all -inf rows).  The p rows' row sums are formed on chip
+    for 16 register chunks (V in (16384, 49152]: 32000, 49152) and read back otherwise,
+    both in one launch when a flat row takes the exact path."""
     _say("verify accept", dtype, vocab, n, w1, filtered)
     g = torch.Generator().manual_seed(vocab + n)
     rows = n * (w1 + 1)
@@ -510,11 +513,16 @@ def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, 
         logits[-1, -1] = 0.0
         logits[-1, -1, 0] = -0.0
         logits[-1, 0] = float("-inf")
+        # a flat row: its top-p cut falls in a bin of every token (the exact path,
+        # whose row sums are read back) beside rows whose sums are formed on chip
+        logits[0, 0] = 1.5
     t = torch.rand(rows, generator=g) + 0.5
     k = torch.where(torch.rand(rows, generator=g) < 0.3, 40, -1)
     p = torch.where(torch.rand(rows, generator=g) < 0.5, 0.9, 1.0)
     if not filtered:
         k, p = torch.full((rows,), -1), torch.ones(rows)
+    else:
+        k[0], p[0] = -1, 0.9  # the flat row's top-p cut
     plan = _host_args(k.tolist(), p.tolist(), vocab)
     q = (torch.randn(n, w1, vocab, generator=g) * 2).softmax(-1)
     u = torch.rand(n, 2 * w1 + 1, generator=g)

@@ -339,9 +339,19 @@ struct Row {
   float* xl;
   float xr[NREG > 0 ? NREG : 1];
 
-  __device__ __forceinline__ bool valid(int j) const {
-    return (int64_t)j * kThreads + threadIdx.x < V;
+  // Column of chunk j of this thread: 1024 j + t, except the sixteen register chunks
+  // of a kSeq row, which hold the first 16384 columns as whole streams of torch-CPU's
+  // float32 row-sum cascade (512-column chunks, 32 streams of 16 steps): register chunk
+  // e of thread t is step e of stream t % 32 of cascade chunk 2 (t / 64) + (t / 32) % 2,
+  // column 512 c + 32 e + s.  A thread then sums its own register chunks in stream
+  // order, and every other cascade chunk lies in LDS in column order.
+  static constexpr bool kSeq = NREG == 16 && NLDS > 0 && NLDS % 16 == 0 && !kTail;
+  __device__ __forceinline__ int64_t col(int j) const {
+    const int t = threadIdx.x;
+    if (kSeq && j < 16) return (t >> 6) * 1024 + ((t >> 5) & 1) * 512 + j * 32 + (t & 31);
+    return (int64_t)j * kThreads + t;
   }
+  __device__ __forceinline__ bool valid(int j) const { return col(j) < V; }
   // chunks past the on-chip ones (kTail: rows longer than kNpt chunks) are re-read
   __device__ __forceinline__ bool on_chip(int j) const { return kNpt > 0 && (!kTail || j < kNpt); }
   __device__ __forceinline__ void set(int j, float v) {
@@ -367,7 +377,7 @@ struct Row {
   }
   __device__ __forceinline__ static void opaque(float& v) { asm volatile("" : "+v"(v)); }
   __device__ __forceinline__ float logit(int j) const {
-    return valid(j) ? load_as_f32<DT>(src, (int64_t)j * kThreads + threadIdx.x) : NAN;
+    return valid(j) ? load_as_f32<DT>(src, col(j)) : NAN;
   }
   __device__ __forceinline__ float mass(float l) const {
     return __builtin_amdgcn_exp2f((l - lmax) * c);
@@ -559,7 +569,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       if (lane == 0) base = atomicAdd(&sh.gather_n, (uint32_t)__popcll(m));
       base = __shfl(base, 0, RLT_WAVE);
       const uint32_t pos = base + __popcll(m & lanemask_lt());
-      if (take && pos < (uint32_t)Shared::kCap) sh.list[pos] = (uint32_t)(j * kThreads + t);
+      if (take && pos < (uint32_t)Shared::kCap) sh.list[pos] = (uint32_t)row.col(j);
     });
     __syncthreads();
     // (a top-p selection without a top-k cut has no bin counts: n = 0 above)
@@ -670,13 +680,123 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
   return out;
 }
 
+// Workgroup barrier that orders LDS accesses only: the row's global stores stay in
+// flight (a __syncthreads() would wait for every one of them to complete).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// What a written row holds, per token: e * inv above the cut bin (bits > chi), 0 below
+// it (bits < clo), and in the cut bin e * inv for the first kept_n tokens of the
+// sorted list, 0 for the others.
+struct Written {
+  float inv;
+  uint32_t clo, chi;
+  uint32_t kept_n;
+};
+
+// The last passes of a kSeq row whose acceptance partials are wanted (pm): every on-chip
+// value becomes the written one in place (e * inv, 0, or for the cut bin's tokens e * inv
+// when the sorted list keeps them; the kept tokens are first marked in their owners'
+// chunk masks), the row-sum partials are formed from those values (the register chunks'
+// streams by their own threads, the LDS chunks' streams read across threads; chunk sums
+// meet in LDS, then stream s of group g adds its chunks in order), and only then is the
+// row stored, so no barrier waits behind the stores.  `cut` false: an unfiltered row.
+template <class Shared, class R>
+__device__ __forceinline__ void seq_finish(Shared& sh, R& row, const Written& wr, bool cut,
+                                           float* __restrict__ pm, float* __restrict__ dst) {
+  static_assert(R::kNpt <= 64 && kThreads <= kBins, "chunk masks");
+  const int t = threadIdx.x;
+  const cascade::RowGeom geo = cascade::row_geom(row.V);
+  lds_barrier();  // the selection's histogram is no longer read
+  unsigned long long km = 0;
+  if (cut) {
+    sh.mass[t] = 0;
+    lds_barrier();
+    for (uint32_t i = t; i < wr.kept_n; i += kThreads) {
+      // owner of column x: below 16384 thread 64 w + 32 h + s, chunk e for x = 1024 w +
+      // 512 h + 32 e + s; above, thread x % 1024, chunk x / 1024
+      const uint32_t x = (uint32_t)sh.list[i];
+      const uint32_t owner = x < 16384u ? (((x >> 4) & 0x3e0u) | (x & 31u)) : (x & 1023u);
+      const uint32_t j = x < 16384u ? ((x >> 5) & 15u) : (x >> 10);
+      atomicOr(&sh.mass[owner], 1ull << j);
+    }
+    lds_barrier();
+    km = sh.mass[t];
+  }
+  auto written = [&](int j, float m) {
+    const bool keep = !cut || __float_as_uint(m) > wr.chi || ((km >> j) & 1ull);
+    return keep ? m * wr.inv : 0.f;  // (padding: NaN stays NaN)
+  };
+#pragma unroll
+  for (int j = 0; j < 16; ++j) row.xr[j] = written(j, row.xr[j]);
+  const int npt = row.npt;  // a multiple of 16
+  for (int j0 = 16; j0 < npt; j0 += 8) {
+    // eight slots read at once (one wait), then rewritten
+    float* slot = row.xl + (j0 - 16) * kThreads + t;
+    float m[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m[u] = slot[u * kThreads];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) R::opaque(m[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) slot[u * kThreads] = written(j0 + u, m[u]);
+  }
+  lds_barrier();  // the LDS chunks hold the written values; the masks are consumed
+  float(*cs)[cascade::kStreams + 1] = reinterpret_cast<float(*)[cascade::kStreams + 1]>(&sh);
+  const int s = t & 31;
+  const int c_thread = 2 * (t >> 6) + ((t >> 5) & 1);
+  if (c_thread < geo.full_chunks) {
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) a += row.xr[e];
+    cs[c_thread][s] = a;
+  }
+  for (int c = 32 + c_thread; c < geo.full_chunks; c += 32) {
+    // LDS slot of column 16384 + i is i (chunk 16 + i / 1024, thread i % 1024)
+    const float* x = row.xl + (c - 32) * 512 + s;
+    float m[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) m[e] = x[32 * e];
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) a += m[e];
+    cs[c][s] = a;
+  }
+  lds_barrier();
+  if (pm) {
+    for (int i = t; i < geo.groups * cascade::kStreams; i += kThreads) {
+      const int g = i / cascade::kStreams, st = i % cascade::kStreams;
+      const int c_end = (int)min((int64_t)(g + 1) * cascade::kGroupChunks, geo.full_chunks);
+      float acc1 = 0.f;
+      for (int c = g * cascade::kGroupChunks; c < c_end; ++c) acc1 += cs[c][st];
+      pm[i] = acc1;
+    }
+  }
+  __attribute__((address_space(1))) float* gdst = (__attribute__((address_space(1))) float*)dst;
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    if (row.xr[j] == row.xr[j]) gdst[row.col(j)] = row.xr[j];
+  for (int j0 = 16; j0 < npt; j0 += 8) {
+    const float* slot = row.xl + (j0 - 16) * kThreads + t;
+    float m[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m[u] = slot[u * kThreads];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) R::opaque(m[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (m[u] == m[u]) gdst[(int64_t)(j0 + u) * kThreads + t] = m[u];
+  }
+}
+
 // Top-k / top-p cut and the output of one row.  Returns false, having written
 // nothing, when a cut falls in a bin more crowded than the list (the caller then
 // runs the exact path).
 template <class Shared, class R>
 __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __restrict__ dst,
                                            bool do_k, bool do_p, unsigned long long kk, float p,
-                                           double z) {
+                                           double z, float* __restrict__ pm) {
   const int t = threadIdx.x;
   int stages = 2;  // histogram stages admitted so far (0 and 1 by the mass pass)
 
@@ -720,6 +840,12 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   const float inv = (float)(kFixScale / (double)cut.kept);
   uint32_t clo, chi;
   bin_bits(cut.bin, clo, chi);
+  if constexpr (R::kSeq) {
+    if (pm) {
+      seq_finish(sh, const_cast<R&>(row), Written{inv, clo, chi, cut.kept_in_bin}, true, pm, dst);
+      return true;
+    }
+  }
   // stores through a global-space pointer: they cannot alias the row's LDS chunks, so
   // the next chunks' LDS reads need not wait for them
   __attribute__((address_space(1))) float* gdst = (__attribute__((address_space(1))) float*)dst;
@@ -728,7 +854,7 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
     // cut bin's tokens are written from the list below (NaN: padding); one store
     const uint32_t bits = __float_as_uint(e);
     const float v = bits > chi ? e * inv : 0.f;
-    if (e == e && (bits > chi || bits < clo)) gdst[(int64_t)j * kThreads + t] = v;
+    if (e == e && (bits > chi || bits < clo)) gdst[row.col(j)] = v;
   });
   const int nl = min((int)sh.list_n, Shared::kCap);
   for (int i = t; i < nl; i += kThreads) {
@@ -835,6 +961,12 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     return;
   }
   __shared__ float xlds[NLDS > 0 ? NLDS * kThreads : 1];
+  // the p row's acceptance partials formed on chip (kSeq rows), else read back below
+  constexpr bool kSeq = Row<DT, NREG, NLDS, kTail>::kSeq;
+  float* const pm_row =
+      kSeq && pm_out ? pm_out + (int64_t)blockIdx.x * cascade::row_geom(V).groups * cascade::kStreams
+                     : nullptr;
+  bool pm_done = false;
   do {
   const int64_t r = blockIdx.x;
   const int64_t src_r = rows ? rows[r] : r;
@@ -859,9 +991,38 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
     lmax = ok ? fmaxf(lmax, l) : lmax;
   };
   auto fetch = [&](int j) {
-    return row.valid(j) ? load_as_f32<DT>(row.src, (int64_t)j * kThreads + t) : 0.f;
+    return row.valid(j) ? load_as_f32<DT>(row.src, row.col(j)) : 0.f;
   };
-  if (NPT > 0) {
+  if constexpr (DT == RLT_F32 && NLDS > 0 && !kTail && NREG <= 16) {
+    // every chunk in flight at once: register chunks into VGPRs, LDS chunks copied
+    // straight into their LDS slots (each lane's dword lands at its own slot), then
+    // the maximum and NaN test of the LDS chunks read back by their own lanes (the
+    // variants with more register chunks keep the batched form below: the copies'
+    // addresses cost them spills)
+    typedef __attribute__((address_space(3))) void lds_void_t;
+    float raw[NREG > 0 ? NREG : 1];
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) raw[j] = fetch(j);
+#pragma unroll
+    for (int jj = 0; jj < NLDS; ++jj) {
+      const int j = NREG + jj;
+      if (row.valid(j))
+        __builtin_amdgcn_global_load_lds(
+            (const void*)((const float*)row.src + row.col(j)),
+            (lds_void_t*)(xlds + jj * kThreads + w * 64), 4, 0, 0);
+      else
+        xlds[jj * kThreads + t] = NAN;
+    }
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) take_raw(j, raw[j]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll 8
+    for (int jj = 0; jj < NLDS; ++jj) {
+      const float l = xlds[jj * kThreads + t];
+      nan |= row.valid(NREG + jj) && l != l;
+      lmax = fmaxf(lmax, l);  // padding holds NaN, which fmaxf ignores
+    }
+  } else if (NPT > 0) {
     // every register chunk and the first LDS batch in flight at once; each LDS
     // batch is consumed while the next one loads
     constexpr int kB = 16;
@@ -958,25 +1119,35 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   const double z = block_sum_f64(sh, zs);
   if (!do_k && !do_p) {
     const float inv = (float)(1.0 / z);
+    if constexpr (kSeq) {
+      if (pm_row) {
+        seq_finish(sh, row, Written{inv, 0u, 0u, 0u}, false, pm_row, dst);
+        pm_done = true;
+        break;
+      }
+    }
     row.for_chunks_e4([&](int j, float e) {
-      if (e == e) dst[(int64_t)j * kThreads + t] = e * inv;
+      if (e == e) dst[row.col(j)] = e * inv;
     });
     break;
   }
 
   const unsigned long long kk =
       (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
-  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z)) {
+  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z, pm_row)) {
     __syncthreads();
     exact::exact_row<DT, kTC>(lds.ex, logits, src_r, row_stride, V, temperature, top_k, top_p,
                               max_top_k, apply_top_p, out, out_stride);
+  } else {
+    pm_done = pm_row != nullptr;
   }
   } while (0);
-  if (pm_out) {
+  if (pm_out && !pm_done) {
     // the written row's float32 row-sum partials for the acceptance sampler (p row r
-    // at pm_out + r * groups * 32): the row is read back from L2 after the barrier,
-    // which makes every wave's stores visible to the workgroup; eight 8192-float
-    // groups per pass, staged like the q rows' blocks above
+    // at pm_out + r * groups * 32) where seq_finish did not form them (rows of the
+    // other variants, the exact path, rows written as NaN): the row is read back after
+    // the barrier, which makes every wave's stores visible to the workgroup; eight
+    // 8192-float groups per pass, staged like the q rows' blocks above
     __syncthreads();
     cascade::ChunkSums* cs = reinterpret_cast<cascade::ChunkSums*>(&lds);
     const cascade::RowGeom geo = cascade::row_geom(V);
