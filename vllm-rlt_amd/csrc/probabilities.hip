@@ -54,6 +54,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace {
 
 #include "probs_exact.h"
@@ -686,6 +688,17 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Store of a written probability, streamed (non-temporal) when no pass of the launch
+// reads the row back: the next launch at most reads it, and lines left dirty in the L2
+// would be written back at the kernel boundary, ahead of that launch's own work.  (A
+// compile-time choice: a runtime branch between the two stores is merged into one
+// plain store by the compiler.)
+template <bool kStream, class P>
+__device__ __forceinline__ void put(P dst, float v) {
+  if constexpr (kStream) __builtin_nontemporal_store(v, dst);
+  else *dst = v;
+}
+
 // What a written row holds, per token: e * inv above the cut bin (bits > chi), 0 below
 // it (bits < clo), and in the cut bin e * inv for the first kept_n tokens of the
 // sorted list, 0 for the others.
@@ -701,7 +714,8 @@ struct Written {
 // chunk masks), the row-sum partials are formed from those values (the register chunks'
 // streams by their own threads, the LDS chunks' streams read across threads; chunk sums
 // meet in LDS, then stream s of group g adds its chunks in order), and only then is the
-// row stored, so no barrier waits behind the stores.  `cut` false: an unfiltered row.
+// row stored (streamed), so no barrier waits behind the stores.  `cut` false: an
+// unfiltered row.
 template <class Shared, class R>
 __device__ __forceinline__ void seq_finish(Shared& sh, R& row, const Written& wr, bool cut,
                                            float* __restrict__ pm, float* __restrict__ dst) {
@@ -776,7 +790,7 @@ __device__ __forceinline__ void seq_finish(Shared& sh, R& row, const Written& wr
   __attribute__((address_space(1))) float* gdst = (__attribute__((address_space(1))) float*)dst;
 #pragma unroll
   for (int j = 0; j < 16; ++j)
-    if (row.xr[j] == row.xr[j]) gdst[row.col(j)] = row.xr[j];
+    if (row.xr[j] == row.xr[j]) put<true>(&gdst[row.col(j)], row.xr[j]);
   for (int j0 = 16; j0 < npt; j0 += 8) {
     const float* slot = row.xl + (j0 - 16) * kThreads + t;
     float m[8];
@@ -786,7 +800,7 @@ __device__ __forceinline__ void seq_finish(Shared& sh, R& row, const Written& wr
     for (int u = 0; u < 8; ++u) R::opaque(m[u]);
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (m[u] == m[u]) gdst[(int64_t)(j0 + u) * kThreads + t] = m[u];
+      if (m[u] == m[u]) put<true>(&gdst[(int64_t)(j0 + u) * kThreads + t], m[u]);
   }
 }
 
@@ -796,7 +810,7 @@ __device__ __forceinline__ void seq_finish(Shared& sh, R& row, const Written& wr
 template <class Shared, class R>
 __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __restrict__ dst,
                                            bool do_k, bool do_p, unsigned long long kk, float p,
-                                           double z, float* __restrict__ pm) {
+                                           double z, float* __restrict__ pm, bool stream) {
   const int t = threadIdx.x;
   int stages = 2;  // histogram stages admitted so far (0 and 1 by the mass pass)
 
@@ -849,19 +863,24 @@ __device__ __forceinline__ bool filter_row(Shared& sh, const R& row, float* __re
   // stores through a global-space pointer: they cannot alias the row's LDS chunks, so
   // the next chunks' LDS reads need not wait for them
   __attribute__((address_space(1))) float* gdst = (__attribute__((address_space(1))) float*)dst;
-  row.for_chunks_e4([&](int j, float e) {
-    // bins before the cut bin hold larger masses (kept), later bins smaller ones; the
-    // cut bin's tokens are written from the list below (NaN: padding); one store
-    const uint32_t bits = __float_as_uint(e);
-    const float v = bits > chi ? e * inv : 0.f;
-    if (e == e && (bits > chi || bits < clo)) gdst[row.col(j)] = v;
-  });
-  const int nl = min((int)sh.list_n, Shared::kCap);
-  for (int i = t; i < nl; i += kThreads) {
-    const unsigned long long v = sh.list[i];
-    const float e = row.mass(key_value(~(uint32_t)(v >> 32)));
-    dst[(uint32_t)v] = (uint32_t)i < cut.kept_in_bin ? e * inv : 0.f;
-  }
+  auto output = [&](auto stream_tag) {
+    constexpr bool kStream = decltype(stream_tag)::value;
+    row.for_chunks_e4([&](int j, float e) {
+      // bins before the cut bin hold larger masses (kept), later bins smaller ones; the
+      // cut bin's tokens are written from the list below (NaN: padding); one store
+      const uint32_t bits = __float_as_uint(e);
+      const float v = bits > chi ? e * inv : 0.f;
+      if (e == e && (bits > chi || bits < clo)) put<kStream>(&gdst[row.col(j)], v);
+    });
+    const int nl = min((int)sh.list_n, Shared::kCap);
+    for (int i = t; i < nl; i += kThreads) {
+      const unsigned long long v = sh.list[i];
+      const float e = row.mass(key_value(~(uint32_t)(v >> 32)));
+      put<kStream>(&dst[(uint32_t)v], (uint32_t)i < cut.kept_in_bin ? e * inv : 0.f);
+    }
+  };
+  if (stream) output(std::true_type{});
+  else output(std::false_type{});
   return true;
 }
 
@@ -1126,15 +1145,20 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
         break;
       }
     }
-    row.for_chunks_e4([&](int j, float e) {
-      if (e == e) dst[row.col(j)] = e * inv;
-    });
+    auto output = [&](auto stream_tag) {
+      constexpr bool kStream = decltype(stream_tag)::value;
+      row.for_chunks_e4([&](int j, float e) {
+        if (e == e) put<kStream>(&dst[row.col(j)], e * inv);
+      });
+    };
+    if (pm_out == nullptr) output(std::true_type{});  // (nothing reads the row back)
+    else output(std::false_type{});
     break;
   }
 
   const unsigned long long kk =
       (unsigned long long)(k_eff < (int64_t)max_top_k ? k_eff : (int64_t)max_top_k);
-  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z, pm_row)) {
+  if (!filter_row(sh, row, dst, do_k, do_p, kk, p, z, pm_row, pm_out == nullptr)) {
     __syncthreads();
     exact::exact_row<DT, kTC>(lds.ex, logits, src_r, row_stride, V, temperature, top_k, top_p,
                               max_top_k, apply_top_p, out, out_stride);

@@ -411,6 +411,8 @@ __device__ __forceinline__ void slice_tiles(const float (&y)[E], int64_t c0, int
   }
 }
 
+typedef float f32v4 __attribute__((ext_vector_type(4)));
+
 template <int DT, int E, bool kVec, bool kFull>
 __device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t c0, int V,
                                            bool nan_row, float lmax, float c, float inv,
@@ -431,13 +433,17 @@ __device__ __forceinline__ void write_body(const void* __restrict__ src, int64_t
 #pragma unroll
   for (int q = 0; q < E / 4; ++q) {
     const uint32_t col = elem_col<E>(base, 4 * q);
+    // streamed stores: no pass of the launch reads the row back (the partials and
+    // tile totals come from y), and lines left dirty in the L2 would be written back
+    // at the kernel boundary, ahead of the next launch's work
     if (kVec && out_vec) {
       if (kFull || (int64_t)col < V)
-        *(float4*)(dst + col) = make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]);
+        __builtin_nontemporal_store(f32v4{y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]},
+                                    (f32v4*)(dst + col));
     } else {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (kFull || (int64_t)col + k < V) dst[col + k] = y[4 * q + k];
+        if (kFull || (int64_t)col + k < V) __builtin_nontemporal_store(y[4 * q + k], dst + col + k);
     }
   }
   if (ts) slice_tiles<E, kFull>(y, c0, V, ts, tf, c0 / (16 * kThreads), tiles);
