@@ -483,6 +483,7 @@ def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vo
     (torch.float16, 151936, 2, 3, True),
     (torch.bfloat16, 5000, 40, 8, True),
     (torch.float32, 49152, 32, 4, True),
+    (torch.float32, 20000, 8, 3, True),  # LDS chunks past V, a partial last cascade group
     # no row filtered: the row-split distributions, whose write launch also sums p
     (torch.float32, 65536, 24, 4, False),
     (torch.float32, 49152, 32, 4, False),
@@ -494,8 +495,8 @@ def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, 
     one launch, then the acceptance) is bitwise verify_distributions over every row
     followed by speculative_accept; its targets equal torch's argmax (NaN rows, ties at
     the maximum, signed zeros, all -inf rows).  The p rows' row sums are formed on chip
-    for 16 register chunks (V in (16384, 49152]: 32000, 49152) and read back otherwise,
-    both in one launch when a flat row takes the exact path."""
+    for 16 register chunks (V in (16384, 49152]: 20000, 32000, 49152) and read back
+    otherwise, both in one launch when a flat row takes the exact path."""
     _say("verify accept", dtype, vocab, n, w1, filtered)
     g = torch.Generator().manual_seed(vocab + n)
     rows = n * (w1 + 1)
