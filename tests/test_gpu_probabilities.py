@@ -332,15 +332,17 @@ def test_crowded_rows_use_the_exact_path(pkg, dev, vocab):
 # ------------------------------------------------------------ draft proposals
 
 @pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 5000),
-                                         (torch.float16, 65536)])
+                                         (torch.float16, 65536), (torch.bfloat16, 20000)])
 def test_propose_drafts_matches_reference_composition(pkg, dev, dtype, vocab):
     """async_speculative.py:645-663: argmax for every drafting row, random rows
-    replaced by categorical(q_o, u); q_o written into the q[:, offset] view."""
+    replaced by categorical(q_o, u); q_o written into the q[:, offset] view (a NaN row,
+    and a flat row whose top-k cut takes the exact path)."""
     _say("propose_drafts", dtype, vocab)
     g = torch.Generator().manual_seed(vocab)
     m = 12
     logits = (torch.randn(m, vocab, generator=g) * 3).to(dtype)
     logits[5, 17] = float("nan")  # a NaN row: argmax picks the NaN, its q row is NaN
+    logits[9] = 1.0  # a flat row: its top-k cut takes the exact path
     random_rows = torch.tensor([0, 3, 4, 5, 9, 11])
     r = len(random_rows)
     t = torch.tensor([0.7, 1.0, 0.5, 1.0, 1.3, 0.9])
