@@ -58,6 +58,116 @@
 
 namespace {
 
+// ------------------------------------------------------------------ lane exchanges
+//
+// The value of lane ^ J, J a power of two below 64, without an LDS round trip (a
+// ds_bpermute per 32 bits): DPP within 16-lane rows for J <= 8 (quad permutations for
+// 1 and 2, the two 4-lane row shifts selected by lane bit 2 for 4, a rotation by 8 for
+// 8), the gfx950 lane-swap instructions for 16 and 32.  Reductions built on them keep
+// the xor-tree order of the shuffles they replace, so every sum has the same bits.
+// Used by the distribution variants with more than 16 register chunks (V > 49152),
+// where they shorten the selection's reductions by several microseconds; the smaller
+// variants measured slightly slower with them (code placement) and keep the shuffles.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t x) {
+  static_assert(J == 1 || J == 2 || J == 4 || J == 8 || J == 16 || J == 32, "lane distance");
+  const int lane = threadIdx.x & 63;
+  const int v = (int)x;
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);  // [1,0,3,2]
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);  // [2,3,0,1]
+  } else if constexpr (J == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, false);  // lane + 4
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // lane - 4
+    return (uint32_t)((lane & 4) ? dn : up);
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // ror 8
+  } else if constexpr (J == 16) {
+    const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? a[0] : a[1];
+  } else {
+    const auto a = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? a[0] : a[1];
+  }
+}
+
+template <int J, typename T>
+__device__ __forceinline__ T xor_val(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "lane value");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, xor_lane<J>(__builtin_bit_cast(uint32_t, v)));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = xor_lane<J>((uint32_t)b), hi = xor_lane<J>((uint32_t)(b >> 32));
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+
+// The value of lane ^ j (j a power of two below 64): lane exchanges (kFast) or a shuffle.
+template <bool kFast, typename T>
+__device__ __forceinline__ T xor_at(T v, int j) {
+  if constexpr (!kFast) {
+    return __shfl_xor(v, j, RLT_WAVE);
+  } else {
+    switch (j) {
+      case 1: return xor_val<1>(v);
+      case 2: return xor_val<2>(v);
+      case 4: return xor_val<4>(v);
+      case 8: return xor_val<8>(v);
+      case 16: return xor_val<16>(v);
+      default: return xor_val<32>(v);
+    }
+  }
+}
+
+// A 32- or 64-bit value moved by a DPP row pattern (lanes without a source read 0).
+template <int kCtrl, typename T>
+__device__ __forceinline__ T dpp_val(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(
+        T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo =
+        (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, kCtrl, 0xf, 0xf, false);
+    const uint64_t hi =
+        (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), kCtrl, 0xf, 0xf, false);
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+
+// Inclusive prefix sum of an integer over the 64 lanes (the same value in any order).
+// kFast: steps within each 16-lane row (row_shr 1, 2, 4, 8), then rows 0 -> 1 and
+// 2 -> 3 (row_bcast 15), then lanes 0..31 -> 32..63 (row_bcast 31); else shuffles.
+template <bool kFast, typename T>
+__device__ __forceinline__ T wave_incl_scan(T x) {
+  static_assert(std::is_integral<T>::value, "integer scan");
+  const int lane = threadIdx.x & 63;
+  if constexpr (!kFast) {
+    for (int off = 1; off < 64; off <<= 1) {
+      const T y = __shfl_up(x, off, RLT_WAVE);
+      if (lane >= off) x += y;
+    }
+    return x;
+  } else {
+    const int r = lane & 15;
+    T y = dpp_val<0x111>(x);
+    if (r >= 1) x += y;
+    y = dpp_val<0x112>(x);
+    if (r >= 2) x += y;
+    y = dpp_val<0x114>(x);
+    if (r >= 4) x += y;
+    y = dpp_val<0x118>(x);
+    if (r >= 8) x += y;
+    y = dpp_val<0x142>(x);
+    if (lane & 16) x += y;
+    y = dpp_val<0x143>(x);
+    if (lane >= 32) x += y;
+    return x;
+  }
+}
+
 #include "probs_exact.h"
 
 constexpr int kThreads = 1024;
@@ -143,9 +253,18 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-template <typename T>
+template <typename T, bool kFast = false>
 __device__ __forceinline__ T wave_sum(T v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, RLT_WAVE);
+  if constexpr (kFast) {
+    v += xor_val<32>(v);
+    v += xor_val<16>(v);
+    v += xor_val<8>(v);
+    v += xor_val<4>(v);
+    v += xor_val<2>(v);
+    v += xor_val<1>(v);
+  } else {
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, RLT_WAVE);
+  }
   return v;
 }
 
@@ -180,8 +299,8 @@ struct SharedT {
 template <class Shared>
 __device__ __forceinline__ void block_sum2(Shared& sh, uint32_t& a, unsigned long long& b) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  a = wave_sum(a);
-  b = wave_sum(b);
+  a = wave_sum<uint32_t, !Shared::kF64Top>(a);
+  b = wave_sum<unsigned long long, !Shared::kF64Top>(b);
   if (lane == 0) {
     sh.wave_u32[w] = a;
     sh.wave_u64[w] = b;
@@ -199,7 +318,7 @@ __device__ __forceinline__ void block_sum2(Shared& sh, uint32_t& a, unsigned lon
 template <class Shared>
 __device__ __forceinline__ double block_sum_f64(Shared& sh, double v) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  v = wave_sum(v);
+  v = wave_sum<double, !Shared::kF64Top>(v);
   if (lane == 0) sh.wave_f64[w] = v;
   __syncthreads();
   double s = 0.0;
@@ -212,9 +331,17 @@ __device__ __forceinline__ double block_sum_f64(Shared& sh, double v) {
 template <class Shared>
 __device__ __forceinline__ void block_minmax(Shared& sh, uint32_t& lo, uint32_t& hi) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int off = 32; off >= 1; off >>= 1) {
-    lo = min(lo, (uint32_t)__shfl_xor(lo, off, RLT_WAVE));
-    hi = max(hi, (uint32_t)__shfl_xor(hi, off, RLT_WAVE));
+  if constexpr (!Shared::kF64Top) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      lo = min(lo, xor_at<true>(lo, off));
+      hi = max(hi, xor_at<true>(hi, off));
+    }
+  } else {
+    for (int off = 32; off >= 1; off >>= 1) {
+      lo = min(lo, (uint32_t)__shfl_xor(lo, off, RLT_WAVE));
+      hi = max(hi, (uint32_t)__shfl_xor(hi, off, RLT_WAVE));
+    }
   }
   if (lane == 0) {
     sh.wave_u32[w] = lo;
@@ -253,12 +380,17 @@ __device__ __forceinline__ void scan_select(Shared& sh, int nb, uint32_t cnt_bef
   }
   const uint32_t c_run = c;
   const unsigned long long m_run = m;
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t cy = __shfl_up(c, off, RLT_WAVE);
-    const unsigned long long my = __shfl_up(m, off, RLT_WAVE);
-    if (lane >= off) {
-      c += cy;
-      m += my;
+  if constexpr (!Shared::kF64Top) {
+    c = wave_incl_scan<true>(c);
+    m = wave_incl_scan<true>(m);
+  } else {
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t cy = __shfl_up(c, off, RLT_WAVE);
+      const unsigned long long my = __shfl_up(m, off, RLT_WAVE);
+      if (lane >= off) {
+        c += cy;
+        m += my;
+      }
     }
   }
   if (t == 0) {
@@ -598,7 +730,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
         for (int k = 2; k <= RLT_WAVE; k <<= 1) {
 #pragma unroll
           for (int j = k >> 1; j > 0; j >>= 1) {
-            const unsigned long long o = __shfl_xor(v, j, RLT_WAVE);
+            const unsigned long long o = xor_at<!Shared::kF64Top>(v, j);
             const bool keep_min = ((lane & k) == 0) == ((lane & j) == 0);
             v = keep_min ? (o < v ? o : v) : (o < v ? v : o);
           }
@@ -610,15 +742,12 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       // while the cut criterion is not reached
       const unsigned long long fm =
           lane < nl ? fixed_mass(row.mass(key_value(~(uint32_t)(v >> 32)))) : 0ull;
-      unsigned long long incl = fm;
-      for (int off = 1; off < 64; off <<= 1) {
-        const unsigned long long y = __shfl_up(incl, off, RLT_WAVE);
-        if (lane >= off) incl += y;
-      }
+      const unsigned long long incl = wave_incl_scan<!Shared::kF64Top>(fm);
       const unsigned long long before = mass_before + incl - fm;
       const bool keep =
           lane < nl && (kMass ? before <= limit : (uint32_t)lane < limit - cnt_before);
-      const unsigned long long km = wave_sum(keep ? fm : 0ull);
+      const unsigned long long km =
+          wave_sum<unsigned long long, !Shared::kF64Top>(keep ? fm : 0ull);
       const uint32_t kn = (uint32_t)__popcll(__ballot(keep));  // (the whole wave votes)
       if (lane == 0) {
         sh.sel_kept_in_bin = kn;
@@ -657,11 +786,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
     if (idx < nl) fm[i] = fixed_mass(row.mass(key_value(~(uint32_t)(sh.list[idx] >> 32))));
     run += fm[i];
   }
-  unsigned long long incl = run;
-  for (int off = 1; off < 64; off <<= 1) {
-    const unsigned long long y = __shfl_up(incl, off, RLT_WAVE);
-    if (lane >= off) incl += y;
-  }
+  const unsigned long long incl = wave_incl_scan<!Shared::kF64Top>(run);
   if (lane == 63) sh.wave_u64[t >> 6] = incl;
   __syncthreads();
   unsigned long long before = mass_before + incl - run;
@@ -1085,7 +1210,12 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
       lmax = fmaxf(lmax, l);  // padding reads NaN, which fmaxf ignores
     });
   }
-  for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, RLT_WAVE));
+  if constexpr (!decltype(lds.fast)::kF64Top) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, xor_at<true>(lmax, off));
+  } else {
+    for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, RLT_WAVE));
+  }
   const uint64_t nan_b = __ballot(nan);
   if (lane == 0) {
     sh.wave_f64[w] = lmax;
