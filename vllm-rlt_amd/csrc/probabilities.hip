@@ -65,9 +65,10 @@ namespace {
 // 1 and 2, the two 4-lane row shifts selected by lane bit 2 for 4, a rotation by 8 for
 // 8), the gfx950 lane-swap instructions for 16 and 32.  Reductions built on them keep
 // the xor-tree order of the shuffles they replace, so every sum has the same bits.
-// Used by the distribution variants with more than 16 register chunks (V > 49152),
-// where they shorten the selection's reductions by several microseconds; the smaller
-// variants measured slightly slower with them (code placement) and keep the shuffles.
+// Used by the distribution variants with more than 16 register chunks (V > 49152) and
+// the long-row variant, where they shorten the selection's reductions (by ~6 us of a
+// 65 us launch at V = 65536); the smaller variants measured slightly slower with them
+// (code placement) and keep the shuffles.
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t x) {
   static_assert(J == 1 || J == 2 || J == 4 || J == 8 || J == 16 || J == 32, "lane distance");
@@ -270,9 +271,11 @@ __device__ __forceinline__ T wave_sum(T v) {
 
 #include "probs_split.h"
 
-template <int CAP, bool F64TOP = false>
+template <int CAP, bool F64TOP = false, bool FAST_LANES = false>
 struct SharedT {
   static constexpr int kCap = CAP;
+  // the selection's reductions and scans by lane exchanges (xor_lane, wave_incl_scan)
+  static constexpr bool kFastLanes = FAST_LANES;
   // the top bins' masses as float64 sums (bin_mass); kernels whose registers are all
   // taken keep fixed-point sums (the float64 conversion costs them spills)
   static constexpr bool kF64Top = F64TOP;
@@ -299,8 +302,8 @@ struct SharedT {
 template <class Shared>
 __device__ __forceinline__ void block_sum2(Shared& sh, uint32_t& a, unsigned long long& b) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  a = wave_sum<uint32_t, !Shared::kF64Top>(a);
-  b = wave_sum<unsigned long long, !Shared::kF64Top>(b);
+  a = wave_sum<uint32_t, Shared::kFastLanes>(a);
+  b = wave_sum<unsigned long long, Shared::kFastLanes>(b);
   if (lane == 0) {
     sh.wave_u32[w] = a;
     sh.wave_u64[w] = b;
@@ -318,7 +321,7 @@ __device__ __forceinline__ void block_sum2(Shared& sh, uint32_t& a, unsigned lon
 template <class Shared>
 __device__ __forceinline__ double block_sum_f64(Shared& sh, double v) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  v = wave_sum<double, !Shared::kF64Top>(v);
+  v = wave_sum<double, Shared::kFastLanes>(v);
   if (lane == 0) sh.wave_f64[w] = v;
   __syncthreads();
   double s = 0.0;
@@ -331,7 +334,7 @@ __device__ __forceinline__ double block_sum_f64(Shared& sh, double v) {
 template <class Shared>
 __device__ __forceinline__ void block_minmax(Shared& sh, uint32_t& lo, uint32_t& hi) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if constexpr (!Shared::kF64Top) {
+  if constexpr (Shared::kFastLanes) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       lo = min(lo, xor_at<true>(lo, off));
@@ -380,7 +383,7 @@ __device__ __forceinline__ void scan_select(Shared& sh, int nb, uint32_t cnt_bef
   }
   const uint32_t c_run = c;
   const unsigned long long m_run = m;
-  if constexpr (!Shared::kF64Top) {
+  if constexpr (Shared::kFastLanes) {
     c = wave_incl_scan<true>(c);
     m = wave_incl_scan<true>(m);
   } else {
@@ -730,7 +733,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
         for (int k = 2; k <= RLT_WAVE; k <<= 1) {
 #pragma unroll
           for (int j = k >> 1; j > 0; j >>= 1) {
-            const unsigned long long o = xor_at<!Shared::kF64Top>(v, j);
+            const unsigned long long o = xor_at<Shared::kFastLanes>(v, j);
             const bool keep_min = ((lane & k) == 0) == ((lane & j) == 0);
             v = keep_min ? (o < v ? o : v) : (o < v ? v : o);
           }
@@ -742,12 +745,12 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
       // while the cut criterion is not reached
       const unsigned long long fm =
           lane < nl ? fixed_mass(row.mass(key_value(~(uint32_t)(v >> 32)))) : 0ull;
-      const unsigned long long incl = wave_incl_scan<!Shared::kF64Top>(fm);
+      const unsigned long long incl = wave_incl_scan<Shared::kFastLanes>(fm);
       const unsigned long long before = mass_before + incl - fm;
       const bool keep =
           lane < nl && (kMass ? before <= limit : (uint32_t)lane < limit - cnt_before);
       const unsigned long long km =
-          wave_sum<unsigned long long, !Shared::kF64Top>(keep ? fm : 0ull);
+          wave_sum<unsigned long long, Shared::kFastLanes>(keep ? fm : 0ull);
       const uint32_t kn = (uint32_t)__popcll(__ballot(keep));  // (the whole wave votes)
       if (lane == 0) {
         sh.sel_kept_in_bin = kn;
@@ -786,7 +789,7 @@ __device__ __forceinline__ Cut select(Shared& sh, const R& row, unsigned long lo
     if (idx < nl) fm[i] = fixed_mass(row.mass(key_value(~(uint32_t)(sh.list[idx] >> 32))));
     run += fm[i];
   }
-  const unsigned long long incl = wave_incl_scan<!Shared::kF64Top>(run);
+  const unsigned long long incl = wave_incl_scan<Shared::kFastLanes>(run);
   if (lane == 63) sh.wave_u64[t >> 6] = incl;
   __syncthreads();
   unsigned long long before = mass_before + incl - run;
@@ -1065,7 +1068,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
   constexpr int kCapV = NLDS > 32 ? 512 : NLDS == 32 ? 1024 : 2048;
   constexpr int kTC = NPT > 0 && !kTail ? NPT : kMaxStreamChunks;
   union Lds {
-    SharedT<kCapV, (NREG <= 16)> fast;
+    SharedT<kCapV, (NREG <= 16), (NREG > 16 || kTail)> fast;
     exact::SharedT<kTC> ex;
   };
   __shared__ Lds lds;
@@ -1210,7 +1213,7 @@ __global__ __launch_bounds__(kThreads) void rlt_probs_kernel(
       lmax = fmaxf(lmax, l);  // padding reads NaN, which fmaxf ignores
     });
   }
-  if constexpr (!decltype(lds.fast)::kF64Top) {
+  if constexpr (decltype(lds.fast)::kFastLanes) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, xor_at<true>(lmax, off));
   } else {
