@@ -526,6 +526,8 @@ def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, 
         k, p = torch.full((rows,), -1), torch.ones(rows)
     else:
         k[0], p[0] = -1, 0.9  # the flat row's top-p cut
+        k[1], p[1] = 1, 1.0  # top-k 1: one kept token, from the cut bin's list
+        k[2], p[2] = -1, 0.0  # top-p 0 keeps one token
     plan = _host_args(k.tolist(), p.tolist(), vocab)
     q = (torch.randn(n, w1, vocab, generator=g) * 2).softmax(-1)
     u = torch.rand(n, 2 * w1 + 1, generator=g)
