@@ -106,6 +106,22 @@ def test_accept_ragged_drafts_and_poisoned_padding(pkg, dev):
     _check_accept(pkg, dev, q, p, u, dt, drafts)
 
 
+@pytest.mark.parametrize("w1,vocab", [(1, 4099), (8, 12289), (32, 4097), (32, 8190)])
+def test_accept_draft_widths_and_unaligned_vocab(pkg, dev, w1, vocab):
+    """Draft widths 1 to 32 (the kernels' limit) with vocabularies that are not a multiple of
+    4, so the weights take the scalar load path; low target noise makes long accepted runs, and
+    ragged draft counts put the stop row at every depth."""
+    _say("accept widths", w1, vocab)
+    g = torch.Generator().manual_seed(w1 * 100003 + vocab)
+    n = 12
+    q, p, u, dt = _verify_inputs(n, w1, vocab, g, noise=0.02)
+    drafts = torch.randint(0, w1 + 1, (n,), generator=g)
+    drafts[0] = w1
+    drafts[1] = 0
+    want = _check_accept(pkg, dev, q, p, u, dt, drafts)
+    assert not want.error.any()
+
+
 def test_accept_high_acceptance_and_unnormalized_weights(pkg, dev):
     _say("accept unnormalized")
     g = torch.Generator().manual_seed(78)
