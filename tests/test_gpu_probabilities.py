@@ -486,11 +486,13 @@ def test_verify_distributions_match_argmax_and_probabilities(pkg, dev, dtype, vo
     (torch.bfloat16, 5000, 40, 8, True),
     (torch.float32, 49152, 32, 4, True),
     (torch.float32, 20000, 8, 3, True),  # LDS chunks past V, a partial last cascade group
+    (torch.float32, 12289, 4, 32, True),  # the 32-draft limit, V off the 4-float alignment
     # no row filtered: the row-split distributions, whose write launch also sums p
     (torch.float32, 65536, 24, 4, False),
     (torch.float32, 49152, 32, 4, False),
     (torch.bfloat16, 40000 + 3, 5, 2, False),
     (torch.float16, 300, 4, 3, False),
+    (torch.float32, 8191, 3, 16, False),
 ])
 def test_verify_accept_equals_the_separate_calls(pkg, dev, dtype, vocab, n, w1, filtered):
     """verify_accept (distributions, argmax targets and the draft rows' partial sums in
