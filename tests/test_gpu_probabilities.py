@@ -332,7 +332,8 @@ def test_crowded_rows_use_the_exact_path(pkg, dev, vocab):
 # ------------------------------------------------------------ draft proposals
 
 @pytest.mark.parametrize("dtype,vocab", [(torch.float32, 49152), (torch.bfloat16, 5000),
-                                         (torch.float16, 65536), (torch.bfloat16, 20000)])
+                                         (torch.float16, 65536), (torch.bfloat16, 20000),
+                                         (torch.float32, 12289), (torch.float16, 4099)])
 def test_propose_drafts_matches_reference_composition(pkg, dev, dtype, vocab):
     """async_speculative.py:645-663: argmax for every drafting row, random rows
     replaced by categorical(q_o, u); q_o written into the q[:, offset] view (a NaN row,
